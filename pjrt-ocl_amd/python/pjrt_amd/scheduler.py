@@ -1,0 +1,599 @@
+"""Tensor VMProgram -> v3 schedule sections (tasks + per-lane entry streams).
+
+Contract with the device (reference: python/pjrt_ocl/scheduler.py:178-197,
+312-433, 451-715; docs/vmprogram.md "v2.1"):
+
+* one TASK per compute instruction; a task is cut into tiles whose count the
+  kernel recomputes identically (``n_tiles``);
+* lane streams hold ENTRIES ``(task, tile_lo, tile_hi)``; a global BARRIER is
+  emitted only where a dependency crosses lanes -- two elementwise ops over the
+  same element count chain on one lane (tile T of both stays on the lane that
+  owns T), every other dependency needs a barrier;
+* the tiles of each unit of a phase are split into contiguous chunks in
+  proportion to the unit's share of the phase cost, then list-scheduled
+  (longest first) onto the least-loaded lane;
+* WHILE / FOR / IF become a uniform control entry in every lane; their
+  sub-lists are scheduled after the root so they live at stream index
+  >= root_len, and the kernel supplies the loop barriers.
+
+The device parameters come from the runtime through the environment the plugin
+gives the lowering subprocess: PJRT_OCL_NLANES, PJRT_OCL_EW_TS, PJRT_OCL_MMA_T,
+PJRT_OCL_COST_TABLE, PJRT_OCL_FUSE (same variable names as the reference,
+plugin.cc:770-780).
+"""
+from __future__ import annotations
+
+import dataclasses
+import json
+import math
+import os
+
+from . import vmprogram as V
+
+# --- device configuration -----------------------------------------------------
+
+# Defaults for one MI355X when no environment is given: one lane per CU.
+DEFAULT_NLANES = 256
+DEFAULT_EW_TS = 4096
+DEFAULT_MMA_T = 128
+
+_COST_KEYS = {
+    V.TOP_EW: "ew_tile_us", V.TOP_MMA: "mma_tile_us",
+    V.TOP_GATHER: "gather_tile_us", V.TOP_GATHER_INDEX: "gather_tile_us",
+    V.TOP_RED_PART: "reduce_tile_us", V.TOP_RED_COMB: "reduce_tile_us",
+}
+
+
+class ScheduleError(NotImplementedError):
+    """Program valid but outside the scheduler's coverage (service exit 2)."""
+
+
+@dataclasses.dataclass
+class DeviceConfig:
+    nlanes: int = DEFAULT_NLANES
+    ew_ts: int = DEFAULT_EW_TS
+    mma_t: int = DEFAULT_MMA_T
+    costs: dict = dataclasses.field(default_factory=dict)
+    fuse: bool = True
+    # Per-task MMA tile selection (extension): pick the largest tile edge that
+    # still gives every lane work; False keeps every MMA at the default edge.
+    mma_autotile: bool = True
+
+    @classmethod
+    def from_env(cls, environ=None) -> "DeviceConfig":
+        env = os.environ if environ is None else environ
+
+        def geti(name, default):
+            try:
+                v = int(env.get(name, "") or default)
+            except ValueError:
+                v = default
+            return v
+
+        costs = {}
+        path = env.get("PJRT_OCL_COST_TABLE", "")
+        if path:
+            try:
+                with open(path) as f:
+                    raw = json.load(f)
+                costs = {k: float(raw[k]) for k in set(_COST_KEYS.values())
+                         if k in raw}
+            except (OSError, ValueError, TypeError):
+                costs = {}
+        return cls(nlanes=max(1, min(4096, geti("PJRT_OCL_NLANES", DEFAULT_NLANES))),
+                   ew_ts=max(64, geti("PJRT_OCL_EW_TS", DEFAULT_EW_TS)),
+                   mma_t=geti("PJRT_OCL_MMA_T", DEFAULT_MMA_T),
+                   costs=costs,
+                   fuse=env.get("PJRT_OCL_FUSE", "1") != "0",
+                   mma_autotile=env.get("PJRT_AMD_MMA_AUTOTILE", "1") != "0")
+
+
+# --- instruction -> task ------------------------------------------------------
+
+_BIN_SUB = {
+    V.OP_ADD_F32: V.SUB_ADD, V.OP_MUL_F32: V.SUB_MUL, V.OP_SUB_F32: V.SUB_SUB,
+    V.OP_DIV_F32: V.SUB_DIV, V.OP_MAX_F32: V.SUB_MAX, V.OP_MIN_F32: V.SUB_MIN,
+    V.OP_POW_F32: V.SUB_POW, V.OP_ATAN2_F32: V.SUB_ATAN2,
+    V.OP_REMAINDER_F32: V.SUB_REMAINDER, V.OP_AND: V.SUB_AND,
+    V.OP_OR: V.SUB_OR, V.OP_XOR: V.SUB_XOR, V.OP_SHL: V.SUB_SHL,
+    V.OP_SHR_L: V.SUB_SHR_L, V.OP_SHR_A: V.SUB_SHR_A,
+}
+_UN_SUB = {
+    V.OP_COPY_F32: V.SUB_COPY, V.OP_NEG_F32: V.SUB_NEG, V.OP_EXP_F32: V.SUB_EXP,
+    V.OP_LOG_F32: V.SUB_LOG, V.OP_SQRT_F32: V.SUB_SQRT,
+    V.OP_RSQRT_F32: V.SUB_RSQRT, V.OP_TANH_F32: V.SUB_TANH,
+    V.OP_ABS_F32: V.SUB_ABS, V.OP_FLOOR_F32: V.SUB_FLOOR,
+    V.OP_CEIL_F32: V.SUB_CEIL, V.OP_SIGN_F32: V.SUB_SIGN,
+    V.OP_LOG1P_F32: V.SUB_LOG1P, V.OP_EXPM1_F32: V.SUB_EXPM1,
+    V.OP_CBRT_F32: V.SUB_CBRT, V.OP_SIN_F32: V.SUB_SIN, V.OP_COS_F32: V.SUB_COS,
+    V.OP_TAN_F32: V.SUB_TAN, V.OP_ROUND_NEAREST_EVEN_F32: V.SUB_RINT,
+    V.OP_ROUND_NEAREST_AFZ_F32: V.SUB_ROUND, V.OP_NOT: V.SUB_NOT,
+    V.OP_GELU: V.SUB_GELU,
+}
+
+
+def red_chunk(n: int, ew_ts: int) -> int:
+    """Elements per REDUCE_PART tile (ops/reduce.py:81-87): at least one EW tile
+    and at most 256 partials."""
+    if n <= 0:
+        return 1
+    return max(ew_ts, math.ceil(n / 256))
+
+
+def mma_tile_edge(task: V.Task, cfg: DeviceConfig) -> int:
+    code = (task.p3 >> 24) & 0xF
+    return V.MMA_CODE_TILE.get(code, cfg.mma_t)
+
+
+def n_tiles(task: V.Task, cfg: DeviceConfig) -> int:
+    """Tile count of a task; the kernel decodes tile indices the same way."""
+    top = task.tile_op
+    if top in (V.TOP_EW, V.TOP_GATHER, V.TOP_IOTA_DIM, V.TOP_SCATTER,
+               V.TOP_DYN_GATHER, V.TOP_DYN_SCATTER, V.TOP_RED_WINDOW,
+               V.TOP_MAP_REGION, V.TOP_GATHER_INDEX, V.TOP_CONV,
+               V.TOP_SCATTER_INDEX):
+        return max(1, math.ceil(task.p1 / cfg.ew_ts))
+    if top == V.TOP_RED_STRIDED:
+        return max(1, math.ceil(task.p0 / cfg.ew_ts))
+    if top == V.TOP_MMA:
+        t = mma_tile_edge(task, cfg)
+        g = max(1, task.p3 & 0xFFFFFF)
+        return math.ceil(task.p0 / t) * math.ceil(task.p1 / t) * g
+    if top == V.TOP_RED_PART:
+        return max(1, math.ceil(task.p0 / task.p1)) if task.p1 else 1
+    if top == V.TOP_RED_COMB:
+        return 1
+    if top in (V.TOP_RED_SEG, V.TOP_SOFTMAX_SEG, V.TOP_LAYERNORM_SEG,
+               V.TOP_ARGMAX_SEG):
+        return max(1, task.p0)
+    if top == V.TOP_FLASH_ATTN:
+        return max(1, task.p1 * task.p2)
+    raise ScheduleError(f"n_tiles: unknown tile_op {top}")
+
+
+def instr_to_task(ins: V.Instr, prog: V.VMProgram, cfg: DeviceConfig) -> V.Task:
+    """One compute instruction -> its task (field meanings: the task table of
+    docs/vmprogram.md and each reference ops/*.py ``*_to_task``)."""
+    op = ins.op
+    bufs = prog.buffers
+    if op in _BIN_SUB:
+        t = V.Task(V.TOP_EW, ins.dst, ins.a, ins.b, _BIN_SUB[op], ins.n,
+                   ins.imm, ins.imm2)
+    elif op in _UN_SUB:
+        t = V.Task(V.TOP_EW, ins.dst, ins.a, ins.a, _UN_SUB[op], ins.n,
+                   ins.imm, 0)
+    elif op == V.OP_FILL_F32:
+        t = V.Task(V.TOP_EW, ins.dst, ins.dst, ins.dst, V.SUB_FILL, ins.n, ins.imm)
+    elif op == V.OP_IOTA_F32:
+        t = V.Task(V.TOP_EW, ins.dst, ins.dst, ins.dst, V.SUB_IOTA_FLAT, ins.n)
+    elif op == V.OP_LTS_F32:
+        t = V.Task(V.TOP_EW, ins.dst, ins.a, ins.b, V.SUB_LTS, 1)
+    elif op == V.OP_CMP_F32:
+        t = V.Task(V.TOP_EW, ins.dst, ins.a, ins.b, V.SUB_CMP, ins.n, ins.imm)
+    elif op == V.OP_SELECT_F32:
+        t = V.Task(V.TOP_EW, ins.dst, ins.a, ins.b, V.SUB_SELECT, ins.n, 0, ins.imm)
+    elif op == V.OP_CONVERT:
+        t = V.Task(V.TOP_EW, ins.dst, ins.a, ins.a, V.SUB_CONVERT, ins.n)
+    elif op == V.OP_BITCAST:
+        t = V.Task(V.TOP_EW, ins.dst, ins.a, ins.a, V.SUB_BITCAST, ins.n)
+    elif op == V.OP_IS_FINITE:
+        t = V.Task(V.TOP_EW, ins.dst, ins.a, ins.a, V.SUB_ISFINITE, ins.n)
+    elif op == V.OP_AFFINE_F32:
+        t = V.Task(V.TOP_EW, ins.dst, ins.a, ins.a, V.SUB_AFFINE, ins.n,
+                   ins.imm, ins.imm2)
+    elif op == V.OP_GATHER_STRIDED:
+        t = V.Task(V.TOP_GATHER, ins.dst, ins.a, ins.a, ins.aux, ins.n)
+    elif op == V.OP_IOTA_DIM:
+        t = V.Task(V.TOP_IOTA_DIM, ins.dst, ins.dst, ins.dst, ins.aux, ins.n)
+    elif op == V.OP_SCATTER:
+        t = V.Task(V.TOP_SCATTER, ins.dst, ins.a, ins.a, ins.aux, ins.n)
+    elif op == V.OP_DYNAMIC_SLICE:
+        t = V.Task(V.TOP_DYN_GATHER, ins.dst, ins.a, ins.a, ins.aux, ins.n)
+    elif op == V.OP_DYNAMIC_UPDATE_SLICE:
+        t = V.Task(V.TOP_DYN_SCATTER, ins.dst, ins.a, ins.a, ins.aux, ins.n)
+    elif op == V.OP_GATHER_INDEX:
+        t = V.Task(V.TOP_GATHER_INDEX, ins.dst, ins.a, ins.a, ins.aux, ins.n)
+    elif op == V.OP_REDUCE:
+        phase, kind = (ins.imm >> 3) & 1, ins.imm & 7
+        if phase == 0:
+            t = V.Task(V.TOP_RED_PART, ins.dst, ins.a, ins.a, ins.n,
+                       red_chunk(ins.n, cfg.ew_ts), kind)
+        else:
+            t = V.Task(V.TOP_RED_COMB, ins.dst, ins.a, ins.a, ins.n, kind)
+    elif op == V.OP_REDUCE_SEG:
+        t = V.Task(V.TOP_RED_SEG, ins.dst, ins.a, ins.a, ins.n,
+                   ins.imm & 0x0FFFFFFF, ins.imm >> 28)
+    elif op == V.OP_REDUCE_STRIDED:
+        t = V.Task(V.TOP_RED_STRIDED, ins.dst, ins.a, ins.a, ins.n,
+                   ins.imm & 0x0FFFFFFF, ins.imm2, ins.imm >> 28)
+    elif op == V.OP_SOFTMAX:
+        t = V.Task(V.TOP_SOFTMAX_SEG, ins.dst, ins.a, ins.a, ins.n, ins.imm)
+    elif op == V.OP_LAYERNORM:
+        t = V.Task(V.TOP_LAYERNORM_SEG, ins.dst, ins.a, ins.a, ins.n, ins.imm,
+                   ins.imm2)
+    elif op == V.OP_LAYERNORM_AFFINE:
+        # aux -> [flags, beta buffer id]; gamma rides in b.
+        flags, beta = prog.aux[ins.aux], prog.aux[ins.aux + 1]
+        t = V.Task(V.TOP_LAYERNORM_SEG, ins.dst, ins.a,
+                   ins.b if flags & V.LN_AFFINE else ins.a, ins.n, ins.imm,
+                   ins.imm2, flags, beta if flags & V.LN_AFFINE else ins.a)
+    elif op == V.OP_ARGMAX_SEG:
+        # dst = index output, b = value output (may alias a scratch), p2 = kind
+        t = V.Task(V.TOP_ARGMAX_SEG, ins.dst, ins.a, ins.b, ins.n, ins.imm,
+                   ins.imm2)
+    elif op == V.OP_MAP_REGION:
+        inp = list(ins.region_inputs) or _region_inputs_from_aux(ins, prog)
+        f = [inp[k] if k < len(inp) else inp[0] for k in range(8)]
+        t = V.Task(V.TOP_MAP_REGION, ins.dst, f[0], f[1], ins.aux, ins.n,
+                   f[2], f[3], f[4], f[5], f[6], f[7])
+    elif op == V.OP_FLASH_ATTN:
+        t = V.Task(V.TOP_FLASH_ATTN, ins.dst, ins.a, ins.b, ins.imm2, ins.n,
+                   ins.imm, ins.aux)
+    elif op == V.OP_DOT:
+        M, N, K, G = ins.n, ins.imm >> 16, ins.imm & 0xFFFF, max(1, ins.imm2)
+        aview, bview, epi, epi_res = ins.aview, ins.bview, ins.epi, ins.epi_res
+        if ins.aux and not (aview or bview or epi):
+            aview, bview, epi, epi_res = prog.aux[ins.aux:ins.aux + 4]
+        if N == 1 and G == 1 and not aview and not bview and not epi:
+            # GEMV: one matrix row per tile through the segmented reduce in dot
+            # mode (ops/dot.py:166-183).
+            t = V.Task(V.TOP_RED_SEG, ins.dst, ins.a, ins.b, M, K, 0, 1)
+        else:
+            code = V.MMA_TILE_CODES.get(ins.mma_tile, 0)
+            if not code and cfg.mma_autotile:
+                code = V.MMA_TILE_CODES[_auto_mma_tile(M, N, G, cfg)]
+            t = V.Task(V.TOP_MMA, ins.dst, ins.a, ins.b, M, N, K,
+                       G | (code << 24), aview, bview, epi,
+                       epi_res if epi else 0)
+    else:
+        raise ScheduleError(f"scheduler: no task mapping for opcode {op}")
+    t.dtype = bufs[ins.dst].dtype
+    t.adtype = bufs[ins.a].dtype if ins.a < len(bufs) else t.dtype
+    return t
+
+
+def _auto_mma_tile(M: int, N: int, G: int, cfg: DeviceConfig) -> int:
+    """Largest output tile edge whose tile count still covers the lanes (big
+    tiles raise MFMA arithmetic intensity; small matmuls need the parallelism)."""
+    for t in (256, 128, 64):
+        if math.ceil(M / t) * math.ceil(N / t) * G >= cfg.nlanes:
+            return t
+    return 64
+
+
+def _region_inputs_from_aux(ins: V.Instr, prog: V.VMProgram) -> list:
+    desc = ins.aux
+    n_in, n_micro = prog.aux[desc], prog.aux[desc + 2]
+    tail = desc + 3 + n_in + 6 * n_micro
+    return [prog.aux[tail + k] for k in range(n_in)]
+
+
+def instr_reads(ins: V.Instr, prog: V.VMProgram) -> set:
+    op = ins.op
+    if op in (V.OP_NOP, V.OP_FILL_F32, V.OP_IOTA_F32, V.OP_IOTA_DIM):
+        return set()
+    if op in _UN_SUB or op in (V.OP_CONVERT, V.OP_BITCAST, V.OP_IS_FINITE,
+                               V.OP_AFFINE_F32, V.OP_GATHER_STRIDED,
+                               V.OP_REDUCE, V.OP_REDUCE_SEG,
+                               V.OP_REDUCE_STRIDED, V.OP_SOFTMAX,
+                               V.OP_LAYERNORM, V.OP_SCATTER):
+        r = {ins.a}
+    elif op == V.OP_SELECT_F32:
+        r = {ins.a, ins.b, ins.imm}
+    elif op == V.OP_LAYERNORM_AFFINE:
+        flags = prog.aux[ins.aux]
+        r = {ins.a} | ({ins.b, prog.aux[ins.aux + 1]} if flags & V.LN_AFFINE else set())
+    elif op == V.OP_ARGMAX_SEG:
+        r = {ins.a}
+    elif op == V.OP_FLASH_ATTN:
+        r = {ins.a, ins.b, ins.imm2}
+    elif op == V.OP_MAP_REGION:
+        r = set(ins.region_inputs or _region_inputs_from_aux(ins, prog))
+    elif op in (V.OP_DYNAMIC_SLICE, V.OP_DYNAMIC_UPDATE_SLICE, V.OP_GATHER_INDEX):
+        r = {ins.a}
+    elif op == V.OP_DOT:
+        r = {ins.a, ins.b}
+        epi_res = ins.epi_res
+        if ins.aux and not (ins.aview or ins.bview or ins.epi):
+            if prog.aux[ins.aux + 2]:
+                epi_res = prog.aux[ins.aux + 3]
+        if epi_res:
+            r.add(epi_res)
+    else:
+        r = {ins.a, ins.b}
+    if op in (V.OP_SCATTER, V.OP_DYNAMIC_UPDATE_SLICE):
+        r.add(ins.dst)        # partial writes keep the rest of dst
+    return r | set(ins.reads_hint)
+
+
+def instr_writes(ins: V.Instr, prog: V.VMProgram) -> set:
+    if ins.op == V.OP_NOP:
+        return set()
+    if ins.op == V.OP_ARGMAX_SEG:
+        return {ins.dst, ins.b}
+    return {ins.dst}
+
+
+# --- cost model ----------------------------------------------------------------
+
+_HBM_GBS = 5000.0          # effective GB/s assumed before calibration
+_MFMA_TFLOPS = 1200.0
+
+
+def task_cost(task: V.Task, cfg: DeviceConfig, prog: V.VMProgram) -> float:
+    """Estimated microseconds for the whole task (calibrated per-tile costs
+    override the analytic model when a cost table is present)."""
+    tiles = n_tiles(task, cfg)
+    key = _COST_KEYS.get(task.tile_op)
+    if key and key in cfg.costs:
+        return tiles * cfg.costs[key]
+    dsz = V.DT_SIZE.get(task.dtype, 4)
+    asz = V.DT_SIZE.get(task.adtype, 4)
+    top = task.tile_op
+    if top == V.TOP_MMA:
+        M, N, K, G = task.p0, task.p1, task.p2, max(1, task.p3 & 0xFFFFFF)
+        flops = 2.0 * M * N * K * G
+        byts = (M * K + K * N) * G * asz + M * N * G * dsz
+        return max(flops / (_MFMA_TFLOPS * 1e6), byts / (_HBM_GBS * 1e3)) + 1.0
+    if top == V.TOP_FLASH_ATTN:
+        H, T = task.p1, task.p2
+        hd = prog.aux[task.p3 + 3] if task.p3 + 3 < len(prog.aux) else 128
+        C = prog.aux[task.p3 + 2] if task.p3 + 2 < len(prog.aux) else T
+        return 4.0 * H * T * C * hd / (_MFMA_TFLOPS * 1e6) + 1.0
+    if top in (V.TOP_RED_SEG, V.TOP_SOFTMAX_SEG, V.TOP_LAYERNORM_SEG,
+               V.TOP_ARGMAX_SEG):
+        n = task.p0 * task.p1
+        return n * (asz + (dsz if top != V.TOP_RED_SEG else 0)) / (_HBM_GBS * 1e3) + 0.5
+    n = max(task.p0, task.p1) if top != V.TOP_EW else task.p1
+    return n * (asz * 2 + dsz) / (_HBM_GBS * 1e3) + 0.3
+
+
+# --- phases ---------------------------------------------------------------------
+
+def _phases(prog, indices, tasks_of, fuse):
+    """Split ``indices`` (program order) into barrier-separated phases. A new
+    phase starts when an instruction has a cross-lane dependency on a member
+    of the current phase (RAW, WAW or WAR through a shared buffer)."""
+    instrs = prog.instrs
+    phases, cur = [], []
+    readers: dict = {}
+    writers: dict = {}
+
+    def is_map(i):
+        return tasks_of(i).tile_op == V.TOP_EW
+
+    def cross(j, i):
+        a, b = instrs[i], instrs[j]
+        wa, wb = instr_writes(a, prog), instr_writes(b, prog)
+        if a.disjoint and a.disjoint == b.disjoint:
+            wa, wb = wa - wb, wb - instr_writes(a, prog)
+        dep = (instr_reads(b, prog) & wa) or (wb & wa) or (instr_reads(a, prog) & wb)
+        if not dep:
+            return False
+        if not fuse:
+            return True
+        # lane-local: both elementwise over the same count, no shared writes
+        return not (is_map(i) and is_map(j) and a.n == b.n and wa.isdisjoint(wb))
+
+    for j in indices:
+        ins = instrs[j]
+        cand = set()
+        for b in instr_reads(ins, prog):
+            cand.update(writers.get(b, ()))
+        for b in instr_writes(ins, prog):
+            cand.update(writers.get(b, ()))
+            cand.update(readers.get(b, ()))
+        if cur and any(cross(j, i) for i in cand):
+            phases.append(cur)
+            cur = []
+            readers.clear()
+            writers.clear()
+        cur.append(j)
+        for b in instr_reads(ins, prog):
+            readers.setdefault(b, []).append(j)
+        for b in instr_writes(ins, prog):
+            writers.setdefault(b, []).append(j)
+    if cur:
+        phases.append(cur)
+    return phases
+
+
+# --- packing --------------------------------------------------------------------
+
+def _tile_quantum(task: V.Task, cfg: DeviceConfig, prog: V.VMProgram) -> int:
+    """Preferred chunk granularity in tiles (chunk boundaries on multiples of
+    it keep the kernel's multi-row blocks whole)."""
+    if task.tile_op == V.TOP_FLASH_ATTN:
+        return 64
+    return 1
+
+
+def pack_units(units, n_lanes: int):
+    """units: [(task_ids, tiles, cost, quantum)] -> [(lane, Entry)].
+
+    Each unit is cut into k = min(tiles/quantum, ceil(n_lanes * cost share))
+    contiguous chunks, and the chunks are placed longest-first on the
+    least-loaded lane; a unit's whole chain runs over each of its chunks."""
+    out = []
+    if not units:
+        return out
+    total = sum(u[2] for u in units) or 1.0
+    chunks = []
+    for uid, (tids, tiles, cost, q) in enumerate(units):
+        blocks = max(1, math.ceil(tiles / q))
+        k = min(blocks, max(1, math.ceil(n_lanes * cost / total)))
+        for j in range(k):
+            lo = min(tiles, (blocks * j // k) * q)
+            hi = min(tiles, (blocks * (j + 1) // k) * q)
+            if hi > lo:
+                chunks.append((cost * (hi - lo) / tiles, uid, tids, lo, hi))
+    chunks.sort(key=lambda c: (-c[0], c[1], c[3]))
+    loads = [0.0] * n_lanes
+    # heap-free least-loaded search: lanes are few (<= 4096) and chunks are
+    # bounded by n_lanes per unit, so the linear scan stays cheap.
+    for cost, _uid, tids, lo, hi in chunks:
+        lane = min(range(n_lanes), key=loads.__getitem__)
+        for tid in tids:
+            out.append((lane, V.Entry(tid, lo, hi)))
+        loads[lane] += cost
+    return out
+
+
+# --- the scheduler ------------------------------------------------------------------
+
+@dataclasses.dataclass
+class _Region:
+    entries: list           # control entry of each lane, patched after scheduling
+    first: list             # WHILE: cond, FOR: [], IF: then
+    second: list            # WHILE/FOR: body, IF: else
+    op: int
+
+
+class _Scheduler:
+    def __init__(self, prog: V.VMProgram, cfg: DeviceConfig):
+        self.prog = prog
+        self.cfg = cfg
+        self.n = cfg.nlanes
+        self.lanes = [[] for _ in range(self.n)]
+        self.tasks: list = []
+        self.task_of: dict = {}
+        self.regions: list = []
+
+    def task_id(self, i: int) -> int:
+        tid = self.task_of.get(i)
+        if tid is None:
+            tid = len(self.tasks)
+            self.task_of[i] = tid
+            self.tasks.append(instr_to_task(self.prog.instrs[i], self.prog, self.cfg))
+        return tid
+
+    def task(self, i: int) -> V.Task:
+        return self.tasks[self.task_id(i)]
+
+    def barrier(self):
+        for s in self.lanes:
+            s.append(V.barrier_entry())
+
+    def levels(self, indices):
+        out, seg = [], []
+
+        def flush():
+            if seg:
+                for ph in _phases(self.prog, list(seg), self.task, self.cfg.fuse):
+                    out.append(("compute", ph))
+                seg.clear()
+
+        for i in indices:
+            op = self.prog.instrs[i].op
+            if op in V.REGION_OPS:
+                flush()
+                out.append(("region", i))
+            elif op != V.OP_NOP:
+                seg.append(i)
+        flush()
+        return out
+
+    def chains(self, map_idx):
+        parent = {i: i for i in map_idx}
+
+        def find(x):
+            while parent[x] != x:
+                parent[x] = parent[parent[x]]
+                x = parent[x]
+            return x
+
+        writer = {}
+        for i in map_idx:
+            for b in instr_writes(self.prog.instrs[i], self.prog):
+                writer[b] = i
+        for j in map_idx:
+            for b in instr_reads(self.prog.instrs[j], self.prog):
+                w = writer.get(b)
+                if w is not None and w != j:
+                    parent[find(w)] = find(j)
+        comps: dict = {}
+        for i in map_idx:
+            comps.setdefault(find(i), []).append(i)
+        return [sorted(v) for v in comps.values()]
+
+    def emit_phase(self, indices):
+        shaped, maps = [], []
+        for i in sorted(indices):
+            (maps if self.task(i).tile_op == V.TOP_EW else shaped).append(i)
+        units = []
+        for i in shaped:
+            t = self.task(i)
+            units.append(([self.task_id(i)], n_tiles(t, self.cfg),
+                          task_cost(t, self.cfg, self.prog),
+                          _tile_quantum(t, self.cfg, self.prog)))
+        for comp in self.chains(maps):
+            tids = [self.task_id(i) for i in comp]
+            t0 = self.tasks[tids[0]]
+            cost = sum(task_cost(self.tasks[t], self.cfg, self.prog) for t in tids)
+            units.append((tids, n_tiles(t0, self.cfg), cost, 1))
+        for lane, e in pack_units(units, self.n):
+            self.lanes[lane].append(e)
+
+    def schedule_range(self, indices, trailing_barrier: bool):
+        lv = self.levels(indices)
+        for k, (kind, payload) in enumerate(lv):
+            if kind == "compute":
+                self.emit_phase(payload)
+            else:
+                self.emit_region(payload)
+            if trailing_barrier or k != len(lv) - 1:
+                self.barrier()
+
+    def emit_region(self, i):
+        ins = self.prog.instrs[i]
+        ents = []
+        for s in self.lanes:
+            if ins.op == V.OP_FOR:
+                e = V.Entry(V.ENT_FOR, 0, 0, ins.b, 0, V.FLAG_NONE)
+            elif ins.op == V.OP_IF:
+                e = V.Entry(V.ENT_IF, 0, 0, 0, 0, ins.dst)
+            else:
+                e = V.Entry(V.ENT_WHILE, 0, 0, 0, 0, ins.dst)
+            s.append(e)
+            ents.append(e)
+        if ins.op == V.OP_FOR:
+            first, second = [], list(range(ins.n, ins.n + ins.imm))
+        else:
+            first = list(range(ins.a, ins.a + ins.b))
+            second = list(range(ins.n, ins.n + ins.imm))
+        self.regions.append(_Region(ents, first, second, ins.op))
+
+    def schedule_region(self, r: _Region):
+        s0 = [len(s) for s in self.lanes]
+        if r.op != V.OP_FOR:
+            self.schedule_range(r.first, trailing_barrier=False)
+        s1 = [len(s) for s in self.lanes]
+        self.schedule_range(r.second, trailing_barrier=False)
+        s2 = [len(s) for s in self.lanes]
+        for lane, e in enumerate(r.entries):
+            if r.op == V.OP_FOR:
+                e.tile_lo, e.tile_hi = s1[lane], s2[lane] - s1[lane]
+            else:
+                # WHILE: cond [tile_lo, +tile_hi), body [wait_flag, +wait_count)
+                # IF:    then [tile_lo, +tile_hi), else [wait_flag, +wait_count)
+                e.tile_lo, e.tile_hi = s0[lane], s1[lane] - s0[lane]
+                e.wait_flag, e.wait_count = s1[lane], s2[lane] - s1[lane]
+
+
+def schedule_program(prog: V.VMProgram, cfg: DeviceConfig | None = None) -> V.Schedule:
+    cfg = cfg or DeviceConfig.from_env()
+    sc = _Scheduler(prog, cfg)
+    # No barrier after the last root level: nothing reads it before the launch
+    # completes, so a one-phase program needs no grid barrier at all.
+    sc.schedule_range(list(range(prog.main_len)), trailing_barrier=False)
+    if not any(sc.lanes):
+        sc.barrier()
+    root_lens = [len(s) for s in sc.lanes]
+    while sc.regions:
+        sc.schedule_region(sc.regions.pop(0))
+    return V.Schedule(cfg.nlanes, sc.tasks, sc.lanes, root_lens)
+
+
+def schedule_bytes(prog: V.VMProgram, cfg: DeviceConfig | None = None) -> bytes:
+    sched = schedule_program(prog, cfg)
+    return V.serialize(prog, sched)

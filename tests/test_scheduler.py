@@ -1,0 +1,161 @@
+"""Scheduler behaviour (restating tests/test_lowering.py:469-701 of the
+reference) plus schedule invariants checked by the oracle's lane simulator."""
+import json
+
+import numpy as np
+import pytest
+
+from pjrt_amd import graph as G
+from pjrt_amd import scheduler as S
+from pjrt_amd import vmprogram as V
+from oracle import vmref
+
+
+def phases(sched):
+    counts = {sum(1 for e in s if e.task == V.ENT_BARRIER) for s in sched.lane_streams}
+    assert len(counts) == 1
+    out = [set() for _ in range(counts.pop() + 1)]
+    for s in sched.lane_streams:
+        p = 0
+        for e in s:
+            if e.task == V.ENT_BARRIER:
+                p += 1
+            elif e.task not in V.CONTROL_SENTINELS:
+                out[p].add(e.task)
+    return out
+
+
+def two_independent():
+    g = G.Graph()
+    a, b, c, d = (g.input((8,)) for _ in range(4))
+    g.output(g.add(a, b), g.mul(c, d))
+    return g.build()
+
+
+def test_two_independent_ops_co_scheduled():
+    prog = two_independent()
+    sched = S.schedule_program(prog, S.DeviceConfig(nlanes=8))
+    assert phases(sched) == [{0, 1}]
+    lanes = [l for l, s in enumerate(sched.lane_streams) for e in s if e.task in (0, 1)]
+    assert len(lanes) == 2 and len(set(lanes)) == 2
+    rng = np.random.default_rng(1234)
+    args = [rng.integers(-16, 16, 8).astype(np.float32) for _ in range(4)]
+    blob = V.serialize(prog, sched)
+    out = vmref.execute_schedule(blob, args)
+    np.testing.assert_array_equal(out[0], args[0] + args[1])
+    np.testing.assert_array_equal(out[1], args[2] * args[3])
+
+
+def test_dependent_elementwise_chain_shares_a_lane():
+    g = G.Graph()
+    a, b, c = (g.input((8,)) for _ in range(3))
+    g.output(g.sub(g.mul(a, b), c))
+    prog = g.build()
+    sched = S.schedule_program(prog, S.DeviceConfig(nlanes=8))
+    assert phases(sched) == [{0, 1}]
+    lanes = {l for l, s in enumerate(sched.lane_streams) for e in s if e.task in (0, 1)}
+    assert len(lanes) == 1
+
+
+def test_shaped_consumer_forces_barrier():
+    g = G.Graph()
+    x = g.input((64, 32))
+    y = g.mul(x, x)
+    s = g.reduce_last(y, V.RED_SUM)
+    g.output(s)
+    prog = g.build()
+    sched = S.schedule_program(prog, S.DeviceConfig(nlanes=4))
+    assert len(phases(sched)) == 2
+
+
+def test_nlanes_and_exact_tile_coverage():
+    g = G.Graph()
+    a, b = g.input((40000,)), g.input((40000,))
+    g.output(g.add(a, b))
+    prog = g.build()
+    cfg = S.DeviceConfig(nlanes=4, ew_ts=16384)
+    sched = S.schedule_program(prog, cfg)
+    ents = sorted((e.tile_lo, e.tile_hi) for s in sched.lane_streams for e in s if e.task == 0)
+    assert ents == [(0, 1), (1, 2), (2, 3)]
+    x = np.arange(40000, dtype=np.float32)
+    (out,) = vmref.execute_schedule(V.serialize(prog, sched), [x, 2 * x], ew_ts=16384)
+    np.testing.assert_array_equal(out, 3 * x)
+
+
+def two_adds(n0, n1):
+    g = G.Graph()
+    a, b = g.input((n0,)), g.input((n0,))
+    c, d = g.input((n1,)), g.input((n1,))
+    g.output(g.add(a, b), g.add(c, d))
+    return g.build()
+
+
+def test_cost_proportional_split_and_lpt_makespan():
+    ts = 4096
+    prog = two_adds(8 * ts, 2 * ts)
+    sched = S.schedule_program(prog, S.DeviceConfig(nlanes=8, ew_ts=ts))
+    l0 = {i for i, s in enumerate(sched.lane_streams) for e in s if e.task == 0}
+    l1 = {i for i, s in enumerate(sched.lane_streams) for e in s if e.task == 1}
+    assert len(l0) > len(l1)
+    loads = [sum(e.tile_hi - e.tile_lo for e in s if e.task not in V.CONTROL_SENTINELS)
+             for s in sched.lane_streams]
+    assert max(loads) == 2
+    vmref.execute_schedule(V.serialize(prog, sched),
+                           [np.zeros(8 * ts, np.float32)] * 2 + [np.zeros(2 * ts, np.float32)] * 2,
+                           ew_ts=ts)
+
+
+def test_equal_cost_even_split():
+    ts = 4096
+    prog = two_adds(4 * ts, 4 * ts)
+    sched = S.schedule_program(prog, S.DeviceConfig(nlanes=8, ew_ts=ts))
+    n0 = sum(1 for s in sched.lane_streams for e in s if e.task == 0)
+    n1 = sum(1 for s in sched.lane_streams for e in s if e.task == 1)
+    assert n0 == n1 == 4
+
+
+def test_device_config_from_env(tmp_path):
+    cost = tmp_path / "cost.json"
+    cost.write_text(json.dumps({"ew_tile_us": 2.5, "mma_tile_us": 40.0,
+                                "gather_tile_us": 3.0, "reduce_tile_us": 5.0}))
+    cfg = S.DeviceConfig.from_env({"PJRT_OCL_NLANES": "16", "PJRT_OCL_EW_TS": "8192",
+                                   "PJRT_OCL_MMA_T": "256",
+                                   "PJRT_OCL_COST_TABLE": str(cost)})
+    assert (cfg.nlanes, cfg.ew_ts, cfg.mma_t) == (16, 8192, 256)
+    assert cfg.costs["mma_tile_us"] == 40.0
+    d = S.DeviceConfig.from_env({})
+    assert d.nlanes == S.DEFAULT_NLANES and d.costs == {}
+    m = S.DeviceConfig.from_env({"PJRT_OCL_COST_TABLE": str(tmp_path / "none.json")})
+    assert m.costs == {}
+
+
+def test_while_control_entry_and_root_len():
+    prog = V.VMProgram(
+        arena_bytes=128, buffers=[V.Buffer(0, 4), V.Buffer(64, 4)],
+        inputs=[], outputs=[0], input_shapes=[], output_shapes=[()],
+        consts=[(1, np.float32(0.0).tobytes())],
+        instrs=[V.Instr(V.OP_WHILE, dst=1, a=1, b=0, n=1, imm=0)], main_len=1)
+    sched = S.schedule_program(prog, S.DeviceConfig(nlanes=8))
+    for lane, s in enumerate(sched.lane_streams):
+        root = s[:sched.root_lens[lane]]
+        w = [e for e in root if e.task == V.ENT_WHILE]
+        assert len(w) == 1
+        assert w[0].tile_lo >= sched.root_lens[lane]
+        assert w[0].wait_flag >= sched.root_lens[lane]
+        assert w[0].signal_flag == 1
+
+
+def test_mma_autotile_picks_parallel_tile():
+    g = G.Graph()
+    a, b = g.input((4096, 4096), "bf16"), g.input((4096, 4096), "bf16")
+    g.output(g.dot(a, b))
+    prog = g.build()
+    sched = S.schedule_program(prog, S.DeviceConfig(nlanes=256, mma_t=128))
+    t = sched.tasks[0]
+    assert t.tile_op == V.TOP_MMA and (t.p3 >> 24) == V.MMA_TILE_CODES[256]
+    assert S.n_tiles(t, S.DeviceConfig(nlanes=256)) == 256
+    g = G.Graph()
+    a, b = g.input((512, 768)), g.input((768, 768))
+    g.output(g.dot(a, b))
+    sched = S.schedule_program(g.build(), S.DeviceConfig(nlanes=256, mma_t=128))
+    assert (sched.tasks[0].p3 >> 24) == V.MMA_TILE_CODES[64]

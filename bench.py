@@ -1,0 +1,263 @@
+"""Benchmark of the MI355X megakernel VM on BASELINE.json's configurations.
+
+Headline (one JSON line on stdout): config 2, fused layernorm(eps 1e-5, affine) +
+tanh-GELU + f32->bf16 on x[8192, 4096] f32 (the HBM-bound
+configuration the metric's "elementwise GB/s as % of roofline" is quoted on).  A
+step is one execution of the program on device-resident inputs; value = algorithmic
+bytes per step / wall time per step.
+
+Also reported under "extra" (same JSON line): config 3 dot_general 4096^3 (bf16 and
+f32 operands, f32 accumulate) and config 4 causal flash attention (B4 H16 S2048
+d128, bf16) as TFLOP/s against their MFMA roofline.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workloads c2,c3,c4] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (os.path.join(ROOT, "pjrt-ocl_amd", "python"), ROOT):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+import numpy as np  # noqa: E402
+
+METRIC = "decode tokens/s; GEMM/attn TFLOP/s and elementwise GB/s as % of MI355X roofline"
+HBM_PEAK_GBS = 8000.0
+MFMA_PEAK_TFLOPS = {"bf16": 2500.0, "f16": 2500.0, "f32": 157.3}
+
+C2_ROWS, C2_D = 8192, 4096
+# algorithmic bytes of config 2: read x (f32), write y (bf16), read gamma + beta
+C2_BYTES = C2_ROWS * C2_D * 4 + C2_ROWS * C2_D * 2 + 2 * C2_D * 4
+
+
+def log(*a):
+    print("[bench]", *a, file=sys.stderr, flush=True)
+
+
+def build_c2():
+    from pjrt_amd import graph as G
+    g = G.Graph()
+    x, ga, be = g.input((C2_ROWS, C2_D)), g.input((C2_D,)), g.input((C2_D,))
+    g.output(g.layernorm(x, ga, be, 1e-5, gelu=True, out_dtype="bf16"))
+    return g.build()
+
+
+def c2_inputs():
+    rng = np.random.default_rng(1002)
+    x = rng.standard_normal((C2_ROWS, C2_D), dtype=np.float32)
+    gamma = rng.uniform(0.5, 1.5, C2_D).astype(np.float32)
+    beta = (rng.standard_normal(C2_D) * 0.1).astype(np.float32)
+    return x, gamma, beta
+
+
+def time_program(rt, lp, dev_in, dev_out, steps, warmup):
+    """Warm up, then time exactly `steps` back-to-back executions: wall clock
+    around the whole region and HIP events on the launch stream."""
+    for _ in range(warmup):
+        lp.enqueue(dev_in, dev_out)
+    rt.synchronize()
+    lp.status()
+    e0, e1 = rt.event(), rt.event()
+    rt.synchronize()
+    t0 = time.perf_counter()
+    e0.record()
+    for _ in range(steps):
+        lp.enqueue(dev_in, dev_out)
+    e1.record()
+    rt.synchronize()
+    wall = time.perf_counter() - t0
+    lp.status()
+    return wall * 1e3 / steps, e0.elapsed_ms(e1) / steps
+
+
+def load_traffic(name):
+    path = os.path.join(ROOT, "profiles", f"traffic_{name}.json")
+    try:
+        with open(path) as f:
+            return json.load(f)
+    except (OSError, ValueError):
+        return None
+
+
+def cpu_baseline_c2(x, gamma, beta, budget_s=10.0):
+    """The reference's CPU engine path for config 2 (decomposed phases), restated in
+    C (oracle/refcpu.c), on the host cores, over the full workload."""
+    lib = ctypes.CDLL(os.path.join(ROOT, "oracle", "librefcpu.so"))
+    lib.refcpu_ln_gelu_bf16.restype = ctypes.c_int
+    lib.refcpu_ln_gelu_bf16.argtypes = [ctypes.c_void_p] * 4 + [ctypes.c_int64, ctypes.c_int64, ctypes.c_float,
+                                                               ctypes.c_void_p, ctypes.c_int]
+    cores = min(16, os.cpu_count() or 1)
+    out = np.empty((C2_ROWS, C2_D), np.uint16)
+    scratch = np.empty(2 * C2_ROWS * C2_D + 2 * C2_ROWS, np.float32)
+
+    def call():
+        lib.refcpu_ln_gelu_bf16(x.ctypes.data, gamma.ctypes.data, beta.ctypes.data, out.ctypes.data, C2_ROWS, C2_D,
+                                1e-5, scratch.ctypes.data, cores)
+
+    call()
+    n, t0 = 0, time.perf_counter()
+    while True:
+        call()
+        n += 1
+        if time.perf_counter() - t0 >= budget_s or n >= 200:
+            break
+    dt = (time.perf_counter() - t0) / n
+    return {"value": round(C2_BYTES / dt / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+            "sample": f"full config-2 workload [8192,4096], {n} timed calls after 1 warm-up, "
+                      f"{dt * 1e3:.1f} ms/call; C restatement of the reference's decomposed CPU-engine phases "
+                      f"(oracle/refcpu.c)"}, out
+
+
+def bench_c2(rt, steps, warmup, with_cpu):
+    prog = build_c2()
+    lp = rt.compile(prog)
+    x, gamma, beta = c2_inputs()
+    dev_in = [rt.to_device(x), rt.to_device(gamma), rt.to_device(beta)]
+    dev_out = lp.alloc_outputs()
+    ms_step, ms_kernel = time_program(rt, lp, dev_in, dev_out, steps, warmup)
+    got = dev_out[0].to_host(np.uint16, (C2_ROWS, C2_D))
+    # spot check against float64 math on a slice of rows
+    rows = slice(0, 256)
+    x64 = x[rows].astype(np.float64)
+    mu = x64.mean(1, keepdims=True)
+    z = (x64 - mu) / np.sqrt(((x64 - mu) ** 2).mean(1, keepdims=True) + 1e-5) * gamma + beta
+    want = 0.5 * z * (1 + np.tanh(0.7978845608 * (z + 0.044715 * z ** 3)))
+    gotf = (got[rows].astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    err = float(np.max(np.abs(gotf - want) / (np.abs(want) + 1e-6)))
+    if err > 2.0 ** -8 + 1e-6:
+        raise SystemExit(f"bench: config-2 result check failed (max rel err {err:.3g})")
+    cpu = None
+    if with_cpu:
+        cpu, cout = cpu_baseline_c2(x, gamma, beta)
+        diff = np.abs((cout.astype(np.uint32) << 16).view(np.float32).astype(np.float64) -
+                      (got.astype(np.uint32) << 16).view(np.float32).astype(np.float64))
+        cpu["max_abs_diff_vs_gpu"] = float(diff.max())
+    achieved = C2_BYTES / (ms_kernel * 1e-3) / 1e9
+    traffic = load_traffic("c2")
+    res = {
+        "value": C2_BYTES / (ms_step * 1e-3) / 1e9, "unit": "GB/s", "ms_per_step": ms_step,
+        "kernel_ms": ms_kernel,
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": traffic.get("bytes_per_launch") if traffic else None},
+        "cpu_baseline": cpu, "max_rel_err_first_256_rows": err,
+    }
+    for b in dev_in + dev_out:
+        b.free()
+    lp.close()
+    return res
+
+
+def bench_gemm(rt, dt, steps, warmup, M=4096, N=4096, K=4096):
+    from pjrt_amd import graph as G
+    from pjrt_amd import vmprogram as V
+    rng = np.random.default_rng(1003)
+    a = (rng.standard_normal((M, K), dtype=np.float32) * 0.125)
+    b = (rng.standard_normal((K, N), dtype=np.float32) * 0.125)
+    g = G.Graph()
+    x, y = g.input((M, K), dt), g.input((K, N), dt)
+    g.output(g.dot(x, y))
+    lp = rt.compile(g.build())
+    if dt == "bf16":
+        a_dev, b_dev = V.f32_to_bf16(a), V.f32_to_bf16(b)
+        a, b = V.bf16_to_f32(a_dev), V.bf16_to_f32(b_dev)
+    else:
+        a_dev, b_dev = a, b
+    dev_in = [rt.to_device(a_dev), rt.to_device(b_dev)]
+    dev_out = lp.alloc_outputs()
+    ms_step, ms_kernel = time_program(rt, lp, dev_in, dev_out, steps, warmup)
+    c = dev_out[0].to_host(np.float32, (M, N))
+    idx = np.random.default_rng(0).integers(0, M, 64)
+    want = a[idx].astype(np.float64) @ b.astype(np.float64)
+    err = float(np.abs(c[idx] - want).max() / np.abs(want).max())
+    flops = 2.0 * M * N * K
+    tf = flops / (ms_kernel * 1e-3) / 1e12
+    for buf in dev_in + dev_out:
+        buf.free()
+    lp.close()
+    return {"workload": f"C3 dot_general {M}x{K}x{N} {dt} -> f32", "tflops": round(flops / (ms_step * 1e-3) / 1e12, 2),
+            "ms_per_step": ms_step, "kernel_ms": ms_kernel,
+            "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": MFMA_PEAK_TFLOPS[dt], "unit": "TFLOP/s",
+                         "frac": round(tf / MFMA_PEAK_TFLOPS[dt], 4)},
+            "max_rel_err_64_rows": err}
+
+
+def bench_attention(rt, steps, warmup, B=4, H=16, S=2048, D=128):
+    from pjrt_amd import graph as G
+    from pjrt_amd import vmprogram as V
+    rng = np.random.default_rng(1004)
+    shape = (B * H, S, D)
+    q, k, v = (V.f32_to_bf16(rng.standard_normal(shape, dtype=np.float32)) for _ in range(3))
+    g = G.Graph()
+    Q, K, Vv = g.input(shape, "bf16"), g.input(shape, "bf16"), g.input(shape, "bf16")
+    g.output(g.flash_attention(Q, K, Vv, 1.0 / math.sqrt(D), True, out_dtype="bf16"))
+    lp = rt.compile(g.build())
+    dev_in = [rt.to_device(q), rt.to_device(k), rt.to_device(v)]
+    dev_out = lp.alloc_outputs()
+    ms_step, ms_kernel = time_program(rt, lp, dev_in, dev_out, steps, warmup)
+    o = V.bf16_to_f32(dev_out[0].to_host(np.uint16, shape))
+    # check two heads against float64 math
+    from oracle import vmref
+    errs = []
+    for h in (0, B * H - 1):
+        qh, kh, vh = (V.bf16_to_f32(t[h:h + 1]) for t in (q, k, v))
+        want = vmref.attention(qh, np.transpose(kh, (0, 2, 1)), vh, 1.0 / math.sqrt(D), True)[0]
+        errs.append(float(np.abs(o[h] - want).max() / np.abs(want).max()))
+    flops = 4.0 * B * H * D * S * (S + 1) / 2
+    tf = flops / (ms_kernel * 1e-3) / 1e12
+    for buf in dev_in + dev_out:
+        buf.free()
+    lp.close()
+    return {"workload": f"C4 causal flash attention B{B} H{H} S{S} d{D} bf16", "tflops": round(flops / (ms_step * 1e-3) / 1e12, 2),
+            "ms_per_step": ms_step, "kernel_ms": ms_kernel,
+            "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": MFMA_PEAK_TFLOPS["bf16"],
+                         "unit": "TFLOP/s", "frac": round(tf / MFMA_PEAK_TFLOPS["bf16"], 4)},
+            "max_rel_err_2_heads": max(errs)}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workloads", default="c2,c3,c4")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        raise SystemExit("bench.py measures one GPU: this build has no multi-GPU path "
+                         "(each GPU would run its own shard of the same megakernel; see DESIGN.md)")
+    from pjrt_amd.runtime import Runtime
+    rt = Runtime(device=0)
+    log(f"device {rt.info['name']} {rt.info['arch']} lanes={rt.info['n_lanes']}")
+    wl = set(args.workloads.split(","))
+    extra = {}
+    if "c3" in wl:
+        for dt in ("bf16", "f32"):
+            log(f"C3 {dt}")
+            extra[f"c3_{dt}"] = bench_gemm(rt, dt, max(5, args.steps // 5), 2)
+    if "c4" in wl:
+        log("C4")
+        extra["c4"] = bench_attention(rt, max(5, args.steps // 5), 2)
+    log("C2")
+    c2 = bench_c2(rt, args.steps, args.warmup, not args.no_cpu)
+    line = {
+        "metric": METRIC, "value": round(c2["value"], 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(c2["ms_per_step"], 5), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": "C2 fused layernorm(eps=1e-5, gamma/beta) + tanh-GELU + f32->bf16 on x[8192,4096] f32",
+                   "rows": C2_ROWS, "d": C2_D, "bytes_per_step": C2_BYTES, "kernel_ms": round(c2["kernel_ms"], 5)},
+        "roofline": c2["roofline"], "cpu_baseline": c2["cpu_baseline"], "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

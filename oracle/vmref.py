@@ -399,8 +399,22 @@ def _convert(x, adt, dt):
     if dt == BOOL:
         return (v != 0).astype(np.uint8)
     if dt in INTS:
+        # float -> int saturates to the target range and maps NaN to 0 (XLA's
+        # convert semantics; the reference's C cast leaves out-of-range values
+        # undefined).
+        info = np.iinfo(NP[dt])
         with np.errstate(all="ignore"):
-            return np.trunc(v).astype(np.int64).astype(NP[dt])
+            tv = np.trunc(v)
+            out = np.zeros(v.shape, NP[dt])
+            ok = ~np.isnan(v)
+            hi = ok & (tv >= float(info.max) + 1.0)
+            lo = ok & (tv < float(info.min))
+            mid = ok & ~hi & ~lo
+            out[hi] = info.max
+            out[lo] = info.min
+            out[mid] = tv[mid].astype(np.int64).astype(NP[dt]) if dt != U32 else \
+                tv[mid].astype(np.uint64).astype(np.uint32)
+            return out
     if dt == BF16:
         return f32_to_bf16(v.astype(np.float32))
     if dt == F16:

@@ -1,0 +1,554 @@
+// Reductions and fused row ops (ops/reduce.cl semantics):
+//   TOP_RED_PART / TOP_RED_COMB  two-phase flat reduce (reduce.cl:90-153, 529-549)
+//   TOP_RED_SEG                  per-row reduce, GEMV dot mode (reduce.cl:165-281)
+//   TOP_RED_STRIDED              reduce over an interior axis (reduce.cl:488-527)
+//   TOP_SOFTMAX_SEG              row softmax (reduce.cl:304-392)
+//   TOP_LAYERNORM_SEG            row layernorm (reduce.cl:399-479) + the affine /
+//                                tanh-GELU / output-convert extension flags
+//   TOP_ARGMAX_SEG               (value, first index) of the row maximum
+// Float reductions accumulate in f32 through DPP wave reductions; integer ones are
+// exact.  Kinds: 0 sum, 1 max, 2 min, 3 prod, 4 and, 5 or, 6 xor.
+#pragma once
+#include "vm_math.h"
+
+namespace vm {
+
+// LDS-only block barrier: orders LDS traffic between the waves of the block
+// without waiting for outstanding global loads (prefetches stay in flight).
+VM_DEV void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+VM_DEV float* lds_f32() { return reinterpret_cast<float*>(vm_smem); }
+
+template <class Op>
+VM_DEV float block_reduce(float x, Op op, float* red) {
+  const float w = wave_reduce(x, op);
+  lds_barrier();
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = w;
+  lds_barrier();
+  float r = red[0];
+#pragma unroll
+  for (int k = 1; k < kWaves; ++k) r = op(r, red[k]);
+  return r;
+}
+
+VM_DEV float fred_ident(uint32_t kind) {
+  return kind == 0 ? 0.0f : kind == 1 ? -INFINITY : kind == 2 ? INFINITY : 1.0f;
+}
+VM_DEV float fred(uint32_t kind, float a, float b) {
+  return kind == 0 ? a + b : kind == 1 ? fmaxf(a, b) : kind == 2 ? fminf(a, b) : a * b;
+}
+VM_DEV float block_reduce_kind(float x, uint32_t kind, float* red) {
+  switch (kind) {
+    case 0: return block_reduce(x, OpSum(), red);
+    case 1: return block_reduce(x, OpMax(), red);
+    case 2: return block_reduce(x, OpMin(), red);
+    default: return block_reduce(x, OpProd(), red);
+  }
+}
+
+// ---- integer kinds (reduce.cl:16-40; u32 compares unsigned) -----------------------------
+template <typename T>
+VM_DEV T ired_ident(uint32_t kind, bool uns) {
+  constexpr bool k64 = sizeof(T) == 8;
+  switch (kind) {
+    case 0: return 0;
+    case 1: return uns ? T(0) : (k64 ? T(INT64_MIN) : T(INT32_MIN));
+    case 2: return uns ? T(~T(0)) : (k64 ? T(INT64_MAX) : T(INT32_MAX));
+    case 3: return 1;
+    case 4: return T(~T(0));
+    default: return 0;
+  }
+}
+template <typename T, typename U>
+VM_DEV T ired(uint32_t kind, bool uns, T a, T b) {
+  switch (kind) {
+    case 0: return T(U(a) + U(b));
+    case 1: return uns ? (U(a) > U(b) ? a : b) : (a > b ? a : b);
+    case 2: return uns ? (U(a) < U(b) ? a : b) : (a < b ? a : b);
+    case 3: return T(U(a) * U(b));
+    case 4: return a & b;
+    case 5: return a | b;
+    default: return a ^ b;
+  }
+}
+
+// Block reduction of an integer value through an LDS tree (exact).
+template <typename T, typename U>
+VM_DEV T block_ireduce(T v, uint32_t kind, bool uns) {
+  T* tree = reinterpret_cast<T*>(vm_smem);
+  lds_barrier();
+  tree[threadIdx.x] = v;
+  lds_barrier();
+  for (int s = kBlock / 2; s > 0; s >>= 1) {
+    if (int(threadIdx.x) < s) tree[threadIdx.x] = ired<T, U>(kind, uns, tree[threadIdx.x], tree[threadIdx.x + s]);
+    lds_barrier();
+  }
+  return tree[0];
+}
+
+VM_DEV int64_t load_i(const gbyte* p, uint32_t dt, uint64_t i) {
+  switch (dt) {
+    case DT_I64: return gcast<int64_t>(p)[i];
+    case DT_U32: return int64_t(gcast<uint32_t>(p)[i]);
+    case DT_BOOL: return p[i] != 0;
+    default: return gcast<int32_t>(p)[i];
+  }
+}
+VM_DEV void store_i(gbyte* p, uint32_t dt, uint64_t i, int64_t v) {
+  switch (dt) {
+    case DT_I64: gcast<int64_t>(p)[i] = v; break;
+    case DT_BOOL: p[i] = uint8_t(v & 1); break;
+    default: gcast<uint32_t>(p)[i] = uint32_t(uint64_t(v)); break;
+  }
+}
+VM_DEV bool is_int_dt(uint32_t dt) { return dt == DT_I32 || dt == DT_U32 || dt == DT_I64 || dt == DT_BOOL; }
+
+// Integer reduction of src[i0, i1) by the whole block.
+VM_DEV int64_t block_int_range(const gbyte* src, uint32_t dt, uint32_t kind, uint64_t i0, uint64_t i1) {
+  if (dt == DT_I64) {
+    int64_t acc = ired_ident<int64_t>(kind, false);
+    for (uint64_t i = i0 + threadIdx.x; i < i1; i += kBlock)
+      acc = ired<int64_t, uint64_t>(kind, false, acc, load_i(src, dt, i));
+    return block_ireduce<int64_t, uint64_t>(acc, kind, false);
+  }
+  const bool uns = dt == DT_U32;
+  int32_t acc = ired_ident<int32_t>(kind, uns);
+  if (dt == DT_BOOL && kind == 1) acc = 0;       // bool max identity is false
+  if (dt == DT_BOOL && kind == 2) acc = 1;       // bool min identity is true
+  for (uint64_t i = i0 + threadIdx.x; i < i1; i += kBlock)
+    acc = ired<int32_t, uint32_t>(kind, uns, acc, int32_t(load_i(src, dt, i)));
+  return int64_t(uint32_t(block_ireduce<int32_t, uint32_t>(acc, kind, uns)));
+}
+
+// ---- TOP_RED_PART / TOP_RED_COMB -----------------------------------------------------
+// RED_PART: p0 n, p1 chunk, p2 kind; tile k reduces [k*chunk, (k+1)*chunk) into dst[k].
+// RED_COMB: p0 n_parts, p1 kind; one tile reduces the partials into dst[0].
+VM_TILE void red_flat_tiles(Args A, uint32_t ti, uint32_t lo, uint32_t hi, bool comb) {
+  A = uargs(A);
+  const VM_K Task& t = task_of(A, ti);
+  const uint32_t n = t.p[0], chunk = comb ? t.p[0] : t.p[1], kind = comb ? t.p[1] : t.p[2];
+  const uint32_t dt = (t.tile_op >> 8) & 0xFF;
+  const gbyte* a = resolve(A, t.a);
+  gbyte* d = resolve(A, t.dst);
+  if (comb) hi = min(hi, 1u);
+  for (uint32_t tile = lo; tile < hi; ++tile) {
+    const uint64_t s0 = uint64_t(tile) * chunk, s1 = min(s0 + chunk, uint64_t(n));
+    if (is_int_dt(dt)) {
+      const int64_t r = block_int_range(a, dt, kind, s0, s1);
+      if (threadIdx.x == 0) store_i(d, dt, tile, r);
+    } else {
+      float acc = fred_ident(kind);
+      for (uint64_t i = s0 + threadIdx.x; i < s1; i += kBlock) acc = fred(kind, acc, load_f(a, dt, i));
+      const float r = block_reduce_kind(acc, kind, lds_f32());
+      if (threadIdx.x == 0) store_f(d, dt, tile, r);
+    }
+  }
+}
+
+// ---- TOP_RED_SEG -----------------------------------------------------------------------
+// p0 n_out, p1 seg, p2 kind, p3 dot mode (row . vector at b, GEMV routing).
+VM_TILE void red_seg_tiles(Args A, uint32_t ti, uint32_t lo, uint32_t hi) {
+  A = uargs(A);
+  const VM_K Task& t = task_of(A, ti);
+  const uint32_t n_out = t.p[0], seg = t.p[1], kind = t.p[2], dot = t.p[3];
+  const uint32_t dt = (t.tile_op >> 8) & 0xFF, adt = (t.tile_op >> 16) & 0xFF;
+  const gbyte* a = resolve(A, t.a);
+  const gbyte* bv = resolve(A, t.b);
+  gbyte* d = resolve(A, t.dst);
+  hi = min(hi, n_out);
+  if (is_int_dt(dt) && !dot) {
+    for (uint32_t o = lo; o < hi; ++o) {
+      const int64_t r = block_int_range(a, dt, kind, uint64_t(o) * seg, uint64_t(o + 1) * seg);
+      if (threadIdx.x == 0) store_i(d, dt, o, r);
+    }
+    return;
+  }
+  if (seg <= 32 && !dot) {             // short rows: one thread per row
+    for (uint32_t o = lo + threadIdx.x; o < hi; o += kBlock) {
+      float acc = fred_ident(kind);
+      for (uint32_t j = 0; j < seg; ++j) acc = fred(kind, acc, load_f(a, adt, uint64_t(o) * seg + j));
+      store_f(d, dt, o, acc);
+    }
+    return;
+  }
+  float* red = lds_f32();
+  const bool vec = adt == DT_F32 && (seg & 3) == 0 && ((uintptr_t(a) | uintptr_t(bv)) & 15) == 0;
+  for (uint32_t o = lo; o < hi; ++o) {
+    const uint64_t base = uint64_t(o) * seg;
+    float acc = dot ? 0.0f : fred_ident(kind);
+    if (vec) {
+      const VM_G v4f* r4 = (const VM_G v4f*)(gcast<float>(a) + base);
+      const VM_G v4f* v4 = (const VM_G v4f*)gcast<float>(bv);
+      for (uint32_t j = threadIdx.x; j < (seg >> 2); j += kBlock) {
+        const v4f x = r4[j];
+        if (dot) {
+          const v4f y = v4[j];
+          acc = fmaf(x.x, y.x, fmaf(x.y, y.y, fmaf(x.z, y.z, fmaf(x.w, y.w, acc))));
+        } else {
+          acc = fred(kind, acc, fred(kind, fred(kind, x.x, x.y), fred(kind, x.z, x.w)));
+        }
+      }
+    } else {
+      for (uint32_t j = threadIdx.x; j < seg; j += kBlock) {
+        const float x = load_f(a, adt, base + j);
+        acc = dot ? fmaf(x, load_f(bv, adt, j), acc) : fred(kind, acc, x);
+      }
+    }
+    const float r = block_reduce_kind(acc, dot ? 0u : kind, red);
+    if (threadIdx.x == 0) store_f(d, dt, o, r);
+  }
+}
+
+// ---- TOP_RED_STRIDED ----------------------------------------------------------------------
+// out[o*inner + i] = reduce_r in[(o*red + r)*inner + i]; p0 n_out, p1 red, p2 inner,
+// p3 kind; tiles of ew_ts outputs, one thread per output.
+VM_TILE void red_strided_tiles(Args A, uint32_t ti, uint32_t lo, uint32_t hi) {
+  A = uargs(A);
+  const VM_K Task& t = task_of(A, ti);
+  const uint32_t n_out = t.p[0], red = t.p[1], inner = t.p[2], kind = t.p[3];
+  const uint32_t dt = (t.tile_op >> 8) & 0xFF, adt = (t.tile_op >> 16) & 0xFF;
+  const gbyte* a = resolve(A, t.a);
+  gbyte* d = resolve(A, t.dst);
+  const uint64_t e0 = uint64_t(lo) * A->ew_ts, e1 = min(uint64_t(hi) * A->ew_ts, uint64_t(n_out));
+  for (uint64_t q = e0 + threadIdx.x; q < e1; q += kBlock) {
+    const uint64_t o = q / inner, i = q % inner;
+    const uint64_t base = o * uint64_t(red) * inner + i;
+    if (is_int_dt(dt)) {
+      if (dt == DT_I64) {
+        int64_t acc = ired_ident<int64_t>(kind, false);
+        for (uint32_t r = 0; r < red; ++r)
+          acc = ired<int64_t, uint64_t>(kind, false, acc, load_i(a, dt, base + uint64_t(r) * inner));
+        store_i(d, dt, q, acc);
+      } else {
+        const bool uns = dt == DT_U32;
+        int32_t acc = ired_ident<int32_t>(kind, uns);
+        if (dt == DT_BOOL && kind == 1) acc = 0;
+        if (dt == DT_BOOL && kind == 2) acc = 1;
+        for (uint32_t r = 0; r < red; ++r)
+          acc = ired<int32_t, uint32_t>(kind, uns, acc, int32_t(load_i(a, dt, base + uint64_t(r) * inner)));
+        store_i(d, dt, q, int64_t(uint32_t(acc)));
+      }
+    } else {
+      float acc = fred_ident(kind);
+      for (uint32_t r = 0; r < red; ++r) acc = fred(kind, acc, load_f(a, adt, base + uint64_t(r) * inner));
+      store_f(d, dt, q, acc);
+    }
+  }
+}
+
+// ---- row-resident fused ops -------------------------------------------------------------
+// A row of `seg` elements is held in registers as NV v4f per thread (thread t
+// owns v4f slots t, t+256, ...), so a row costs one HBM read and one write.
+// The next row's loads are issued before the current row's reductions.
+
+template <int NV>
+struct Row { v4f v[NV]; };
+
+VM_DEV v4f ld4(const gbyte* p, uint32_t dt, uint64_t e) {   // e: element index (multiple of 4)
+  if (dt == DT_F32) return *(const VM_G v4f*)(gcast<float>(p) + e);
+  const v2u w = *(const VM_G v2u*)(gcast<uint16_t>(p) + e);
+  if (dt == DT_BF16)
+    return v4f_make(__uint_as_float(w.x << 16), __uint_as_float(w.x & 0xFFFF0000u),
+                       __uint_as_float(w.y << 16), __uint_as_float(w.y & 0xFFFF0000u));
+  return v4f_make(f16_to_f32(w.x & 0xFFFF), f16_to_f32(w.x >> 16), f16_to_f32(w.y & 0xFFFF),
+                     f16_to_f32(w.y >> 16));
+}
+VM_DEV void st4(gbyte* p, uint32_t dt, uint64_t e, v4f v) {
+  if (dt == DT_F32) {
+    *(VM_G v4f*)(gcast<float>(p) + e) = v;
+  } else if (dt == DT_BF16) {
+    *(VM_G v2u*)(gcast<uint16_t>(p) + e) = v2u_make(f32_to_bf16(v.x) | (uint32_t(f32_to_bf16(v.y)) << 16),
+                                                         f32_to_bf16(v.z) | (uint32_t(f32_to_bf16(v.w)) << 16));
+  } else {
+    *(VM_G v2u*)(gcast<uint16_t>(p) + e) = v2u_make(f32_to_f16(v.x) | (uint32_t(f32_to_f16(v.y)) << 16),
+                                                         f32_to_f16(v.z) | (uint32_t(f32_to_f16(v.w)) << 16));
+  }
+}
+
+template <int NV>
+VM_DEV void row_load(Row<NV>& r, const gbyte* p, uint32_t dt, uint64_t base, uint32_t nv4) {
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    const uint32_t q = threadIdx.x + k * kBlock;
+    if (q < nv4) r.v[k] = ld4(p, dt, base + 4ull * q);
+  }
+}
+
+// LAYERNORM_SEG over rows [r0, r1): p0 n_out, p1 seg, p2 eps bits, p3 flags,
+// b = gamma, p4 = beta (LN_AFFINE).
+template <int NV>
+VM_TILE void ln_rows_vec(Args A, uint32_t ti, uint32_t r0, uint32_t r1) {
+  A = uargs(A);
+  const VM_K Task& t = task_of(A, ti);
+  float* red = lds_f32();
+  const uint32_t seg = t.p[1], flags = t.p[3];
+  const float eps = __uint_as_float(t.p[2]);
+  const uint32_t dt = (t.tile_op >> 8) & 0xFF, adt = (t.tile_op >> 16) & 0xFF;
+  const gbyte* a = resolve(A, t.a);
+  gbyte* d = resolve(A, t.dst);
+  const bool affine = flags & LN_AFFINE, do_gelu = flags & LN_GELU, two_pass = flags & LN_TWO_PASS;
+  const gbyte* gp = resolve(A, affine ? t.b : t.a);
+  const gbyte* bp = resolve(A, affine ? t.p[4] : t.a);
+  const uint32_t nv4 = seg >> 2;
+  const float inv_n = 1.0f / float(seg);
+  // gamma / beta slots of this thread stay in registers for every row
+  Row<NV> g, be;
+  if (affine) {
+    row_load(g, gp, DT_F32, 0, nv4);
+    row_load(be, bp, DT_F32, 0, nv4);
+  }
+  Row<NV> x, xn;
+  row_load(x, a, adt, uint64_t(r0) * seg, nv4);
+  for (uint32_t r = r0; r < r1; ++r) {
+    if (r + 1 < r1) row_load(xn, a, adt, uint64_t(r + 1) * seg, nv4);
+    float s = 0.0f, s2 = 0.0f;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      if (threadIdx.x + k * kBlock < nv4) {
+        const v4f v = x.v[k];
+        s += (v.x + v.y) + (v.z + v.w);
+        if (!two_pass) s2 = fmaf(v.x, v.x, fmaf(v.y, v.y, fmaf(v.z, v.z, fmaf(v.w, v.w, s2))));
+      }
+    }
+    const float mean = block_reduce(s, OpSum(), red) * inv_n;
+    float var;
+    if (two_pass) {
+      float q = 0.0f;
+#pragma unroll
+      for (int k = 0; k < NV; ++k) {
+        if (threadIdx.x + k * kBlock < nv4) {
+          const v4f v = x.v[k];
+          const float dx = v.x - mean, dy = v.y - mean, dz = v.z - mean, dw = v.w - mean;
+          q = fmaf(dx, dx, fmaf(dy, dy, fmaf(dz, dz, fmaf(dw, dw, q))));
+        }
+      }
+      var = block_reduce(q, OpSum(), red + kWaves) * inv_n;
+    } else {
+      var = block_reduce(s2, OpSum(), red + kWaves) * inv_n - mean * mean;
+    }
+    const float rstd = rsqrtf(var + eps);
+    const float shift = -mean * rstd;
+    const uint64_t base = uint64_t(r) * seg;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      const uint32_t q = threadIdx.x + k * kBlock;
+      if (q < nv4) {
+        float y[4] = {x.v[k].x, x.v[k].y, x.v[k].z, x.v[k].w};
+        const float gg[4] = {g.v[k].x, g.v[k].y, g.v[k].z, g.v[k].w};
+        const float bb[4] = {be.v[k].x, be.v[k].y, be.v[k].z, be.v[k].w};
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          float z = fmaf(y[c], rstd, shift);
+          if (affine) z = fmaf(z, gg[c], bb[c]);
+          if (do_gelu) z = gelu(z);
+          y[c] = z;
+        }
+        st4(d, dt, base + 4ull * q, v4f_make(y[0], y[1], y[2], y[3]));
+      }
+    }
+    if (r + 1 < r1) x = xn;
+  }
+}
+
+// Any seg / alignment: three passes over the row in global memory.
+VM_TILE void ln_rows_generic(Args A, uint32_t ti, uint32_t r0, uint32_t r1) {
+  A = uargs(A);
+  const VM_K Task& t = task_of(A, ti);
+  float* red = lds_f32();
+  const uint32_t seg = t.p[1], flags = t.p[3];
+  const float eps = __uint_as_float(t.p[2]);
+  const uint32_t dt = (t.tile_op >> 8) & 0xFF, adt = (t.tile_op >> 16) & 0xFF;
+  const gbyte* a = resolve(A, t.a);
+  gbyte* d = resolve(A, t.dst);
+  const bool affine = flags & LN_AFFINE, do_gelu = flags & LN_GELU, two_pass = flags & LN_TWO_PASS;
+  const gbyte* gp = resolve(A, affine ? t.b : t.a);
+  const gbyte* bp = resolve(A, affine ? t.p[4] : t.a);
+  const float inv_n = 1.0f / float(seg);
+  for (uint32_t r = r0; r < r1; ++r) {
+    const uint64_t base = uint64_t(r) * seg;
+    float s = 0.0f, s2 = 0.0f;
+    for (uint32_t j = threadIdx.x; j < seg; j += kBlock) {
+      const float v = load_f(a, adt, base + j);
+      s += v;
+      s2 = fmaf(v, v, s2);
+    }
+    const float mean = block_reduce(s, OpSum(), red) * inv_n;
+    float var;
+    if (two_pass) {
+      float q = 0.0f;
+      for (uint32_t j = threadIdx.x; j < seg; j += kBlock) {
+        const float dv = load_f(a, adt, base + j) - mean;
+        q = fmaf(dv, dv, q);
+      }
+      var = block_reduce(q, OpSum(), red + kWaves) * inv_n;
+    } else {
+      var = block_reduce(s2, OpSum(), red + kWaves) * inv_n - mean * mean;
+    }
+    const float rstd = rsqrtf(var + eps);
+    const float shift = -mean * rstd;
+    for (uint32_t j = threadIdx.x; j < seg; j += kBlock) {
+      float z = fmaf(load_f(a, adt, base + j), rstd, shift);
+      if (affine) z = fmaf(z, load_f(gp, DT_F32, j), load_f(bp, DT_F32, j));
+      if (do_gelu) z = gelu(z);
+      store_f(d, dt, base + j, z);
+    }
+  }
+}
+
+VM_DEV bool row_vec_ok(uint32_t seg, const gbyte* a, const gbyte* d, uint32_t adt, uint32_t dt) {
+  const bool fmt = (adt == DT_F32 || adt == DT_BF16 || adt == DT_F16) &&
+                   (dt == DT_F32 || dt == DT_BF16 || dt == DT_F16);
+  return fmt && (seg & 3) == 0 && seg <= 8 * 4 * kBlock && ((uintptr_t(a) | uintptr_t(d)) & 15) == 0;
+}
+
+VM_TILE void layernorm_tiles(Args A, uint32_t ti, uint32_t lo, uint32_t hi) {
+  A = uargs(A);
+  const VM_K Task& t = task_of(A, ti);
+  const uint32_t n_out = t.p[0], seg = t.p[1];
+  const uint32_t dt = (t.tile_op >> 8) & 0xFF, adt = (t.tile_op >> 16) & 0xFF;
+  hi = min(hi, n_out);
+  if (lo >= hi) return;
+  bool ok = row_vec_ok(seg, resolve(A, t.a), resolve(A, t.dst), adt, dt);
+  if (ok && (t.p[3] & LN_AFFINE)) ok = ((uintptr_t(resolve(A, t.b)) | uintptr_t(resolve(A, t.p[4]))) & 15) == 0;
+  if (!ok) return ln_rows_generic(A, ti, lo, hi);
+  const uint32_t nv4 = seg >> 2;
+  if (nv4 <= 1 * kBlock) return ln_rows_vec<1>(A, ti, lo, hi);
+  if (nv4 <= 2 * kBlock) return ln_rows_vec<2>(A, ti, lo, hi);
+  if (nv4 <= 4 * kBlock) return ln_rows_vec<4>(A, ti, lo, hi);
+  return ln_rows_vec<8>(A, ti, lo, hi);
+}
+
+// SOFTMAX_SEG rows: exp(x - max) / sum.
+template <int NV>
+VM_TILE void softmax_rows_vec(Args A, uint32_t ti, uint32_t r0, uint32_t r1) {
+  A = uargs(A);
+  const VM_K Task& t = task_of(A, ti);
+  float* red = lds_f32();
+  const uint32_t seg = t.p[1];
+  const uint32_t dt = (t.tile_op >> 8) & 0xFF, adt = (t.tile_op >> 16) & 0xFF;
+  const gbyte* a = resolve(A, t.a);
+  gbyte* d = resolve(A, t.dst);
+  const uint32_t nv4 = seg >> 2;
+  Row<NV> x, xn;
+  row_load(x, a, adt, uint64_t(r0) * seg, nv4);
+  for (uint32_t r = r0; r < r1; ++r) {
+    if (r + 1 < r1) row_load(xn, a, adt, uint64_t(r + 1) * seg, nv4);
+    float m = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < NV; ++k)
+      if (threadIdx.x + k * kBlock < nv4) m = fmaxf(m, fmaxf(fmaxf(x.v[k].x, x.v[k].y), fmaxf(x.v[k].z, x.v[k].w)));
+    m = block_reduce(m, OpMax(), red);
+    float s = 0.0f;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      if (threadIdx.x + k * kBlock < nv4) {
+        x.v[k].x = __expf(x.v[k].x - m);
+        x.v[k].y = __expf(x.v[k].y - m);
+        x.v[k].z = __expf(x.v[k].z - m);
+        x.v[k].w = __expf(x.v[k].w - m);
+        s += (x.v[k].x + x.v[k].y) + (x.v[k].z + x.v[k].w);
+      }
+    }
+    s = block_reduce(s, OpSum(), red + kWaves);
+    const float inv = 1.0f / s;
+    const uint64_t base = uint64_t(r) * seg;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      const uint32_t q = threadIdx.x + k * kBlock;
+      if (q < nv4) st4(d, dt, base + 4ull * q, v4f_make(x.v[k].x * inv, x.v[k].y * inv, x.v[k].z * inv, x.v[k].w * inv));
+    }
+    if (r + 1 < r1) x = xn;
+  }
+}
+
+VM_TILE void softmax_tiles(Args A, uint32_t ti, uint32_t lo, uint32_t hi) {
+  A = uargs(A);
+  const VM_K Task& t = task_of(A, ti);
+  float* red = lds_f32();
+  const uint32_t n_out = t.p[0], seg = t.p[1];
+  const uint32_t dt = (t.tile_op >> 8) & 0xFF, adt = (t.tile_op >> 16) & 0xFF;
+  hi = min(hi, n_out);
+  if (lo >= hi) return;
+  const gbyte* a = resolve(A, t.a);
+  gbyte* d = resolve(A, t.dst);
+  if (row_vec_ok(seg, a, d, adt, dt)) {
+    const uint32_t nv4 = seg >> 2;
+    if (nv4 <= 1 * kBlock) return softmax_rows_vec<1>(A, ti, lo, hi);
+    if (nv4 <= 2 * kBlock) return softmax_rows_vec<2>(A, ti, lo, hi);
+    if (nv4 <= 4 * kBlock) return softmax_rows_vec<4>(A, ti, lo, hi);
+    return softmax_rows_vec<8>(A, ti, lo, hi);
+  }
+  for (uint32_t r = lo; r < hi; ++r) {
+    const uint64_t base = uint64_t(r) * seg;
+    float m = -INFINITY;
+    for (uint32_t j = threadIdx.x; j < seg; j += kBlock) m = fmaxf(m, load_f(a, adt, base + j));
+    m = block_reduce(m, OpMax(), red);
+    float s = 0.0f;
+    for (uint32_t j = threadIdx.x; j < seg; j += kBlock) s += __expf(load_f(a, adt, base + j) - m);
+    s = block_reduce(s, OpSum(), red + kWaves);
+    const float inv = 1.0f / s;
+    for (uint32_t j = threadIdx.x; j < seg; j += kBlock) store_f(d, dt, base + j, __expf(load_f(a, adt, base + j) - m) * inv);
+  }
+}
+
+// ARGMAX_SEG: dst = first index of the row maximum (a NaN wins: its first index),
+// b = that value (a's dtype).  p0 n_out, p1 seg.
+VM_DEV bool amax_better(float v, uint32_t i, float bv, uint32_t bi) {
+  const bool vn = v != v, bn = bv != bv;
+  if (vn != bn) return vn;
+  if (vn) return i < bi;
+  if (v != bv) return v > bv;
+  return i < bi;
+}
+VM_TILE void argmax_tiles(Args A, uint32_t ti, uint32_t lo, uint32_t hi) {
+  A = uargs(A);
+  const VM_K Task& t = task_of(A, ti);
+  const uint32_t n_out = t.p[0], seg = t.p[1];
+  const uint32_t dt = (t.tile_op >> 8) & 0xFF, adt = (t.tile_op >> 16) & 0xFF;
+  const gbyte* a = resolve(A, t.a);
+  gbyte* di = resolve(A, t.dst);
+  gbyte* dv = resolve(A, t.b);
+  float* sv = lds_f32();
+  uint32_t* si = reinterpret_cast<uint32_t*>(sv + kBlock);
+  hi = min(hi, n_out);
+  for (uint32_t o = lo; o < hi; ++o) {
+    const uint64_t base = uint64_t(o) * seg;
+    float bv = -INFINITY;
+    uint32_t bi = 0xFFFFFFFFu;
+    for (uint32_t j = threadIdx.x; j < seg; j += kBlock) {
+      const float v = load_f(a, adt, base + j);
+      if (bi == 0xFFFFFFFFu || amax_better(v, j, bv, bi)) {
+        bv = v;
+        bi = j;
+      }
+    }
+    lds_barrier();
+    sv[threadIdx.x] = bv;
+    si[threadIdx.x] = bi;
+    lds_barrier();
+    for (int s = kBlock / 2; s > 0; s >>= 1) {
+      if (int(threadIdx.x) < s) {
+        const float v2 = sv[threadIdx.x + s];
+        const uint32_t i2 = si[threadIdx.x + s];
+        if (i2 != 0xFFFFFFFFu &&
+            (si[threadIdx.x] == 0xFFFFFFFFu || amax_better(v2, i2, sv[threadIdx.x], si[threadIdx.x]))) {
+          sv[threadIdx.x] = v2;
+          si[threadIdx.x] = i2;
+        }
+      }
+      lds_barrier();
+    }
+    if (threadIdx.x == 0) {
+      const uint32_t idx = si[0] == 0xFFFFFFFFu ? 0u : si[0];
+      if (dt == DT_I64) gcast<int64_t>(di)[o] = idx;
+      else gcast<uint32_t>(di)[o] = idx;
+      store_f(dv, adt, o, si[0] == 0xFFFFFFFFu ? -INFINITY : sv[0]);
+    }
+  }
+}
+
+}  // namespace vm

@@ -1,0 +1,248 @@
+// Device-side helpers of the persistent VM: address spaces, buffer handle
+// resolution, element conversions, wave64 DPP reductions, the grid barrier.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "vm_abi.h"
+
+namespace vm {
+
+constexpr int kBlock = 256;              // threads per lane (4 wave64s)
+constexpr int kWaves = kBlock / 64;
+
+#define VM_DEV __device__ __forceinline__
+// Tile-op entry points and their large specialisations are real device functions:
+// each gets its own register allocation and instruction schedule (the kernel
+// reserves the maximum), which keeps the one-kernel build tractable.
+#define VM_TILE __device__ __attribute__((noinline))
+
+// Address spaces: tensor data is global memory (global_load/store with an SGPR
+// base), the kernel-argument block and the read-only program tables (tasks,
+// entries, lane table, aux) are read through the constant address space so
+// wave-uniform reads become scalar loads.
+#define VM_G __attribute__((address_space(1)))
+#define VM_K __attribute__((address_space(4)))
+typedef VM_G uint8_t gbyte;
+typedef const VM_K VmArgs* Args;
+
+// The lane's LDS: one dynamic allocation shared by every tile op (the largest
+// user sizes it).  Declared at namespace scope so non-inlined tile functions
+// address it as LDS directly.
+extern __shared__ __align__(16) uint8_t vm_smem[];
+
+VM_DEV uint32_t uni(uint32_t x) { return __builtin_amdgcn_readfirstlane(x); }
+
+// A pointer argument of a non-inlined function arrives in VGPRs; make it
+// wave-uniform again so reads through it are scalar.
+template <typename T>
+VM_DEV T* uni_ptr(T* p) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint64_t lo = uni(uint32_t(v)), hi = uni(uint32_t(v >> 32));
+  return reinterpret_cast<T*>((hi << 32) | lo);
+}
+VM_DEV Args uargs(Args A) { return uni_ptr(A); }
+
+template <typename T>
+VM_DEV VM_G T* gcast(gbyte* p) { return (VM_G T*)p; }
+template <typename T>
+VM_DEV const VM_G T* gcast(const gbyte* p) { return (const VM_G T*)p; }
+
+// Builtin vector types (clang ext vectors load and store through address-space
+// qualified pointers, unlike HIP's float4 class).
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+typedef uint32_t v2u __attribute__((ext_vector_type(2)));
+VM_DEV v4f v4f_make(float a, float b, float c, float d) { return v4f{a, b, c, d}; }
+VM_DEV v4u v4u_make(uint32_t a, uint32_t b, uint32_t c, uint32_t d) { return v4u{a, b, c, d}; }
+VM_DEV v2u v2u_make(uint32_t a, uint32_t b) { return v2u{a, b}; }
+
+// Value load through a typed global pointer (an rvalue without the address space).
+template <typename T>
+VM_DEV T gld(const VM_G T* p) { return *p; }
+
+// Control records read field by field from the constant address space.
+VM_DEV Entry load_entry(const VM_K Entry* p) {
+  Entry e;
+  e.task = p->task;
+  e.tile_lo = p->tile_lo;
+  e.tile_hi = p->tile_hi;
+  e.wait_flag = p->wait_flag;
+  e.wait_count = p->wait_count;
+  e.signal_flag = p->signal_flag;
+  e.slots = p->slots;
+  e.pad = p->pad;
+  return e;
+}
+VM_DEV LaneSpan load_span(const VM_K LaneSpan* p) {
+  LaneSpan s;
+  s.off = p->off;
+  s.count = p->count;
+  s.root_len = p->root_len;
+  s.pad = p->pad;
+  return s;
+}
+
+VM_DEV const VM_K int32_t* aux_of(Args A) { return (const VM_K int32_t*)A->aux; }
+VM_DEV const VM_K Task& task_of(Args A, uint32_t i) { return ((const VM_K Task*)A->tasks)[uni(i)]; }
+
+// Handles are wave-uniform: an arena byte offset, or PORT_BIT | port index.
+VM_DEV gbyte* resolve(Args A, uint32_t h) {
+  h = uni(h);
+  uint8_t* p = (h & PORT_BIT) ? A->ports[h & (kMaxPorts - 1)] : A->arena + h;
+  return (gbyte*)p;
+}
+
+// ---- element formats ------------------------------------------------------------------
+VM_DEV float bf16_to_f32(uint16_t b) { return __uint_as_float(uint32_t(b) << 16); }
+
+// Round-to-nearest-even f32 -> bf16 (vm_common.cl:66-70).  A NaN keeps a NaN
+// pattern (quiet bit set) instead of the carry the bit formula would produce.
+VM_DEV uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return uint16_t((u >> 16) | 0x40u);
+  return uint16_t((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+}
+VM_DEV float f16_to_f32(uint16_t h) { return float(__builtin_bit_cast(_Float16, h)); }
+VM_DEV uint16_t f32_to_f16(float f) { return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f)); }
+
+// Element size in bytes of a dtype.
+VM_DEV uint32_t dt_size(uint32_t dt) {
+  return (dt == DT_I64 || dt == DT_F64) ? 8u : dt == DT_BOOL ? 1u
+       : (dt == DT_F16 || dt == DT_BF16) ? 2u : 4u;
+}
+
+// Load element i of a buffer as f32 (the VM's arithmetic domain).
+VM_DEV float load_f(const gbyte* base, uint32_t dt, uint64_t i) {
+  switch (dt) {
+    case DT_BF16: return bf16_to_f32(gcast<uint16_t>(base)[i]);
+    case DT_F16: return f16_to_f32(gcast<uint16_t>(base)[i]);
+    case DT_I32: return float(gcast<int32_t>(base)[i]);
+    case DT_U32: return float(gcast<uint32_t>(base)[i]);
+    case DT_BOOL: return float(base[i]);
+    case DT_I64: return float(gcast<int64_t>(base)[i]);
+    case DT_F64: return float(gcast<double>(base)[i]);
+    default: return gcast<float>(base)[i];
+  }
+}
+VM_DEV void store_f(gbyte* base, uint32_t dt, uint64_t i, float v) {
+  switch (dt) {
+    case DT_BF16: gcast<uint16_t>(base)[i] = f32_to_bf16(v); break;
+    case DT_F16: gcast<uint16_t>(base)[i] = f32_to_f16(v); break;
+    case DT_F64: gcast<double>(base)[i] = double(v); break;
+    case DT_I32: gcast<int32_t>(base)[i] = int32_t(v); break;
+    case DT_U32: gcast<uint32_t>(base)[i] = uint32_t(int64_t(v)); break;
+    case DT_I64: gcast<int64_t>(base)[i] = int64_t(v); break;
+    case DT_BOOL: base[i] = v != 0.0f; break;
+    default: gcast<float>(base)[i] = v; break;
+  }
+}
+
+// ---- wave64 reductions through DPP ----------------------------------------------
+// quad_perm [1,0,3,2] and [2,3,0,1], then row_ror 4 and 8: every lane of a
+// 16-lane row holds the row total; four v_readlane_b32 combine the rows.
+template <int CTRL>
+VM_DEV float dpp(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+VM_DEV float lane_read(float x, int l) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), l));
+}
+
+struct OpSum { VM_DEV float operator()(float a, float b) const { return a + b; } };
+struct OpMax { VM_DEV float operator()(float a, float b) const { return fmaxf(a, b); } };
+struct OpMin { VM_DEV float operator()(float a, float b) const { return fminf(a, b); } };
+struct OpProd { VM_DEV float operator()(float a, float b) const { return a * b; } };
+
+// Reduce over the 64 lanes of a wave; the result is wave-uniform.
+template <class Op>
+VM_DEV float wave_reduce(float x, Op op) {
+  x = op(x, dpp<0xB1>(x));     // quad_perm [1,0,3,2]
+  x = op(x, dpp<0x4E>(x));     // quad_perm [2,3,0,1]
+  x = op(x, dpp<0x124>(x));    // row_ror:4
+  x = op(x, dpp<0x128>(x));    // row_ror:8
+  return op(op(lane_read(x, 0), lane_read(x, 16)), op(lane_read(x, 32), lane_read(x, 48)));
+}
+VM_DEV float wave_sum(float x) { return wave_reduce(x, OpSum()); }
+VM_DEV float wave_max(float x) { return wave_reduce(x, OpMax()); }
+
+// ---- grid barrier ----------------------------------------------------------------------
+// Self-resetting generation barrier over ctl[BAR_COUNT] / ctl[BAR_GEN].  The block's
+// stores are published at agent scope (L2 write-back across the 8 XCDs) by thread 0
+// after the block barrier, and the acquire on exit invalidates this CU's caches
+// before any thread reads other lanes' results (the reference's device-scope
+// fence pair, vm_common.cl:231-300).  The spin reads the generation word with a
+// plain atomic load, and gives up after `timeout_ticks` of the 100 MHz constant
+// clock so a broken schedule ends the launch with an error instead of hanging.
+// Returns false when the launch must abort.
+VM_DEV bool grid_barrier(Args A) {
+  __shared__ uint32_t s_ok;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t* ctl = A->ctl;
+    uint32_t ok = 1;
+    const uint32_t gen = __hip_atomic_load(&ctl[BAR_GEN], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t arrived =
+        __hip_atomic_fetch_add(&ctl[BAR_COUNT], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    if (arrived == A->n_lanes - 1) {
+      __hip_atomic_store(&ctl[BAR_COUNT], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_fetch_add(&ctl[BAR_GEN], 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+    } else {
+      const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+      while (__hip_atomic_load(&ctl[BAR_GEN], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gen) {
+        if (__hip_atomic_load(&ctl[BAR_ERROR], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
+          ok = 0;
+          break;
+        }
+        if (__builtin_amdgcn_s_memrealtime() - t0 > A->timeout_ticks) {
+          uint32_t expect = 0;
+          __hip_atomic_compare_exchange_strong(&ctl[BAR_ERROR], &expect, uint32_t(VM_ERR_BARRIER_TIMEOUT),
+                                               __ATOMIC_RELAXED, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          ok = 0;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+      }
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    }
+    s_ok = ok;
+  }
+  __syncthreads();
+  return s_ok != 0;
+}
+
+// Record an error from a lane (first error wins) so the host can report it.
+VM_DEV void raise_error(Args A, uint32_t code, uint32_t info) {
+  if (threadIdx.x == 0) {
+    uint32_t expect = 0;
+    if (__hip_atomic_compare_exchange_strong(&A->ctl[BAR_ERROR], &expect, code, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT))
+      __hip_atomic_store(&A->ctl[BAR_ERRINFO], info, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+// Coherent read of a control-flow condition (a value another lane may have written
+// in the previous phase).  `fmt` = byte width | 0x100 for float types (the sign bit
+// alone does not make a float condition true).
+VM_DEV bool read_cond(const gbyte* p, uint32_t fmt) {
+  const uint32_t w = fmt & 0xFF;
+  uint64_t bits;
+  if (w == 8) {
+    bits = __hip_atomic_load((const uint64_t*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (fmt & 0x100) bits &= 0x7FFFFFFFFFFFFFFFull;
+  } else {
+    // aligned 4-byte word that holds the value (buffers are 64-byte aligned)
+    const uint32_t word = __hip_atomic_load((const uint32_t*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    bits = w == 1 ? (word & 0xFFu) : w == 2 ? (word & 0xFFFFu) : word;
+    if (fmt & 0x100) bits &= (w == 2 ? 0x7FFFull : 0x7FFFFFFFull);
+  }
+  return bits != 0;
+}
+
+// Coherent read of a runtime index scalar (dynamic-slice starts).
+VM_DEV int64_t read_index(const gbyte* p, bool is64) {
+  if (is64) return __hip_atomic_load((const int64_t*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return __hip_atomic_load((const int32_t*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+}  // namespace vm

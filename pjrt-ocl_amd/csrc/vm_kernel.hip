@@ -1,0 +1,188 @@
+// The persistent VM: one workgroup per lane, each walking its own entry stream
+// (reference: pjrt_plugin/kernels/vm_main.cl:107-258 `vm2`).
+//
+// Stream walk: a frame stack (depth 8) of {pc, end, owning control entry, phase}.
+//   BARRIER  -> grid barrier across all lanes
+//   WHILE    -> cond sub-list, barrier, read cond, body sub-list, barrier, repeat
+//   FOR      -> body sub-list, barrier, x trip count (wait_flag)
+//   IF       -> then / else sub-list chosen by the cond value
+//   NOP      -> skip
+//   task     -> run tiles [tile_lo, tile_hi) of tasks[task]
+// Consecutive task entries of one lane form a fused chain: a block barrier with a
+// workgroup fence separates them, because a tile op maps elements to threads
+// differently from its producer (vm_main.cl:82-100).
+#include <hip/hip_runtime.h>
+
+#include "tile_attn.h"
+#include "tile_ew.h"
+#include "tile_index.h"
+#include "tile_mma.h"
+#include "tile_reduce.h"
+
+namespace vm {
+
+constexpr int kMaxDepth = 8;
+constexpr uint32_t kRootOwner = 0xFFFFFFFFu;
+
+// LDS shared by the tile ops of one lane (the matmul's double-buffered operand
+// slabs are the largest user).
+constexpr int kSmemBytes = (kMmaLdsBytes > kAttnLdsBytes ? kMmaLdsBytes : kAttnLdsBytes);
+
+VM_DEV void exec_tiles(Args A, uint32_t ti, uint32_t lo, uint32_t hi) {
+  switch (task_of(A, ti).tile_op & 0xFF) {
+    case TOP_EW: ew_tile(A, ti, lo, hi); break;
+    case TOP_MMA: mma_tiles(A, ti, lo, hi); break;
+    case TOP_GATHER: gather_tiles(A, ti, lo, hi, false); break;
+    case TOP_RED_PART: red_flat_tiles(A, ti, lo, hi, false); break;
+    case TOP_RED_COMB: red_flat_tiles(A, ti, lo, hi, true); break;
+    case TOP_IOTA_DIM: iota_tiles(A, ti, lo, hi); break;
+    case TOP_SCATTER: gather_tiles(A, ti, lo, hi, true); break;
+    case TOP_DYN_GATHER: dyn_tiles(A, ti, lo, hi, false); break;
+    case TOP_DYN_SCATTER: dyn_tiles(A, ti, lo, hi, true); break;
+    case TOP_RED_SEG: red_seg_tiles(A, ti, lo, hi); break;
+    case TOP_SOFTMAX_SEG: softmax_tiles(A, ti, lo, hi); break;
+    case TOP_LAYERNORM_SEG: layernorm_tiles(A, ti, lo, hi); break;
+    case TOP_MAP_REGION: map_region_tiles(A, ti, lo, hi); break;
+    case TOP_FLASH_ATTN: flash_attn_tiles(A, ti, lo, hi); break;
+    case TOP_RED_STRIDED: red_strided_tiles(A, ti, lo, hi); break;
+    case TOP_GATHER_INDEX: gather_index_tiles(A, ti, lo, hi); break;
+    case TOP_ARGMAX_SEG: argmax_tiles(A, ti, lo, hi); break;
+    default: raise_error(A, VM_ERR_BAD_TASK, task_of(A, ti).tile_op); break;
+  }
+}
+
+__global__ __launch_bounds__(kBlock, 1) void vm_main(VmArgs args) {
+  // The VmArgs block is the kernel's only explicit argument: offset 0 of the
+  // kernarg segment, read in place through the constant address space.
+  (void)args;
+  const Args A = (Args)__builtin_amdgcn_kernarg_segment_ptr();
+  const uint32_t lane = blockIdx.x;
+  const LaneSpan span = load_span((const VM_K LaneSpan*)A->lanes + lane);
+  const VM_K Entry* ents = (const VM_K Entry*)A->entries + span.off;
+
+  uint32_t f_pc[kMaxDepth], f_end[kMaxDepth], f_own[kMaxDepth], f_phase[kMaxDepth];
+  int sp = 0;
+  f_pc[0] = 0;
+  f_end[0] = span.root_len;
+  f_own[0] = kRootOwner;
+  f_phase[0] = 0;
+  bool pub = false;     // a tile entry ran since the last barrier
+
+  for (;;) {
+    if (f_pc[sp] >= f_end[sp]) {
+      if (f_own[sp] == kRootOwner) break;
+      const Entry w = load_entry(ents + f_own[sp]);
+      if (w.task == ENT_IF) {                 // branch done
+        --sp;
+        ++f_pc[sp];
+        continue;
+      }
+      // loop bodies end with a grid barrier that publishes the carries
+      if (!grid_barrier(A)) return;
+      pub = false;
+      if (w.task == ENT_FOR) {
+        if (--f_phase[sp] != 0) {
+          f_pc[sp] = w.tile_lo;
+          f_end[sp] = w.tile_lo + w.tile_hi;
+        } else {
+          --sp;
+          ++f_pc[sp];
+        }
+        continue;
+      }
+      if (f_phase[sp] == 0) {                 // while-cond done: test
+        if (read_cond(resolve(A, w.signal_flag), w.pad)) {
+          f_pc[sp] = w.wait_flag;
+          f_end[sp] = w.wait_flag + w.wait_count;
+          f_phase[sp] = 1;
+        } else {
+          --sp;
+          ++f_pc[sp];
+        }
+      } else {                                // while-body done: re-test
+        f_pc[sp] = w.tile_lo;
+        f_end[sp] = w.tile_lo + w.tile_hi;
+        f_phase[sp] = 0;
+      }
+      continue;
+    }
+
+    const uint32_t epc = f_pc[sp];
+    const Entry en = load_entry(ents + epc);
+    if (en.task == ENT_BARRIER) {
+      if (!grid_barrier(A)) return;
+      pub = false;
+      ++f_pc[sp];
+      continue;
+    }
+    if (en.task == ENT_WHILE || en.task == ENT_FOR || en.task == ENT_IF) {
+      uint32_t start, len, phase;
+      if (en.task == ENT_WHILE) {
+        start = en.tile_lo;
+        len = en.tile_hi;
+        phase = 0;
+      } else if (en.task == ENT_FOR) {
+        if (en.wait_flag == 0) {
+          ++f_pc[sp];
+          continue;
+        }
+        start = en.tile_lo;
+        len = en.tile_hi;
+        phase = en.wait_flag;
+      } else {
+        const bool c = read_cond(resolve(A, en.signal_flag), en.pad);
+        start = c ? en.tile_lo : en.wait_flag;
+        len = c ? en.tile_hi : en.wait_count;
+        phase = 2;
+        if (len == 0) {
+          ++f_pc[sp];
+          continue;
+        }
+      }
+      if (sp + 1 >= kMaxDepth) {
+        raise_error(A, VM_ERR_FRAME_DEPTH, lane);
+        return;
+      }
+      ++sp;
+      f_pc[sp] = start;
+      f_end[sp] = start + len;
+      f_own[sp] = epc;
+      f_phase[sp] = phase;
+      continue;
+    }
+    if (en.task != ENT_NOP) {
+      if (pub) __syncthreads();
+      pub = true;
+      exec_tiles(A, en.task, en.tile_lo, en.tile_hi);
+    }
+    ++f_pc[sp];
+  }
+}
+
+}  // namespace vm
+
+// ---- host side of the launch (called by the runtime) ------------------------------------
+extern "C" int vm_kernel_smem_bytes() { return vm::kSmemBytes; }
+
+extern "C" hipError_t vm_kernel_prepare() {
+  return hipFuncSetAttribute(reinterpret_cast<const void*>(&vm::vm_main), hipFuncAttributeMaxDynamicSharedMemorySize,
+                             vm::kSmemBytes);
+}
+
+extern "C" hipError_t vm_kernel_occupancy(int* blocks_per_cu) {
+  return hipOccupancyMaxActiveBlocksPerMultiprocessor(blocks_per_cu, reinterpret_cast<const void*>(&vm::vm_main),
+                                                      vm::kBlock, vm::kSmemBytes);
+}
+
+// cooperative != 0: hipLaunchCooperativeKernel (co-residency of every lane is
+// guaranteed or the launch fails); otherwise a plain launch, used only when the
+// lane count fits the occupancy the runtime verified.
+extern "C" hipError_t vm_kernel_launch(const vm::VmArgs* args, hipStream_t stream, int cooperative) {
+  vm::VmArgs a = *args;
+  void* params[] = {&a};
+  if (cooperative)
+    return hipLaunchCooperativeKernel(reinterpret_cast<const void*>(&vm::vm_main), dim3(a.n_lanes), dim3(vm::kBlock),
+                                      params, vm::kSmemBytes, stream);
+  return hipLaunchKernel(reinterpret_cast<const void*>(&vm::vm_main), dim3(a.n_lanes), dim3(vm::kBlock), params,
+                         vm::kSmemBytes, stream);
+}

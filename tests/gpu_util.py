@@ -1,0 +1,74 @@
+"""Helpers of the GPU parity tests: one Runtime per session, programs scheduled for
+the device and checked against the CPU oracle (oracle/vmref.py)."""
+from __future__ import annotations
+
+import sys
+
+import numpy as np
+
+from oracle import vmref
+from pjrt_amd import scheduler as S
+from pjrt_amd import vmprogram as V
+
+_RT = None
+
+
+def runtime():
+    """The session's Runtime (device 0).  Raises when no MI355X / libvmrt.so."""
+    global _RT
+    if _RT is None:
+        from pjrt_amd.runtime import Runtime
+        _RT = Runtime()
+        print(f"[gpu] {_RT.info['name']} {_RT.info['arch']} lanes={_RT.info['n_lanes']}"
+              f"/{_RT.info['max_lanes']} lds={_RT.info['lds_bytes']}", file=sys.stderr, flush=True)
+    return _RT
+
+
+def blob_for(prog: V.VMProgram, nlanes=None, ew_ts=4096, mma_t=128, **kw) -> tuple:
+    rt = runtime()
+    cfg = S.DeviceConfig(nlanes=nlanes or rt.info["n_lanes"], ew_ts=ew_ts, mma_t=mma_t, **kw)
+    return V.serialize(prog, S.schedule_program(prog, cfg)), cfg
+
+
+def run_gpu(blob: bytes, args, ew_ts=4096, mma_t=128):
+    rt = runtime()
+    lp = rt.load(blob, ew_ts=ew_ts, mma_t=mma_t)
+    try:
+        return lp(*args)
+    finally:
+        lp.close()
+
+
+def run_both(prog, args, nlanes=None, ew_ts=4096, mma_t=128, oracle="schedule", **kw):
+    """(gpu outputs, oracle outputs) for a tensor program scheduled for the device."""
+    if isinstance(prog, bytes):
+        blob = prog
+    else:
+        blob, _ = blob_for(prog, nlanes=nlanes, ew_ts=ew_ts, mma_t=mma_t, **kw)
+    print(f"[gpu] case: {len(blob)} bytes, lanes={vmref.parse(blob).n_lanes}, ew_ts={ew_ts}, mma_t={mma_t}",
+          file=sys.stderr, flush=True)
+    got = run_gpu(blob, args, ew_ts=ew_ts, mma_t=mma_t)
+    if oracle == "schedule":
+        want = vmref.execute_schedule(blob, args, ew_ts=ew_ts, mma_t=mma_t, check_order=False)
+    elif oracle == "tensor":
+        want = vmref.execute(blob, args, ew_ts=ew_ts, mma_t=mma_t)
+    else:
+        want = None
+    return got, want
+
+
+def as_f32(x, dt):
+    return vmref.bf16_to_f32(x) if dt == V.DT_BF16 else np.asarray(x, np.float32)
+
+
+def assert_rel(got, want, rtol, atol=0.0, what=""):
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    assert got.shape == want.shape, (got.shape, want.shape)
+    bad = ~(np.abs(got - want) <= atol + rtol * np.abs(want))
+    both_nan = np.isnan(got) & np.isnan(want)
+    bad &= ~both_nan
+    if bad.any():
+        idx = np.argwhere(bad)[:5]
+        raise AssertionError(f"{what}: {int(bad.sum())} of {bad.size} outside rtol={rtol} atol={atol}; "
+                             f"first {[(tuple(i), float(got[tuple(i)]), float(want[tuple(i)])) for i in idx]}")

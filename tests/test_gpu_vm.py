@@ -1,0 +1,364 @@
+"""GPU parity: the HIP megakernel VM (libvmrt.so, called through its C ABI) against
+the CPU oracle on the same seeded inputs.
+
+Bars: bit-exact for integer, bool, index and control
+flow; rel 1e-5 for f32 elementwise / reduce (a few ulp of device libm); GEMM and
+attention rel 1e-3 (f32) / 1e-2 (bf16) against float64; bf16 outputs of f32 math
+within one bf16 ulp (2^-8 relative) of the oracle's rounding."""
+import numpy as np
+import pytest
+
+import vmprogs as P
+from gpu_util import as_f32, assert_rel, run_both, runtime
+from oracle import vmref
+from pjrt_amd import graph as G
+from pjrt_amd import vmprogram as V
+
+pytestmark = pytest.mark.gpu
+
+BF16_ULP = 2.0 ** -8
+
+
+def test_runtime_opens_device():
+    info = runtime().info
+    assert info["arch"].startswith("gfx950")
+    assert info["n_lanes"] >= 1 and info["max_lanes"] >= info["n_lanes"]
+
+
+# --- reference known answers (runtime_test.cc:136-267) --------------------------------
+
+def test_runtime_test_a_two_level_ew():
+    blob, args, want = P.raw_two_level_ew(256)
+    got, _ = run_both(blob, args, ew_ts=256, oracle=None)
+    np.testing.assert_array_equal(got[0], want[0])
+
+
+def test_runtime_test_b_while_doubling():
+    blob, args, want = P.raw_while_doubling(256)
+    got, _ = run_both(blob, args, ew_ts=256, oracle=None)
+    np.testing.assert_array_equal(got[0], want[0])
+
+
+def test_runtime_test_c_region_gelu():
+    blob, args, want = P.raw_region_gelu(256)
+    got, _ = run_both(blob, args, ew_ts=256, oracle=None)
+    assert np.max(np.abs(got[0] - want[0])) <= 1e-5
+
+
+@pytest.mark.parametrize("name", sorted(P.WHILE_CASES))
+@pytest.mark.parametrize("nlanes", [3, 256])
+def test_control_flow_closed_forms(name, nlanes):
+    prog, args, want = P.WHILE_CASES[name]()
+    got, _ = run_both(prog, args, nlanes=nlanes, ew_ts=256, oracle=None)
+    for g, w in zip(got, want):
+        np.testing.assert_array_equal(g.reshape(np.shape(w)), w)
+
+
+# --- elementwise ----------------------------------------------------------------------------
+
+BIN = ["add", "mul", "sub", "div", "maximum", "minimum", "pow", "atan2", "remainder"]
+UN = ["copy", "neg", "exp", "log", "sqrt", "rsqrt", "tanh", "abs", "floor", "ceil", "sign", "log1p",
+      "expm1", "cbrt", "sin", "cos", "tan", "rint", "round", "gelu"]
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+@pytest.mark.parametrize("n", [1, 1000, 70001])
+def test_ew_float_ops(dt, n):
+    rng = np.random.default_rng(11)
+    a = (np.abs(rng.standard_normal(n)) + 0.25).astype(np.float32)
+    b = (np.abs(rng.standard_normal(n)) + 0.5).astype(np.float32)
+    g = G.Graph()
+    x, y = g.input((n,), dt), g.input((n,), dt)
+    outs = [getattr(g, op)(x, y) for op in BIN] + [g.unary(op, x) for op in UN]
+    outs.append(g.affine(x, 1.5, -0.25))
+    g.output(*outs)
+    got, want = run_both(g.build(), [a, b], ew_ts=1024)
+    for k, (gv, wv) in enumerate(zip(got, want)):
+        tol = BF16_ULP if dt == "bf16" else 4e-6
+        assert_rel(as_f32(gv, V.DT_BY_NAME[dt]), as_f32(wv, V.DT_BY_NAME[dt]), tol, 1e-6, f"{dt} op {k}")
+
+
+@pytest.mark.parametrize("dt", ["i32", "u32", "i64"])
+def test_ew_integer_ops_bit_exact(dt):
+    rng = np.random.default_rng(12)
+    n = 5003
+    npdt = V.DT_NUMPY[V.DT_BY_NAME[dt]]
+    info = np.iinfo(npdt)
+    a = rng.integers(info.min // 2, info.max // 2, n, dtype=np.int64).astype(npdt)
+    b = rng.integers(-70, 70, n).astype(npdt)
+    b[::7] = 0
+    g = G.Graph()
+    x, y = g.input((n,), dt), g.input((n,), dt)
+    outs = [g.add(x, y), g.sub(x, y), g.mul(x, y), g.div(x, y), g.maximum(x, y), g.minimum(x, y),
+            g.bit_and(x, y), g.bit_or(x, y), g.bit_xor(x, y), g.shl(x, y), g.shr_l(x, y), g.shr_a(x, y),
+            g.unary("neg", x), g.unary("abs", x), g.unary("sign", x), g.unary("not", x)]
+    g.output(*outs)
+    got, want = run_both(g.build(), [a, b], ew_ts=512)
+    for k, (gv, wv) in enumerate(zip(got, want)):
+        np.testing.assert_array_equal(gv, wv, err_msg=f"{dt} op {k}")
+
+
+def test_compare_select_convert_bitcast_isfinite():
+    rng = np.random.default_rng(13)
+    n = 4099
+    a = rng.standard_normal(n).astype(np.float32) * 3e9
+    a[::11] = np.nan
+    a[::13] = np.inf
+    b = rng.standard_normal(n).astype(np.float32)
+    g = G.Graph()
+    x, y = g.input((n,)), g.input((n,))
+    outs = []
+    for pred in ("EQ", "NE", "LT", "LE", "GT", "GE"):
+        outs.append(g.compare(x, y, pred))
+    c = g.compare(x, y, "GT")
+    outs.append(g.select(c, x, y))
+    for dt in ("i32", "u32", "i64", "bf16", "f16", "bool", "f64"):
+        outs.append(g.convert(x, dt))
+    outs.append(g.bitcast(x, "i32"))
+    outs.append(g.is_finite(x))
+    i = g.convert(y, "i32")
+    outs.append(g.convert(i, "i64"))
+    outs.append(g.convert(g.convert(i, "i64"), "u32"))
+    g.output(*outs)
+    got, want = run_both(g.build(), [a, b], ew_ts=256)
+    for k, (gv, wv) in enumerate(zip(got, want)):
+        np.testing.assert_array_equal(gv.view(np.uint8), wv.view(np.uint8), err_msg=f"output {k}")
+
+
+# --- reductions and row ops ------------------------------------------------------------------
+
+@pytest.mark.parametrize("kind", [0, 1, 2, 3])
+def test_float_reductions(kind):
+    rng = np.random.default_rng(20 + kind)
+    a = (rng.standard_normal((37, 1000)) * (0.01 if kind == 3 else 1.0) + (1.0 if kind == 3 else 0.0))
+    a = a.astype(np.float32)
+    g = G.Graph()
+    x = g.input(a.shape)
+    g.output(g.reduce_all(x, kind, ew_ts=1024), g.reduce_last(x, kind), g.reduce_axis(x, 0, kind))
+    got, want = run_both(g.build(), [a], ew_ts=1024)
+    for k, (gv, wv) in enumerate(zip(got, want)):
+        assert_rel(gv, wv, 1e-5 if kind != 3 else 1e-4, 1e-5, f"kind {kind} out {k}")
+
+
+@pytest.mark.parametrize("dt", ["i32", "u32", "i64", "bool"])
+@pytest.mark.parametrize("kind", [0, 1, 2, 3, 4, 5, 6])
+def test_integer_reductions_bit_exact(dt, kind):
+    rng = np.random.default_rng(30 + kind)
+    npdt = V.DT_NUMPY[V.DT_BY_NAME[dt]]
+    if dt == "bool":
+        a = (rng.random((9, 700)) < 0.5).astype(np.uint8)
+    else:
+        a = rng.integers(-5 if dt != "u32" else 0, 6, (9, 700)).astype(npdt)
+    g = G.Graph()
+    x = g.input(a.shape, dt)
+    g.output(g.reduce_all(x, kind, ew_ts=512), g.reduce_last(x, kind), g.reduce_axis(x, 0, kind))
+    got, want = run_both(g.build(), [a], ew_ts=512)
+    for k, (gv, wv) in enumerate(zip(got, want)):
+        np.testing.assert_array_equal(gv, wv, err_msg=f"{dt} kind {kind} out {k}")
+
+
+def test_argmax_rows():
+    rng = np.random.default_rng(40)
+    a = rng.standard_normal((33, 513)).astype(np.float32)
+    a[3, 100] = a[3].max() + 1
+    a[3, 200] = a[3, 100]          # tie: first index wins
+    a[5, 7] = np.nan
+    g = G.Graph()
+    x = g.input(a.shape)
+    val, idx = g.argmax_last(x)
+    g.output(val, idx)
+    got, want = run_both(g.build(), [a])
+    np.testing.assert_array_equal(got[1], want[1])
+    np.testing.assert_array_equal(got[0].view(np.uint32), want[0].view(np.uint32))
+
+
+@pytest.mark.parametrize("seg", [96, 768, 1000, 4096, 8192])
+def test_softmax_and_layernorm_rows(seg):
+    rng = np.random.default_rng(50)
+    rows = 61
+    a = (rng.standard_normal((rows, seg)) * 2 + 0.5).astype(np.float32)
+    g = G.Graph()
+    x = g.input(a.shape)
+    g.output(g.softmax_last(x), g.layernorm_core(x, 1e-5))
+    got, want = run_both(g.build(), [a])
+    assert_rel(got[0], want[0], 2e-5, 1e-9, "softmax")
+    assert_rel(got[1], want[1], 1e-5, 2e-5, "layernorm core")
+
+
+@pytest.mark.parametrize("in_dt", ["f32", "bf16"])
+@pytest.mark.parametrize("out_dt", ["f32", "bf16"])
+def test_fused_layernorm_affine_gelu(in_dt, out_dt):
+    rng = np.random.default_rng(1002)
+    rows, d = 64, 4096
+    x_np = rng.standard_normal((rows, d)).astype(np.float32)
+    gamma = rng.uniform(0.5, 1.5, d).astype(np.float32)
+    beta = (rng.standard_normal(d) * 0.1).astype(np.float32)
+    g = G.Graph()
+    x = g.input((rows, d), in_dt)
+    ga, be = g.input((d,)), g.input((d,))
+    g.output(g.layernorm(x, ga, be, 1e-5, gelu=True, out_dtype=out_dt))
+    got, want = run_both(g.build(), [x_np, gamma, beta])
+    odt = V.DT_BY_NAME[out_dt]
+    assert_rel(as_f32(got[0], odt), as_f32(want[0], odt), BF16_ULP if out_dt == "bf16" else 1e-5, 1e-5, "ln")
+
+
+def test_config2_full_size_layernorm_gelu_bf16():
+    """Config 2 at its real shape [8192, 4096] (seed 1002)."""
+    rng = np.random.default_rng(1002)
+    rows, d = 8192, 4096
+    x_np = rng.standard_normal((rows, d), dtype=np.float32)
+    gamma = rng.uniform(0.5, 1.5, d).astype(np.float32)
+    beta = (rng.standard_normal(d) * 0.1).astype(np.float32)
+    g = G.Graph()
+    x = g.input((rows, d))
+    ga, be = g.input((d,)), g.input((d,))
+    g.output(g.layernorm(x, ga, be, 1e-5, gelu=True, out_dtype="bf16"))
+    got, _ = run_both(g.build(), [x_np, gamma, beta], oracle=None)
+    x64 = x_np.astype(np.float64)
+    mu = x64.mean(1, keepdims=True)
+    var = ((x64 - mu) ** 2).mean(1, keepdims=True)
+    z = (x64 - mu) / np.sqrt(var + 1e-5) * gamma + beta
+    want = 0.5 * z * (1 + np.tanh(0.7978845608 * (z + 0.044715 * z ** 3)))
+    assert_rel(vmref.bf16_to_f32(got[0]), want, BF16_ULP, 1e-6, "config 2")
+
+
+# --- data movement ---------------------------------------------------------------------------
+
+def test_gather_scatter_iota_dyn_embedding():
+    rng = np.random.default_rng(60)
+    a = rng.standard_normal((6, 7, 5)).astype(np.float32)
+    table = rng.standard_normal((50, 16)).astype(np.float32)
+    ids = np.array([3, 0, 49, 77, -4, 12], np.int32)
+    start = np.array([2], np.int32)
+    g = G.Graph()
+    x = g.input(a.shape)
+    tb = g.input(table.shape)
+    ix = g.input(ids.shape, "i32")
+    st = g.input((1,), "i32")
+    outs = [g.transpose(x, (2, 0, 1)), g.slice(x, (1, 2, 0), (5, 7, 5), (2, 1, 2)),
+            g.broadcast(g.slice(x, (0, 0, 0), (1, 7, 5)), (3, 7, 5), (0, 1, 2)),
+            g.concatenate([x, g.slice(x, (0, 0, 0), (2, 7, 5))], 0),
+            g.iota((4, 9, 3), 1, "i32"), g.iota((5, 6), 0, "f32"),
+            g.take_rows(tb, ix)]
+    s0 = g.reshape(st, ())
+    zero = g.const(np.array(0, np.int32))
+    outs.append(g.dynamic_slice(x, [s0, zero, zero], (3, 7, 5)))
+    buf = g.unary("copy", x)
+    g.dynamic_update_slice(buf, g.slice(x, (0, 0, 0), (1, 7, 5)), [s0, zero, zero])
+    outs.append(buf)
+    g.output(*outs)
+    got, want = run_both(g.build(), [a, table, ids, start], ew_ts=64)
+    for k, (gv, wv) in enumerate(zip(got, want)):
+        np.testing.assert_array_equal(gv, wv, err_msg=f"output {k}")
+
+
+# --- matmul --------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+@pytest.mark.parametrize("M,K,N,tile", [(64, 64, 64, 64), (100, 37, 130, 64), (256, 96, 256, 128),
+                                        (300, 200, 260, 256), (1, 768, 2304, 64)])
+def test_dot_integer_valued_exact(dt, M, K, N, tile):
+    """Small-integer operands: every product and partial sum is exact in f32, so the
+    result is exact (the reference's own trick, tests/test_ops_dot.py:1-20)."""
+    rng = np.random.default_rng(70)
+    a = rng.integers(-3, 4, (M, K)).astype(np.float32)
+    b = rng.integers(-3, 4, (K, N)).astype(np.float32)
+    g = G.Graph()
+    x, y = g.input((M, K), dt), g.input((K, N), dt)
+    g.output(g.dot(x, y, tile=tile))
+    got, want = run_both(g.build(), [a, b])
+    np.testing.assert_array_equal(got[0], a.astype(np.float64) @ b.astype(np.float64))
+
+
+@pytest.mark.parametrize("dt,rtol", [("f32", 1e-3), ("bf16", 1e-2)])
+def test_dot_random_tolerance_and_tiles(dt, rtol):
+    rng = np.random.default_rng(1003)
+    M, K, N = 512, 384, 640
+    a = (rng.standard_normal((M, K)) * 0.125).astype(np.float32)
+    b = (rng.standard_normal((K, N)) * 0.125).astype(np.float32)
+    if dt == "bf16":
+        a, b = vmref.bf16_to_f32(vmref.f32_to_bf16(a)), vmref.bf16_to_f32(vmref.f32_to_bf16(b))
+    want = a.astype(np.float64) @ b.astype(np.float64)
+    for tile in (64, 128, 256):
+        g = G.Graph()
+        x, y = g.input((M, K), dt), g.input((K, N), dt)
+        g.output(g.dot(x, y, tile=tile))
+        got, _ = run_both(g.build(), [a, b], oracle=None)
+        err = np.abs(got[0] - want).max() / np.abs(want).max()
+        assert err <= rtol, (tile, err)
+
+
+def test_dot_views_batch_epilogue():
+    rng = np.random.default_rng(71)
+    Gb, M, K, N = 3, 40, 24, 56
+    a = rng.integers(-2, 3, (Gb, M, K)).astype(np.float32)
+    bt = rng.integers(-2, 3, (Gb, N, K)).astype(np.float32)
+    res = rng.integers(-4, 5, (Gb, M, N)).astype(np.float32)
+    w = rng.integers(-2, 3, (N, K)).astype(np.float32)
+    bias = rng.integers(-4, 5, (N,)).astype(np.float32)
+    g = G.Graph()
+    x = g.input(a.shape)
+    yt = g.input(bt.shape)
+    r = g.input(res.shape)
+    wt = g.input(w.shape)
+    bb = g.input(bias.shape)
+    y = g.transpose_view(yt, (0, 2, 1))                        # [G,K,N] view of [G,N,K]
+    out1 = g.dot(x, y, epilogue=[(V.SUB_AFFINE, 0, 0.5, 1.0), (V.SUB_ADD, 1, 0.0, 0.0)], residual=r)
+    out2 = g.dot(g.reshape(x, (Gb * M, K)), g.transpose_view(wt, (1, 0)),
+                 epilogue=[(V.SUB_ADD, 2, 0.0, 0.0), (V.SUB_GELU, 0, 0.0, 0.0)], residual=bb)
+    g.output(out1, out2)
+    got, want = run_both(g.build(), [a, bt, res, w, bias], mma_t=64)
+    np.testing.assert_array_equal(got[0], want[0])
+    assert_rel(got[1], want[1], 1e-5, 1e-6, "epilogue gelu")
+
+
+# --- attention ------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("dt,hd,causal,T,C", [("bf16", 128, True, 256, 256), ("bf16", 128, False, 128, 384),
+                                              ("bf16", 64, True, 384, 512), ("f16", 128, True, 128, 128),
+                                              ("f32", 32, True, 40, 56), ("bf16", 80, False, 64, 100)])
+def test_flash_attention(dt, hd, causal, T, C):
+    rng = np.random.default_rng(1004)
+    H = 3
+    q = rng.standard_normal((H, T, hd)).astype(np.float32)
+    k = rng.standard_normal((H, C, hd)).astype(np.float32)
+    v = rng.standard_normal((H, C, hd)).astype(np.float32)
+    if dt == "bf16":
+        q, k, v = (vmref.bf16_to_f32(vmref.f32_to_bf16(t)) for t in (q, k, v))
+    elif dt == "f16":
+        q, k, v = (t.astype(np.float16).astype(np.float32) for t in (q, k, v))
+    g = G.Graph()
+    Q, K, Vv = g.input(q.shape, dt), g.input(k.shape, dt), g.input(v.shape, dt)
+    g.output(g.flash_attention(Q, K, Vv, 1.0 / np.sqrt(hd), causal, out_dtype="f32"))
+    got, _ = run_both(g.build(), [q, k, v], oracle=None)
+    want = vmref.attention(q, np.transpose(k, (0, 2, 1)), v, 1.0 / np.sqrt(hd), causal)
+    tol = 1e-3 if dt == "f32" else 1e-2
+    err = np.abs(got[0] - want).max() / max(1e-6, np.abs(want).max())
+    assert err <= tol, err
+
+
+# --- loader validation ----------------------------------------------------------------------------
+
+def test_loader_rejects_out_of_bounds_task():
+    from pjrt_amd.runtime import VmrtError, INVALID_ARGUMENT
+    g = G.Graph()
+    x = g.input((100,))
+    g.output(g.unary("exp", x))
+    prog = g.build()
+    prog.instrs[0].n = 10_000            # reads past the 100-element buffers
+    blob = V.serialize(prog, __import__("pjrt_amd.scheduler", fromlist=["x"]).schedule_program(
+        prog, __import__("pjrt_amd.scheduler", fromlist=["x"]).DeviceConfig(nlanes=4, ew_ts=256)))
+    with pytest.raises(VmrtError) as ei:
+        runtime().load(blob, ew_ts=256)
+    assert ei.value.code == INVALID_ARGUMENT
+
+
+def test_loader_rejects_more_lanes_than_resident():
+    from pjrt_amd.runtime import VmrtError
+    g = G.Graph()
+    x = g.input((100,))
+    g.output(g.unary("exp", x))
+    from pjrt_amd import scheduler as S
+    blob = V.serialize(g.build(), S.schedule_program(g.build(), S.DeviceConfig(nlanes=4096, ew_ts=256)))
+    with pytest.raises(VmrtError):
+        runtime().load(blob, ew_ts=256)

@@ -132,7 +132,7 @@ def bench_c2(rt, steps, warmup, with_cpu):
     want = 0.5 * z * (1 + np.tanh(0.7978845608 * (z + 0.044715 * z ** 3)))
     gotf = (got[rows].astype(np.uint32) << 16).view(np.float32).astype(np.float64)
     err = float(np.max(np.abs(gotf - want) / (np.abs(want) + 1e-6)))
-    if err > 2.0 ** -8 + 1e-6:
+    if err > 2.0 ** -7 + 1e-6:       # one bf16 ulp of the float64 result
         raise SystemExit(f"bench: config-2 result check failed (max rel err {err:.3g})")
     cpu = None
     if with_cpu:

@@ -38,10 +38,10 @@ typedef struct vmrt_program vmrt_program;
 
 typedef struct {
   int32_t device;              /* HIP device ordinal */
-  uint32_t n_lanes;            /* 0: CUs x resident lanes per CU */
+  uint32_t n_lanes;            /* 0: one lane per compute unit */
   uint32_t ew_ts;              /* elements per EW tile; 0: 4096 */
   uint32_t mma_t;              /* default MMA output tile edge; 0: 128 */
-  uint32_t cooperative;        /* 1 (default via 0xFFFFFFFF): cooperative launch; 0: plain */
+  uint32_t cooperative;        /* 1: cooperative launch; 0 (default via 0xFFFFFFFF): plain */
   uint32_t barrier_timeout_ms; /* grid-barrier wait limit; 0: 2000 ms */
 } vmrt_options;
 

@@ -318,8 +318,7 @@ VM_TILE void ew_special(Args A, uint32_t ti, uint64_t e0, uint64_t e1) {
         VM_G v2u* d4 = (VM_G v2u*)(gcast<uint16_t>(d) + e0);
         for (uint64_t j = tid; j < nv; j += kBlock) {
           const v4f x = a4[j];
-          d4[j] = v2u_make(f32_to_bf16(x.x) | (uint32_t(f32_to_bf16(x.y)) << 16),
-                             f32_to_bf16(x.z) | (uint32_t(f32_to_bf16(x.w)) << 16));
+          d4[j] = v2u_make(pack_bf16x2(x.x, x.y), pack_bf16x2(x.z, x.w));
         }
         for (uint64_t i = e0 + (nv << 2) + tid; i < e1; i += kBlock)
           gcast<uint16_t>(d)[i] = f32_to_bf16(gcast<float>(a)[i]);

@@ -261,8 +261,7 @@ VM_DEV void st4(gbyte* p, uint32_t dt, uint64_t e, v4f v) {
   if (dt == DT_F32) {
     *(VM_G v4f*)(gcast<float>(p) + e) = v;
   } else if (dt == DT_BF16) {
-    *(VM_G v2u*)(gcast<uint16_t>(p) + e) = v2u_make(f32_to_bf16(v.x) | (uint32_t(f32_to_bf16(v.y)) << 16),
-                                                         f32_to_bf16(v.z) | (uint32_t(f32_to_bf16(v.w)) << 16));
+    *(VM_G v2u*)(gcast<uint16_t>(p) + e) = v2u_make(pack_bf16x2(v.x, v.y), pack_bf16x2(v.z, v.w));
   } else {
     *(VM_G v2u*)(gcast<uint16_t>(p) + e) = v2u_make(f32_to_f16(v.x) | (uint32_t(f32_to_f16(v.y)) << 16),
                                                          f32_to_f16(v.z) | (uint32_t(f32_to_f16(v.w)) << 16));
@@ -354,6 +353,282 @@ VM_TILE void ln_rows_vec(Args A, uint32_t ti, uint32_t r0, uint32_t r1) {
   }
 }
 
+// Wave-per-row layernorm, specialised on the input / output formats.  Each wave64
+// owns every fourth row of the lane's range and holds a row as NV groups of 4
+// elements per thread (thread t: groups t, t+64, ...; f32 rows as float4, bf16 rows
+// packed two per register).  Rows stream through three rotating register buffers,
+// so two rows are in flight while the third is reduced (DPP only, no block
+// barriers) and written.  gamma / beta (1 / 0 when the op has no affine) are staged
+// once into LDS.
+template <bool BF16>
+struct RowFmt {
+  typedef v4f Raw;                       // f32: 4 elements in a float4
+  static VM_DEV v4f unpack(Raw r) { return r; }
+};
+template <>
+struct RowFmt<true> {
+  typedef v2u Raw;                       // bf16: 4 elements in two registers
+  static VM_DEV v4f unpack(Raw r) {
+    return v4f_make(__uint_as_float(r.x << 16), __uint_as_float(r.x & 0xFFFF0000u), __uint_as_float(r.y << 16),
+                    __uint_as_float(r.y & 0xFFFF0000u));
+  }
+};
+
+struct LnRow {                 // per-row constants of one layernorm task
+  const gbyte* a;
+  gbyte* d;
+  const v4f* lg;
+  const v4f* lb;
+  uint32_t seg, nv4, lane;
+  float eps, inv_n;
+  bool two_pass;
+};
+
+// Loads are never predicated: a load inside an exec-masked block makes the
+// compiler drain every outstanding load (s_waitcnt vmcnt(0)) at the block
+// boundary, which would serialise the row prefetch.  Groups past the row end
+// re-read the row's last group and are masked out of the sums and stores.
+template <int NV, bool IN_BF16, bool FULL>
+VM_DEV void ln_load(typename RowFmt<IN_BF16>::Raw (&buf)[NV], const LnRow& L, uint32_t r) {
+  typedef typename RowFmt<IN_BF16>::Raw Raw;
+  const VM_G Raw* rp = (const VM_G Raw*)(L.a + uint64_t(r) * L.seg * (IN_BF16 ? 2 : 4));
+#pragma unroll
+  for (int k = 0; k < NV; ++k) buf[k] = rp[FULL ? L.lane + 64 * k : min(L.lane + 64 * k, L.nv4 - 1)];
+}
+
+template <int NV, bool IN_BF16, bool OUT_BF16, bool GELU, bool FULL>
+VM_DEV void ln_process(const typename RowFmt<IN_BF16>::Raw (&buf)[NV], const LnRow& L, uint32_t r) {
+  float s = 0.0f, s2 = 0.0f;
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    const bool valid = FULL || L.lane + 64 * k < L.nv4;
+    const v4f x = RowFmt<IN_BF16>::unpack(buf[k]);
+    const float ps = (x.x + x.y) + (x.z + x.w);
+    s += valid ? ps : 0.0f;
+    if (!L.two_pass) {
+      const float p2 = fmaf(x.x, x.x, fmaf(x.y, x.y, fmaf(x.z, x.z, x.w * x.w)));
+      s2 += valid ? p2 : 0.0f;
+    }
+  }
+  const float mean = wave_sum(s) * L.inv_n;
+  float var;
+  if (L.two_pass) {
+    float q2 = 0.0f;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      const bool valid = FULL || L.lane + 64 * k < L.nv4;
+      const v4f dv = RowFmt<IN_BF16>::unpack(buf[k]) - mean;
+      const float p2 = fmaf(dv.x, dv.x, fmaf(dv.y, dv.y, fmaf(dv.z, dv.z, dv.w * dv.w)));
+      q2 += valid ? p2 : 0.0f;
+    }
+    var = wave_sum(q2) * L.inv_n;
+  } else {
+    var = wave_sum(s2) * L.inv_n - mean * mean;
+  }
+  const float rstd = rsqrtf(var + L.eps);
+  const float shift = -mean * rstd;
+  gbyte* rowd = L.d + uint64_t(r) * L.seg * (OUT_BF16 ? 2 : 4);
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    // one group at a time: keeps the GELU temporaries of 4 elements live, not 64
+    __builtin_amdgcn_sched_barrier(0);
+    const uint32_t q = FULL ? L.lane + 64 * k : min(L.lane + 64 * k, L.nv4 - 1);
+    {
+      const v4f x = RowFmt<IN_BF16>::unpack(buf[k]);
+      const v4f gg = L.lg[q], bb = L.lb[q];
+      v4f z;
+      z.x = fmaf(fmaf(x.x, rstd, shift), gg.x, bb.x);
+      z.y = fmaf(fmaf(x.y, rstd, shift), gg.y, bb.y);
+      z.z = fmaf(fmaf(x.z, rstd, shift), gg.z, bb.z);
+      z.w = fmaf(fmaf(x.w, rstd, shift), gg.w, bb.w);
+      if constexpr (GELU) {
+        z.x = gelu(z.x);
+        z.y = gelu(z.y);
+        z.z = gelu(z.z);
+        z.w = gelu(z.w);
+      }
+      if (FULL || L.lane + 64 * k < L.nv4) {
+        if constexpr (OUT_BF16)
+          ((VM_G v2u*)rowd)[q] = v2u_make(pack_bf16x2(z.x, z.y), pack_bf16x2(z.z, z.w));
+        else
+          ((VM_G v4f*)rowd)[q] = z;
+      }
+    }
+  }
+}
+
+// Rows i = 0..mine-1 of this wave (row rbase + 4i) through rotating register
+// buffers: while one row is reduced and written, the next one or two are in
+// flight.  The prefetch is unconditional (past the last row it re-reads the last
+// row) so no load sits behind a branch; `mine` is wave-uniform, so the loop exits
+// are scalar branches.
+template <int NV, bool IN_BF16, bool OUT_BF16, bool GELU, bool FULL>
+VM_DEV void ln_stream(const LnRow& L, uint32_t rbase, uint32_t mine) {
+  typedef typename RowFmt<IN_BF16>::Raw Raw;
+  if (mine == 0) return;
+  const uint32_t lastr = rbase + kWaves * (mine - 1);
+  if constexpr (NV * sizeof(Raw) / 4 > 32) {
+    // a row larger than 32 registers: two buffers (one row in flight)
+    Raw b0[NV], b1[NV];
+    ln_load<NV, IN_BF16, FULL>(b0, L, rbase);
+    for (uint32_t i = 0; i < mine; i += 2) {
+      const uint32_t r = rbase + kWaves * i;
+      ln_load<NV, IN_BF16, FULL>(b1, L, min(r + kWaves, lastr));
+      ln_process<NV, IN_BF16, OUT_BF16, GELU, FULL>(b0, L, r);
+      if (i + 1 >= mine) break;
+      ln_load<NV, IN_BF16, FULL>(b0, L, min(r + 2 * kWaves, lastr));
+      ln_process<NV, IN_BF16, OUT_BF16, GELU, FULL>(b1, L, r + kWaves);
+    }
+    return;
+  }
+  Raw b0[NV], b1[NV], b2[NV];
+  ln_load<NV, IN_BF16, FULL>(b0, L, rbase);
+  ln_load<NV, IN_BF16, FULL>(b1, L, min(rbase + kWaves, lastr));
+  for (uint32_t i = 0; i < mine; i += 3) {
+    const uint32_t r = rbase + kWaves * i;
+    ln_load<NV, IN_BF16, FULL>(b2, L, min(r + 2 * kWaves, lastr));
+    ln_process<NV, IN_BF16, OUT_BF16, GELU, FULL>(b0, L, r);
+    if (i + 1 >= mine) break;
+    ln_load<NV, IN_BF16, FULL>(b0, L, min(r + 3 * kWaves, lastr));
+    ln_process<NV, IN_BF16, OUT_BF16, GELU, FULL>(b1, L, r + kWaves);
+    if (i + 2 >= mine) break;
+    ln_load<NV, IN_BF16, FULL>(b1, L, min(r + 4 * kWaves, lastr));
+    ln_process<NV, IN_BF16, OUT_BF16, GELU, FULL>(b2, L, r + 2 * kWaves);
+  }
+}
+
+template <int NV, bool IN_BF16, bool OUT_BF16, bool FULL>
+VM_TILE void ln_rows_fast(Args A, uint32_t ti, uint32_t r0, uint32_t r1) {
+  A = uargs(A);
+  const VM_K Task& t = task_of(A, ti);
+  r0 = uni(r0);
+  r1 = uni(r1);
+  const uint32_t flags = t.p[3];
+  const bool affine = flags & LN_AFFINE;
+  LnRow L;
+  L.seg = t.p[1];
+  L.nv4 = L.seg >> 2;
+  L.eps = __uint_as_float(t.p[2]);
+  L.inv_n = 1.0f / float(L.seg);
+  L.two_pass = flags & LN_TWO_PASS;
+  L.a = resolve(A, t.a);
+  L.d = resolve(A, t.dst);
+  L.lane = threadIdx.x & 63;
+  const uint32_t wave = uni(threadIdx.x >> 6);       // wave-uniform: scalar loop control
+  v4f* lg = reinterpret_cast<v4f*>(vm_smem);
+  v4f* lb = lg + L.nv4;
+  {
+    const VM_G v4f* g4 = (const VM_G v4f*)gcast<float>(resolve(A, affine ? t.b : t.a));
+    const VM_G v4f* b4 = (const VM_G v4f*)gcast<float>(resolve(A, affine ? t.p[4] : t.a));
+    for (uint32_t q = threadIdx.x; q < L.nv4; q += kBlock) {
+      lg[q] = affine ? g4[q] : v4f{1.0f, 1.0f, 1.0f, 1.0f};
+      lb[q] = affine ? b4[q] : v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+  }
+  L.lg = lg;
+  L.lb = lb;
+  __syncthreads();
+  const uint32_t mine = r1 > r0 + wave ? (r1 - r0 - wave + kWaves - 1) / kWaves : 0;
+  if (flags & LN_GELU) ln_stream<NV, IN_BF16, OUT_BF16, true, FULL>(L, r0 + wave, mine);
+  else ln_stream<NV, IN_BF16, OUT_BF16, false, FULL>(L, r0 + wave, mine);
+}
+
+// Wave-per-row layernorm for rows up to 4096 elements: each wave64 owns every
+// fourth row of the lane's range, holds it as NV float4 per thread (thread t:
+// float4 slots t, t+64, ...), prefetches its next row before reducing the current
+// one, and reduces with DPP only -- no block barriers, four rows in flight per CU.
+// gamma / beta are staged once into LDS and read back per row.
+template <int NV>
+VM_TILE void ln_rows_wave(Args A, uint32_t ti, uint32_t r0, uint32_t r1) {
+  A = uargs(A);
+  const VM_K Task& t = task_of(A, ti);
+  const uint32_t seg = t.p[1], flags = t.p[3];
+  const float eps = __uint_as_float(t.p[2]);
+  const uint32_t dt = (t.tile_op >> 8) & 0xFF, adt = (t.tile_op >> 16) & 0xFF;
+  const gbyte* a = resolve(A, t.a);
+  gbyte* d = resolve(A, t.dst);
+  const bool affine = flags & LN_AFFINE, do_gelu = flags & LN_GELU, two_pass = flags & LN_TWO_PASS;
+  const uint32_t nv4 = seg >> 2;
+  const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  v4f* lg = reinterpret_cast<v4f*>(vm_smem);
+  v4f* lb = lg + nv4;
+  if (affine) {
+    const VM_G v4f* g4 = (const VM_G v4f*)gcast<float>(resolve(A, t.b));
+    const VM_G v4f* b4 = (const VM_G v4f*)gcast<float>(resolve(A, t.p[4]));
+    for (uint32_t q = threadIdx.x; q < nv4; q += kBlock) {
+      lg[q] = g4[q];
+      lb[q] = b4[q];
+    }
+  }
+  __syncthreads();
+  const float inv_n = 1.0f / float(seg);
+  v4f x[NV], xn[NV];
+  auto load_row = [&](v4f (&dst)[NV], uint32_t r) {
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      const uint32_t q = lane + 64 * k;
+      if (q < nv4) dst[k] = ld4(a, adt, uint64_t(r) * seg + 4ull * q);
+    }
+  };
+  uint32_t r = r0 + wave;
+  if (r < r1) load_row(x, r);
+  for (; r < r1; r += kWaves) {
+    if (r + kWaves < r1) load_row(xn, r + kWaves);
+    float s = 0.0f, s2 = 0.0f;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      if (lane + 64 * k < nv4) {
+        s += (x[k].x + x[k].y) + (x[k].z + x[k].w);
+        if (!two_pass) s2 = fmaf(x[k].x, x[k].x, fmaf(x[k].y, x[k].y, fmaf(x[k].z, x[k].z, fmaf(x[k].w, x[k].w, s2))));
+      }
+    }
+    const float mean = wave_sum(s) * inv_n;
+    float var;
+    if (two_pass) {
+      float q2 = 0.0f;
+#pragma unroll
+      for (int k = 0; k < NV; ++k) {
+        if (lane + 64 * k < nv4) {
+          const v4f dv = x[k] - mean;
+          q2 = fmaf(dv.x, dv.x, fmaf(dv.y, dv.y, fmaf(dv.z, dv.z, fmaf(dv.w, dv.w, q2))));
+        }
+      }
+      var = wave_sum(q2) * inv_n;
+    } else {
+      var = wave_sum(s2) * inv_n - mean * mean;
+    }
+    const float rstd = rsqrtf(var + eps);
+    const float shift = -mean * rstd;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      const uint32_t q = lane + 64 * k;
+      if (q < nv4) {
+        v4f z;
+        z.x = fmaf(x[k].x, rstd, shift);
+        z.y = fmaf(x[k].y, rstd, shift);
+        z.z = fmaf(x[k].z, rstd, shift);
+        z.w = fmaf(x[k].w, rstd, shift);
+        if (affine) {
+          const v4f gg = lg[q], bb = lb[q];
+          z.x = fmaf(z.x, gg.x, bb.x);
+          z.y = fmaf(z.y, gg.y, bb.y);
+          z.z = fmaf(z.z, gg.z, bb.z);
+          z.w = fmaf(z.w, gg.w, bb.w);
+        }
+        if (do_gelu) {
+          z.x = gelu(z.x);
+          z.y = gelu(z.y);
+          z.z = gelu(z.z);
+          z.w = gelu(z.w);
+        }
+        st4(d, dt, uint64_t(r) * seg + 4ull * q, z);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < NV; ++k) x[k] = xn[k];
+  }
+}
+
 // Any seg / alignment: three passes over the row in global memory.
 VM_TILE void ln_rows_generic(Args A, uint32_t ti, uint32_t r0, uint32_t r1) {
   A = uargs(A);
@@ -416,6 +691,25 @@ VM_TILE void layernorm_tiles(Args A, uint32_t ti, uint32_t lo, uint32_t hi) {
   if (ok && (t.p[3] & LN_AFFINE)) ok = ((uintptr_t(resolve(A, t.b)) | uintptr_t(resolve(A, t.p[4]))) & 15) == 0;
   if (!ok) return ln_rows_generic(A, ti, lo, hi);
   const uint32_t nv4 = seg >> 2;
+  if ((adt == DT_F32 || adt == DT_BF16) && (dt == DT_F32 || dt == DT_BF16) && nv4 <= 16 * 64) {
+    const bool ib = adt == DT_BF16, ob = dt == DT_BF16;
+#define VM_LN_FAST(NVV, FULLV)                                                               \
+    {                                                                                         \
+      if (ib) return ob ? ln_rows_fast<NVV, true, true, FULLV>(A, ti, lo, hi)                  \
+                        : ln_rows_fast<NVV, true, false, FULLV>(A, ti, lo, hi);                \
+      return ob ? ln_rows_fast<NVV, false, true, FULLV>(A, ti, lo, hi)                         \
+                : ln_rows_fast<NVV, false, false, FULLV>(A, ti, lo, hi);                       \
+    }
+    if (nv4 == 4 * 64) VM_LN_FAST(4, true)
+    if (nv4 < 4 * 64) VM_LN_FAST(4, false)
+    if (nv4 == 16 * 64) VM_LN_FAST(16, true)
+    VM_LN_FAST(16, false)
+#undef VM_LN_FAST
+  }
+  if (nv4 <= 2 * 64) return ln_rows_wave<2>(A, ti, lo, hi);
+  if (nv4 <= 4 * 64) return ln_rows_wave<4>(A, ti, lo, hi);
+  if (nv4 <= 8 * 64) return ln_rows_wave<8>(A, ti, lo, hi);
+  if (nv4 <= 16 * 64) return ln_rows_wave<16>(A, ti, lo, hi);
   if (nv4 <= 1 * kBlock) return ln_rows_vec<1>(A, ti, lo, hi);
   if (nv4 <= 2 * kBlock) return ln_rows_vec<2>(A, ti, lo, hi);
   if (nv4 <= 4 * kBlock) return ln_rows_vec<4>(A, ti, lo, hi);

@@ -103,6 +103,14 @@ VM_DEV uint16_t f32_to_bf16(float f) {
   if ((u & 0x7FFFFFFFu) > 0x7F800000u) return uint16_t((u >> 16) | 0x40u);
   return uint16_t((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
 }
+// Two f32 -> packed bf16 pair (low half = a) with gfx950's v_cvt_pk_bf16_f32:
+// round-to-nearest-even, the same result as f32_to_bf16 (checked bit-exact over
+// 2^24 patterns including NaN / Inf / denormals by the GPU tests).
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+VM_DEV uint32_t pack_bf16x2(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t{a, b}), bf16x2_t));
+}
 VM_DEV float f16_to_f32(uint16_t h) { return float(__builtin_bit_cast(_Float16, h)); }
 VM_DEV uint16_t f32_to_f16(float f) { return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f)); }
 

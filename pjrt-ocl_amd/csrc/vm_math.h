@@ -11,12 +11,14 @@ namespace vm {
 // c1 = 0.044715 (ew.cl:7-17), evaluated as x * sigmoid(2*c0*(x + c1*x^3)):
 // 0.5*(1 + tanh(u)) == 1/(1 + exp(-2u)), so one v_exp_f32 and one v_rcp_f32
 // replace tanh.  exp(-2u) = 2^(-2*log2(e)*u).
+// With the constants folded, -2*log2(e)*u = x * (k0 + k1*x^2):
+// mul, fma, mul, v_exp_f32, add, v_rcp_f32, mul.
 VM_DEV float gelu(float x) {
-  constexpr float kC0 = 0.7978845608f;
-  constexpr float kC1 = 0.044715f;
-  constexpr float kNeg2Log2e = -2.0f * 1.4426950408889634f;
-  const float u = kC0 * fmaf(kC1 * x, x * x, x);
-  const float e = __builtin_amdgcn_exp2f(kNeg2Log2e * u);
+  constexpr double kC0 = 0.7978845608, kC1 = 0.044715, kNeg2Log2e = -2.0 * 1.4426950408889634;
+  constexpr float k0 = float(kNeg2Log2e * kC0);
+  constexpr float k1 = float(kNeg2Log2e * kC0 * kC1);
+  const float t = x * fmaf(k1, x * x, k0);
+  const float e = __builtin_amdgcn_exp2f(t);
   return x * __builtin_amdgcn_rcpf(1.0f + e);
 }
 

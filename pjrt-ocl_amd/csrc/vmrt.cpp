@@ -626,7 +626,11 @@ int vmrt_create(const vmrt_options* opts, vmrt_runtime** out, char* err, size_t 
   I.mma_t = o.mma_t ? o.mma_t : 128;
   if (I.ew_ts % 64 || (I.mma_t != 64 && I.mma_t != 128 && I.mma_t != 256))
     return set_err(err, errlen, VMRT_INVALID_ARGUMENT, "ew_ts must be a multiple of 64, mma_t one of 64/128/256");
-  I.cooperative = o.cooperative == 0xFFFFFFFFu ? 1u : (o.cooperative ? 1u : 0u);
+  // Plain launch by default: hipLaunchCooperativeKernel costs ~20 us of launch gap
+  // per call on ROCm 7, while co-residency of all lanes already holds because
+  // n_lanes <= CUs x resident workgroups per CU; a lane that never became resident
+  // would surface as a grid-barrier timeout error, never as a hang.
+  I.cooperative = o.cooperative == 0xFFFFFFFFu ? 0u : (o.cooperative ? 1u : 0u);
   if (const char* s = std::getenv("PJRT_AMD_COOPERATIVE")) I.cooperative = std::atoi(s) != 0;
   I.lds_bytes = uint32_t(vm_kernel_smem_bytes());
   std::snprintf(I.arch, sizeof I.arch, "%s", prop.gcnArchName);

@@ -4,7 +4,9 @@ the CPU oracle on the same seeded inputs.
 Bars: bit-exact for integer, bool, index and control
 flow; rel 1e-5 for f32 elementwise / reduce (a few ulp of device libm); GEMM and
 attention rel 1e-3 (f32) / 1e-2 (bf16) against float64; bf16 outputs of f32 math
-within one bf16 ulp (2^-8 relative) of the oracle's rounding."""
+within one bf16 ulp of the oracle's rounding (the device's f32 result and the
+oracle's float64 one can straddle a bf16 rounding boundary); one ulp is at most
+2^-7 of the value."""
 import numpy as np
 import pytest
 
@@ -16,7 +18,7 @@ from pjrt_amd import vmprogram as V
 
 pytestmark = pytest.mark.gpu
 
-BF16_ULP = 2.0 ** -8
+BF16_ULP = 2.0 ** -7
 
 
 def test_runtime_opens_device():
@@ -123,6 +125,28 @@ def test_compare_select_convert_bitcast_isfinite():
     got, want = run_both(g.build(), [a, b], ew_ts=256)
     for k, (gv, wv) in enumerate(zip(got, want)):
         np.testing.assert_array_equal(gv.view(np.uint8), wv.view(np.uint8), err_msg=f"output {k}")
+
+
+def test_convert_f32_to_bf16_bit_patterns():
+    """f32 -> bf16 rounds to nearest even, bit-exact with the closed-form rule
+    (u + 0x7fff + ((u >> 16) & 1)) >> 16 (vm_common.cl:66-70), NaN kept a quiet NaN,
+    over 2^24 random patterns plus ties, boundaries and specials."""
+    rng = np.random.default_rng(7)
+    u = rng.integers(0, 2 ** 32, 2 ** 24, dtype=np.uint64).astype(np.uint32)
+    hi = rng.integers(0, 2 ** 16, 4096, dtype=np.uint64).astype(np.uint32) << 16
+    ties = np.concatenate([hi | 0x8000, hi | 0x7FFF, hi | 0x8001, hi | 0xFFFF, hi])
+    specials = np.array([0, 0x80000000, 0x7F800000, 0xFF800000, 0x7F800001, 0x7FC00000, 0xFFFFFFFF,
+                         0x7FFFFFFF, 0x00000001, 0x007FFFFF, 0x3F808000, 0x3F818000, 0x7F7FFFFF,
+                         0x7F7F8000, 0xFF7FFFFF, 0x00008000, 0x80008000], np.uint32)
+    bits = np.concatenate([u, ties, specials])
+    x = bits.view(np.float32)
+    g = G.Graph()
+    xi = g.input(x.shape)
+    g.output(g.convert(xi, "bf16"))
+    got, _ = run_both(g.build(), [x], oracle=None)
+    want = vmref.f32_to_bf16(x)
+    bad = np.nonzero(got[0] != want)[0]
+    assert bad.size == 0, [(hex(int(bits[i])), hex(int(got[0][i])), hex(int(want[i]))) for i in bad[:8]]
 
 
 # --- reductions and row ops ------------------------------------------------------------------

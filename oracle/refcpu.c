@@ -117,3 +117,49 @@ int refcpu_sgemm(const float* A, const float* B, float* C, int64_t M, int64_t N,
 }
 
 int refcpu_max_threads(void) { return omp_get_max_threads(); }
+
+/* Pins the f32 -> bf16 bit formula (u + 0x7fff + ((u >> 16) & 1)) >> 16
+ * (vm_common.cl:66-70) against round-to-nearest-even computed independently in
+ * double precision, over the bit patterns whose high half lies in [hi0, hi1)
+ * (all 2^32 patterns for [0, 65536)).  For finite x with exponent e, the bf16
+ * quantum is 2^(max(e, -126) - 7); x / quantum is exact in double, so nearbyint
+ * (ties to even) gives the correctly rounded bf16 value, and values that round to
+ * 2^128 overflow to infinity.  NaN inputs must map to a NaN.  Returns the number
+ * of mismatching patterns; *first receives the smallest one.  plant != 0 checks
+ * plain truncation (u >> 16) instead, which the check must reject. */
+int64_t refcpu_bf16_rne_check(int plant, uint32_t hi0, uint32_t hi1, uint32_t* first) {
+  int64_t bad = 0;
+  uint32_t first_bad = 0xFFFFFFFFu;
+#pragma omp parallel for schedule(static) reduction(+ : bad) reduction(min : first_bad)
+  for (int64_t hi = hi0; hi < (int64_t)hi1; ++hi) {
+    for (uint32_t lo = 0; lo < 65536; ++lo) {
+      const uint32_t u = (uint32_t)(hi << 16) | lo;
+      float f;
+      memcpy(&f, &u, 4);
+      const uint16_t got = plant ? (uint16_t)(u >> 16) : f32_to_bf16_rne(f);
+      uint16_t want;
+      if (isnan(f)) {
+        if ((got & 0x7F80u) == 0x7F80u && (got & 0x7Fu) != 0) continue;
+        want = 0xFFFF;   /* any non-NaN result is a mismatch */
+      } else if (f == 0.0f || isinf(f)) {
+        want = (uint16_t)(u >> 16);
+      } else {
+        const double d = (double)f;
+        int e = ilogb(d);
+        if (e < -126) e = -126;
+        const double q = ldexp(1.0, e - 7);
+        const double r = nearbyint(d / q) * q;
+        const float rf = (float)r; /* exact, or +-inf for |r| = 2^128 */
+        uint32_t rb;
+        memcpy(&rb, &rf, 4);
+        want = (uint16_t)(rb >> 16);
+      }
+      if (got != want) {
+        ++bad;
+        if (u < first_bad) first_bad = u;
+      }
+    }
+  }
+  if (first) *first = first_bad;
+  return bad;
+}

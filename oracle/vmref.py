@@ -61,7 +61,8 @@ PINS = {
     "format": "golden bytes tests/test_lowering.py:109-171 + field layout 174-243",
     "ew_f32": "numpy float64 closed forms at rel 1e-6; integer-valued exact",
     "ew_int": "closed forms, bit-exact; shift masks ew.cl:420-458",
-    "bf16": "exhaustive 2^32 RNE check against the bit formula (C, oracle/bf16check.c)",
+    "bf16": "bit formula == RNE computed in double over all 2^32 patterns (oracle/refcpu.c "
+            "refcpu_bf16_rne_check, tests/test_refcpu.py); GPU convert == formula on 2^24 patterns",
     "gelu": "closed form, runtime_test.cc:256-262 (<=1e-5)",
     "control": "runtime_test.cc:136-215 known answers; _while_e2e_body.py closed forms",
     "reduce": "closed forms + identity table, bit-exact for int",

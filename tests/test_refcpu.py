@@ -47,3 +47,28 @@ def test_sgemm(lib):
     c = np.empty((M, N), np.float32)
     lib.refcpu_sgemm(a.ctypes.data, b.ctypes.data, c.ctypes.data, M, N, K, 4)
     np.testing.assert_array_equal(c, a.astype(np.float64) @ b.astype(np.float64))
+
+
+def test_bf16_rne_formula_exhaustive(lib):
+    """All 2^32 f32 patterns: the bit formula equals round-to-nearest-even
+    computed in double precision; NaN stays NaN."""
+    lib.refcpu_bf16_rne_check.restype = ctypes.c_int64
+    lib.refcpu_bf16_rne_check.argtypes = [ctypes.c_int, ctypes.c_uint32, ctypes.c_uint32,
+                                          ctypes.POINTER(ctypes.c_uint32)]
+    first = ctypes.c_uint32(0)
+    assert lib.refcpu_bf16_rne_check(0, 0, 65536, ctypes.byref(first)) == 0, hex(first.value)
+    # a planted mistake (truncation instead of rounding) must be caught
+    assert lib.refcpu_bf16_rne_check(1, 0x3F80, 0x3F81, ctypes.byref(first)) > 0
+
+
+def test_bf16_formula_matches_numpy_oracle(lib):
+    """The numpy oracle's f32_to_bf16 is the same bit formula (sampled patterns)."""
+    rng = np.random.default_rng(7)
+    u = np.concatenate([rng.integers(0, 2 ** 32, 1 << 20, dtype=np.uint64).astype(np.uint32),
+                        np.array([0x7F7FFFFF, 0x7F7F8000, 0x3F808000, 0x3F818000, 0x00008000, 0x7FC00001,
+                                  0xFF800000, 0x80000000], np.uint32)])
+    got = vmref.f32_to_bf16(u.view(np.float32))
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    want = ((u.astype(np.uint64) + 0x7FFF + ((u.astype(np.uint64) >> 16) & 1)) >> 16).astype(np.uint16)
+    assert np.array_equal(got[~nan], want[~nan])
+    assert np.all(((got[nan] & 0x7F80) == 0x7F80) & ((got[nan] & 0x7F) != 0))

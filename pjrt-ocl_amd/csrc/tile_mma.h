@@ -261,6 +261,245 @@ VM_TILE void mma_tile16(Args A, const MmaDesc* Dp, uint32_t tile) {
 }
 
 // ---------------------------------------------------------------------------------
+// 16-bit fast path: 256 x 256 output tiles, K slabs of 64
+// ---------------------------------------------------------------------------------
+// For unviewed row-major operands with M and N multiples of 256 and K a multiple of
+// 64 (the big square GEMMs).  Each wave owns a 128 x 128 quadrant as 4 x 4 blocks
+// of 32 x 32 accumulators (all 256 AGPRs).  The A slab (256 x 64) is staged
+// row-major; the B slab (64 x 256) is transposed in registers on its way to LDS
+// (8 x 8 blocks of 16-bit values, v_perm_b32), so that every MFMA operand fragment
+// is one ds_read_b128.  Rows are padded to 72 elements (144 B): the eight lanes of
+// a ds_read_b128 / ds_write_b128 phase then hit disjoint banks.  Global loads for
+// slab s+1 are in flight while the matrix cores consume slab s.
+constexpr int kFBK = 64;                          // K slab (elements)
+constexpr int kFLd = kFBK + 8;                    // LDS row stride (elements)
+constexpr int kFBuf = 2 * 256 * kFLd;             // elements per stage: A + B^T
+constexpr int kFastLdsBytes = 2 * kFBuf * 2;      // two stages of 16-bit elements
+
+struct FastStage {
+  v4u ra[8], rb[8];
+
+  // A: chunk c = t + 256 j is row c / 8, k chunk c % 8.  B: thread t takes the
+  // 8 x 8 block of k group t % 8 and n chunk t / 8 (one 16-byte row piece per k).
+  // a, b: uniform slab origins (A at row m0 / column k0, B at row k0 / column n0);
+  // per-thread offsets are 32-bit so the loads take an SGPR base.
+  VM_DEV void load(const gbyte* a, const gbyte* b, uint32_t K, uint32_t N) {
+    const uint32_t t = threadIdx.x;
+    const uint32_t oa = ((t >> 3) * K + (t & 7) * 8) * 2;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) ra[j] = *(const VM_G v4u*)(a + (oa + uint32_t(j) * 64u * K));
+    const uint32_t ob = ((t & 7) * 8 * N + (t >> 3) * 8) * 2;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) rb[i] = *(const VM_G v4u*)(b + (ob + uint32_t(i) * 2u * N));
+  }
+
+  VM_DEV void store_a(uint16_t* s) const {
+    const uint32_t t = threadIdx.x;
+    uint16_t* la = s + (t >> 3) * kFLd + (t & 7) * 8;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) *reinterpret_cast<v4u*>(la + 32 * j * kFLd) = ra[j];
+  }
+  VM_DEV void store_b(uint16_t* s) {
+    const uint32_t t = threadIdx.x;
+    uint16_t* lb = s + 256 * kFLd + (t >> 3) * 8 * kFLd + (t & 7) * 8;
+    // Pin the transpose here: without this the compiler hoists the v_perm_b32s up
+    // to the global loads and waits for them at the top of the slab.
+#pragma unroll
+    for (int i = 0; i < 8; ++i) asm volatile("" : "+v"(rb[i]));
+#pragma unroll
+    for (int jn = 0; jn < 8; ++jn) {
+      // column n = 8 * (t / 8) + jn: its 16-bit value from each of the 8 k rows
+      const uint32_t sel = (jn & 1) ? 0x07060302u : 0x05040100u;
+      const int w = jn >> 1;
+      v4u o;
+      o.x = __builtin_amdgcn_perm(rb[1][w], rb[0][w], sel);
+      o.y = __builtin_amdgcn_perm(rb[3][w], rb[2][w], sel);
+      o.z = __builtin_amdgcn_perm(rb[5][w], rb[4][w], sel);
+      o.w = __builtin_amdgcn_perm(rb[7][w], rb[6][w], sel);
+      *reinterpret_cast<v4u*>(lb + jn * kFLd) = o;
+    }
+  }
+  VM_DEV void store(uint16_t* s) {
+    store_a(s);
+    store_b(s);
+  }
+};
+
+// Tile index -> origin.  When the tile grid splits evenly over the 8 XCDs, tile t
+// (which the scheduler places on lane t, and the dispatcher on XCD t % 8) is
+// mapped so that each XCD owns a compact band of 4-row groups: its tiles share A
+// and B panels in that XCD's L2.  Any bijection is correct; this one is faster.
+VM_DEV void fast_origin(const MmaDesc& D, uint32_t tile, uint32_t* g, uint32_t* m0, uint32_t* n0) {
+  const uint32_t per = D.tm * D.tn;
+  *g = tile / per;
+  uint32_t loc = tile % per;
+  if (per % 8 == 0 && D.tm % 4 == 0) {
+    loc = (loc % 8) * (per / 8) + loc / 8;
+    const uint32_t grp = loc / (4 * D.tn), in = loc % (4 * D.tn);
+    *m0 = (grp * 4 + in % 4) * 256;
+    *n0 = (in / 4) * 256;
+  } else {
+    *m0 = (loc / D.tn) * 256;
+    *n0 = (loc % D.tn) * 256;
+  }
+}
+
+// Epilogue kinds the lowering fuses into a matmul store (affine, GELU, a binary op
+// with the residual or a per-column operand), evaluated inline by the fast path:
+// a call would force the 256 live accumulator AGPRs through scratch.
+VM_DEV bool epi_inline_ok(Args A, uint32_t epi) {
+  if (!epi) return true;
+  const VM_K int32_t* e = aux_of(A) + (epi - 1);
+  const int nm = e[0];
+  for (int k = 0; k < nm; ++k) {
+    const uint32_t kind = uint32_t(e[1 + 4 * k]);
+    if (!(kind == SUB_AFFINE || kind == SUB_GELU || kind == SUB_COPY || kind <= SUB_DIV || kind == SUB_MAX ||
+          kind == SUB_MIN))
+      return false;
+  }
+  return true;
+}
+
+VM_DEV float epi_inline(uint32_t kind, float x, float y, float s, float t) {
+  switch (kind) {
+    case SUB_AFFINE: return fmaf(x, s, t);
+    case SUB_GELU: return gelu(x);
+    case SUB_ADD: return x + y;
+    case SUB_MUL: return x * y;
+    case SUB_SUB: return x - y;
+    case SUB_DIV: return x / y;
+    case SUB_MAX: return fmaxf(x, y);
+    case SUB_MIN: return fminf(x, y);
+    default: return x;
+  }
+}
+
+// Tile store through LDS: the accumulators of half the tile (rows 0-63 and
+// 128-191 of every wave's quadrant) are scattered into a 128 x 256 f32 staging
+// tile, then the whole block writes full rows with 16-byte (f32) or 8-byte
+// (16-bit) stores, applying the epilogue on the way.  No call is made while the
+// accumulators are live.
+template <bool F32>
+VM_DEV void store_fast(Args A, const MmaDesc& D, const f32x16 (&acc)[4][4], uint32_t g, uint32_t m0, uint32_t n0) {
+  constexpr int LD = 256 + 4;
+  float* st = reinterpret_cast<float*>(vm_smem);
+  const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint32_t wm = wave >> 1, wn = wave & 1;
+  const uint64_t tile0 = (uint64_t(g) * D.M + m0) * D.N + n0;
+  gbyte* d = D.d + tile0 * (F32 ? 4 : 2);
+  const bool bf = D.dt == DT_BF16;
+  const VM_K int32_t* e = aux_of(A) + (D.epi ? D.epi - 1 : 0);
+  const int nm = D.epi ? e[0] : 0;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    __syncthreads();
+#pragma unroll
+    for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t c = wn * 128 + j * 32 + (lane & 31);
+        const uint32_t r0 = wm * 64 + ii * 32 + 4 * (lane >> 5);
+#pragma unroll
+        for (int v = 0; v < 16; ++v) st[(r0 + 8 * (v >> 2) + (v & 3)) * LD + c] = acc[2 * h + ii][j][v];
+      }
+    __syncthreads();
+#pragma unroll 2
+    for (uint32_t it = 0; it < 32; ++it) {
+      const uint32_t idx = it * kBlock + threadIdx.x;
+      const uint32_t rs = idx >> 6, c = (idx & 63) * 4;
+      const uint32_t row = (rs >> 6) * 128 + h * 64 + (rs & 63);
+      v4f x = *reinterpret_cast<const v4f*>(st + rs * LD + c);
+      const uint32_t off = row * D.N + c;
+      for (int k = 0; k < nm; ++k) {
+        const uint32_t kind = uint32_t(e[1 + 4 * k]), src = uint32_t(e[2 + 4 * k]);
+        const float s = __int_as_float(e[3 + 4 * k]), t = __int_as_float(e[4 + 4 * k]);
+        v4f y = x;
+        if (src == 1) y = *(const VM_G v4f*)(D.res + (tile0 + off) * 4);
+        else if (src == 2) y = *(const VM_G v4f*)(D.res + (uint64_t(n0) + c) * 4);
+        x.x = epi_inline(kind, x.x, y.x, s, t);
+        x.y = epi_inline(kind, x.y, y.y, s, t);
+        x.z = epi_inline(kind, x.z, y.z, s, t);
+        x.w = epi_inline(kind, x.w, y.w, s, t);
+      }
+      if constexpr (F32) {
+        *(VM_G v4f*)(d + off * 4u) = x;
+      } else {
+        const uint32_t lo = bf ? pack_bf16x2(x.x, x.y) : (uint32_t(f32_to_f16(x.x)) | uint32_t(f32_to_f16(x.y)) << 16);
+        const uint32_t hi = bf ? pack_bf16x2(x.z, x.w) : (uint32_t(f32_to_f16(x.z)) | uint32_t(f32_to_f16(x.w)) << 16);
+        *(VM_G v2u*)(d + off * 2u) = v2u_make(lo, hi);
+      }
+    }
+  }
+}
+
+template <bool BF16>
+VM_TILE void mma_tile16_fast(Args A, const MmaDesc* Dp, uint32_t tile) {
+  A = uargs(A);
+  const MmaDesc D = load_desc(Dp);
+  uint16_t* lds = reinterpret_cast<uint16_t*>(vm_smem);
+  uint32_t g, m0, n0;
+  fast_origin(D, uni(tile), &g, &m0, &n0);
+  const uint32_t K = D.K, N = D.N;
+  const gbyte* a = D.a + (uint64_t(g) * D.M + m0) * K * 2;        // A[g, m0, 0]
+  const gbyte* b = D.b + (uint64_t(g) * K * N + n0) * 2;           // B[g, 0, n0]
+  const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint32_t wm = wave >> 1, wn = wave & 1;
+  f32x16 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
+  const uint32_t nk = K / kFBK;
+  FastStage st;
+  st.load(a, b, K, N);
+  __syncthreads();                      // the previous user of the LDS is done
+  st.store(lds);
+  __syncthreads();
+  const uint32_t fa = (wm * 128 + (lane & 31)) * kFLd + (lane >> 5) * 8;
+  const uint32_t fb = 256 * kFLd + (wn * 128 + (lane & 31)) * kFLd + (lane >> 5) * 8;
+  for (uint32_t ks = 0; ks < nk; ++ks) {
+    const uint16_t* cur = lds + (ks & 1) * kFBuf;
+    // next slab (the last iteration reloads the last slab into the idle stage)
+    const uint32_t kn = min(ks + 1, nk - 1) * kFBK;
+    st.load(a + uint64_t(kn) * 2, b + uint64_t(kn) * N * 2, K, N);
+    __builtin_amdgcn_sched_barrier(0);  // keep the slab loads ahead of the MFMAs
+    // Operand fragments double-buffered across the four 16-deep k steps: the
+    // reads for step kk+1 are issued before the MFMAs of step kk.  The staged
+    // next slab goes to the idle LDS stage in between (A after step 1, B after
+    // step 2), hidden behind the matrix cores.
+    u16x8 af[2][4], bfr[2][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) af[0][i] = *reinterpret_cast<const u16x8*>(cur + fa + i * 32 * kFLd);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) bfr[0][j] = *reinterpret_cast<const u16x8*>(cur + fb + j * 32 * kFLd);
+    uint16_t* nxt = lds + ((ks + 1) & 1) * kFBuf;
+#pragma unroll
+    for (int kk = 0; kk < kFBK / 16; ++kk) {
+      const int p = kk & 1;
+      if (kk + 1 < kFBK / 16) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          af[p ^ 1][i] = *reinterpret_cast<const u16x8*>(cur + fa + i * 32 * kFLd + (kk + 1) * 16);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          bfr[p ^ 1][j] = *reinterpret_cast<const u16x8*>(cur + fb + j * 32 * kFLd + (kk + 1) * 16);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = mfma16<BF16>(af[p][i], bfr[p][j], acc[i][j]);
+      __builtin_amdgcn_sched_barrier(0);
+      if (kk == 1) st.store_a(nxt);
+      if (kk == 2) st.store_b(nxt);
+    }
+    __syncthreads();
+  }
+  if (D.dt == DT_F32) store_fast<true>(A, D, acc, g, m0, n0);
+  else store_fast<false>(A, D, acc, g, m0, n0);
+}
+
+// ---------------------------------------------------------------------------------
 // f32 operands
 // ---------------------------------------------------------------------------------
 constexpr int kBK32 = 16;
@@ -372,7 +611,8 @@ VM_TILE void mma_tile32(Args A, const MmaDesc* Dp, uint32_t tile) {
 }
 
 // LDS bytes the matmul tile op needs at its largest tile.
-constexpr int kMmaLdsBytes = Lds16<256>::kBytes > Lds32<256>::kBytes ? Lds16<256>::kBytes : Lds32<256>::kBytes;
+constexpr int kMmaLdsBytes0 = Lds16<256>::kBytes > Lds32<256>::kBytes ? Lds16<256>::kBytes : Lds32<256>::kBytes;
+constexpr int kMmaLdsBytes = kFastLdsBytes > kMmaLdsBytes0 ? kFastLdsBytes : kMmaLdsBytes0;
 
 VM_TILE void mma_tiles(Args A, uint32_t ti, uint32_t lo, uint32_t hi) {
   A = uargs(A);
@@ -397,8 +637,14 @@ VM_TILE void mma_tiles(Args A, uint32_t ti, uint32_t lo, uint32_t hi) {
   D.adt = (t.tile_op >> 16) & 0xFF;
   hi = min(hi, D.tm * D.tn * D.G);
   const bool h16 = D.adt == DT_BF16 || D.adt == DT_F16, bf = D.adt == DT_BF16;
+  const bool fast = h16 && T == 256 && !D.av && !D.bv && D.M % 256 == 0 && D.N % 256 == 0 && D.K % kFBK == 0 &&
+                    D.N < (1u << 22) && ((uintptr_t(D.a) | uintptr_t(D.b)) & 15) == 0 &&
+                    (D.dt == DT_F32 || D.dt == DT_BF16 || D.dt == DT_F16) && epi_inline_ok(A, D.epi);
   for (uint32_t tile = lo; tile < hi; ++tile) {
-    if (h16) {
+    if (fast) {
+      if (bf) mma_tile16_fast<true>(A, &D, tile);
+      else mma_tile16_fast<false>(A, &D, tile);
+    } else if (h16) {
       if (T == 256) { if (bf) mma_tile16<256, true>(A, &D, tile); else mma_tile16<256, false>(A, &D, tile); }
       else if (T == 128) { if (bf) mma_tile16<128, true>(A, &D, tile); else mma_tile16<128, false>(A, &D, tile); }
       else { if (bf) mma_tile16<64, true>(A, &D, tile); else mma_tile16<64, false>(A, &D, tile); }

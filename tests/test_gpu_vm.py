@@ -312,6 +312,51 @@ def test_dot_random_tolerance_and_tiles(dt, rtol):
         assert err <= rtol, (tile, err)
 
 
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+@pytest.mark.parametrize("Gb,M,K,N", [(1, 512, 320, 768), (1, 1024, 128, 2048), (2, 256, 192, 1024)])
+def test_dot_fast_path_exact(dt, Gb, M, K, N):
+    """256 x 256 output tiles with K slabs of 64 (the MFMA fast path; 1024 x 2048
+    also takes the XCD tile swizzle, Gb=2 the batch offsets): integer-valued
+    operands give the exact f32 result."""
+    rng = np.random.default_rng(72)
+    a = rng.integers(-3, 4, (Gb, M, K)).astype(np.float32)
+    b = rng.integers(-3, 4, (Gb, K, N)).astype(np.float32)
+    g = G.Graph()
+    x, y = g.input(a.shape, dt), g.input(b.shape, dt)
+    g.output(g.dot(x, y, tile=256))
+    got, _ = run_both(g.build(), [a, b], oracle=None)
+    np.testing.assert_array_equal(got[0], np.matmul(a.astype(np.float64), b.astype(np.float64)))
+
+
+def test_dot_fast_path_epilogue_bf16_out():
+    """Fast path with a fused store epilogue (affine, + residual, GELU) and a bf16
+    output, against the oracle within one bf16 ulp."""
+    rng = np.random.default_rng(73)
+    M, K, N = 512, 256, 512
+    a = rng.integers(-2, 3, (M, K)).astype(np.float32)
+    b = rng.integers(-2, 3, (K, N)).astype(np.float32)
+    res = (rng.standard_normal((M, N)) * 2).astype(np.float32)
+    g = G.Graph()
+    x, y, r = g.input(a.shape, "bf16"), g.input(b.shape, "bf16"), g.input(res.shape)
+    g.output(g.dot(x, y, out_dtype="bf16", tile=256, residual=r,
+                   epilogue=[(V.SUB_AFFINE, 0, 0.125, -0.5), (V.SUB_ADD, 1, 0.0, 0.0), (V.SUB_GELU, 0, 0.0, 0.0)]))
+    got, want = run_both(g.build(), [a, b, res], oracle="tensor")
+    assert_rel(as_f32(got[0], V.DT_BF16), as_f32(want[0], V.DT_BF16), BF16_ULP, 1e-6, "fast epilogue")
+
+
+def test_dot_fast_path_random_bf16():
+    rng = np.random.default_rng(1003)
+    M = K = N = 1024
+    a = vmref.bf16_to_f32(vmref.f32_to_bf16((rng.standard_normal((M, K)) * 0.125).astype(np.float32)))
+    b = vmref.bf16_to_f32(vmref.f32_to_bf16((rng.standard_normal((K, N)) * 0.125).astype(np.float32)))
+    g = G.Graph()
+    x, y = g.input((M, K), "bf16"), g.input((K, N), "bf16")
+    g.output(g.dot(x, y, tile=256))
+    got, _ = run_both(g.build(), [a, b], oracle=None)
+    want = a.astype(np.float64) @ b.astype(np.float64)
+    assert np.abs(got[0] - want).max() / np.abs(want).max() <= 1e-3
+
+
 def test_dot_views_batch_epilogue():
     rng = np.random.default_rng(71)
     Gb, M, K, N = 3, 40, 24, 56

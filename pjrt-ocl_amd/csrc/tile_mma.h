@@ -283,14 +283,21 @@ struct FastStage {
   // 8 x 8 block of k group t % 8 and n chunk t / 8 (one 16-byte row piece per k).
   // a, b: uniform slab origins (A at row m0 / column k0, B at row k0 / column n0);
   // per-thread offsets are 32-bit so the loads take an SGPR base.
-  VM_DEV void load(const gbyte* a, const gbyte* b, uint32_t K, uint32_t N) {
+  VM_DEV void load_a(const gbyte* a, uint32_t K) {
     const uint32_t t = threadIdx.x;
     const uint32_t oa = ((t >> 3) * K + (t & 7) * 8) * 2;
 #pragma unroll
     for (int j = 0; j < 8; ++j) ra[j] = *(const VM_G v4u*)(a + (oa + uint32_t(j) * 64u * K));
+  }
+  VM_DEV void load_b(const gbyte* b, uint32_t N) {
+    const uint32_t t = threadIdx.x;
     const uint32_t ob = ((t & 7) * 8 * N + (t >> 3) * 8) * 2;
 #pragma unroll
     for (int i = 0; i < 8; ++i) rb[i] = *(const VM_G v4u*)(b + (ob + uint32_t(i) * 2u * N));
+  }
+  VM_DEV void load(const gbyte* a, const gbyte* b, uint32_t K, uint32_t N) {
+    load_a(a, K);
+    load_b(b, N);
   }
 
   VM_DEV void store_a(uint16_t* s) const {
@@ -299,13 +306,16 @@ struct FastStage {
 #pragma unroll
     for (int j = 0; j < 8; ++j) *reinterpret_cast<v4u*>(la + 32 * j * kFLd) = ra[j];
   }
-  VM_DEV void store_b(uint16_t* s) {
-    const uint32_t t = threadIdx.x;
-    uint16_t* lb = s + 256 * kFLd + (t >> 3) * 8 * kFLd + (t & 7) * 8;
-    // Pin the transpose here: without this the compiler hoists the v_perm_b32s up
-    // to the global loads and waits for them at the top of the slab.
+  // Pins the staged B registers at this point: the transpose below cannot be
+  // hoisted above it (up to the global loads, which would wait for them at the top
+  // of the slab).
+  VM_DEV void pin_b() {
 #pragma unroll
     for (int i = 0; i < 8; ++i) asm volatile("" : "+v"(rb[i]));
+  }
+  VM_DEV void store_b(uint16_t* s) const {
+    const uint32_t t = threadIdx.x;
+    uint16_t* lb = s + 256 * kFLd + (t >> 3) * 8 * kFLd + (t & 7) * 8;
 #pragma unroll
     for (int jn = 0; jn < 8; ++jn) {
       // column n = 8 * (t / 8) + jn: its 16-bit value from each of the 8 k rows
@@ -321,6 +331,7 @@ struct FastStage {
   }
   VM_DEV void store(uint16_t* s) {
     store_a(s);
+    pin_b();
     store_b(s);
   }
 };
@@ -457,43 +468,73 @@ VM_TILE void mma_tile16_fast(Args A, const MmaDesc* Dp, uint32_t tile) {
   __syncthreads();
   const uint32_t fa = (wm * 128 + (lane & 31)) * kFLd + (lane >> 5) * 8;
   const uint32_t fb = 256 * kFLd + (wn * 128 + (lane & 31)) * kFLd + (lane >> 5) * 8;
+  // Operand fragments of one 16-deep k step, double-buffered: the fragments of
+  // step kk+1 are read while the MFMAs of step kk run.  Per slab:
+  //   kk 0: MFMAs
+  //   kk 1: MFMAs interleaved with the next slab's A going into the idle stage,
+  //         then the A loads of the slab after it
+  //   kk 2: the same for B, transposed on the way
+  //   block barrier (the idle stage is complete; the current one fully read)
+  //   kk 3: MFMAs, while the first fragments of the next slab are read
+  u16x8 af[2][4], bfr[2][4];
+  auto frags = [&](int p, const uint16_t* stage, int kk) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) af[p][i] = *reinterpret_cast<const u16x8*>(stage + fa + i * 32 * kFLd + kk * 16);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) bfr[p][j] = *reinterpret_cast<const u16x8*>(stage + fb + j * 32 * kFLd + kk * 16);
+  };
+  auto mfmas = [&](int p) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i][j] = mfma16<BF16>(af[p][i], bfr[p][j], acc[i][j]);
+  };
+  // The staged registers hold slab ks+1 during slab ks; each half is refilled with
+  // slab ks+2 right after it is written to LDS, so a load has about a whole slab
+  // of MFMAs to land.  (Past the last slab the last slab is reloaded: harmless.)
+  auto slab_a = [&](uint32_t s) { return a + uint64_t(min(s, nk - 1) * kFBK) * 2; };
+  auto slab_b = [&](uint32_t s) { return b + uint64_t(min(s, nk - 1) * kFBK) * N * 2; };
+  st.load(slab_a(1), slab_b(1), K, N);
+  frags(0, lds, 0);
   for (uint32_t ks = 0; ks < nk; ++ks) {
     const uint16_t* cur = lds + (ks & 1) * kFBuf;
-    // next slab (the last iteration reloads the last slab into the idle stage)
-    const uint32_t kn = min(ks + 1, nk - 1) * kFBK;
-    st.load(a + uint64_t(kn) * 2, b + uint64_t(kn) * N * 2, K, N);
-    __builtin_amdgcn_sched_barrier(0);  // keep the slab loads ahead of the MFMAs
-    // Operand fragments double-buffered across the four 16-deep k steps: the
-    // reads for step kk+1 are issued before the MFMAs of step kk.  The staged
-    // next slab goes to the idle LDS stage in between (A after step 1, B after
-    // step 2), hidden behind the matrix cores.
-    u16x8 af[2][4], bfr[2][4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) af[0][i] = *reinterpret_cast<const u16x8*>(cur + fa + i * 32 * kFLd);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) bfr[0][j] = *reinterpret_cast<const u16x8*>(cur + fb + j * 32 * kFLd);
     uint16_t* nxt = lds + ((ks + 1) & 1) * kFBuf;
+    __builtin_amdgcn_sched_barrier(0);
+    frags(1, cur, 1);
+    __builtin_amdgcn_sched_barrier(0);
+    mfmas(0);
+    __builtin_amdgcn_sched_barrier(0);
+    frags(0, cur, 2);
+    __builtin_amdgcn_sched_barrier(0);
+    mfmas(1);
+    st.store_a(nxt);
 #pragma unroll
-    for (int kk = 0; kk < kFBK / 16; ++kk) {
-      const int p = kk & 1;
-      if (kk + 1 < kFBK / 16) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          af[p ^ 1][i] = *reinterpret_cast<const u16x8*>(cur + fa + i * 32 * kFLd + (kk + 1) * 16);
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          bfr[p ^ 1][j] = *reinterpret_cast<const u16x8*>(cur + fb + j * 32 * kFLd + (kk + 1) * 16);
-      }
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = mfma16<BF16>(af[p][i], bfr[p][j], acc[i][j]);
-      __builtin_amdgcn_sched_barrier(0);
-      if (kk == 1) st.store_a(nxt);
-      if (kk == 2) st.store_b(nxt);
+    for (int q = 0; q < 8; ++q) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);   // 1 MFMA
+      __builtin_amdgcn_sched_group_barrier(0x200, 1, 1);   // 1 DS write
     }
+    __builtin_amdgcn_sched_group_barrier(0x008, 8, 1);
+    __builtin_amdgcn_sched_barrier(0);
+    st.load_a(slab_a(ks + 2), K);
+    frags(1, cur, 3);
+    st.pin_b();
+    __builtin_amdgcn_sched_barrier(0);
+    mfmas(0);
+    st.store_b(nxt);
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 2);   // 1 MFMA
+      __builtin_amdgcn_sched_group_barrier(0x002, 4, 2);   // 4 VALU (v_perm_b32)
+      __builtin_amdgcn_sched_group_barrier(0x200, 1, 2);   // 1 DS write
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 8, 2);
+    __builtin_amdgcn_sched_barrier(0);
+    st.load_b(slab_b(ks + 2), N);
     __syncthreads();
+    frags(0, nxt, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    mfmas(1);
+    __builtin_amdgcn_sched_barrier(0);
   }
   if (D.dt == DT_F32) store_fast<true>(A, D, acc, g, m0, n0);
   else store_fast<false>(A, D, acc, g, m0, n0);

@@ -56,7 +56,7 @@ constexpr uint32_t FLAG_NONE = 0xFFFFFFFFu;
 // A buffer handle is an arena byte offset, or a port index with bit 31 set
 // (vm_common.cl:41-45).  Ports are caller-owned device buffers bound per execute.
 constexpr uint32_t PORT_BIT = 0x80000000u;
-constexpr int kMaxPorts = 64;
+constexpr int kMaxPorts = 256;          // power of two: handles mask the port index
 
 // Barrier / status words at the head of the per-program control buffer.
 enum : uint32_t {

@@ -735,7 +735,7 @@ int vmrt_load(vmrt_runtime* rt, const void* bytes, size_t len, uint32_t ew_ts, u
     }
   }
 
-  // ---- ports: a buffer that is only an input or only an output, first 64 ----
+  // ---- ports: a buffer that is only an input or only an output, first kMaxPorts ----
   std::set<uint32_t> in_ids(P.inputs.begin(), P.inputs.end()), out_ids(P.outputs.begin(), P.outputs.end());
   std::map<uint32_t, int> port_of;
   int next_port = 0;

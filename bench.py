@@ -6,11 +6,13 @@ configuration the metric's "elementwise GB/s as % of roofline" is quoted on).  A
 step is one execution of the program on device-resident inputs; value = algorithmic
 bytes per step / wall time per step.
 
-Also reported under "extra" (same JSON line): config 3 dot_general 4096^3 (bf16 and
-f32 operands, f32 accumulate) and config 4 causal flash attention (B4 H16 S2048
-d128, bf16) as TFLOP/s against their MFMA roofline.
+Also reported under "extra" (same JSON line): config 1 (f32 MLP), config 3
+dot_general 4096^3 (bf16 and f32 operands, f32 accumulate) and config 4 causal
+flash attention (B4 H16 S2048 d128, bf16) as TFLOP/s against their MFMA roofline,
+and config 5 (GPT decoder, greedy decode) as tokens/s against the per-token HBM
+bytes.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workloads c2,c3,c4,copy] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workloads c1,c2,c3,c4,c5,copy] [--no-cpu]
 
 "copy" adds a plain device-to-device copy of 128 MiB, the calibration kernel for
 the HBM byte counters.
@@ -228,6 +230,64 @@ def bench_attention(rt, steps, warmup, B=4, H=16, S=2048, D=128):
             "max_rel_err_2_heads": max(errs)}
 
 
+def bench_c1(rt, steps):
+    """Config 1: the f32 two-layer MLP forward, on the GPU."""
+    from pjrt_amd import configs as CF
+    args = CF.mlp_c1_inputs()
+    lp = rt.compile(CF.mlp_c1())
+    dev_in = [rt.to_device(a) for a in args]
+    dev_out = lp.alloc_outputs()
+    ms_step, ms_kernel = time_program(rt, lp, dev_in, dev_out, steps, 5)
+    y = dev_out[0].to_host(np.float32, (256, 64))
+    x, w1, b1, w2, b2 = (a.astype(np.float64) for a in args)
+    want = np.maximum(x @ w1 + b1, 0) @ w2 + b2
+    err = float(np.abs(y - want).max() / np.abs(want).max())
+    flops = 2.0 * 256 * 128 * 512 + 2.0 * 256 * 512 * 64
+    for b in dev_in + dev_out:
+        b.free()
+    lp.close()
+    return {"workload": "C1 f32 MLP x[256,128] @ W1[128,512] + b1, relu, @ W2[512,64] + b2",
+            "ms_per_step": ms_step, "kernel_ms": ms_kernel,
+            "gflops": round(flops / (ms_kernel * 1e-3) / 1e9, 2), "max_rel_err": err}
+
+
+def bench_c5(rt, reps=3):
+    """Config 5: GPT decoder (12 layers, d 768, vocab 32000, bf16), 512-token
+    prompt then 128 greedy decode steps in one FOR loop.  Decode tokens/s comes
+    from the difference between the full program and the same program cut to 8
+    loop trips (prefill and launch cancel)."""
+    import dataclasses
+    from pjrt_amd import configs as CF
+    c = CF.C5
+    args = CF.gpt_inputs(c)
+    dev_in = [rt.to_device(a) for a in args]
+    times = {}
+    toks = None
+    for trips in (c.steps, 8):
+        lp = rt.compile(CF.gpt_c5(c, trips=trips))
+        dev_out = lp.alloc_outputs()
+        _, ms = time_program(rt, lp, dev_in, dev_out, reps, 1)
+        times[trips] = ms
+        if trips == c.steps:
+            toks = np.concatenate([dev_out[0].to_host(np.int32, (1,)), dev_out[1].to_host(np.int32, (c.steps,))])
+        for b in dev_out:
+            b.free()
+        lp.close()
+    for b in dev_in:
+        b.free()
+    per_tok = (times[c.steps] - times[8]) / (c.steps - 8)
+    ctx_avg = c.prompt + (c.steps - 1) / 2.0
+    bytes_tok = 219021312 + 36864 * ctx_avg              # weights + LM head + KV read per token
+    achieved = bytes_tok / (per_tok * 1e-3) / 1e9
+    assert toks.min() >= 0 and toks.max() < c.vocab
+    return {"workload": "C5 GPT decoder 12L d768 H12 mlp3072 vocab32000 bf16, prompt 512, 128 greedy steps "
+                        "in one FOR loop",
+            "decode_tokens_per_s": round(1e3 / per_tok, 1), "ms_per_token": round(per_tok, 4),
+            "program_ms": round(times[c.steps], 3), "prefill_plus_8_steps_ms": round(times[8], 3),
+            "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(achieved / HBM_PEAK_GBS, 4), "bytes_per_token": int(bytes_tok)}}
+
+
 def bench_copy(rt, steps, nbytes=128 << 20):
     """A plain device-to-device copy of known size (the runtime's hipMemcpyAsync):
     the calibration kernel for the FETCH_SIZE / WRITE_SIZE counters."""
@@ -252,7 +312,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workloads", default="c2,c3,c4")
+    ap.add_argument("--workloads", default="c1,c2,c3,c4,c5")
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -270,6 +330,12 @@ def main():
     if "c4" in wl:
         log("C4")
         extra["c4"] = bench_attention(rt, max(5, args.steps // 5), 2)
+    if "c1" in wl:
+        log("C1")
+        extra["c1"] = bench_c1(rt, max(5, args.steps))
+    if "c5" in wl:
+        log("C5")
+        extra["c5"] = bench_c5(rt)
     if "copy" in wl:
         log("copy")
         extra["copy"] = bench_copy(rt, max(5, args.steps // 5))

@@ -117,10 +117,12 @@ def gpt_inputs(c: GptConfig = C5, seed=1005):
     return arrays
 
 
-def gpt_c5(c: GptConfig = C5, emit_logits: bool = False):
+def gpt_c5(c: GptConfig = C5, emit_logits: bool = False, trips: int | None = None):
     """Prefill + greedy decode program.  Outputs: the first generated token [1]
     (argmax after the prompt), the ``steps`` tokens decoded after it [steps], and
-    with ``emit_logits`` the f32 logits of every step [steps + 1, vocab]."""
+    with ``emit_logits`` the f32 logits of every step [steps + 1, vocab].
+    ``trips`` runs only that many decode steps (same inputs and outputs; for
+    separating prefill from decode time)."""
     g = G.Graph()
     H, hd, T, C, D = c.heads, c.hd, c.prompt, c.ctx, c.d
     ids = g.input((T,), "i32")
@@ -204,7 +206,7 @@ def gpt_c5(c: GptConfig = C5, emit_logits: bool = False):
     g.copy_into(pos, g.add(pos, one))
     g.copy_into(step, g.add(step, one))
     body = g.end()
-    g.for_loop(c.steps, body)
+    g.for_loop(c.steps if trips is None else trips, body)
     g.output(first, out)
     if emit_logits:
         g.output(logits_all)

@@ -24,7 +24,8 @@ enum TileOp : uint32_t {
   TOP_SCATTER_INDEX = 18,
   // extension of this build: variadic (value, index) reduce -> argmax
   TOP_ARGMAX_SEG = 19,
-  TOP_COUNT = 20
+  TOP_GEMV = 20,
+  TOP_COUNT = 21
 };
 
 // ---- elementwise subops (vm_common.cl:118-146) -----------------------------------
@@ -56,15 +57,21 @@ constexpr uint32_t FLAG_NONE = 0xFFFFFFFFu;
 // A buffer handle is an arena byte offset, or a port index with bit 31 set
 // (vm_common.cl:41-45).  Ports are caller-owned device buffers bound per execute.
 constexpr uint32_t PORT_BIT = 0x80000000u;
+
+// TOP_GEMV tiling shared by the kernel and the loader: output columns per tile,
+// rows (M) per task at most.
+constexpr uint32_t kGemvCols = 256;
+constexpr uint32_t kGemvMaxM = 8;
 constexpr int kMaxPorts = 256;          // power of two: handles mask the port index
 
-// Barrier / status words at the head of the per-program control buffer.
+// Per-program control buffer: status words, then one arrival word per lane.
+constexpr uint32_t kMaxLanes = 4096;
 enum : uint32_t {
-  BAR_COUNT = 0,      // arrivals in the current barrier
-  BAR_GEN = 1,        // generation, bumped by the last arrival
+  BAR_GEN = 1,        // release epoch, written by lane 0 when every lane arrived
   BAR_ERROR = 2,      // nonzero: a lane aborted (see VmError)
   BAR_ERRINFO = 3,    // lane / detail of the first error
-  BAR_WORDS = 16
+  BAR_FLAGS = 64,     // [kMaxLanes] arrival epochs, one word per lane
+  BAR_WORDS = BAR_FLAGS + kMaxLanes
 };
 enum VmError : uint32_t {
   VM_OK = 0,
@@ -98,11 +105,12 @@ struct VmArgs {
   const Task* tasks;
   const Entry* entries;
   const LaneSpan* lanes;
-  uint32_t* ctl;            // BAR_WORDS control words
+  uint32_t* ctl;            // BAR_WORDS control words (status + arrival flags)
   uint32_t n_lanes;
   uint32_t ew_ts;           // elements per EW tile (scheduler PJRT_OCL_EW_TS)
   uint32_t mma_t;           // default MMA output tile edge (PJRT_OCL_MMA_T)
   uint32_t timeout_ticks;   // barrier wait limit in s_memrealtime ticks (100 MHz)
+  uint8_t* scratch;         // per-program scratch (GEMV split partials and counters)
   uint8_t* ports[kMaxPorts];
 };
 

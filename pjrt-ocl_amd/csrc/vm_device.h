@@ -175,47 +175,77 @@ VM_DEV float wave_sum(float x) { return wave_reduce(x, OpSum()); }
 VM_DEV float wave_max(float x) { return wave_reduce(x, OpMax()); }
 
 // ---- grid barrier ----------------------------------------------------------------------
-// Self-resetting generation barrier over ctl[BAR_COUNT] / ctl[BAR_GEN].  The block's
-// stores are published at agent scope (L2 write-back across the 8 XCDs) by thread 0
-// after the block barrier, and the acquire on exit invalidates this CU's caches
-// before any thread reads other lanes' results (the reference's device-scope
-// fence pair, vm_common.cl:231-300).  The spin reads the generation word with a
-// plain atomic load, and gives up after `timeout_ticks` of the 100 MHz constant
-// clock so a broken schedule ends the launch with an error instead of hanging.
-// Returns false when the launch must abort.
+// Grid barrier: arrival flags and a master lane.  Barrier number k of a launch
+// has epoch e0 + k, where e0 is ctl[BAR_GEN] when the launch starts (equal for all
+// lanes: the previous launch ended with every lane past its last barrier).  A lane
+// arrives by storing the epoch into its own word ctl[BAR_FLAGS + lane] with
+// release semantics -- a plain store to a private word, so arrivals never queue
+// on one atomic -- then spins until ctl[BAR_GEN] reaches the epoch.  Lane 0 is the
+// master: its 256 threads poll the other lanes' words until all have reached the
+// epoch and then publish it in ctl[BAR_GEN].  The release before each arrival and
+// the acquire after the wait make every lane's writes before the barrier visible
+// to every lane after it across the XCDs' L2s (the reference's device-scope fence
+// pair, vm_common.cl:231-300).  Every wait gives up after `timeout_ticks` of the
+// 100 MHz constant clock, so a broken schedule ends the launch with an error
+// instead of hanging.  Returns false when the launch must abort.
+__shared__ uint32_t vm_bar_epoch;      // epoch of this lane's last barrier
+
+VM_DEV void grid_barrier_init(Args A) {
+  if (threadIdx.x == 0)
+    vm_bar_epoch = __hip_atomic_load(&A->ctl[BAR_GEN], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+}
+
+VM_DEV bool barrier_timed_out(Args A, uint64_t t0) {
+  uint32_t* ctl = A->ctl;
+  if (__hip_atomic_load(&ctl[BAR_ERROR], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) return true;
+  if (__builtin_amdgcn_s_memrealtime() - t0 > A->timeout_ticks) {
+    uint32_t expect = 0;
+    __hip_atomic_compare_exchange_strong(&ctl[BAR_ERROR], &expect, uint32_t(VM_ERR_BARRIER_TIMEOUT), __ATOMIC_RELAXED,
+                                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return true;
+  }
+  return false;
+}
+
 VM_DEV bool grid_barrier(Args A) {
   __shared__ uint32_t s_ok;
   __syncthreads();
-  if (threadIdx.x == 0) {
-    uint32_t* ctl = A->ctl;
-    uint32_t ok = 1;
-    const uint32_t gen = __hip_atomic_load(&ctl[BAR_GEN], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const uint32_t arrived =
-        __hip_atomic_fetch_add(&ctl[BAR_COUNT], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-    if (arrived == A->n_lanes - 1) {
-      __hip_atomic_store(&ctl[BAR_COUNT], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_fetch_add(&ctl[BAR_GEN], 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
-    } else {
-      const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
-      while (__hip_atomic_load(&ctl[BAR_GEN], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gen) {
-        if (__hip_atomic_load(&ctl[BAR_ERROR], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
-          ok = 0;
-          break;
-        }
-        if (__builtin_amdgcn_s_memrealtime() - t0 > A->timeout_ticks) {
-          uint32_t expect = 0;
-          __hip_atomic_compare_exchange_strong(&ctl[BAR_ERROR], &expect, uint32_t(VM_ERR_BARRIER_TIMEOUT),
-                                               __ATOMIC_RELAXED, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          ok = 0;
-          break;
-        }
-        __builtin_amdgcn_s_sleep(1);
-      }
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  uint32_t* ctl = A->ctl;
+  const uint32_t epoch = vm_bar_epoch + 1;
+  const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+  if (blockIdx.x == 0) {
+    if (threadIdx.x == 0) s_ok = 1;
+    for (;;) {
+      bool mine = true;
+      for (uint32_t l = threadIdx.x + 1; l < A->n_lanes; l += kBlock)
+        if (int32_t(__hip_atomic_load(&ctl[BAR_FLAGS + l], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - epoch) < 0)
+          mine = false;
+      if (__syncthreads_and(mine)) break;
+      if (threadIdx.x == 0 && barrier_timed_out(A, t0)) s_ok = 0;
+      __syncthreads();
+      if (!s_ok) break;
+      __builtin_amdgcn_s_sleep(1);
     }
+    if (threadIdx.x == 0 && s_ok) {
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+      __hip_atomic_store(&ctl[BAR_GEN], epoch, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  } else if (threadIdx.x == 0) {
+    uint32_t ok = 1;
+    __hip_atomic_store(&ctl[BAR_FLAGS + blockIdx.x], epoch, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+    while (int32_t(__hip_atomic_load(&ctl[BAR_GEN], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - epoch) < 0) {
+      if (barrier_timed_out(A, t0)) {
+        ok = 0;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     s_ok = ok;
   }
   __syncthreads();
+  if (threadIdx.x == 0) vm_bar_epoch = epoch;   // read again only after the next barrier's block sync
   return s_ok != 0;
 }
 

@@ -15,6 +15,7 @@
 
 #include "tile_attn.h"
 #include "tile_ew.h"
+#include "tile_gemv.h"
 #include "tile_index.h"
 #include "tile_mma.h"
 #include "tile_reduce.h"
@@ -47,6 +48,7 @@ VM_DEV void exec_tiles(Args A, uint32_t ti, uint32_t lo, uint32_t hi) {
     case TOP_RED_STRIDED: red_strided_tiles(A, ti, lo, hi); break;
     case TOP_GATHER_INDEX: gather_index_tiles(A, ti, lo, hi); break;
     case TOP_ARGMAX_SEG: argmax_tiles(A, ti, lo, hi); break;
+    case TOP_GEMV: gemv_tiles(A, ti, lo, hi); break;
     default: raise_error(A, VM_ERR_BAD_TASK, task_of(A, ti).tile_op); break;
   }
 }
@@ -57,6 +59,7 @@ __global__ __launch_bounds__(kBlock, 1) void vm_main(VmArgs args) {
   (void)args;
   const Args A = (Args)__builtin_amdgcn_kernarg_segment_ptr();
   const uint32_t lane = blockIdx.x;
+  grid_barrier_init(A);
   const LaneSpan span = load_span((const VM_K LaneSpan*)A->lanes + lane);
   const VM_K Entry* ents = (const VM_K Entry*)A->entries + span.off;
 

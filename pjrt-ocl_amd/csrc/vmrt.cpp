@@ -270,6 +270,7 @@ struct Checker {
   const Program& P;
   uint32_t ew_ts, mma_t;
   std::string* err;
+  uint32_t lds_bytes;
 
   bool fail(uint32_t ti, const std::string& m) {
     *err = fmt("task %u: ", ti) + m;
@@ -322,6 +323,8 @@ struct Checker {
       case TOP_RED_SEG: case TOP_SOFTMAX_SEG: case TOP_LAYERNORM_SEG: case TOP_ARGMAX_SEG:
         return std::max<uint64_t>(1, t.p[0]);
       case TOP_FLASH_ATTN: return std::max<uint64_t>(1, uint64_t(t.p[1]) * t.p[2]);
+      case TOP_GEMV:
+        return std::max<uint64_t>(1, t.p[3]) * t.p[4] * cdiv(t.p[1], uint64_t(kGemvCols));
       default: return 0;
     }
   }
@@ -507,11 +510,44 @@ struct Checker {
         }
         return true;
       }
+      case TOP_GEMV: {
+        const uint64_t M = t.p[0], N = t.p[1], K = t.p[2], G = std::max<uint32_t>(1, t.p[3]), S = t.p[4];
+        if (adt != DT_F32 && adt != DT_BF16 && adt != DT_F16) return fail(ti, "gemv operand dtype");
+        if (dt != DT_F32 && dt != DT_BF16 && dt != DT_F16) return fail(ti, "gemv result dtype");
+        if (M < 1 || M > kGemvMaxM || N < 8 || N % 8 || K < 1 || S < 1 || S > K)
+          return fail(ti, "gemv shape / splits");
+        const uint64_t kspan = (K + S - 1) / S;
+        if ((((M * kspan + 3) & ~uint64_t(3)) + 8 * M * uint64_t(kGemvCols)) * 4 > uint64_t(lds_bytes))
+          return fail(ti, "gemv K slice does not fit the LDS");
+        if (!has(t.a, G * M * K, adt) || !has(t.b, G * K * N, adt)) return fail(ti, "gemv operands");
+        if (!has(t.dst, G * M * N, dt)) return fail(ti, "gemv result");
+        if (t.p[6]) {
+          const uint32_t e = t.p[6] - 1;
+          if (!aux_ok(e, 1) || P.aux[e] < 0 || !aux_ok(e, 1 + 4 * int64_t(P.aux[e]))) return fail(ti, "epilogue");
+          for (int k = 0; k < P.aux[e]; ++k) {
+            const int32_t kind = P.aux[e + 1 + 4 * k], src = P.aux[e + 2 + 4 * k];
+            if (!(kind == SUB_AFFINE || kind == SUB_GELU || kind == SUB_COPY || (kind >= 0 && kind <= SUB_DIV) ||
+                  kind == SUB_MAX || kind == SUB_MIN))
+              return fail(ti, "gemv epilogue kind");
+            if (src == 1 && !has(t.p[7], G * M * N, DT_F32)) return fail(ti, "epilogue residual");
+            if (src == 2 && !has(t.p[7], N, DT_F32)) return fail(ti, "epilogue bias");
+          }
+        }
+        return true;
+      }
       default:
         return fail(ti, fmt("tile op %u is not supported by this runtime", top));
     }
   }
 };
+
+// Scratch bytes of a TOP_GEMV task: arrival counters [G][column blocks] (256-byte
+// aligned) then the split partials [G][S][M][N] f32.  Zero for S = 1.
+static uint64_t gemv_scratch_bytes(const Task& t) {
+  if (t.p[4] <= 1) return 0;
+  const uint64_t G = std::max<uint32_t>(1, t.p[3]), ncb = (uint64_t(t.p[1]) + uint64_t(kGemvCols) - 1) / uint64_t(kGemvCols);
+  return ((G * ncb * 4 + 255) & ~uint64_t(255)) + G * t.p[4] * uint64_t(t.p[0]) * t.p[1] * 4;
+}
 
 // ---- pool ------------------------------------------------------------------------------
 struct Pool {
@@ -576,6 +612,8 @@ struct vmrt_program {
   Entry* entries = nullptr;
   LaneSpan* lanes = nullptr;
   uint32_t* ctl = nullptr;
+  uint8_t* scratch = nullptr;                 // GEMV split partials + arrival counters
+  uint64_t scratch_bytes = 0;
   std::vector<int> input_port, output_port;   // -1 = arena copy
   std::vector<uint32_t> in_bytes, out_bytes;
   VmArgs args{};
@@ -617,6 +655,7 @@ int vmrt_create(const vmrt_options* opts, vmrt_runtime** out, char* err, size_t 
   I.lanes_per_cu = uint32_t(per_cu);
   I.max_lanes = I.compute_units * I.lanes_per_cu;
   // One lane per CU by default: every tile op is written for a whole CU.
+  I.max_lanes = std::min(I.max_lanes, kMaxLanes);
   I.n_lanes = o.n_lanes ? std::min(o.n_lanes, I.max_lanes) : I.compute_units;
   if (const char* s = std::getenv("PJRT_OCL_VM_LANES")) {
     const long v = std::strtol(s, nullptr, 10);
@@ -662,8 +701,10 @@ int vmrt_device_info_get(vmrt_runtime* rt, vmrt_device_info* out) {
 
 static void free_program_memory(vmrt_program* p) {
   for (void* q : {static_cast<void*>(p->arena), static_cast<void*>(p->aux), static_cast<void*>(p->tasks),
-                  static_cast<void*>(p->entries), static_cast<void*>(p->lanes), static_cast<void*>(p->ctl)})
+                  static_cast<void*>(p->entries), static_cast<void*>(p->lanes), static_cast<void*>(p->ctl),
+                  static_cast<void*>(p->scratch)})
     if (q) hipFree(q);
+  p->scratch = nullptr;
   p->arena = nullptr;
   p->aux = nullptr;
   p->tasks = nullptr;
@@ -713,7 +754,7 @@ int vmrt_load(vmrt_runtime* rt, const void* bytes, size_t len, uint32_t ew_ts, u
     }
   }
   // task footprints and entry tile ranges
-  Checker chk{P, lp->ew_ts, lp->mma_t, &msg};
+  Checker chk{P, lp->ew_ts, lp->mma_t, &msg, uint32_t(vm_kernel_smem_bytes())};
   for (uint32_t i = 0; i < P.tasks.size(); ++i)
     if (!chk.check(i)) {
       const uint32_t top = P.tasks[i].tile_op & 0xFF;
@@ -774,6 +815,14 @@ int vmrt_load(vmrt_runtime* rt, const void* bytes, size_t len, uint32_t ew_ts, u
       for (int k = 2; k < 8; ++k) t.p[k] = handle(k < n_in ? orig.p[k] : orig.a);
     }
     if (top == TOP_LAYERNORM_SEG && (orig.p[3] & LN_AFFINE)) t.p[4] = handle(orig.p[4]);
+    if (top == TOP_GEMV) {
+      if (orig.p[6]) t.p[7] = handle(orig.p[7]);
+      // each GEMV task gets its own scratch region (tasks of one phase run at once)
+      t.p[5] = uint32_t(lp->scratch_bytes);
+      lp->scratch_bytes += (gemv_scratch_bytes(orig) + 255) & ~uint64_t(255);
+      if (lp->scratch_bytes > 0xFFFFFFFFull)
+        return set_err(err, errlen, VMRT_RESOURCE_EXHAUSTED, "LoadedProgram: GEMV scratch exceeds 4 GiB");
+    }
   }
   // ---- patch aux: runtime start-scalar / index-buffer locations (runtime.cc:883-924) ----
   std::vector<int32_t> aux = P.aux;
@@ -823,6 +872,8 @@ int vmrt_load(vmrt_runtime* rt, const void* bytes, size_t len, uint32_t ew_ts, u
   if (e == hipSuccess) e = up(reinterpret_cast<void**>(&lp->lanes), P.lanes.data(), P.lanes.size() * sizeof(LaneSpan));
   if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&lp->ctl), BAR_WORDS * 4);
   if (e == hipSuccess) e = hipMemset(lp->ctl, 0, BAR_WORDS * 4);
+  if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&lp->scratch), std::max<uint64_t>(lp->scratch_bytes, 256));
+  if (e == hipSuccess) e = hipMemset(lp->scratch, 0, std::max<uint64_t>(lp->scratch_bytes, 256));
   for (auto& c : P.consts) {
     if (e != hipSuccess) break;
     if (!c.second.empty()) e = hipMemcpy(lp->arena + P.buffers[c.first].off, c.second.data(), c.second.size(), hipMemcpyHostToDevice);
@@ -842,6 +893,7 @@ int vmrt_load(vmrt_runtime* rt, const void* bytes, size_t len, uint32_t ew_ts, u
   a.ew_ts = lp->ew_ts;
   a.mma_t = lp->mma_t;
   a.timeout_ticks = rt->timeout_ticks;
+  a.scratch = lp->scratch;
   for (int k = 0; k < kMaxPorts; ++k) a.ports[k] = lp->arena;   // unbound ports point at the arena
   *out = lp.release();
   return VMRT_OK;
@@ -907,6 +959,8 @@ static int check_status(vmrt_program* p, char* err, size_t errlen) {
   if (e != hipSuccess) return set_err(err, errlen, VMRT_INTERNAL, "status read: " + hip_msg(e));
   if (st[BAR_ERROR] == VM_OK) return VMRT_OK;
   hipMemset(p->ctl, 0, BAR_WORDS * 4);
+  // an aborted run can leave GEMV arrival counters part-way: start them from zero
+  if (p->scratch) hipMemset(p->scratch, 0, std::max<uint64_t>(p->scratch_bytes, 256));
   const char* what = st[BAR_ERROR] == VM_ERR_BARRIER_TIMEOUT ? "grid barrier timed out (lanes not co-resident, "
                                                                 "or non-uniform control across lanes)"
                      : st[BAR_ERROR] == VM_ERR_FRAME_DEPTH ? "control frame stack overflow"

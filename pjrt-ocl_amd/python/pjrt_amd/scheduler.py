@@ -58,6 +58,8 @@ class DeviceConfig:
     # Per-task MMA tile selection (extension): pick the largest tile edge that
     # still gives every lane work; False keeps every MMA at the default edge.
     mma_autotile: bool = True
+    # Matmuls of at most 8 rows as split-K TOP_GEMV tasks (extension).
+    gemv: bool = True
 
     @classmethod
     def from_env(cls, environ=None) -> "DeviceConfig":
@@ -85,7 +87,8 @@ class DeviceConfig:
                    mma_t=geti("PJRT_OCL_MMA_T", DEFAULT_MMA_T),
                    costs=costs,
                    fuse=env.get("PJRT_OCL_FUSE", "1") != "0",
-                   mma_autotile=env.get("PJRT_AMD_MMA_AUTOTILE", "1") != "0")
+                   mma_autotile=env.get("PJRT_AMD_MMA_AUTOTILE", "1") != "0",
+                   gemv=env.get("PJRT_AMD_GEMV", "1") != "0")
 
 
 # --- instruction -> task ------------------------------------------------------
@@ -148,7 +151,44 @@ def n_tiles(task: V.Task, cfg: DeviceConfig) -> int:
         return max(1, task.p0)
     if top == V.TOP_FLASH_ATTN:
         return max(1, task.p1 * task.p2)
+    if top == V.TOP_GEMV:
+        return max(1, task.p3) * task.p4 * gemv_col_blocks(task.p1)
     raise ScheduleError(f"n_tiles: unknown tile_op {top}")
+
+
+# --- skinny matmuls (TOP_GEMV) ------------------------------------------------------
+
+GEMV_MAX_M = 8
+GEMV_COLS = 256                 # output columns per tile
+GEMV_LDS_FLOATS = 147456 // 4   # the kernel's LDS: x slice + row-phase sums
+_EPI_INLINE = {V.SUB_AFFINE, V.SUB_GELU, V.SUB_COPY, V.SUB_ADD, V.SUB_MUL, V.SUB_SUB, V.SUB_DIV,
+               V.SUB_MAX, V.SUB_MIN}
+
+
+def gemv_col_blocks(N: int) -> int:
+    return -(-N // GEMV_COLS)
+
+
+def gemv_splits(M: int, N: int, K: int, G: int, nlanes: int) -> int:
+    """K splits of a skinny matmul: enough tiles to cover the lanes, at least 8
+    rows per split, and the x slice [M][K/S] plus the [8][M][256] row-phase sums
+    inside the kernel's LDS."""
+    s = max(1, min(-(-nlanes // (G * gemv_col_blocks(N))), max(1, K // 8)))
+    while s < K and (M * -(-K // s) + 3) // 4 * 4 + 8 * M * GEMV_COLS > GEMV_LDS_FLOATS:
+        s += 1
+    return s
+
+
+def gemv_eligible(M, N, K, G, aview, bview, epi, adt, dt, prog) -> bool:
+    if not (1 <= M <= GEMV_MAX_M and N % 8 == 0 and N >= 8 and K >= 1) or aview or bview:
+        return False
+    if adt not in (V.DT_BF16, V.DT_F16, V.DT_F32) or dt not in (V.DT_F32, V.DT_BF16, V.DT_F16):
+        return False
+    if epi:
+        nm = prog.aux[epi - 1]
+        if any(prog.aux[epi + 4 * k] not in _EPI_INLINE for k in range(nm)):
+            return False
+    return True
 
 
 def instr_to_task(ins: V.Instr, prog: V.VMProgram, cfg: DeviceConfig) -> V.Task:
@@ -234,10 +274,15 @@ def instr_to_task(ins: V.Instr, prog: V.VMProgram, cfg: DeviceConfig) -> V.Task:
         aview, bview, epi, epi_res = ins.aview, ins.bview, ins.epi, ins.epi_res
         if ins.aux and not (aview or bview or epi):
             aview, bview, epi, epi_res = prog.aux[ins.aux:ins.aux + 4]
+        adt, dt = bufs[ins.a].dtype, bufs[ins.dst].dtype
         if N == 1 and G == 1 and not aview and not bview and not epi:
             # GEMV: one matrix row per tile through the segmented reduce in dot
             # mode (ops/dot.py:166-183).
             t = V.Task(V.TOP_RED_SEG, ins.dst, ins.a, ins.b, M, K, 0, 1)
+        elif cfg.gemv and gemv_eligible(M, N, K, G, aview, bview, epi, adt, dt, prog):
+            t = V.Task(V.TOP_GEMV, ins.dst, ins.a, ins.b, M, N, K, G,
+                       gemv_splits(M, N, K, G, cfg.nlanes), 0, epi,
+                       epi_res if epi else 0)
         else:
             code = V.MMA_TILE_CODES.get(ins.mma_tile, 0)
             if not code and cfg.mma_autotile:
@@ -335,6 +380,9 @@ def task_cost(task: V.Task, cfg: DeviceConfig, prog: V.VMProgram) -> float:
         flops = 2.0 * M * N * K * G
         byts = (M * K + K * N) * G * asz + M * N * G * dsz
         return max(flops / (_MFMA_TFLOPS * 1e6), byts / (_HBM_GBS * 1e3)) + 1.0
+    if top == V.TOP_GEMV:
+        M, N, K, G = task.p0, task.p1, task.p2, max(1, task.p3)
+        return (K * N * asz + M * N * dsz) * G / (_HBM_GBS * 1e3) + 2.0
     if top == V.TOP_FLASH_ATTN:
         H, T = task.p1, task.p2
         hd = prog.aux[task.p3 + 3] if task.p3 + 3 < len(prog.aux) else 128

@@ -34,7 +34,10 @@ which does not use them is byte-for-byte a reference program):
   (0 = the runtime default advertised as PJRT_OCL_MMA_T);
 * tensor opcode ``OP_ARGMAX_SEG`` (67) / tile op ``TOP_ARGMAX_SEG`` (19):
   the variadic (value, index) reduce that ``jnp.argmax`` lowers to, which the
-  reference rejects (python/pjrt_ocl/ops/reduce.py:165-168).
+  reference rejects (python/pjrt_ocl/ops/reduce.py:165-168);
+* tile op ``TOP_GEMV`` (20): the scheduler's split-K form of an ``OP_DOT`` with
+  at most 8 rows (decode-time matmuls); p0 M, p1 N, p2 K, p3 G, p4 splits, p5
+  scratch offset (the loader's), p6 epilogue + 1, p7 residual.
 """
 from __future__ import annotations
 
@@ -134,7 +137,8 @@ TOP_EW, TOP_MMA, TOP_GATHER, TOP_RED_PART, TOP_RED_COMB, TOP_IOTA_DIM, \
     TOP_FLASH_ATTN, TOP_RED_STRIDED, TOP_GATHER_INDEX, TOP_CONV, \
     TOP_SCATTER_INDEX = range(19)
 TOP_ARGMAX_SEG = 19          # extension
-TOP_MAX = TOP_ARGMAX_SEG
+TOP_GEMV = 20                # extension
+TOP_MAX = TOP_GEMV
 
 # ---- EW subops (vm_common.cl:118-146) ------------------------------------------
 SUB_ADD, SUB_MUL, SUB_SUB, SUB_DIV, SUB_MAX, SUB_MIN, SUB_POW, SUB_COPY, \

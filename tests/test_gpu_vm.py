@@ -11,7 +11,7 @@ import numpy as np
 import pytest
 
 import vmprogs as P
-from gpu_util import as_f32, assert_rel, run_both, runtime
+from gpu_util import as_f32, assert_rel, blob_for, run_both, runtime
 from oracle import vmref
 from pjrt_amd import graph as G
 from pjrt_amd import vmprogram as V
@@ -355,6 +355,47 @@ def test_dot_fast_path_random_bf16():
     got, _ = run_both(g.build(), [a, b], oracle=None)
     want = a.astype(np.float64) @ b.astype(np.float64)
     assert np.abs(got[0] - want).max() / np.abs(want).max() <= 1e-3
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
+@pytest.mark.parametrize("Gb,M,K,N", [(1, 1, 768, 2304), (1, 1, 3072, 768), (1, 3, 200, 1000), (12, 1, 640, 64),
+                                      (1, 8, 64, 32000), (2, 5, 7, 8)])
+def test_gemv_split_k_exact(dt, Gb, M, K, N):
+    """Skinny matmuls (TOP_GEMV, split K with the last-arriving split summing the
+    partials): integer-valued operands give the exact result, on two executions
+    in a row (the arrival counters reset themselves)."""
+    rng = np.random.default_rng(74)
+    a = rng.integers(-3, 4, (Gb, M, K)).astype(np.float32)
+    b = rng.integers(-3, 4, (Gb, K, N)).astype(np.float32)
+    g = G.Graph()
+    x, y = g.input(a.shape, dt), g.input(b.shape, dt)
+    g.output(g.dot(x, y))
+    blob, cfg = blob_for(g.build())
+    assert any(tk.top == V.TOP_GEMV for tk in vmref.parse(blob).tasks)
+    lp = runtime().load(blob)
+    try:
+        want = np.matmul(a.astype(np.float64), b.astype(np.float64))
+        for _ in range(2):
+            np.testing.assert_array_equal(lp(a, b)[0], want)
+    finally:
+        lp.close()
+
+
+def test_gemv_epilogue_bf16_out():
+    rng = np.random.default_rng(75)
+    M, K, N = 1, 768, 3072
+    a = (rng.standard_normal((M, K)) * 0.5).astype(np.float32)
+    b = (rng.standard_normal((K, N)) * 0.05).astype(np.float32)
+    bias = rng.standard_normal(N).astype(np.float32)
+    res = rng.standard_normal((M, N)).astype(np.float32)
+    g = G.Graph()
+    x, y, bb, rr = g.input(a.shape, "bf16"), g.input(b.shape, "bf16"), g.input(bias.shape), g.input(res.shape)
+    h = g.dot(x, y, out_dtype="bf16", residual=bb, epilogue=[(V.SUB_ADD, 2, 0.0, 0.0), (V.SUB_GELU, 0, 0.0, 0.0)])
+    o = g.dot(x, y, residual=rr, epilogue=[(V.SUB_AFFINE, 0, 0.5, 0.25), (V.SUB_ADD, 1, 0.0, 0.0)])
+    g.output(h, o)
+    got, want = run_both(g.build(), [a, b, bias, res], oracle="tensor")
+    assert_rel(as_f32(got[0], V.DT_BF16), as_f32(want[0], V.DT_BF16), BF16_ULP, 1e-6, "gemv gelu bf16")
+    assert_rel(got[1], want[1], 1e-5, 1e-5, "gemv affine + residual")
 
 
 def test_dot_views_batch_epilogue():

@@ -159,3 +159,64 @@ def test_mma_autotile_picks_parallel_tile():
     g.output(g.dot(a, b))
     sched = S.schedule_program(g.build(), S.DeviceConfig(nlanes=256, mma_t=128))
     assert (sched.tasks[0].p3 >> 24) == V.MMA_TILE_CODES[64]
+
+
+# --- skinny matmuls as split-K TOP_GEMV tasks ----------------------------------------
+
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+@pytest.mark.parametrize("Gb,M,K,N", [(1, 1, 5, 8), (1, 3, 64, 264), (3, 8, 700, 1000), (1, 1, 3072, 768)])
+def test_gemv_split_k_tiles_exact(dt, Gb, M, K, N):
+    """Integer-valued operands: the split partials and their in-order sum are exact,
+    so the lane simulator (tiles in forward and reverse lane order) must give the
+    float64 product bit for bit."""
+    from oracle import vmref
+    rng = np.random.default_rng(7)
+    a = rng.integers(-3, 4, (Gb, M, K)).astype(np.float32)
+    b = rng.integers(-3, 4, (Gb, K, N)).astype(np.float32)
+    g = G.Graph()
+    x, y = g.input(a.shape, dt), g.input(b.shape, dt)
+    g.output(g.dot(x, y))
+    prog = g.build()
+    cfg = S.DeviceConfig(nlanes=16)
+    sched = S.schedule_program(prog, cfg)
+    gemv = [t for t in sched.tasks if t.tile_op == V.TOP_GEMV]
+    assert len(gemv) == 1 and gemv[0].p4 >= 1
+    blob = V.serialize(prog, sched)
+    got = vmref.execute_schedule(blob, [a, b])[0]
+    np.testing.assert_array_equal(got, np.matmul(a.astype(np.float64), b.astype(np.float64)))
+
+
+def test_gemv_epilogue_matches_tensor_semantics():
+    from oracle import vmref
+    rng = np.random.default_rng(8)
+    M, K, N = 2, 96, 520
+    a = rng.standard_normal((M, K)).astype(np.float32)
+    b = rng.standard_normal((K, N)).astype(np.float32)
+    bias = rng.standard_normal(N).astype(np.float32)
+    g = G.Graph()
+    x, y, bb = g.input(a.shape), g.input(b.shape), g.input(bias.shape)
+    g.output(g.dot(x, y, residual=bb, epilogue=[(V.SUB_ADD, 2, 0.0, 0.0), (V.SUB_GELU, 0, 0.0, 0.0)]))
+    prog = g.build()
+    blob = V.serialize(prog, S.schedule_program(prog, S.DeviceConfig(nlanes=32)))
+    got = vmref.execute_schedule(blob, [a, b, bias])[0]
+    want = vmref.execute(blob, [a, b, bias])[0]            # tensor level: one matmul
+    np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-6)
+
+
+def test_gemv_splits_cover_lanes_and_fit_lds():
+    for M, N, K, G_ in [(1, 2304, 768, 1), (1, 32000, 768, 1), (8, 768, 3072, 1), (1, 64, 640, 12),
+                        (8, 8, 100000, 1)]:
+        s = S.gemv_splits(M, N, K, G_, 256)
+        kspan = -(-K // s)
+        assert 1 <= s <= K
+        assert ((M * kspan + 3) // 4 * 4 + 8 * M * S.GEMV_COLS) * 4 <= 147456
+        assert G_ * s * S.gemv_col_blocks(N) >= min(256, G_ * S.gemv_col_blocks(N) * max(1, K // 8))
+
+
+def test_gemv_not_chosen_for_views_or_wide_m():
+    g = G.Graph()
+    x, w = g.input((16, 64), "bf16"), g.input((64, 128), "bf16")
+    wt = g.input((128, 64), "bf16")
+    g.output(g.dot(x, w), g.dot(g.slice(x, (0, 0), (1, 64)), g.transpose_view(wt, (1, 0))))
+    sched = S.schedule_program(g.build(), S.DeviceConfig(nlanes=16))
+    assert all(t.tile_op != V.TOP_GEMV for t in sched.tasks)

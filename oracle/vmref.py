@@ -685,38 +685,24 @@ class TaskRunner:
             have[g, r0:r1, c0:c1] = blk
         self.m.store_f(t.dst, slice(0, G * M * N), have.reshape(-1), t.dt)
 
-    # 20: split-K skinny matmul (extension).  Tile ((g*S)+s)*NCB + nb is the
-    # partial of K rows [s*K//S, (s+1)*K//S) for columns [256 nb, 256 nb + 256);
-    # once all S partials of a column block exist they are summed in split order,
-    # the epilogue applied and C written -- whatever order the lanes ran in.
+    # 20: skinny matmul (extension): tile g * ceil(N / CW) + nb is the column
+    # strip [CW nb, CW nb + CW) of batch g over the whole K (p4 = CW).
     def top20(self, t, lo, hi):
         m = self.m
-        M, N, K, G, S = t.p[0], t.p[1], t.p[2], max(1, t.p[3]), t.p[4]
-        ncb = -(-N // 256)
+        M, N, K, G, CW = t.p[0], t.p[1], t.p[2], max(1, t.p[3]), t.p[4]
+        ncb = -(-N // CW)
         A = m.load_f(t.a, t.adt)[:G * M * K].reshape(G, M, K)
         B = m.load_f(t.b, t.adt)[:G * K * N].reshape(G, K, N)
-        parts = getattr(self, "_gemv_parts", None)
-        if parts is None:
-            parts = self._gemv_parts = {}
-        key = (id(m), t.dst, t.a, t.b, t.p)
         res = m.load_f(t.p[7]) if t.p[6] else None
+        have = m.load_f(t.dst, t.dt)[:G * M * N].reshape(G, M, N).copy()
         for tile in range(lo, hi):
-            nb, s, g = tile % ncb, (tile // ncb) % S, tile // (ncb * S)
-            k0, k1 = s * K // S, (s + 1) * K // S
-            c0, c1 = nb * 256, min(nb * 256 + 256, N)
-            blk = (A[g, :, k0:k1].astype(np.float64) @ B[g, k0:k1, c0:c1].astype(np.float64)).astype(np.float32)
-            got = parts.setdefault(key + (g, nb), {})
-            got[s] = blk
-            if len(got) == S:
-                acc = np.zeros_like(blk)
-                for q in range(S):
-                    acc = (acc + got[q]).astype(np.float32)
-                del parts[key + (g, nb)]
-                if t.p[6]:
-                    acc = self._epilogue(t, acc, g, 0, M, c0, c1, M, N, res)
-                have = m.load_f(t.dst, t.dt)[:G * M * N].reshape(G, M, N).copy()
-                have[g, :, c0:c1] = acc
-                m.store_f(t.dst, slice(0, G * M * N), have.reshape(-1), t.dt)
+            nb, g = tile % ncb, tile // ncb
+            c0, c1 = nb * CW, min(nb * CW + CW, N)
+            blk = (A[g].astype(np.float64) @ B[g, :, c0:c1].astype(np.float64)).astype(np.float32)
+            if t.p[6]:
+                blk = self._epilogue(t, blk, g, 0, M, c0, c1, M, N, res)
+            have[g, :, c0:c1] = blk
+        m.store_f(t.dst, slice(0, G * M * N), have.reshape(-1), t.dt)
 
     def _epilogue(self, t, v, g, r0, r1, c0, c1, M, N, res):
         aux = self.m.p.aux
@@ -1079,7 +1065,7 @@ def _whole_tiles(t: Task, ew_ts: int, mma_t: int) -> int:
     if t.top == 14:
         return max(1, p[1] * p[2])
     if t.top == 20:
-        return max(1, p[3]) * p[4] * -(-p[1] // 256)
+        return max(1, p[3]) * -(-p[1] // p[4])
     raise NotImplementedError(t.top)
 
 

@@ -1,39 +1,57 @@
 // TOP_GEMV: C[g] = A[g] (M x K) . B[g] (K x N) for skinny M (decode-time matmuls:
 // one token's activations against a weight matrix), the weight stream being the
 // whole cost.  The reference sends these through its matmul tiles
-// (ops/dot.py:94-161, mma.cl:362-434), whose K loop runs serially inside one
-// tile; here K is split so every CU streams a slice of the weights at once.
+// (ops/dot.py:94-161, mma.cl:362-434); here each tile is a narrow column strip of
+// B with the full K, so a launch has a tile per CU even for N = 768 and no tile
+// ever exchanges partial sums with another (no cross-CU synchronisation, no
+// scratch, deterministic).
 //
-// Task: p0 M (<= kGemvMaxM), p1 N (multiple of 8), p2 K, p3 G, p4 S (K splits),
-// p5 scratch byte offset (assigned by the loader), p6 epilogue descriptor + 1,
-// p7 residual handle.  Operands contiguous row-major, A/B of one dtype
-// (bf16 / f16 / f32), f32 accumulation.
+// Task: p0 M (<= kGemvMaxM), p1 N (multiple of 8), p2 K, p3 G, p4 CW (columns
+// per tile: 8 x a power of two, at most 256), p6 epilogue descriptor + 1, p7
+// residual handle.  Operands contiguous row-major, A/B of one dtype (bf16 / f16 /
+// f32), f32 accumulation.
 //
-// Tile t = ((g * S) + s) * NCB + nb covers output columns [256 nb, 256 nb + 256)
-// of batch g over the K rows of split s.  Threads: 32 column groups of 8 columns
-// (one 16-byte bf16 load per row) x 8 row phases.  The 8 row phases are summed
-// through LDS into the split's partial [M][256], stored in the scratch area;
-// a per-(g, nb) arrival counter then elects the last split to finish, which sums
-// the S partials in split order (deterministic), applies the store epilogue and
-// writes C.  The counter is reset by that last tile, so the next execution (or
-// loop trip) starts from zero.
+// Tile t = g * ceil(N / CW) + nb covers columns [CW nb, CW nb + CW) of batch g.
+// Threads: CW / 8 column groups (one 16-byte bf16 load per row each) x RP =
+// 2048 / CW row phases; thread (cg, rp) accumulates rows rp, rp + RP, ... with up
+// to 16 row loads in flight.  The RP row-phase sums are added in a fixed order
+// through LDS.
 #pragma once
 #include "tile_mma.h"
 
 namespace vm {
 
-VM_DEV uint32_t gemv_ncb(uint32_t N) { return (N + kGemvCols - 1) / kGemvCols; }
-
-// 8 consecutive elements of row k starting at column c, as f32.
+// Rows rp, rp + RP, ... of this thread's 8 columns.  Loads run in chunks of U rows
+// into two register buffers: chunk c+1 is in flight while chunk c is consumed.
+// Rows past K re-read row K - 1 and are not accumulated; col is always a valid
+// column group (callers clamp it), so no load sits behind a branch; xs rows past
+// M re-read row M - 1 (results unused).
 template <uint32_t ADT>
-VM_DEV void gemv_row8(const gbyte* b, uint64_t elem, float (&w)[8]) {
+struct GemvRaw {
+  typedef v4u T;                          // 8 x 16-bit
+};
+template <>
+struct GemvRaw<DT_F32> {
+  struct T {
+    v4f lo, hi;
+  };
+};
+
+template <uint32_t ADT>
+VM_DEV typename GemvRaw<ADT>::T gemv_ld(const gbyte* b, uint64_t elem) {
+  if constexpr (ADT == DT_F32)
+    return {*(const VM_G v4f*)(b + elem * 4), *(const VM_G v4f*)(b + elem * 4 + 16)};
+  else
+    return *(const VM_G v4u*)(b + elem * 2);
+}
+
+template <uint32_t ADT>
+VM_DEV void gemv_cvt(const typename GemvRaw<ADT>::T& r, float (&w)[8]) {
   if constexpr (ADT == DT_F32) {
-    const v4f lo = *(const VM_G v4f*)(b + elem * 4), hi = *(const VM_G v4f*)(b + elem * 4 + 16);
-    w[0] = lo.x; w[1] = lo.y; w[2] = lo.z; w[3] = lo.w;
-    w[4] = hi.x; w[5] = hi.y; w[6] = hi.z; w[7] = hi.w;
+    w[0] = r.lo.x; w[1] = r.lo.y; w[2] = r.lo.z; w[3] = r.lo.w;
+    w[4] = r.hi.x; w[5] = r.hi.y; w[6] = r.hi.z; w[7] = r.hi.w;
   } else {
-    const v4u q = *(const VM_G v4u*)(b + elem * 2);
-    const uint32_t u[4] = {q.x, q.y, q.z, q.w};
+    const uint32_t u[4] = {r.x, r.y, r.z, r.w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       if constexpr (ADT == DT_BF16) {
@@ -47,35 +65,30 @@ VM_DEV void gemv_row8(const gbyte* b, uint64_t elem, float (&w)[8]) {
   }
 }
 
-// Rows k0 + rp, k0 + rp + 8, ... of this thread's 8 columns (rp = row phase),
-// four rows in flight.  col is always a valid column group (callers clamp it), so
-// no load sits behind a branch; xs rows past M re-read row M - 1 (results unused).
+constexpr int kGemvU = 8;                 // rows per load chunk and thread
+
+template <uint32_t ADT>
+VM_DEV void gemv_issue(typename GemvRaw<ADT>::T (&raw)[kGemvU], const gbyte* b, uint32_t N, uint32_t K, uint32_t k,
+                       uint32_t RP, uint32_t col) {
+#pragma unroll
+  for (int u = 0; u < kGemvU; ++u) raw[u] = gemv_ld<ADT>(b, uint64_t(min(k + u * RP, K - 1)) * N + col);
+}
+
 template <uint32_t ADT, int MM>
-VM_DEV void gemv_accumulate(const gbyte* b, uint32_t N, uint32_t M, uint32_t k0, uint32_t k1, uint32_t col,
-                            const float* xs, uint32_t kspan, float (&acc)[MM][8]) {
-  const uint32_t rp = threadIdx.x >> 5;
-  uint32_t k = k0 + rp;
-  for (; k + 24 < k1; k += 32) {
-    float w[4][8];
+VM_DEV void gemv_consume(const typename GemvRaw<ADT>::T (&raw)[kGemvU], uint32_t M, uint32_t K, uint32_t k,
+                         uint32_t RP, const float* xs, float (&acc)[MM][8]) {
 #pragma unroll
-    for (int u = 0; u < 4; ++u) gemv_row8<ADT>(b, uint64_t(k + 8 * u) * N + col, w[u]);
-#pragma unroll
-    for (int u = 0; u < 4; ++u)
+  for (int u = 0; u < kGemvU; ++u) {
+    const uint32_t kk = k + u * RP;
+    if (kk < K) {
+      float w[8];
+      gemv_cvt<ADT>(raw[u], w);
 #pragma unroll
       for (int m = 0; m < MM; ++m) {
-        const float xv = xs[min(uint32_t(m), M - 1) * kspan + (k + 8 * u - k0)];
+        const float xv = xs[min(uint32_t(m), M - 1) * K + kk];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc[m][j] = fmaf(xv, w[u][j], acc[m][j]);
+        for (int j = 0; j < 8; ++j) acc[m][j] = fmaf(xv, w[j], acc[m][j]);
       }
-  }
-  for (; k < k1; k += 8) {
-    float w[8];
-    gemv_row8<ADT>(b, uint64_t(k) * N + col, w);
-#pragma unroll
-    for (int m = 0; m < MM; ++m) {
-      const float xv = xs[min(uint32_t(m), M - 1) * kspan + (k - k0)];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) acc[m][j] = fmaf(xv, w[j], acc[m][j]);
     }
   }
 }
@@ -84,94 +97,75 @@ template <uint32_t ADT, int MM>
 VM_TILE void gemv_tile(Args A, uint32_t ti, uint32_t tile) {
   A = uargs(A);
   const VM_K Task& t = task_of(A, ti);
-  const uint32_t M = t.p[0], N = t.p[1], K = t.p[2], S = t.p[4];
-  const uint32_t ncb = gemv_ncb(N);
+  const uint32_t M = t.p[0], N = t.p[1], K = t.p[2], CW = t.p[4];
+  const uint32_t ncb = (N + CW - 1) / CW;
   tile = uni(tile);
-  const uint32_t nb = tile % ncb, s = (tile / ncb) % S, g = tile / (ncb * S);
+  const uint32_t nb = tile % ncb, g = tile / ncb;
   const uint32_t esz = ADT == DT_F32 ? 4 : 2;
   const gbyte* a = resolve(A, t.a) + uint64_t(g) * M * K * esz;
   const gbyte* b = resolve(A, t.b) + uint64_t(g) * K * N * esz;
-  const uint32_t k0 = uint32_t(uint64_t(s) * K / S), k1 = uint32_t(uint64_t(s + 1) * K / S);
-  const uint32_t kspan = k1 - k0;
-  // LDS: x slice [M][kspan] then the row-phase sums [8][M][256] (the loader
-  // checks that (M * kspan rounded up to 4 + 2048 M) floats fit)
+  const uint32_t cgs = CW / 8, RP = kBlock / cgs;
+  // LDS: x [M][K], then the row-phase sums [RP][M][CW] (= 2048 M floats), then the
+  // first-pass sums; the loader checks that M * K + 4096 M floats fit
   float* xs = reinterpret_cast<float*>(vm_smem);
-  float* red = xs + ((M * kspan + 3) & ~3u);
+  float* red = xs + ((M * K + 3) & ~3u);
+  float* tmp = red + 2048 * M;
 
+  const uint32_t cg = threadIdx.x % cgs, rp = threadIdx.x / cgs;
+  // column groups past N (the last strip's tail) read the last group instead
+  const uint32_t col = min(nb * CW + cg * 8, N - 8);
+  // the first weight chunk is in flight while x is staged
+  typename GemvRaw<ADT>::T r0[kGemvU], r1[kGemvU];
+  gemv_issue<ADT>(r0, b, N, K, rp, RP, col);
   __syncthreads();                       // the previous user of the LDS is done
-  for (uint32_t i = threadIdx.x; i < M * kspan; i += kBlock) {
-    const uint32_t m = i / kspan, k = k0 + i % kspan;
-    xs[i] = load_f(a, ADT, uint64_t(m) * K + k);
-  }
+  for (uint32_t i = threadIdx.x; i < M * K; i += kBlock) xs[i] = load_f(a, ADT, i);
   __syncthreads();
 
-  const uint32_t cg = threadIdx.x & 31, rp = threadIdx.x >> 5;
-  // column groups past N (the last block's tail) read the last group instead
-  const uint32_t col = min(nb * kGemvCols + cg * 8, N - 8);
   float acc[MM][8];
 #pragma unroll
   for (int m = 0; m < MM; ++m)
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc[m][j] = 0.0f;
-  if (kspan) gemv_accumulate<ADT, MM>(b, N, M, k0, k1, col, xs, kspan, acc);
-
-  // sum the 8 row phases: red[rp][m][cg * 8 + j]
+  // uniform loop over chunk pairs; the prefetch is unconditional (clamped rows)
+  const uint32_t step = kGemvU * RP;
+  for (uint32_t kb = 0; kb < K; kb += 2 * step) {
+    gemv_issue<ADT>(r1, b, N, K, kb + step + rp, RP, col);
+    gemv_consume<ADT, MM>(r0, M, K, kb + rp, RP, xs, acc);
+    if (kb + step >= K) break;
+    gemv_issue<ADT>(r0, b, N, K, kb + 2 * step + rp, RP, col);
+    gemv_consume<ADT, MM>(r1, M, K, kb + step + rp, RP, xs, acc);
+  }
 #pragma unroll
   for (int m = 0; m < MM; ++m)
     if (m < int(M))
 #pragma unroll
-      for (int j = 0; j < 8; ++j) red[(rp * M + m) * kGemvCols + cg * 8 + j] = acc[m][j];
+      for (int j = 0; j < 8; ++j) red[(rp * M + m) * CW + cg * 8 + j] = acc[m][j];
+  __syncthreads();
+
+  // Sum the RP row phases of each of the M * CW outputs in a fixed order: J
+  // threads per output each add every J-th phase, then one thread adds the J.
+  const uint32_t outs = M * CW;
+  const uint32_t J = outs >= kBlock ? 1u : kBlock / outs;
+  for (uint32_t i = threadIdx.x; i < outs * J; i += kBlock) {
+    const uint32_t o = i % outs, j = i / outs;
+    float v = 0.0f;
+    for (uint32_t r = j; r < RP; r += J) v += red[r * outs + o];
+    tmp[j * outs + o] = v;
+  }
   __syncthreads();
 
   const uint32_t dt = (t.tile_op >> 8) & 0xFF;
   const uint32_t epi = t.p[6];
   gbyte* d = resolve(A, t.dst);
-  uint8_t* scratch = A->scratch + t.p[5];
-  uint32_t* counters = reinterpret_cast<uint32_t*>(scratch);
-  float* part = reinterpret_cast<float*>(scratch + ((uint64_t(t.p[3]) * ncb * 4 + 255) & ~uint64_t(255)));
-  const uint32_t c = threadIdx.x;                                  // column within the tile
-  const uint32_t n = nb * kGemvCols + c;
-  // partial of this split, one column per thread
-  float pm[kGemvMaxM];
-#pragma unroll
-  for (uint32_t m = 0; m < kGemvMaxM; ++m) {
-    float v = 0.0f;
-    if (m < M)
-#pragma unroll
-      for (int r = 0; r < 8; ++r) v += red[(r * M + m) * kGemvCols + c];
-    pm[m] = v;
-  }
-
-  __shared__ uint32_t s_last;
-  if (S > 1) {
-    if (n < N)
-      for (uint32_t m = 0; m < M; ++m) part[((uint64_t(g) * S + s) * M + m) * N + n] = pm[m];
-    __threadfence();                     // partials visible device-wide before the arrival
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      uint32_t* cnt = counters + g * ncb + nb;
-      const uint32_t old = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-      const bool last = old == S - 1;
-      if (last) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      s_last = last;
-    }
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();                     // see every split's partial
-    if (n < N)
-      for (uint32_t m = 0; m < M; ++m) {
-        float v = 0.0f;
-        for (uint32_t q = 0; q < S; ++q) v += part[((uint64_t(g) * S + q) * M + m) * N + n];
-        pm[m] = v;
-      }
-  }
-  if (n >= N) return;
   const VM_K int32_t* e = aux_of(A) + (epi ? epi - 1 : 0);
   const int nm = epi ? e[0] : 0;
   const gbyte* res = epi ? resolve(A, t.p[7]) : nullptr;
-  for (uint32_t m = 0; m < M; ++m) {
+  for (uint32_t o = threadIdx.x; o < outs; o += kBlock) {
+    const uint32_t m = o / CW, n = nb * CW + o % CW;
+    if (n >= N) continue;
+    float x = 0.0f;
+    for (uint32_t j = 0; j < J; ++j) x += tmp[j * outs + o];
     const uint64_t elem = (uint64_t(g) * M + m) * N + n;
-    float x = pm[m];
     for (int k = 0; k < nm; ++k) {
       const uint32_t kind = uint32_t(e[1 + 4 * k]), src = uint32_t(e[2 + 4 * k]);
       float y = x;
@@ -187,7 +181,7 @@ VM_TILE void gemv_tiles(Args A, uint32_t ti, uint32_t lo, uint32_t hi) {
   A = uargs(A);
   const VM_K Task& t = task_of(A, ti);
   const uint32_t M = t.p[0], adt = (t.tile_op >> 16) & 0xFF;
-  const uint32_t total = max(1u, t.p[3]) * t.p[4] * gemv_ncb(t.p[1]);
+  const uint32_t total = max(1u, t.p[3]) * ((t.p[1] + t.p[4] - 1) / t.p[4]);
   hi = min(hi, total);
   for (uint32_t tile = lo; tile < hi; ++tile) {
     if (adt == DT_BF16) {

@@ -58,9 +58,7 @@ constexpr uint32_t FLAG_NONE = 0xFFFFFFFFu;
 // (vm_common.cl:41-45).  Ports are caller-owned device buffers bound per execute.
 constexpr uint32_t PORT_BIT = 0x80000000u;
 
-// TOP_GEMV tiling shared by the kernel and the loader: output columns per tile,
-// rows (M) per task at most.
-constexpr uint32_t kGemvCols = 256;
+// TOP_GEMV: rows (M) per task at most.
 constexpr uint32_t kGemvMaxM = 8;
 constexpr int kMaxPorts = 256;          // power of two: handles mask the port index
 
@@ -73,6 +71,11 @@ enum : uint32_t {
   BAR_FLAGS = 64,     // [kMaxLanes] arrival epochs, one word per lane
   BAR_WORDS = BAR_FLAGS + kMaxLanes
 };
+// Profiling counters (100 MHz ticks of s_memrealtime): [0] lane-time in grid
+// barriers, [1] lane-barriers; task i at kStatTask + 4 i: lane-time summed over
+// its entries, longest single entry, entry count.
+constexpr uint32_t kStatTask = 4;
+
 enum VmError : uint32_t {
   VM_OK = 0,
   VM_ERR_BARRIER_TIMEOUT = 1,
@@ -110,7 +113,7 @@ struct VmArgs {
   uint32_t ew_ts;           // elements per EW tile (scheduler PJRT_OCL_EW_TS)
   uint32_t mma_t;           // default MMA output tile edge (PJRT_OCL_MMA_T)
   uint32_t timeout_ticks;   // barrier wait limit in s_memrealtime ticks (100 MHz)
-  uint8_t* scratch;         // per-program scratch (GEMV split partials and counters)
+  uint64_t* stats;          // profiling counters (null: off), see kStat*
   uint8_t* ports[kMaxPorts];
 };
 

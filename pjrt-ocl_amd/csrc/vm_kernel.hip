@@ -53,6 +53,18 @@ VM_DEV void exec_tiles(Args A, uint32_t ti, uint32_t lo, uint32_t hi) {
   }
 }
 
+// grid_barrier, with the lane's wait added to the profiling counters when on
+VM_DEV bool timed_barrier(Args A) {
+  if (!A->stats) return grid_barrier(A);
+  const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+  const bool ok = grid_barrier(A);
+  if (threadIdx.x == 0) {
+    __hip_atomic_fetch_add(A->stats, __builtin_amdgcn_s_memrealtime() - t0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_fetch_add(A->stats + 1, uint64_t(1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  return ok;
+}
+
 __global__ __launch_bounds__(kBlock, 1) void vm_main(VmArgs args) {
   // The VmArgs block is the kernel's only explicit argument: offset 0 of the
   // kernarg segment, read in place through the constant address space.
@@ -81,7 +93,7 @@ __global__ __launch_bounds__(kBlock, 1) void vm_main(VmArgs args) {
         continue;
       }
       // loop bodies end with a grid barrier that publishes the carries
-      if (!grid_barrier(A)) return;
+      if (!timed_barrier(A)) return;
       pub = false;
       if (w.task == ENT_FOR) {
         if (--f_phase[sp] != 0) {
@@ -113,7 +125,7 @@ __global__ __launch_bounds__(kBlock, 1) void vm_main(VmArgs args) {
     const uint32_t epc = f_pc[sp];
     const Entry en = load_entry(ents + epc);
     if (en.task == ENT_BARRIER) {
-      if (!grid_barrier(A)) return;
+      if (!timed_barrier(A)) return;
       pub = false;
       ++f_pc[sp];
       continue;
@@ -156,7 +168,20 @@ __global__ __launch_bounds__(kBlock, 1) void vm_main(VmArgs args) {
     if (en.task != ENT_NOP) {
       if (pub) __syncthreads();
       pub = true;
-      exec_tiles(A, en.task, en.tile_lo, en.tile_hi);
+      if (A->stats) {
+        const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+        exec_tiles(A, en.task, en.tile_lo, en.tile_hi);
+        __syncthreads();
+        if (threadIdx.x == 0) {
+          const uint64_t dt = __builtin_amdgcn_s_memrealtime() - t0;
+          uint64_t* st = A->stats + kStatTask + 4ull * en.task;
+          __hip_atomic_fetch_add(st, dt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          __hip_atomic_fetch_max(st + 1, dt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          __hip_atomic_fetch_add(st + 2, uint64_t(1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+      } else {
+        exec_tiles(A, en.task, en.tile_lo, en.tile_hi);
+      }
     }
     ++f_pc[sp];
   }

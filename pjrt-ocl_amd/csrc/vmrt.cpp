@@ -323,8 +323,7 @@ struct Checker {
       case TOP_RED_SEG: case TOP_SOFTMAX_SEG: case TOP_LAYERNORM_SEG: case TOP_ARGMAX_SEG:
         return std::max<uint64_t>(1, t.p[0]);
       case TOP_FLASH_ATTN: return std::max<uint64_t>(1, uint64_t(t.p[1]) * t.p[2]);
-      case TOP_GEMV:
-        return std::max<uint64_t>(1, t.p[3]) * t.p[4] * cdiv(t.p[1], uint64_t(kGemvCols));
+      case TOP_GEMV: return t.p[4] ? std::max<uint64_t>(1, t.p[3]) * cdiv(t.p[1], t.p[4]) : 0;
       default: return 0;
     }
   }
@@ -511,14 +510,13 @@ struct Checker {
         return true;
       }
       case TOP_GEMV: {
-        const uint64_t M = t.p[0], N = t.p[1], K = t.p[2], G = std::max<uint32_t>(1, t.p[3]), S = t.p[4];
+        const uint64_t M = t.p[0], N = t.p[1], K = t.p[2], G = std::max<uint32_t>(1, t.p[3]), CW = t.p[4];
         if (adt != DT_F32 && adt != DT_BF16 && adt != DT_F16) return fail(ti, "gemv operand dtype");
         if (dt != DT_F32 && dt != DT_BF16 && dt != DT_F16) return fail(ti, "gemv result dtype");
-        if (M < 1 || M > kGemvMaxM || N < 8 || N % 8 || K < 1 || S < 1 || S > K)
-          return fail(ti, "gemv shape / splits");
-        const uint64_t kspan = (K + S - 1) / S;
-        if ((((M * kspan + 3) & ~uint64_t(3)) + 8 * M * uint64_t(kGemvCols)) * 4 > uint64_t(lds_bytes))
-          return fail(ti, "gemv K slice does not fit the LDS");
+        if (M < 1 || M > kGemvMaxM || N < 8 || N % 8 || K < 1 || CW < 8 || CW > 256 || (CW & (CW - 1)))
+          return fail(ti, "gemv shape / strip width");
+        if ((((M * K + 3) & ~uint64_t(3)) + 4096 * M) * 4 > uint64_t(lds_bytes))
+          return fail(ti, "gemv x row does not fit the LDS");
         if (!has(t.a, G * M * K, adt) || !has(t.b, G * K * N, adt)) return fail(ti, "gemv operands");
         if (!has(t.dst, G * M * N, dt)) return fail(ti, "gemv result");
         if (t.p[6]) {
@@ -540,14 +538,6 @@ struct Checker {
     }
   }
 };
-
-// Scratch bytes of a TOP_GEMV task: arrival counters [G][column blocks] (256-byte
-// aligned) then the split partials [G][S][M][N] f32.  Zero for S = 1.
-static uint64_t gemv_scratch_bytes(const Task& t) {
-  if (t.p[4] <= 1) return 0;
-  const uint64_t G = std::max<uint32_t>(1, t.p[3]), ncb = (uint64_t(t.p[1]) + uint64_t(kGemvCols) - 1) / uint64_t(kGemvCols);
-  return ((G * ncb * 4 + 255) & ~uint64_t(255)) + G * t.p[4] * uint64_t(t.p[0]) * t.p[1] * 4;
-}
 
 // ---- pool ------------------------------------------------------------------------------
 struct Pool {
@@ -612,8 +602,8 @@ struct vmrt_program {
   Entry* entries = nullptr;
   LaneSpan* lanes = nullptr;
   uint32_t* ctl = nullptr;
-  uint8_t* scratch = nullptr;                 // GEMV split partials + arrival counters
-  uint64_t scratch_bytes = 0;
+  uint64_t* stats = nullptr;                  // profiling counters (PJRT_AMD_PROFILE=1)
+  size_t stats_words = 0;
   std::vector<int> input_port, output_port;   // -1 = arena copy
   std::vector<uint32_t> in_bytes, out_bytes;
   VmArgs args{};
@@ -702,9 +692,9 @@ int vmrt_device_info_get(vmrt_runtime* rt, vmrt_device_info* out) {
 static void free_program_memory(vmrt_program* p) {
   for (void* q : {static_cast<void*>(p->arena), static_cast<void*>(p->aux), static_cast<void*>(p->tasks),
                   static_cast<void*>(p->entries), static_cast<void*>(p->lanes), static_cast<void*>(p->ctl),
-                  static_cast<void*>(p->scratch)})
+                  static_cast<void*>(p->stats)})
     if (q) hipFree(q);
-  p->scratch = nullptr;
+  p->stats = nullptr;
   p->arena = nullptr;
   p->aux = nullptr;
   p->tasks = nullptr;
@@ -815,14 +805,7 @@ int vmrt_load(vmrt_runtime* rt, const void* bytes, size_t len, uint32_t ew_ts, u
       for (int k = 2; k < 8; ++k) t.p[k] = handle(k < n_in ? orig.p[k] : orig.a);
     }
     if (top == TOP_LAYERNORM_SEG && (orig.p[3] & LN_AFFINE)) t.p[4] = handle(orig.p[4]);
-    if (top == TOP_GEMV) {
-      if (orig.p[6]) t.p[7] = handle(orig.p[7]);
-      // each GEMV task gets its own scratch region (tasks of one phase run at once)
-      t.p[5] = uint32_t(lp->scratch_bytes);
-      lp->scratch_bytes += (gemv_scratch_bytes(orig) + 255) & ~uint64_t(255);
-      if (lp->scratch_bytes > 0xFFFFFFFFull)
-        return set_err(err, errlen, VMRT_RESOURCE_EXHAUSTED, "LoadedProgram: GEMV scratch exceeds 4 GiB");
-    }
+    if (top == TOP_GEMV && orig.p[6]) t.p[7] = handle(orig.p[7]);
   }
   // ---- patch aux: runtime start-scalar / index-buffer locations (runtime.cc:883-924) ----
   std::vector<int32_t> aux = P.aux;
@@ -872,8 +855,11 @@ int vmrt_load(vmrt_runtime* rt, const void* bytes, size_t len, uint32_t ew_ts, u
   if (e == hipSuccess) e = up(reinterpret_cast<void**>(&lp->lanes), P.lanes.data(), P.lanes.size() * sizeof(LaneSpan));
   if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&lp->ctl), BAR_WORDS * 4);
   if (e == hipSuccess) e = hipMemset(lp->ctl, 0, BAR_WORDS * 4);
-  if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&lp->scratch), std::max<uint64_t>(lp->scratch_bytes, 256));
-  if (e == hipSuccess) e = hipMemset(lp->scratch, 0, std::max<uint64_t>(lp->scratch_bytes, 256));
+  if (const char* prof = std::getenv("PJRT_AMD_PROFILE"); e == hipSuccess && prof && std::atoi(prof) != 0) {
+    lp->stats_words = kStatTask + 4 * tasks.size();
+    e = hipMalloc(reinterpret_cast<void**>(&lp->stats), lp->stats_words * 8);
+    if (e == hipSuccess) e = hipMemset(lp->stats, 0, lp->stats_words * 8);
+  }
   for (auto& c : P.consts) {
     if (e != hipSuccess) break;
     if (!c.second.empty()) e = hipMemcpy(lp->arena + P.buffers[c.first].off, c.second.data(), c.second.size(), hipMemcpyHostToDevice);
@@ -893,7 +879,7 @@ int vmrt_load(vmrt_runtime* rt, const void* bytes, size_t len, uint32_t ew_ts, u
   a.ew_ts = lp->ew_ts;
   a.mma_t = lp->mma_t;
   a.timeout_ticks = rt->timeout_ticks;
-  a.scratch = lp->scratch;
+  a.stats = lp->stats;
   for (int k = 0; k < kMaxPorts; ++k) a.ports[k] = lp->arena;   // unbound ports point at the arena
   *out = lp.release();
   return VMRT_OK;
@@ -959,8 +945,6 @@ static int check_status(vmrt_program* p, char* err, size_t errlen) {
   if (e != hipSuccess) return set_err(err, errlen, VMRT_INTERNAL, "status read: " + hip_msg(e));
   if (st[BAR_ERROR] == VM_OK) return VMRT_OK;
   hipMemset(p->ctl, 0, BAR_WORDS * 4);
-  // an aborted run can leave GEMV arrival counters part-way: start them from zero
-  if (p->scratch) hipMemset(p->scratch, 0, std::max<uint64_t>(p->scratch_bytes, 256));
   const char* what = st[BAR_ERROR] == VM_ERR_BARRIER_TIMEOUT ? "grid barrier timed out (lanes not co-resident, "
                                                                 "or non-uniform control across lanes)"
                      : st[BAR_ERROR] == VM_ERR_FRAME_DEPTH ? "control frame stack overflow"
@@ -997,6 +981,20 @@ int vmrt_program_status(vmrt_program* p, char* err, size_t errlen) {
   hipError_t e = hipDeviceSynchronize();
   if (e != hipSuccess) return set_err(err, errlen, VMRT_INTERNAL, "synchronize: " + hip_msg(e));
   return check_status(p, err, errlen);
+}
+
+int vmrt_program_profile(vmrt_program* p, uint64_t* out, size_t n_words, int reset, char* err, size_t errlen) {
+  if (!p) return set_err(err, errlen, VMRT_INVALID_ARGUMENT, "null program");
+  if (!p->stats) return set_err(err, errlen, VMRT_FAILED_PRECONDITION, "profiling is off (load with PJRT_AMD_PROFILE=1)");
+  if (!out || n_words < p->stats_words)
+    return set_err(err, errlen, VMRT_INVALID_ARGUMENT, fmt("profile needs %zu words", p->stats_words));
+  std::lock_guard<std::mutex> g(p->rt->mu);
+  hipSetDevice(p->rt->device);
+  hipError_t e = hipStreamSynchronize(p->rt->stream);
+  if (e == hipSuccess) e = hipMemcpy(out, p->stats, p->stats_words * 8, hipMemcpyDeviceToHost);
+  if (e == hipSuccess && reset) e = hipMemset(p->stats, 0, p->stats_words * 8);
+  if (e != hipSuccess) return set_err(err, errlen, VMRT_INTERNAL, "profile read: " + hip_msg(e));
+  return VMRT_OK;
 }
 
 int vmrt_alloc(vmrt_runtime* rt, size_t bytes, void** dptr, char* err, size_t errlen) {

@@ -132,7 +132,9 @@ def gpt_c5(c: GptConfig = C5, emit_logits: bool = False, trips: int | None = Non
     zero = g.scalar(0, "i32")
     one = g.scalar(1, "i32")
     scale = 1.0 / math.sqrt(hd)
-    cache_k = [g.fill((H, C, hd), 0.0, "bf16") for _ in range(c.layers)]
+    # K is cached transposed, [H, hd, C]: the decode scores q . K^T are then a
+    # contiguous skinny matmul, like P . V over the [H, C, hd] V cache
+    cache_k = [g.fill((H, hd, C), 0.0, "bf16") for _ in range(c.layers)]
     cache_v = [g.fill((H, C, hd), 0.0, "bf16") for _ in range(c.layers)]
     logits_all = g.fill((c.steps + 1, c.vocab), 0.0) if emit_logits else None
 
@@ -160,7 +162,7 @@ def gpt_c5(c: GptConfig = C5, emit_logits: bool = False, trips: int | None = Non
         qkv = g.dot(h, P[f"h{l}.w_qkv"], out_dtype="bf16", residual=P[f"h{l}.b_qkv"],
                     epilogue=[(V.SUB_ADD, 2, 0.0, 0.0)])
         q, k, v = (g.materialize(g.view(qkv, (H, T, hd), (hd, 3 * D, 1), s * D)) for s in range(3))
-        g.dynamic_update_slice(cache_k[l], k, [zero, zero, zero])
+        g.dynamic_update_slice(cache_k[l], g.transpose(k, (0, 2, 1)), [zero, zero, zero])
         g.dynamic_update_slice(cache_v[l], v, [zero, zero, zero])
         att = g.flash_attention(q, k, v, scale, True)                       # [H, T, hd] bf16
         att_rows = g.reshape(g.transpose_view(att, (1, 0, 2)), (T, D))    # [T, H*hd]
@@ -190,9 +192,9 @@ def gpt_c5(c: GptConfig = C5, emit_logits: bool = False, trips: int | None = Non
         qkv = g.dot(h, P[f"h{l}.w_qkv"], out_dtype="bf16", residual=P[f"h{l}.b_qkv"],
                     epilogue=[(V.SUB_ADD, 2, 0.0, 0.0)])
         q, k, v = (g.materialize(g.view(qkv, (H, 1, hd), (hd, 3 * D, 1), s * D)) for s in range(3))
-        g.dynamic_update_slice(cache_k[l], k, [zero, pos, zero])
+        g.dynamic_update_slice(cache_k[l], g.reshape(k, (H, hd, 1)), [zero, zero, pos])
         g.dynamic_update_slice(cache_v[l], v, [zero, pos, zero])
-        s = g.dot(q, g.transpose_view(cache_k[l], (0, 2, 1)), epilogue=[(V.SUB_AFFINE, 0, scale, 0.0)])
+        s = g.dot(q, cache_k[l], epilogue=[(V.SUB_AFFINE, 0, scale, 0.0)])      # [H, 1, C]
         s = g.select(masked, neg_inf, s)
         p = g.convert(g.softmax_last(s), "bf16")
         att = g.dot(p, cache_v[l], out_dtype="bf16")                           # [H, 1, hd]

@@ -79,6 +79,7 @@ SIGNATURES = {
     "vmrt_execute": (ctypes.c_int, [_VP, ctypes.POINTER(_VP), _SZ, ctypes.POINTER(_VP), _SZ, _CP, _SZ]),
     "vmrt_enqueue": (ctypes.c_int, [_VP, ctypes.POINTER(_VP), _SZ, ctypes.POINTER(_VP), _SZ, _VP, _CP, _SZ]),
     "vmrt_program_status": (ctypes.c_int, [_VP, _CP, _SZ]),
+    "vmrt_program_profile": (ctypes.c_int, [_VP, ctypes.POINTER(ctypes.c_uint64), _SZ, ctypes.c_int, _CP, _SZ]),
     "vmrt_alloc": (ctypes.c_int, [_VP, _SZ, ctypes.POINTER(_VP), _CP, _SZ]),
     "vmrt_free": (ctypes.c_int, [_VP, _VP]),
     "vmrt_h2d": (ctypes.c_int, [_VP, _VP, _VP, _SZ, _CP, _SZ]),
@@ -261,7 +262,9 @@ class Runtime:
         err = ctypes.create_string_buffer(_ERRLEN)
         _check(self._lib.vmrt_load(self._h, ctypes.cast(buf, _VP), len(blob), ew_ts, mma_t, ctypes.byref(p),
                                    err, _ERRLEN), err)
-        return LoadedProgram(self, p)
+        lp = LoadedProgram(self, p)
+        lp._blob = blob
+        return lp
 
     def compile(self, prog: V.VMProgram, **cfg_overrides) -> "LoadedProgram":
         """Schedule a tensor program for this device and load it."""
@@ -375,6 +378,19 @@ class LoadedProgram:
         """Synchronize and raise if the VM aborted (barrier time-out etc.)."""
         err = ctypes.create_string_buffer(_ERRLEN)
         _check(self.rt._lib.vmrt_program_status(self._h, err, _ERRLEN), err)
+
+    def profile(self, reset: bool = True) -> dict:
+        """Per-task device time since the last reset (the program must have been
+        loaded with PJRT_AMD_PROFILE=1): {"barrier_us", "barriers", "tasks":
+        [(task, lane_us_sum, max_entry_us, entries)]}, microseconds."""
+        n_tasks = len(V.parse(self._blob).schedule.tasks)
+        words = 4 + 4 * n_tasks
+        buf = (ctypes.c_uint64 * words)()
+        err = ctypes.create_string_buffer(_ERRLEN)
+        _check(self.rt._lib.vmrt_program_profile(self._h, buf, words, int(reset), err, _ERRLEN), err)
+        v = np.frombuffer(buf, np.uint64).astype(np.float64)
+        return {"barrier_us": v[0] / 100.0, "barriers": int(v[1]),
+                "tasks": [(i, v[4 + 4 * i] / 100.0, v[5 + 4 * i] / 100.0, int(v[6 + 4 * i])) for i in range(n_tasks)]}
 
     def __call__(self, *args):
         """Host convenience: numpy arrays in, numpy arrays out."""

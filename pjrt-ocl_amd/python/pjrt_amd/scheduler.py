@@ -58,8 +58,10 @@ class DeviceConfig:
     # Per-task MMA tile selection (extension): pick the largest tile edge that
     # still gives every lane work; False keeps every MMA at the default edge.
     mma_autotile: bool = True
-    # Matmuls of at most 8 rows as split-K TOP_GEMV tasks (extension).
+    # Matmuls of at most 8 rows as column-strip TOP_GEMV tasks (extension), and
+    # the narrowest strip width they may use.
     gemv: bool = True
+    gemv_min_strip: int = 8
 
     @classmethod
     def from_env(cls, environ=None) -> "DeviceConfig":
@@ -88,7 +90,8 @@ class DeviceConfig:
                    costs=costs,
                    fuse=env.get("PJRT_OCL_FUSE", "1") != "0",
                    mma_autotile=env.get("PJRT_AMD_MMA_AUTOTILE", "1") != "0",
-                   gemv=env.get("PJRT_AMD_GEMV", "1") != "0")
+                   gemv=env.get("PJRT_AMD_GEMV", "1") != "0",
+                   gemv_min_strip=max(8, min(256, geti("PJRT_AMD_GEMV_STRIP", 8))))
 
 
 # --- instruction -> task ------------------------------------------------------
@@ -152,35 +155,33 @@ def n_tiles(task: V.Task, cfg: DeviceConfig) -> int:
     if top == V.TOP_FLASH_ATTN:
         return max(1, task.p1 * task.p2)
     if top == V.TOP_GEMV:
-        return max(1, task.p3) * task.p4 * gemv_col_blocks(task.p1)
+        return max(1, task.p3) * -(-task.p1 // task.p4)
     raise ScheduleError(f"n_tiles: unknown tile_op {top}")
 
 
 # --- skinny matmuls (TOP_GEMV) ------------------------------------------------------
 
 GEMV_MAX_M = 8
-GEMV_COLS = 256                 # output columns per tile
-GEMV_LDS_FLOATS = 147456 // 4   # the kernel's LDS: x slice + row-phase sums
+GEMV_LDS_FLOATS = 147456 // 4   # the kernel's LDS: x rows + row-phase sums
 _EPI_INLINE = {V.SUB_AFFINE, V.SUB_GELU, V.SUB_COPY, V.SUB_ADD, V.SUB_MUL, V.SUB_SUB, V.SUB_DIV,
                V.SUB_MAX, V.SUB_MIN}
 
 
-def gemv_col_blocks(N: int) -> int:
-    return -(-N // GEMV_COLS)
-
-
-def gemv_splits(M: int, N: int, K: int, G: int, nlanes: int) -> int:
-    """K splits of a skinny matmul: enough tiles to cover the lanes, at least 8
-    rows per split, and the x slice [M][K/S] plus the [8][M][256] row-phase sums
-    inside the kernel's LDS."""
-    s = max(1, min(-(-nlanes // (G * gemv_col_blocks(N))), max(1, K // 8)))
-    while s < K and (M * -(-K // s) + 3) // 4 * 4 + 8 * M * GEMV_COLS > GEMV_LDS_FLOATS:
-        s += 1
-    return s
+def gemv_strip(N: int, G: int, nlanes: int, min_strip: int = 8) -> int:
+    """Columns per TOP_GEMV tile: the narrowest strip (min_strip, ... 256, powers
+    of two) that keeps the tile count within two per lane."""
+    cw = 8
+    while cw < min_strip:
+        cw *= 2
+    while cw < 256 and G * -(-N // cw) > 2 * nlanes:
+        cw *= 2
+    return cw
 
 
 def gemv_eligible(M, N, K, G, aview, bview, epi, adt, dt, prog) -> bool:
     if not (1 <= M <= GEMV_MAX_M and N % 8 == 0 and N >= 8 and K >= 1) or aview or bview:
+        return False
+    if (M * K + 3) // 4 * 4 + 4096 * M > GEMV_LDS_FLOATS:
         return False
     if adt not in (V.DT_BF16, V.DT_F16, V.DT_F32) or dt not in (V.DT_F32, V.DT_BF16, V.DT_F16):
         return False
@@ -281,7 +282,7 @@ def instr_to_task(ins: V.Instr, prog: V.VMProgram, cfg: DeviceConfig) -> V.Task:
             t = V.Task(V.TOP_RED_SEG, ins.dst, ins.a, ins.b, M, K, 0, 1)
         elif cfg.gemv and gemv_eligible(M, N, K, G, aview, bview, epi, adt, dt, prog):
             t = V.Task(V.TOP_GEMV, ins.dst, ins.a, ins.b, M, N, K, G,
-                       gemv_splits(M, N, K, G, cfg.nlanes), 0, epi,
+                       gemv_strip(N, G, cfg.nlanes, cfg.gemv_min_strip), 0, epi,
                        epi_res if epi else 0)
         else:
             code = V.MMA_TILE_CODES.get(ins.mma_tile, 0)

@@ -35,9 +35,9 @@ which does not use them is byte-for-byte a reference program):
 * tensor opcode ``OP_ARGMAX_SEG`` (67) / tile op ``TOP_ARGMAX_SEG`` (19):
   the variadic (value, index) reduce that ``jnp.argmax`` lowers to, which the
   reference rejects (python/pjrt_ocl/ops/reduce.py:165-168);
-* tile op ``TOP_GEMV`` (20): the scheduler's split-K form of an ``OP_DOT`` with
-  at most 8 rows (decode-time matmuls); p0 M, p1 N, p2 K, p3 G, p4 splits, p5
-  scratch offset (the loader's), p6 epilogue + 1, p7 residual.
+* tile op ``TOP_GEMV`` (20): the scheduler's column-strip form of an ``OP_DOT``
+  with at most 8 rows (decode-time matmuls); p0 M, p1 N, p2 K, p3 G, p4 strip
+  width, p6 epilogue + 1, p7 residual.
 """
 from __future__ import annotations
 

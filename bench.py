@@ -63,11 +63,17 @@ def c2_inputs():
     return x, gamma, beta
 
 
-def time_program(rt, lp, dev_in, dev_out, steps, warmup):
-    """Warm up, then time exactly `steps` back-to-back executions: wall clock
-    around the whole region and HIP events on the launch stream."""
-    for _ in range(warmup):
+def time_program(rt, lp, dev_in, dev_out, steps, warmup, min_warm_s=0.3):
+    """Warm up (at least `warmup` executions and `min_warm_s` seconds, so the GPU
+    clocks have ramped up), then time exactly `steps` back-to-back executions:
+    wall clock around the whole region and HIP events on the launch stream."""
+    t_warm = time.perf_counter()
+    n = 0
+    while n < warmup or time.perf_counter() - t_warm < min_warm_s:
         lp.enqueue(dev_in, dev_out)
+        n += 1
+        if n % 8 == 0:
+            rt.synchronize()
     rt.synchronize()
     lp.status()
     e0, e1 = rt.event(), rt.event()

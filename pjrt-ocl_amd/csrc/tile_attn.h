@@ -4,16 +4,30 @@
 // p1 = H, p2 = T, p3 = aux descriptor {H, T, C, hd, scale bits, causal, qv, kv, vv}.
 // Tiles are query rows (H*T of them); causal masks key c > m + (C - T).
 //
-// Matrix-core path (bf16/f16, hd = 64 or 128, K read through the usual [H,hd,C]
-// transpose view of a [H,C,hd] buffer): a lane takes 128 query rows, 32 per
-// wave, and streams K/V in 32-key blocks staged through LDS.  Each wave computes
-//   S^T (32 keys x 32 queries) = K_blk (32 x hd) . Q^T (hd x 32)
+// Matrix-core path (bf16/f16, hd = 64 or 128, scale > 0, K read through the usual
+// [H,hd,C] transpose view of a [H,C,hd] buffer): a lane takes 256 query rows, 64
+// per wave as two 32-row sub-tiles, and streams K/V in 64-key blocks staged
+// through LDS (double-buffered, one barrier per block).  Per sub-tile each wave
+// computes
+//   S^T (keys x 32 queries) = K_blk (keys x hd) . Q^T (hd x 32)
 // so both MFMA operands are contiguous along hd, and the S^T accumulators are
 // already the B operand of
-//   O^T (hd x 32 queries) += V_blk^T (hd x 32 keys) . P^T (32 keys x 32 queries).
-// Key rows of a block are permuted (kperm) so that the 8 keys a lane holds per
-// 16-key MFMA step are consecutive.  Causal query blocks are visited in zig-zag
-// order (block b, then nb-1-b) so contiguous tile chunks cost the same.
+//   O^T (hd x 32 queries) += V_blk^T (hd x keys) . P^T (keys x 32 queries).
+// V is stored transposed in LDS (rows = hd, columns = keys; transposed in
+// registers with byte permutes on the way in) so an A fragment of V^T is one
+// 16-byte LDS read.  Key rows of a 32-key half are read permuted (kperm) so that
+// the 8 keys a lane holds per 16-key MFMA step are consecutive.  K and V
+// fragments are read once per wave and used by both sub-tiles.
+//
+// Softmax in base 2 against a per-row reference maximum fixed at the row's first
+// block with a visible key (the same algebra as the online update, with the
+// rescale factor folded into the reference): O and l accumulate exp2(scale' s -
+// m_ref), so no accumulator is ever rescaled inside the key loop.  Should a later
+// block's probabilities exceed 2^24 (2^14 for f16) the 256-row block is redone
+// with exact row maxima (a max-only pass, then probabilities <= 1).  The row sum
+// is kept per lane and the two lanes holding a row are added at the end.  Causal
+// query blocks are visited in zig-zag order (block b, then nb-1-b) so contiguous
+// tile chunks cost the same.
 #pragma once
 #include "tile_ew.h"
 #include "tile_mma.h"
@@ -22,14 +36,19 @@
 
 namespace vm {
 
-constexpr int kAttnKeys = 32;            // keys per streamed block
-constexpr int kAttnRows = 128;           // query rows per lane step (4 waves x 32)
-constexpr int kAttnLdK = 128 + 8;        // K row stride (elements): 16-byte aligned rows
-constexpr int kAttnLdV = 128 + 4;        // V row stride: odd multiple of 8 bytes
-constexpr int kAttnBuf = kAttnKeys * (kAttnLdK + kAttnLdV);     // elements per buffer
-constexpr int kAttnLdsBytes = 2 * kAttnBuf * 2;
+constexpr int kAttnKeys = 64;            // keys per streamed block
+constexpr int kAttnRows = 256;           // query rows per lane step (4 waves x 64)
+constexpr int kAttnLdV = kAttnKeys + 8;  // V^T row stride (elements): 16-byte aligned rows
+template <int HD>
+struct AttnLds {
+  static constexpr int kLdK = HD + 8;                         // K row stride (elements)
+  static constexpr int kKBuf = kAttnKeys * kLdK;
+  static constexpr int kBuf = kKBuf + HD * kAttnLdV;          // elements per stage
+  static constexpr int kBytes = 2 * kBuf * 2;
+};
+constexpr int kAttnLdsBytes = AttnLds<128>::kBytes;
 
-// Row r of an S^T accumulator block holds key kperm(r) of the 32-key block:
+// Row r of an S^T accumulator block holds key kperm(r) of the 32-key half:
 // r = 8j + 4g + i (j = v/4 register group, g = lane/32, i = v%4) -> key
 // 16*(j/2) + 8g + 4*(j%2) + i, so lane group g owns keys 16s + 8g + 0..7 in
 // MFMA step s (registers 8s..8s+7).
@@ -61,6 +80,26 @@ VM_DEV AttnDesc attn_desc(Args A, const VM_K Task& t) {
   return D;
 }
 
+// c + lo(x) + hi(x) for a packed bf16 / f16 pair (v_dot2_f32_{bf16,f16} with 1, 1)
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+template <bool BF16>
+VM_DEV float dot2_ones(uint32_t x, float c) {
+  if constexpr (BF16)
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, x), __builtin_bit_cast(bf16x2_t, 0x3F803F80u),
+                                           c, false);
+  else
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, x), __builtin_bit_cast(f16x2_t, 0x3C003C00u), c, false);
+}
+
+template <bool BF16>
+VM_DEV uint32_t pack_h2(float a, float b) {
+  if constexpr (BF16) return pack_bf16x2(a, b);
+  else return uint32_t(f32_to_f16(a)) | (uint32_t(f32_to_f16(b)) << 16);
+}
+
+// One 256-row query block of head h against keys [0, kend).  Real rows row0 + i;
+// the caller's span owns virtual rows [vlo, vhi) of the virtual block starting at
+// vrow0 (the zig-zag order maps virtual block -> real block).
 template <int HD, bool BF16>
 VM_TILE void attn_block_mfma(Args A, uint32_t ti, uint32_t h, uint32_t row0, uint32_t vrow0, uint32_t vlo,
                              uint32_t vhi) {
@@ -72,150 +111,289 @@ VM_TILE void attn_block_mfma(Args A, uint32_t ti, uint32_t h, uint32_t row0, uin
   vrow0 = uni(vrow0);
   vlo = uni(vlo);
   vhi = uni(vhi);
+  typedef AttnLds<HD> L;
   const uint32_t T = P.T, C = P.C, dt = (t.tile_op >> 8) & 0xFF;
   uint16_t* lds = reinterpret_cast<uint16_t*>(vm_smem);
   constexpr int KS = HD / 16;            // MFMA steps over hd for S
   constexpr int DB = HD / 32;            // 32-row d blocks of O^T
-  const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6, g = lane >> 5;
-  const uint32_t qloc = wave * 32 + (lane & 31);           // 0..127 within the block
-  const uint32_t q = row0 + qloc;                           // real query row
-  const bool qvalid = q < T && vrow0 + qloc >= vlo && vrow0 + qloc < vhi;
+  const uint32_t lane = threadIdx.x & 63, wave = uni(threadIdx.x >> 6), g = lane >> 5;
+  const uint32_t qw0 = row0 + 64 * wave;                    // this wave's first row
   const VM_G uint16_t* Q = gcast<uint16_t>(resolve(A, t.a)) + uint64_t(h) * T * HD;
   const VM_G uint16_t* K = gcast<uint16_t>(resolve(A, t.b)) + uint64_t(h) * C * HD;
   const VM_G uint16_t* V = gcast<uint16_t>(resolve(A, t.p[0])) + uint64_t(h) * C * HD;
   gbyte* Ob = resolve(A, t.dst);
 
-  // Q^T fragments (B operand): column = query, 8 consecutive hd values.
-  u16x8 qf[KS];
-  {
-    const uint32_t qr = q < T ? q : T - 1;
+  // Q^T fragments (B operand) of both sub-tiles: column = query, 8 consecutive hd
+  // values; rows past T re-read row T - 1 (results not stored)
+  u16x8 qf[2][KS];
 #pragma unroll
-    for (int s = 0; s < KS; ++s) qf[s] = *(const VM_G u16x8*)(Q + uint64_t(qr) * HD + s * 16 + 8 * g);
+  for (int u = 0; u < 2; ++u) {
+    const uint32_t qr = min(qw0 + 32 * u + (lane & 31), T - 1);
+#pragma unroll
+    for (int s = 0; s < KS; ++s) qf[u][s] = *(const VM_G u16x8*)(Q + uint64_t(qr) * HD + s * 16 + 8 * g);
   }
-  f32x16 o[DB];
+  f32x16 o[2][DB];
 #pragma unroll
-  for (int i = 0; i < DB; ++i) o[i] = f32x16{};
-  float m_run = -INFINITY, l_run = 0.0f;
+  for (int u = 0; u < 2; ++u)
+#pragma unroll
+    for (int i = 0; i < DB; ++i) o[u][i] = f32x16{};
+  float m_run[2] = {-INFINITY, -INFINITY}, l_part[2] = {0.0f, 0.0f};
   const float sl2 = P.scale * 1.4426950408889634f;
 
   // keys this block needs: up to the last query's causal limit
+  const int32_t shift = int32_t(C) - int32_t(T);
   const uint32_t qmax = min(row0 + kAttnRows, T) - 1;
   uint32_t kend = C;
-  if (P.causal) kend = min(C, uint32_t(max(0, int(qmax) + int(C) - int(T) + 1)));
+  if (P.causal) kend = min(C, uint32_t(max(0, int32_t(qmax) + shift + 1)));
   const uint32_t nblk = (kend + kAttnKeys - 1) / kAttnKeys;
+  // this wave: rows [qw0, qw0 + 64) (those below T); last visible key of its first
+  // and last row
+  const bool wave_rows = qw0 < T;
+  const int32_t wq_lo = int32_t(qw0) + shift;
+  const int32_t wq_hi = int32_t(min(qw0 + 63, T - 1)) + shift;
 
-  // staging: K and V blocks are 32 x HD = 4*HD chunks of 8 elements each
-  constexpr int kChunks = kAttnKeys * HD / 8 / kBlock;      // per tensor per thread
-  v4u rk[kChunks], rv[kChunks];
+  // Staging.  K: 64 keys x HD/8 chunks of 8 elements, HD/32 per thread, stored as
+  // rows.  V: groups of KG consecutive keys x one 8-element chunk, one group per
+  // thread, transposed into V^T rows.
+  constexpr int NK = kAttnKeys * HD / 8 / kBlock;
+  constexpr int KG = HD == 128 ? 4 : 2;
+  constexpr int NG = kAttnKeys / KG;                         // key groups per block
+  v4u rk[NK], rv[KG];
+  const uint32_t vg = threadIdx.x % NG, vdc = threadIdx.x / NG;
   auto gload = [&](uint32_t kb) {
 #pragma unroll
-    for (int j = 0; j < kChunks; ++j) {
+    for (int j = 0; j < NK; ++j) {
       const uint32_t c = threadIdx.x + j * kBlock;
-      const uint32_t r = c / (HD / 8), cc = (c % (HD / 8)) * 8;
-      const uint32_t key = kb * kAttnKeys + r;
-      if (key < C) {
-        rk[j] = *(const VM_G v4u*)(K + uint64_t(key) * HD + cc);
-        rv[j] = *(const VM_G v4u*)(V + uint64_t(key) * HD + cc);
-      } else {
-        rk[j] = v4u_make(0, 0, 0, 0);
-        rv[j] = v4u_make(0, 0, 0, 0);
-      }
+      const uint32_t key = min(kb * kAttnKeys + c / (HD / 8), C - 1);
+      rk[j] = *(const VM_G v4u*)(K + uint64_t(key) * HD + (c % (HD / 8)) * 8);
+    }
+#pragma unroll
+    for (int i = 0; i < KG; ++i) {
+      const uint32_t key = min(kb * kAttnKeys + vg * KG + i, C - 1);
+      rv[i] = *(const VM_G v4u*)(V + uint64_t(key) * HD + vdc * 8);
     }
   };
-  auto lstore = [&](uint16_t* buf) {
+  auto lstore = [&](uint16_t* buf, uint32_t kb) {
     uint16_t* lk = buf;
-    uint16_t* lv = buf + kAttnKeys * kAttnLdK;
+    uint16_t* lv = buf + L::kKBuf;
 #pragma unroll
-    for (int j = 0; j < kChunks; ++j) {
+    for (int j = 0; j < NK; ++j) {
       const uint32_t c = threadIdx.x + j * kBlock;
-      const uint32_t r = c / (HD / 8), cc = (c % (HD / 8)) * 8;
-      *reinterpret_cast<v4u*>(lk + r * kAttnLdK + cc) = rk[j];
-      v2u* pv = reinterpret_cast<v2u*>(lv + r * kAttnLdV + cc);
-      pv[0] = v2u_make(rv[j].x, rv[j].y);
-      pv[1] = v2u_make(rv[j].z, rv[j].w);
+      *reinterpret_cast<v4u*>(lk + (c / (HD / 8)) * L::kLdK + (c % (HD / 8)) * 8) = rk[j];
+    }
+    // keys past C hold a copy of key C - 1: zero them so 0-weight rows add 0
+    if (kb * kAttnKeys + kAttnKeys > C) {
+#pragma unroll
+      for (int i = 0; i < KG; ++i)
+        if (kb * kAttnKeys + vg * KG + i >= C) rv[i] = v4u_make(0, 0, 0, 0);
+    }
+    uint32_t x[KG][4];
+#pragma unroll
+    for (int i = 0; i < KG; ++i) {
+      x[i][0] = rv[i].x;
+      x[i][1] = rv[i].y;
+      x[i][2] = rv[i].z;
+      x[i][3] = rv[i].w;
+    }
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      uint16_t* r0 = lv + (vdc * 8 + 2 * p) * kAttnLdV + vg * KG;
+      uint16_t* r1 = r0 + kAttnLdV;
+      if constexpr (KG == 4) {
+        *reinterpret_cast<v2u*>(r0) = v2u_make(__builtin_amdgcn_perm(x[1][p], x[0][p], 0x05040100u),
+                                               __builtin_amdgcn_perm(x[3][p], x[2][p], 0x05040100u));
+        *reinterpret_cast<v2u*>(r1) = v2u_make(__builtin_amdgcn_perm(x[1][p], x[0][p], 0x07060302u),
+                                               __builtin_amdgcn_perm(x[3][p], x[2][p], 0x07060302u));
+      } else {
+        *reinterpret_cast<uint32_t*>(r0) = __builtin_amdgcn_perm(x[1][p], x[0][p], 0x05040100u);
+        *reinterpret_cast<uint32_t*>(r1) = __builtin_amdgcn_perm(x[1][p], x[0][p], 0x07060302u);
+      }
     }
   };
 
-  __syncthreads();                      // LDS free from the previous user
-  if (nblk) {
-    gload(0);
-    lstore(lds);
-  }
-  __syncthreads();
-  const int32_t qlim = int32_t(q) + int32_t(C) - int32_t(T);     // last visible key
   const uint32_t krow = kperm(lane & 31);
-  for (uint32_t kb = 0; kb < nblk; ++kb) {
-    const uint16_t* buf = lds + (kb & 1) * kAttnBuf;
-    const uint16_t* lk = buf;
-    const uint16_t* lv = buf + kAttnKeys * kAttnLdK;
-    if (kb + 1 < nblk) gload(kb + 1);
-    // S^T = K_blk . Q^T
-    f32x16 s = f32x16{};
+  const int32_t qlim0 = int32_t(qw0 + (lane & 31)) + shift;   // last visible key, sub-tile 0
+  // probabilities of a pass are exp2(scale' s - m_ref) with m_ref fixed per row; a
+  // row sum partial above this bound flags the block for the exact pass (P must
+  // stay finite in bf16 / f16)
+  const float bound = BF16 ? 16777216.0f : 16384.0f;
+  bool redo = false;
+
+  // masked entries (keys past the row's causal limit or past C) -> -inf
+  auto mask_s = [&](f32x16 (&s)[2], int u, uint32_t key0) {
+    const int32_t lim = (P.causal ? min(qlim0 + 32 * u, int32_t(C) - 1) : int32_t(C) - 1) - int32_t(key0);
 #pragma unroll
-    for (int st = 0; st < KS; ++st) {
-      const u16x8 kf = *reinterpret_cast<const u16x8*>(lk + krow * kAttnLdK + st * 16 + 8 * g);
-      s = mfma16<BF16>(kf, qf[st], s);
-    }
-    // scale, mask, online softmax (each query lives in lanes l and l^32)
-    const uint32_t key0 = kb * kAttnKeys;
-    float p[16];
+    for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int32_t kr = 32 * kh + 16 * (v >> 3) + 8 * int32_t(g) + (v & 7);
+        if (kr > lim) s[kh][v] = -INFINITY;
+      }
+  };
+  // scaled row maximum of a block, the same in both lanes of a row
+  auto row_max = [&](const f32x16 (&s)[2]) -> float {
     float mx = -INFINITY;
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      const uint32_t r = 8 * (v >> 2) + 4 * g + (v & 3);
-      const int32_t key = int32_t(key0 + kperm(r));
-      float x = s[v] * sl2;
-      if (key >= int32_t(C) || (P.causal && key > qlim)) x = -INFINITY;
-      p[v] = x;
-      mx = fmaxf(mx, x);
+    for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s[kh][v]);
+    return fmaxf(mx, xor32(mx)) * sl2;
+  };
+  // P^T fragments (bf16/f16) and the row-sum partial of sub-tile u.  With MAXC (a
+  // sweep's first block and the masked blocks) a row whose reference is still
+  // unset (no visible key so far, so its O and l are 0) takes this block's
+  // maximum; every other block of an unmasked run sees keys for all rows after
+  // the first, so its rows all have a reference.
+  auto probs = [&](auto maxc, const f32x16 (&s)[2], int u, u16x8 (&pf)[4]) {
+    if constexpr (decltype(maxc)::value) {
+      const float mx = row_max(s);
+      m_run[u] = m_run[u] == -INFINITY ? mx : m_run[u];
     }
-    mx = fmaxf(mx, xor32(mx));
-    const float m_new = fmaxf(m_run, mx);
-    const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-    const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+    const float mu = m_run[u] == -INFINITY ? 0.0f : m_run[u];
     float rs = 0.0f;
 #pragma unroll
-    for (int v = 0; v < 16; ++v) {
-      p[v] = __builtin_amdgcn_exp2f(p[v] - m_use);
-      rs += p[v];
+    for (int ks = 0; ks < 4; ++ks) {
+      float e[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) e[i] = __builtin_amdgcn_exp2f(fmaf(s[ks >> 1][8 * (ks & 1) + i], sl2, -mu));
+      v4u w = v4u_make(pack_h2<BF16>(e[0], e[1]), pack_h2<BF16>(e[2], e[3]), pack_h2<BF16>(e[4], e[5]),
+                       pack_h2<BF16>(e[6], e[7]));
+      pf[ks] = __builtin_bit_cast(u16x8, w);
+      // the row sum adds the rounded probabilities (the ones the MFMA multiplies),
+      // two per dot instruction
+      rs = dot2_ones<BF16>(w.x, rs);
+      rs = dot2_ones<BF16>(w.y, rs);
+      rs = dot2_ones<BF16>(w.z, rs);
+      rs = dot2_ones<BF16>(w.w, rs);
     }
-    rs += xor32(rs);
-    l_run = l_run * alpha + rs;
-    m_run = m_new;
+    redo = redo || !(rs <= bound);      // also catches inf (NaN rows propagate as in the reference)
+    l_part[u] += rs;
+  };
+  auto s_tiles = [&](const uint16_t* lk, f32x16 (&s0)[2], f32x16 (&s1)[2]) {
+    // the two 32-key halves are independent accumulation chains: alternate them
+    // so consecutive MFMAs never wait on each other's result
+    u16x8 kf[2][KS];
 #pragma unroll
-    for (int i = 0; i < DB; ++i) o[i] *= alpha;
-    // P^T fragments: registers 8s..8s+7 = keys 16s + 8g + 0..7
-    u16x8 pf[2];
+    for (int kh = 0; kh < 2; ++kh)
 #pragma unroll
-    for (int st = 0; st < 2; ++st)
+      for (int st = 0; st < KS; ++st)
+        kf[kh][st] = *reinterpret_cast<const u16x8*>(lk + (kh * 32 + krow) * L::kLdK + st * 16 + 8 * g);
+    s0[0] = s0[1] = s1[0] = s1[1] = f32x16{};
 #pragma unroll
-      for (int e = 0; e < 8; ++e) pf[st][e] = uint16_t(BF16 ? f32_to_bf16(p[8 * st + e]) : f32_to_f16(p[8 * st + e]));
-    // O^T += V^T . P^T
+    for (int st = 0; st < KS; ++st)
 #pragma unroll
-    for (int db = 0; db < DB; ++db) {
-      const uint32_t d = db * 32 + (lane & 31);
+      for (int kh = 0; kh < 2; ++kh) s0[kh] = mfma16<BF16>(kf[kh][st], qf[0][st], s0[kh]);
 #pragma unroll
-      for (int st = 0; st < 2; ++st) {
-        u16x8 vf;
-        const uint32_t kr = 16 * st + 8 * g;
+    for (int st = 0; st < KS; ++st)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) vf[e] = lv[(kr + e) * kAttnLdV + d];
-        o[db] = mfma16<BF16>(vf, pf[st], o[db]);
-      }
+      for (int kh = 0; kh < 2; ++kh) s1[kh] = mfma16<BF16>(kf[kh][st], qf[1][st], s1[kh]);
+  };
+  // One 64-key block: S^T of both sub-tiles (K fragments read once, used twice),
+  // sub-tile 0's softmax while sub-tile 1's S^T is on the matrix cores, then
+  // P^T . V of sub-tile 0 while sub-tile 1's softmax runs (V^T fragments read
+  // once, used twice).
+  auto body = [&](auto maskc, auto maxc, const uint16_t* lk, const uint16_t* lv, uint32_t key0) {
+    f32x16 s0[2], s1[2];
+    s_tiles(lk, s0, s1);
+    u16x8 p0[4], p1[4];
+    if constexpr (decltype(maskc)::value) mask_s(s0, 0, key0);
+    probs(maxc, s0, 0, p0);
+    if constexpr (decltype(maskc)::value) mask_s(s1, 1, key0);
+    u16x8 vf[DB][4];
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks)
+        vf[db][ks] = *reinterpret_cast<const u16x8*>(lv + (db * 32 + (lane & 31)) * kAttnLdV + ks * 16 + 8 * g);
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int db = 0; db < DB; ++db) o[0][db] = mfma16<BF16>(vf[db][ks], p0[ks], o[0][db]);
+    probs(maxc, s1, 1, p1);
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int db = 0; db < DB; ++db) o[1][db] = mfma16<BF16>(vf[db][ks], p1[ks], o[1][db]);
+  };
+  // Exact pass 1: the true scaled row maxima over all visible keys.
+  auto max_body = [&](auto maskc, auto, const uint16_t* lk, const uint16_t* lv, uint32_t key0) {
+    f32x16 s0[2], s1[2];
+    s_tiles(lk, s0, s1);
+    if constexpr (decltype(maskc)::value) {
+      mask_s(s0, 0, key0);
+      mask_s(s1, 1, key0);
     }
-    if (kb + 1 < nblk) lstore(lds + ((kb + 1) & 1) * kAttnBuf);
+    m_run[0] = fmaxf(m_run[0], row_max(s0));
+    m_run[1] = fmaxf(m_run[1], row_max(s1));
+  };
+
+  // One sweep over the key blocks: per block, prefetch the next into registers,
+  // compute on this one, store the next into the other LDS stage.  Blocks wholly
+  // below this wave's diagonal (and inside the keys) run unmasked; the rest are
+  // masked, and those past the wave's last row's causal limit are skipped.  The
+  // two kinds run in two loops (not one loop with a branch) so the body is laid
+  // out once per loop.
+  uint32_t nfull = wave_rows ? min(nblk, C / kAttnKeys) : 0u;
+  if (P.causal) nfull = min(nfull, wq_lo >= kAttnKeys - 1 ? uint32_t(wq_lo - (kAttnKeys - 1)) / kAttnKeys + 1 : 0u);
+  auto sweep = [&](auto fn) {
+    __syncthreads();                    // LDS free from the previous user
+    if (nblk) {
+      gload(0);
+      lstore(lds, 0);
+    }
+    // every global load so far (the Q fragments too) has landed: said explicitly
+    // so the compiler's wait counting does not carry the Q loads into the loop
+    // (where their waits would stall on the next block's K/V prefetch)
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     __syncthreads();
+    auto step = [&](auto maskc, auto maxc, uint32_t kb) {
+      const uint16_t* buf = lds + (kb & 1) * L::kBuf;
+      if (kb + 1 < nblk) gload(kb + 1);
+      const uint32_t key0 = kb * kAttnKeys;
+      if constexpr (decltype(maskc)::value) {
+        if (wave_rows && (!P.causal || int32_t(key0) <= wq_hi)) fn(maskc, maxc, buf, buf + L::kKBuf, key0);
+      } else {
+        fn(maskc, maxc, buf, buf + L::kKBuf, key0);
+      }
+      if (kb + 1 < nblk) lstore(lds + ((kb + 1) & 1) * L::kBuf, kb + 1);
+      __syncthreads();
+    };
+    uint32_t kb = 0;
+    if (nfull) step(std::false_type{}, std::true_type{}, kb++);
+    for (; kb < nfull; ++kb) step(std::false_type{}, std::false_type{}, kb);
+    for (; kb < nblk; ++kb) step(std::true_type{}, std::true_type{}, kb);
+  };
+  sweep(body);
+  if (__syncthreads_or(redo)) {
+    // some row's scores rose too far above its first block's maximum: redo the
+    // block with exact maxima (pass 1), then probabilities <= 1 (pass 2)
+    m_run[0] = m_run[1] = -INFINITY;
+    sweep(max_body);
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      l_part[u] = 0.0f;
+#pragma unroll
+      for (int i = 0; i < DB; ++i) o[u][i] = f32x16{};
+    }
+    sweep(body);
   }
-  if (qvalid) {
-    const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
-    const uint64_t obase = (uint64_t(h) * T + q) * HD;
 #pragma unroll
-    for (int db = 0; db < DB; ++db) {
+  for (int u = 0; u < 2; ++u) {
+    const uint32_t ql = 64 * wave + 32 * u + (lane & 31);   // 0..255 within the block
+    const uint32_t q = row0 + ql;
+    const float l = l_part[u] + xor32(l_part[u]);
+    if (q < T && vrow0 + ql >= vlo && vrow0 + ql < vhi) {
+      const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+      const uint64_t obase = (uint64_t(h) * T + q) * HD;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const uint32_t d = db * 32 + 8 * j + 4 * g;
-        st4(Ob, dt, obase + d,
-            v4f_make(o[db][4 * j] * inv, o[db][4 * j + 1] * inv, o[db][4 * j + 2] * inv, o[db][4 * j + 3] * inv));
+      for (int db = 0; db < DB; ++db) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t d = db * 32 + 8 * j + 4 * g;
+          st4(Ob, dt, obase + d,
+              v4f_make(o[u][db][4 * j] * inv, o[u][db][4 * j + 1] * inv, o[u][db][4 * j + 2] * inv,
+                       o[u][db][4 * j + 3] * inv));
+        }
       }
     }
   }
@@ -301,25 +479,28 @@ VM_TILE void flash_attn_tiles(Args A, uint32_t ti, uint32_t lo, uint32_t hi) {
   const AttnDesc P = attn_desc(A, t);
   const uint32_t adt = (t.tile_op >> 16) & 0xFF, dt = (t.tile_op >> 8) & 0xFF;
   const bool fast = (adt == DT_BF16 || adt == DT_F16) && (P.hd == 64 || P.hd == 128) && !P.qv && !P.vv &&
-                    is_kt_view(aux_of(A), P.kv, P.H, P.C, P.hd) && (P.T % kAttnRows) == 0 &&
+                    is_kt_view(aux_of(A), P.kv, P.H, P.C, P.hd) && P.scale > 0.0f &&
                     (dt == DT_F32 || dt == DT_BF16 || dt == DT_F16);
   if (!fast) return attn_rows_generic(A, ti, lo, hi);
   const uint32_t T = P.T;
   hi = min(hi, P.H * T);
-  const uint32_t nb = T / kAttnRows;
-  // virtual 128-row blocks intersecting [lo, hi)
-  for (uint32_t vb0 = (lo / kAttnRows) * kAttnRows; vb0 < hi; vb0 += kAttnRows) {
-    const uint32_t h = vb0 / T, vb = (vb0 % T) / kAttnRows;
-    const uint32_t rb = P.causal ? ((vb & 1) ? nb - 1 - (vb >> 1) : (vb >> 1)) : vb;
-    const uint32_t row0 = rb * kAttnRows, vrow0 = vb0 % T;
-    const uint32_t vlo = (lo > vb0 ? lo - vb0 : 0u) + vrow0;      // valid virtual rows
-    const uint32_t vhi = min(hi - vb0, uint32_t(kAttnRows)) + vrow0;
-    if (adt == DT_BF16) {
-      if (P.hd == 128) attn_block_mfma<128, true>(A, ti, h, row0, vrow0, vlo, vhi);
-      else attn_block_mfma<64, true>(A, ti, h, row0, vrow0, vlo, vhi);
-    } else {
-      if (P.hd == 128) attn_block_mfma<128, false>(A, ti, h, row0, vrow0, vlo, vhi);
-      else attn_block_mfma<64, false>(A, ti, h, row0, vrow0, vlo, vhi);
+  const uint32_t nb = (T + kAttnRows - 1) / kAttnRows;
+  // zig-zag only when every block is whole (it maps virtual onto real blocks)
+  const bool zig = P.causal && T % kAttnRows == 0;
+  // per head, the virtual 256-row blocks intersecting [lo, hi)
+  for (uint32_t h = lo / T; h * T < hi; ++h) {
+    const uint32_t a = max(lo, h * T) - h * T, b = min(hi - h * T, T);     // virtual rows [a, b)
+    for (uint32_t vb = a / kAttnRows; vb * kAttnRows < b; ++vb) {
+      const uint32_t rb = zig ? ((vb & 1) ? nb - 1 - (vb >> 1) : (vb >> 1)) : vb;
+      const uint32_t vrow0 = vb * kAttnRows;
+      const uint32_t vlo = max(a, vrow0), vhi = min(b, vrow0 + kAttnRows);
+      if (adt == DT_BF16) {
+        if (P.hd == 128) attn_block_mfma<128, true>(A, ti, h, rb * kAttnRows, vrow0, vlo, vhi);
+        else attn_block_mfma<64, true>(A, ti, h, rb * kAttnRows, vrow0, vlo, vhi);
+      } else {
+        if (P.hd == 128) attn_block_mfma<128, false>(A, ti, h, rb * kAttnRows, vrow0, vlo, vhi);
+        else attn_block_mfma<64, false>(A, ti, h, rb * kAttnRows, vrow0, vlo, vhi);
+      }
     }
   }
 }

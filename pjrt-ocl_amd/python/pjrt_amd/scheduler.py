@@ -453,35 +453,54 @@ def _tile_quantum(task: V.Task, cfg: DeviceConfig, prog: V.VMProgram) -> int:
     """Preferred chunk granularity in tiles (chunk boundaries on multiples of
     it keep the kernel's multi-row blocks whole)."""
     if task.tile_op == V.TOP_FLASH_ATTN:
-        return 64
+        # the matrix-core kernel works on 256-row blocks of one head
+        T = task.p2
+        if T % 256 == 0:
+            return 256
+        return T if T < 256 else 64
     return 1
 
 
+def xcd_lane_order(n_lanes: int, n_xcd: int = 8) -> list:
+    """Lanes grouped by XCD: workgroup (lane) i runs on XCD i % n_xcd, so this
+    order lists XCD 0's lanes first, then XCD 1's, ...  Consecutive chunks
+    placed in this order share an XCD and its L2."""
+    if n_lanes % n_xcd:
+        return list(range(n_lanes))
+    return [x + n_xcd * j for x in range(n_xcd) for j in range(n_lanes // n_xcd)]
+
+
 def pack_units(units, n_lanes: int):
-    """units: [(task_ids, tiles, cost, quantum)] -> [(lane, Entry)].
+    """units: [(task_ids, tiles, cost, quantum[, xcd_grouped])] -> [(lane, Entry)].
 
     Each unit is cut into k = min(tiles/quantum, ceil(n_lanes * cost share))
     contiguous chunks, and the chunks are placed longest-first on the
-    least-loaded lane; a unit's whole chain runs over each of its chunks."""
+    least-loaded lane; a unit's whole chain runs over each of its chunks.  Ties
+    between equally loaded lanes go to the lowest lane, or, for an xcd_grouped
+    unit (neighbouring chunks read the same operands), to the first lane in
+    XCD-grouped order, so neighbouring chunks land on one XCD."""
     out = []
     if not units:
         return out
     total = sum(u[2] for u in units) or 1.0
     chunks = []
-    for uid, (tids, tiles, cost, q) in enumerate(units):
+    for uid, unit in enumerate(units):
+        tids, tiles, cost, q = unit[:4]
+        grouped = len(unit) > 4 and bool(unit[4])
         blocks = max(1, math.ceil(tiles / q))
         k = min(blocks, max(1, math.ceil(n_lanes * cost / total)))
         for j in range(k):
             lo = min(tiles, (blocks * j // k) * q)
             hi = min(tiles, (blocks * (j + 1) // k) * q)
             if hi > lo:
-                chunks.append((cost * (hi - lo) / tiles, uid, tids, lo, hi))
+                chunks.append((cost * (hi - lo) / tiles, uid, tids, lo, hi, grouped))
     chunks.sort(key=lambda c: (-c[0], c[1], c[3]))
     loads = [0.0] * n_lanes
+    plain, grouped_order = range(n_lanes), xcd_lane_order(n_lanes)
     # heap-free least-loaded search: lanes are few (<= 4096) and chunks are
     # bounded by n_lanes per unit, so the linear scan stays cheap.
-    for cost, _uid, tids, lo, hi in chunks:
-        lane = min(range(n_lanes), key=loads.__getitem__)
+    for cost, _uid, tids, lo, hi, grouped in chunks:
+        lane = min(grouped_order if grouped else plain, key=loads.__getitem__)
         for tid in tids:
             out.append((lane, V.Entry(tid, lo, hi)))
         loads[lane] += cost
@@ -574,7 +593,8 @@ class _Scheduler:
             t = self.task(i)
             units.append(([self.task_id(i)], n_tiles(t, self.cfg),
                           task_cost(t, self.cfg, self.prog),
-                          _tile_quantum(t, self.cfg, self.prog)))
+                          _tile_quantum(t, self.cfg, self.prog),
+                          t.tile_op == V.TOP_FLASH_ATTN))
         for comp in self.chains(maps):
             tids = [self.task_id(i) for i in comp]
             t0 = self.tasks[tids[0]]

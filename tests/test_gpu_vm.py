@@ -447,6 +447,36 @@ def test_flash_attention(dt, hd, causal, T, C):
     assert err <= tol, err
 
 
+@pytest.mark.parametrize("dt,causal,T,C,target", [("bf16", True, 512, 512, 150.0), ("f16", False, 256, 384, 22.0)])
+def test_flash_attention_score_jump(dt, causal, T, C, target):
+    """A key late in the sequence whose scaled score with one query is `target`
+    above the rest: probabilities against the first block's maximum would
+    overflow (f32 for bf16 at 150, f16 at 22), so the kernel must take its exact
+    two-pass route for that block; the result still matches float64 math."""
+    rng = np.random.default_rng(1006)
+    H, hd = 2, 128
+    q = rng.standard_normal((H, T, hd)).astype(np.float32)
+    k = rng.standard_normal((H, C, hd)).astype(np.float32)
+    v = rng.standard_normal((H, C, hd)).astype(np.float32)
+    qi, kj = T - 3, C - 20                 # query row and the far key (past the first block)
+    for h in range(H):
+        k[h, kj] = q[h, qi] * (target * np.sqrt(hd) / float(q[h, qi] @ q[h, qi]))
+    if dt == "bf16":
+        q, k, v = (vmref.bf16_to_f32(vmref.f32_to_bf16(t)) for t in (q, k, v))
+    else:
+        q, k, v = (t.astype(np.float16).astype(np.float32) for t in (q, k, v))
+    g = G.Graph()
+    Q, K, Vv = g.input(q.shape, dt), g.input(k.shape, dt), g.input(v.shape, dt)
+    g.output(g.flash_attention(Q, K, Vv, 1.0 / np.sqrt(hd), causal, out_dtype="f32"))
+    got, _ = run_both(g.build(), [q, k, v], oracle=None)
+    want = vmref.attention(q, np.transpose(k, (0, 2, 1)), v, 1.0 / np.sqrt(hd), causal)
+    assert np.isfinite(got[0]).all()
+    err = np.abs(got[0] - want).max() / max(1e-6, np.abs(want).max())
+    assert err <= 1e-2, err
+    # the jump row follows the far key's value row
+    np.testing.assert_allclose(got[0][:, qi], want[:, qi], rtol=0, atol=2e-2 * np.abs(want).max())
+
+
 # --- loader validation ----------------------------------------------------------------------------
 
 def test_loader_rejects_out_of_bounds_task():

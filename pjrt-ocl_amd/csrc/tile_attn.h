@@ -101,9 +101,8 @@ VM_DEV uint32_t pack_h2(float a, float b) {
 // the caller's span owns virtual rows [vlo, vhi) of the virtual block starting at
 // vrow0 (the zig-zag order maps virtual block -> real block).
 template <int HD, bool BF16>
-VM_TILE void attn_block_mfma(Args A, uint32_t ti, uint32_t h, uint32_t row0, uint32_t vrow0, uint32_t vlo,
-                             uint32_t vhi) {
-  A = uargs(A);
+VM_DEV void attn_block_mfma(Args A, uint32_t ti, uint32_t h, uint32_t row0, uint32_t vrow0, uint32_t vlo,
+                            uint32_t vhi) {
   const VM_K Task& t = task_of(A, ti);
   const AttnDesc P = attn_desc(A, t);
   h = uni(h);
@@ -473,6 +472,29 @@ VM_DEV bool is_kt_view(const VM_K int32_t* aux, uint32_t kv, uint32_t H, uint32_
          uint32_t(x[4]) == C * hd && x[5] == 1 && uint32_t(x[6]) == hd && x[7] == 0;
 }
 
+// The lane's query blocks: per head, the virtual 256-row blocks intersecting
+// [lo, hi), each mapped to its real block (zig-zag when causal and every block is
+// whole, since it maps virtual onto real blocks).  One call per lane, so the
+// register save / restore of the call is paid once.
+template <int HD, bool BF16>
+VM_TILE void attn_fast(Args A, uint32_t ti, uint32_t lo, uint32_t hi) {
+  A = uargs(A);
+  const VM_K Task& t = task_of(A, ti);
+  const AttnDesc P = attn_desc(A, t);
+  const uint32_t T = P.T;
+  hi = min(hi, P.H * T);
+  const uint32_t nb = (T + kAttnRows - 1) / kAttnRows;
+  const bool zig = P.causal && T % kAttnRows == 0;
+  for (uint32_t h = lo / T; h * T < hi; ++h) {
+    const uint32_t a = max(lo, h * T) - h * T, b = min(hi - h * T, T);     // virtual rows [a, b)
+    for (uint32_t vb = a / kAttnRows; vb * kAttnRows < b; ++vb) {
+      const uint32_t rb = zig ? ((vb & 1) ? nb - 1 - (vb >> 1) : (vb >> 1)) : vb;
+      const uint32_t vrow0 = vb * kAttnRows;
+      attn_block_mfma<HD, BF16>(A, ti, h, rb * kAttnRows, vrow0, max(a, vrow0), min(b, vrow0 + kAttnRows));
+    }
+  }
+}
+
 VM_TILE void flash_attn_tiles(Args A, uint32_t ti, uint32_t lo, uint32_t hi) {
   A = uargs(A);
   const VM_K Task& t = task_of(A, ti);
@@ -482,26 +504,12 @@ VM_TILE void flash_attn_tiles(Args A, uint32_t ti, uint32_t lo, uint32_t hi) {
                     is_kt_view(aux_of(A), P.kv, P.H, P.C, P.hd) && P.scale > 0.0f &&
                     (dt == DT_F32 || dt == DT_BF16 || dt == DT_F16);
   if (!fast) return attn_rows_generic(A, ti, lo, hi);
-  const uint32_t T = P.T;
-  hi = min(hi, P.H * T);
-  const uint32_t nb = (T + kAttnRows - 1) / kAttnRows;
-  // zig-zag only when every block is whole (it maps virtual onto real blocks)
-  const bool zig = P.causal && T % kAttnRows == 0;
-  // per head, the virtual 256-row blocks intersecting [lo, hi)
-  for (uint32_t h = lo / T; h * T < hi; ++h) {
-    const uint32_t a = max(lo, h * T) - h * T, b = min(hi - h * T, T);     // virtual rows [a, b)
-    for (uint32_t vb = a / kAttnRows; vb * kAttnRows < b; ++vb) {
-      const uint32_t rb = zig ? ((vb & 1) ? nb - 1 - (vb >> 1) : (vb >> 1)) : vb;
-      const uint32_t vrow0 = vb * kAttnRows;
-      const uint32_t vlo = max(a, vrow0), vhi = min(b, vrow0 + kAttnRows);
-      if (adt == DT_BF16) {
-        if (P.hd == 128) attn_block_mfma<128, true>(A, ti, h, rb * kAttnRows, vrow0, vlo, vhi);
-        else attn_block_mfma<64, true>(A, ti, h, rb * kAttnRows, vrow0, vlo, vhi);
-      } else {
-        if (P.hd == 128) attn_block_mfma<128, false>(A, ti, h, rb * kAttnRows, vrow0, vlo, vhi);
-        else attn_block_mfma<64, false>(A, ti, h, rb * kAttnRows, vrow0, vlo, vhi);
-      }
-    }
+  if (adt == DT_BF16) {
+    if (P.hd == 128) attn_fast<128, true>(A, ti, lo, hi);
+    else attn_fast<64, true>(A, ti, lo, hi);
+  } else {
+    if (P.hd == 128) attn_fast<128, false>(A, ti, lo, hi);
+    else attn_fast<64, false>(A, ti, lo, hi);
   }
 }
 

@@ -12,7 +12,8 @@ flash attention (B4 H16 S2048 d128, bf16) as TFLOP/s against their MFMA roofline
 and config 5 (GPT decoder, greedy decode) as tokens/s against the per-token HBM
 bytes.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workloads c1,c2,c3,c4,c5,copy] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workloads c1,c2,c3,c3_bf16,c3_f32,c4,c5,copy]
+                    [--no-cpu] [--skip-c2]
 
 "copy" adds a plain device-to-device copy of 128 MiB, the calibration kernel for
 the HBM byte counters.
@@ -320,6 +321,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workloads", default="c1,c2,c3,c4,c5")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--skip-c2", action="store_true",
+                    help="profiling aid: run only the --workloads extras and print them as one JSON line "
+                         "(no headline C2 measurement)")
     args = ap.parse_args()
     if args.gpus != 1:
         raise SystemExit("bench.py measures one GPU: this build has no multi-GPU path "
@@ -329,8 +333,8 @@ def main():
     log(f"device {rt.info['name']} {rt.info['arch']} lanes={rt.info['n_lanes']}")
     wl = set(args.workloads.split(","))
     extra = {}
-    if "c3" in wl:
-        for dt in ("bf16", "f32"):
+    for dt in ("bf16", "f32"):
+        if "c3" in wl or f"c3_{dt}" in wl:
             log(f"C3 {dt}")
             extra[f"c3_{dt}"] = bench_gemm(rt, dt, max(5, args.steps // 5), 2)
     if "c4" in wl:
@@ -345,6 +349,9 @@ def main():
     if "copy" in wl:
         log("copy")
         extra["copy"] = bench_copy(rt, max(5, args.steps // 5))
+    if args.skip_c2:
+        print(json.dumps({"extra": extra}), flush=True)
+        return
     log("C2")
     c2 = bench_c2(rt, args.steps, args.warmup, not args.no_cpu)
     line = {

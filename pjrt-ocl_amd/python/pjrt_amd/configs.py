@@ -179,24 +179,28 @@ def gpt_c5(c: GptConfig = C5, emit_logits: bool = False, trips: int | None = Non
     pos = g.fill((), T, "i32")
     step = g.fill((), 0, "i32")
     out = g.fill((c.steps,), 0, "i32")
-    ctx_idx = g.iota((H, 1, C), 2, "i32")
-    neg_inf = g.fill((H, 1, C), -np.inf)
+    # causal mask of the decode scores as a per-position bias added by the score
+    # matmul's epilogue: 0 for the prompt and every decoded position so far,
+    # -inf beyond; each step opens its own position
+    mask_bias = g.fill((C,), -np.inf)                  # rebuilt on every execution
+    g.dynamic_update_slice(mask_bias, g.fill((T,), 0.0), [zero])
+    zero_f = g.scalar(0.0)
 
     g.begin()
     x = g.add(g.convert(g.take_rows(P["wte"], cur), "f32"),
               g.convert(g.dynamic_slice(P["wpe"], [pos, zero], [1, D]), "f32"))
-    pos_b = g.broadcast_view(pos, (H, 1, C), ())
-    masked = g.compare(ctx_idx, g.materialize(pos_b), "GT")                # context beyond pos
+    g.dynamic_update_slice(mask_bias, g.reshape(zero_f, (1,)), [pos])
     for l in range(c.layers):
         h = g.layernorm(x, P[f"h{l}.ln1_g"], P[f"h{l}.ln1_b"], c.eps, out_dtype="bf16")
         qkv = g.dot(h, P[f"h{l}.w_qkv"], out_dtype="bf16", residual=P[f"h{l}.b_qkv"],
                     epilogue=[(V.SUB_ADD, 2, 0.0, 0.0)])
-        q, k, v = (g.materialize(g.view(qkv, (H, 1, hd), (hd, 3 * D, 1), s * D)) for s in range(3))
+        # q, k, v are contiguous thirds of the one row: aliases, not copies
+        q, k, v = (g.alias(qkv, s * D, (H, 1, hd)) for s in range(3))
         g.dynamic_update_slice(cache_k[l], g.reshape(k, (H, hd, 1)), [zero, zero, pos])
         g.dynamic_update_slice(cache_v[l], v, [zero, pos, zero])
-        s = g.dot(q, cache_k[l], epilogue=[(V.SUB_AFFINE, 0, scale, 0.0)])      # [H, 1, C]
-        s = g.select(masked, neg_inf, s)
-        p = g.convert(g.softmax_last(s), "bf16")
+        s = g.dot(q, cache_k[l], residual=mask_bias,                           # [H, 1, C]
+                  epilogue=[(V.SUB_AFFINE, 0, scale, 0.0), (V.SUB_ADD, 2, 0.0, 0.0)])
+        p = g.softmax_last(s, out_dtype="bf16")
         att = g.dot(p, cache_v[l], out_dtype="bf16")                           # [H, 1, hd]
         att_rows = g.reshape(att, (1, D))
         xb = g.add(x, g.reshape(P[f"h{l}.b_o"], (1, D)))

@@ -69,6 +69,7 @@ class Graph:
         self.outputs: list = []
         self._stack: list = []          # instruction lists under construction
         self._disjoint = 0
+        self.aliases: dict = {}         # buffer -> (parent buffer, byte offset)
 
     # ---- buffers / io -----------------------------------------------------
     def _new(self, shape, dtype) -> Tensor:
@@ -137,6 +138,22 @@ class Graph:
     def transpose_view(self, src: Tensor, perm) -> Tensor:
         st = _row_major_strides(src.shape)
         return self.view(src, [src.shape[p] for p in perm], [st[p] for p in perm])
+
+    def alias(self, src: Tensor, elem_off: int, shape) -> Tensor:
+        """A contiguous slice of ``src`` as a buffer of its own that shares src's
+        memory (no copy): elements [elem_off, elem_off + prod(shape)).  The
+        scheduler orders accesses to overlapping buffers like accesses to one."""
+        src = self.materialize(src)
+        shape = tuple(int(x) for x in shape)
+        if elem_off < 0 or elem_off + _prod(shape) > src.n:
+            raise GraphError("alias outside its source")
+        byte_off = elem_off * V.DT_SIZE[src.dtype]
+        if byte_off % 16:
+            raise GraphError("alias offset must keep 16-byte alignment")
+        parent, base = self.aliases.get(src.buf, (src.buf, 0))
+        t = self._new(shape, src.dtype)
+        self.aliases[t.buf] = (parent, base + byte_off)
+        return t
 
     def materialize(self, t: Tensor) -> Tensor:
         if not t.view:
@@ -359,9 +376,9 @@ class Graph:
                           n=idx.n, imm=seg))
         return val, idx
 
-    def softmax_last(self, a: Tensor) -> Tensor:
+    def softmax_last(self, a: Tensor, out_dtype=None) -> Tensor:
         a = self.materialize(a)
-        dst = self._new(a.shape, a.dtype)
+        dst = self._new(a.shape, a.dtype if out_dtype is None else out_dtype)
         self.emit(V.Instr(V.OP_SOFTMAX, dst=dst.buf, a=a.buf,
                           n=a.n // a.shape[-1], imm=a.shape[-1]))
         return dst
@@ -558,8 +575,12 @@ class Graph:
             if not progress:
                 raise GraphError("region instruction not reachable from root")
         bufs, off = [], 0
-        for n, dt in self.buffers:
+        for i, (n, dt) in enumerate(self.buffers):
             size = n * V.DT_SIZE[dt]
+            if i in self.aliases:           # shares its parent's memory
+                parent, byte_off = self.aliases[i]
+                bufs.append(V.Buffer(bufs[parent].arena_byte_offset + byte_off, size, dt))
+                continue
             bufs.append(V.Buffer(off, size, dt))
             off += max(ARENA_SLOT, -(-size // V.ARENA_ALIGN) * V.ARENA_ALIGN)
         return V.VMProgram(

@@ -314,7 +314,51 @@ def _region_inputs_from_aux(ins: V.Instr, prog: V.VMProgram) -> list:
     return [prog.aux[tail + k] for k in range(n_in)]
 
 
+def overlap_groups(prog: V.VMProgram) -> list:
+    """Buffer id -> the lowest id of its group of arena-overlapping buffers, so
+    that accesses to aliasing buffers (a contiguous slice kept as a buffer of its
+    own) are ordered like accesses to one buffer."""
+    bufs = prog.buffers
+    cached = getattr(prog, "_overlap_groups", None)
+    if cached is not None and len(cached) == len(bufs):
+        return cached
+    group = list(range(len(bufs)))
+    members, end = [], -1
+    for i in sorted(range(len(bufs)), key=lambda k: (bufs[k].arena_byte_offset, k)):
+        b = bufs[i]
+        if b.size_bytes <= 0:
+            continue
+        if members and b.arena_byte_offset < end:
+            members.append(i)
+            end = max(end, b.arena_byte_offset + b.size_bytes)
+        else:
+            if len(members) > 1:
+                root = min(members)
+                for m in members:
+                    group[m] = root
+            members, end = [i], b.arena_byte_offset + b.size_bytes
+    if len(members) > 1:
+        root = min(members)
+        for m in members:
+            group[m] = root
+    try:
+        prog._overlap_groups = group
+    except AttributeError:
+        pass
+    return group
+
+
 def instr_reads(ins: V.Instr, prog: V.VMProgram) -> set:
+    grp = overlap_groups(prog)
+    return {grp[b] if 0 <= b < len(grp) else b for b in _instr_reads(ins, prog)}
+
+
+def instr_writes(ins: V.Instr, prog: V.VMProgram) -> set:
+    grp = overlap_groups(prog)
+    return {grp[b] if 0 <= b < len(grp) else b for b in _instr_writes(ins, prog)}
+
+
+def _instr_reads(ins: V.Instr, prog: V.VMProgram) -> set:
     op = ins.op
     if op in (V.OP_NOP, V.OP_FILL_F32, V.OP_IOTA_F32, V.OP_IOTA_DIM):
         return set()
@@ -352,7 +396,7 @@ def instr_reads(ins: V.Instr, prog: V.VMProgram) -> set:
     return r | set(ins.reads_hint)
 
 
-def instr_writes(ins: V.Instr, prog: V.VMProgram) -> set:
+def _instr_writes(ins: V.Instr, prog: V.VMProgram) -> set:
     if ins.op == V.OP_NOP:
         return set()
     if ins.op == V.OP_ARGMAX_SEG:

@@ -224,3 +224,37 @@ def test_gemv_not_chosen_for_views_or_wide_m():
     g.output(g.dot(x, w), g.dot(g.slice(x, (0, 0), (1, 64)), g.transpose_view(wt, (1, 0))))
     sched = S.schedule_program(g.build(), S.DeviceConfig(nlanes=16))
     assert all(t.tile_op != V.TOP_GEMV for t in sched.tasks)
+
+
+def test_alias_shares_memory_and_orders_like_its_parent():
+    """An alias is a buffer placed inside its parent's bytes (no arena of its
+    own), and the scheduler separates a write of the parent from a read of the
+    alias by a barrier, like two accesses to one buffer."""
+    g = G.Graph()
+    x = g.input((4, 96))
+    w = g.input((96, 96))
+    y = g.dot(x, w)                                   # writes y on several lanes
+    hi = g.alias(y, 2 * 96, (2, 96))                  # rows 2..3 of y, in place
+    z = g.reduce_last(hi, V.RED_SUM)                  # reads the alias
+    g.output(z)
+    prog = g.build()
+    assert prog.buffers[hi.buf].arena_byte_offset == prog.buffers[y.buf].arena_byte_offset + 2 * 96 * 4
+    assert prog.buffers[hi.buf].size_bytes == 2 * 96 * 4
+    grp = S.overlap_groups(prog)
+    assert grp[hi.buf] == grp[y.buf] and grp[x.buf] != grp[y.buf]
+    sched = S.schedule_program(prog, S.DeviceConfig(nlanes=8, mma_t=64))
+    assert len(phases(sched)) == 2
+    rng = np.random.default_rng(1007)
+    a = rng.integers(-4, 5, (4, 96)).astype(np.float32)
+    b = rng.integers(-4, 5, (96, 96)).astype(np.float32)
+    out = vmref.execute_schedule(V.serialize(prog, sched), [a, b])
+    np.testing.assert_array_equal(out[0], (a @ b)[2:].sum(-1))
+
+
+def test_alias_rejects_unaligned_or_outside():
+    g = G.Graph()
+    y = g.input((10,), "bf16")
+    with pytest.raises(G.GraphError):
+        g.alias(y, 3, (2,))                           # 6-byte offset
+    with pytest.raises(G.GraphError):
+        g.alias(y, 8, (4,))                           # past the end

@@ -70,6 +70,9 @@ PINS = {
     "softmax": "float64 closed form",
     "dot": "integer-valued small-K inputs exact (test_ops_dot.py trick); float64",
     "flash": "float64 closed form of ops/attention.py:53-64",
+    "decode_attn": "extension without a reference counterpart: brute-force loops on tiny "
+                   "inputs, and equal to the decomposed dot / mask / softmax / dot chain "
+                   "of pinned ops with the cache column at pos holding k, v",
     "gather/scatter/dyn": "brute force index loops on tiny inputs",
 }
 
@@ -486,6 +489,21 @@ def attention(Q, Kb, Vb, scale, causal):
     return np.einsum("htc,hcd->htd", p, Vb.astype(np.float64)).astype(np.float32)
 
 
+def decode_attention(q, Kt, Vc, k, v, pos, scale):
+    """Extension OP_DECODE_ATTN (no reference counterpart; it is the per-step
+    attention of the reference's decode idiom, DOT(q K^T) -> mask -> softmax ->
+    DOT(P V), with the step's key/value appended to the cache prefix).
+    q, k, v [H, hd]; Kt [H, hd, C]; Vc [H, C, hd]; pos clamped to [0, C]."""
+    C = Kt.shape[2]
+    p = min(max(int(pos), 0), C)
+    keys = np.concatenate([Kt[:, :, :p].transpose(0, 2, 1), k[:, None, :]], 1).astype(np.float64)
+    vals = np.concatenate([Vc[:, :p], v[:, None, :]], 1).astype(np.float64)
+    s = np.einsum("hd,hcd->hc", q.astype(np.float64), keys) * scale
+    e = np.exp(s - s.max(-1, keepdims=True))
+    e /= e.sum(-1, keepdims=True)
+    return np.einsum("hc,hcd->hd", e, vals)
+
+
 def _epi_micro(kind, x, y, s, t):
     if kind in IS_BIN:
         return _float_bin(kind, x, y)
@@ -895,6 +913,23 @@ class TaskRunner:
                     out[g, tile % T] = O[tile % T]
         self.m.store_f(t.dst, slice(0, H * T * hd), out.reshape(-1), t.dt)
 
+    # 21: decode-step attention, one head per tile (extension)
+    def top21(self, t, lo, hi):
+        H, hd, C = t.p[4], t.p[5], t.p[6]
+        h0, h1 = lo, min(hi, H)
+        if h0 >= h1:
+            return
+        ld = lambda bid, n: self.m.load_f(bid, t.adt)[:n]
+        q = ld(t.a, H * hd).reshape(H, hd)
+        Kt = ld(t.b, H * hd * C).reshape(H, hd, C)
+        Vc = ld(t.p[0], H * C * hd).reshape(H, C, hd)
+        k = ld(t.p[1], H * hd).reshape(H, hd)
+        v = ld(t.p[2], H * hd).reshape(H, hd)
+        pos = int(self.m.view(t.p[3], I32)[0])
+        sl = slice(h0, h1)
+        o = decode_attention(q[sl], Kt[sl], Vc[sl], k[sl], v[sl], pos, float(_bits_f32(t.p[7])))
+        self.m.store_f(t.dst, slice(h0 * hd, h1 * hd), o.reshape(-1).astype(np.float32), t.dt)
+
     # 15: strided partial-axis reduce
     def top15(self, t, lo, hi):
         n_out, red, inner, kind = t.p[0], t.p[1], t.p[2], t.p[3]
@@ -1035,6 +1070,9 @@ def _instr_task(prog: Prog, ins, ew_ts: int, mma_t: int):
         top, p = 13, [aux, n] + f[2:]
     elif op == 58:
         top, p[:4] = 14, [imm2, n, imm, aux]
+    elif op == 68:
+        hd, kb, vb, posb, sbits = prog.aux[aux:aux + 5]
+        top, p = 21, [imm2, kb, vb, posb, n, hd, imm, sbits]
     elif op == 27:
         M, N, K, G = n, imm >> 16, imm & 0xFFFF, max(1, imm2)
         views = prog.aux[aux:aux + 4] if aux else [0, 0, 0, 0]
@@ -1066,6 +1104,8 @@ def _whole_tiles(t: Task, ew_ts: int, mma_t: int) -> int:
         return max(1, p[1] * p[2])
     if t.top == 20:
         return max(1, p[3]) * -(-p[1] // p[4])
+    if t.top == 21:
+        return max(1, p[4])
     raise NotImplementedError(t.top)
 
 

@@ -25,7 +25,8 @@ enum TileOp : uint32_t {
   // extension of this build: variadic (value, index) reduce -> argmax
   TOP_ARGMAX_SEG = 19,
   TOP_GEMV = 20,
-  TOP_COUNT = 21
+  TOP_DECODE_ATTN = 21,
+  TOP_COUNT = 22
 };
 
 // ---- elementwise subops (vm_common.cl:118-146) -----------------------------------

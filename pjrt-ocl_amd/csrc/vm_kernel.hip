@@ -14,6 +14,7 @@
 #include <hip/hip_runtime.h>
 
 #include "tile_attn.h"
+#include "tile_decode.h"
 #include "tile_ew.h"
 #include "tile_gemv.h"
 #include "tile_index.h"
@@ -27,7 +28,8 @@ constexpr uint32_t kRootOwner = 0xFFFFFFFFu;
 
 // LDS shared by the tile ops of one lane (the matmul's double-buffered operand
 // slabs are the largest user).
-constexpr int kSmemBytes = (kMmaLdsBytes > kAttnLdsBytes ? kMmaLdsBytes : kAttnLdsBytes);
+constexpr int kSmemBytes0 = (kMmaLdsBytes > kAttnLdsBytes ? kMmaLdsBytes : kAttnLdsBytes);
+constexpr int kSmemBytes = (kSmemBytes0 > int(kDecLdsBytes) ? kSmemBytes0 : int(kDecLdsBytes));
 
 VM_DEV void exec_tiles(Args A, uint32_t ti, uint32_t lo, uint32_t hi) {
   switch (task_of(A, ti).tile_op & 0xFF) {
@@ -49,6 +51,7 @@ VM_DEV void exec_tiles(Args A, uint32_t ti, uint32_t lo, uint32_t hi) {
     case TOP_GATHER_INDEX: gather_index_tiles(A, ti, lo, hi); break;
     case TOP_ARGMAX_SEG: argmax_tiles(A, ti, lo, hi); break;
     case TOP_GEMV: gemv_tiles(A, ti, lo, hi); break;
+    case TOP_DECODE_ATTN: decode_attn_tiles(A, ti, lo, hi); break;
     default: raise_error(A, VM_ERR_BAD_TASK, task_of(A, ti).tile_op); break;
   }
 }

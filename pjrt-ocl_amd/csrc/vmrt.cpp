@@ -324,6 +324,7 @@ struct Checker {
         return std::max<uint64_t>(1, t.p[0]);
       case TOP_FLASH_ATTN: return std::max<uint64_t>(1, uint64_t(t.p[1]) * t.p[2]);
       case TOP_GEMV: return t.p[4] ? std::max<uint64_t>(1, t.p[3]) * cdiv(t.p[1], t.p[4]) : 0;
+      case TOP_DECODE_ATTN: return std::max<uint64_t>(1, t.p[4]);
       default: return 0;
     }
   }
@@ -532,6 +533,17 @@ struct Checker {
           }
         }
         return true;
+      }
+      case TOP_DECODE_ATTN: {
+        const uint64_t H = t.p[4], hd = t.p[5], C = t.p[6];
+        if (dt != adt || (adt != DT_F32 && adt != DT_BF16 && adt != DT_F16)) return fail(ti, "decode attention dtype");
+        if (H < 1 || hd < 8 || hd > 256 || hd % 8 || C < 8 || C % 8) return fail(ti, "decode attention shape");
+        if (!has(t.a, H * hd, adt) || !has(t.p[1], H * hd, adt) || !has(t.p[2], H * hd, adt))
+          return fail(ti, "decode attention q / k / v");
+        if (!has(t.b, H * hd * C, adt) || !has(t.p[0], H * C * hd, adt)) return fail(ti, "decode attention caches");
+        if (t.p[3] >= nb || P.buffers[t.p[3]].dtype != DT_I32 || !has(t.p[3], 1, DT_I32))
+          return fail(ti, "decode attention position (i32 scalar)");
+        return has(t.dst, H * hd, dt) || fail(ti, "decode attention output");
       }
       default:
         return fail(ti, fmt("tile op %u is not supported by this runtime", top));
@@ -806,6 +818,8 @@ int vmrt_load(vmrt_runtime* rt, const void* bytes, size_t len, uint32_t ew_ts, u
     }
     if (top == TOP_LAYERNORM_SEG && (orig.p[3] & LN_AFFINE)) t.p[4] = handle(orig.p[4]);
     if (top == TOP_GEMV && orig.p[6]) t.p[7] = handle(orig.p[7]);
+    if (top == TOP_DECODE_ATTN)
+      for (int k = 0; k < 4; ++k) t.p[k] = handle(orig.p[k]);
   }
   // ---- patch aux: runtime start-scalar / index-buffer locations (runtime.cc:883-924) ----
   std::vector<int32_t> aux = P.aux;

@@ -124,7 +124,8 @@ def gpt_c5(c: GptConfig = C5, emit_logits: bool = False, trips: int | None = Non
     ``trips`` runs only that many decode steps (same inputs and outputs; for
     separating prefill from decode time)."""
     g = G.Graph()
-    H, hd, T, C, D = c.heads, c.hd, c.prompt, c.ctx, c.d
+    H, hd, T, D = c.heads, c.hd, c.prompt, c.d
+    C = -(-c.ctx // 8) * 8        # cache capacity: whole 16-byte runs of keys
     ids = g.input((T,), "i32")
     P = {}
     for name, shape, dt in gpt_param_shapes(c):
@@ -132,8 +133,8 @@ def gpt_c5(c: GptConfig = C5, emit_logits: bool = False, trips: int | None = Non
     zero = g.scalar(0, "i32")
     one = g.scalar(1, "i32")
     scale = 1.0 / math.sqrt(hd)
-    # K is cached transposed, [H, hd, C]: the decode scores q . K^T are then a
-    # contiguous skinny matmul, like P . V over the [H, C, hd] V cache
+    # K is cached transposed, [H, hd, C]: a decode step reads each channel's
+    # keys as one contiguous run, and V as [H, C, hd] rows
     cache_k = [g.fill((H, hd, C), 0.0, "bf16") for _ in range(c.layers)]
     cache_v = [g.fill((H, C, hd), 0.0, "bf16") for _ in range(c.layers)]
     logits_all = g.fill((c.steps + 1, c.vocab), 0.0) if emit_logits else None
@@ -179,32 +180,24 @@ def gpt_c5(c: GptConfig = C5, emit_logits: bool = False, trips: int | None = Non
     pos = g.fill((), T, "i32")
     step = g.fill((), 0, "i32")
     out = g.fill((c.steps,), 0, "i32")
-    # causal mask of the decode scores as a per-position bias added by the score
-    # matmul's epilogue: 0 for the prompt and every decoded position so far,
-    # -inf beyond; each step opens its own position
-    mask_bias = g.fill((C,), -np.inf)                  # rebuilt on every execution
-    g.dynamic_update_slice(mask_bias, g.fill((T,), 0.0), [zero])
-    zero_f = g.scalar(0.0)
 
     g.begin()
     x = g.add(g.convert(g.take_rows(P["wte"], cur), "f32"),
               g.convert(g.dynamic_slice(P["wpe"], [pos, zero], [1, D]), "f32"))
-    g.dynamic_update_slice(mask_bias, g.reshape(zero_f, (1,)), [pos])
     for l in range(c.layers):
         h = g.layernorm(x, P[f"h{l}.ln1_g"], P[f"h{l}.ln1_b"], c.eps, out_dtype="bf16")
         qkv = g.dot(h, P[f"h{l}.w_qkv"], out_dtype="bf16", residual=P[f"h{l}.b_qkv"],
                     epilogue=[(V.SUB_ADD, 2, 0.0, 0.0)])
         # q, k, v are contiguous thirds of the one row: aliases, not copies
-        q, k, v = (g.alias(qkv, s * D, (H, 1, hd)) for s in range(3))
+        q, k, v = (g.alias(qkv, s * D, (H, hd)) for s in range(3))
+        xb = g.add(x, g.reshape(P[f"h{l}.b_o"], (1, D)))      # beside the QKV matmul
+        # attention over the cache prefix [0, pos) and this step's own k, v; the
+        # cache takes k, v afterwards, beside the output projection
+        att = g.decode_attention(q, k, v, cache_k[l], cache_v[l], pos, scale)  # [H, hd] bf16
         g.dynamic_update_slice(cache_k[l], g.reshape(k, (H, hd, 1)), [zero, zero, pos])
-        g.dynamic_update_slice(cache_v[l], v, [zero, pos, zero])
-        s = g.dot(q, cache_k[l], residual=mask_bias,                           # [H, 1, C]
-                  epilogue=[(V.SUB_AFFINE, 0, scale, 0.0), (V.SUB_ADD, 2, 0.0, 0.0)])
-        p = g.softmax_last(s, out_dtype="bf16")
-        att = g.dot(p, cache_v[l], out_dtype="bf16")                           # [H, 1, hd]
-        att_rows = g.reshape(att, (1, D))
-        xb = g.add(x, g.reshape(P[f"h{l}.b_o"], (1, D)))
-        x = g.dot(att_rows, P[f"h{l}.w_o"], residual=xb, epilogue=[(V.SUB_ADD, 1, 0.0, 0.0)])
+        g.dynamic_update_slice(cache_v[l], g.reshape(v, (H, 1, hd)), [zero, pos, zero])
+        x = g.dot(g.reshape(att, (1, D)), P[f"h{l}.w_o"], residual=xb,
+                  epilogue=[(V.SUB_ADD, 1, 0.0, 0.0)])
         x = mlp_block(x, l, 1)
     nxt = head(x, g.add(step, one))
     g.dynamic_update_slice(out, nxt, [step])

@@ -472,6 +472,43 @@ class Graph:
                           imm=T, aux=desc, imm2=v.buf))
         return dst
 
+    def decode_attention(self, q: Tensor, k: Tensor, v: Tensor, cache_kt: Tensor,
+                         cache_v: Tensor, pos: Tensor, scale: float) -> Tensor:
+        """One decode step of attention per head (extension opcode
+        OP_DECODE_ATTN): the keys are the cache prefix K^T[h, :, :pos] and the
+        step's own key k[h], the values V[h, :pos] and v[h], so the step reads
+        its new key/value straight from where they were computed and the cache
+        update can run beside the next matmul.  q, k, v: [H, hd] (any shape of
+        H * hd elements); cache_kt: [H, hd, C]; cache_v: [H, C, hd]; pos: i32
+        scalar, clamped to [0, C].  All float operands share one dtype; the
+        output [H, hd] has it too.  Equals the decomposed
+        dot -> (mask beyond pos) -> softmax -> dot chain with pos's column of the
+        cache holding k and v."""
+        if cache_kt.view or cache_v.view:
+            raise GraphError("decode_attention: caches must be plain buffers")
+        q, k, v = self.materialize(q), self.materialize(k), self.materialize(v)
+        if len(cache_kt.shape) != 3 or len(cache_v.shape) != 3:
+            raise GraphError("decode_attention: caches are [H, hd, C] and [H, C, hd]")
+        H, hd, C = cache_kt.shape
+        if cache_v.shape != (H, C, hd):
+            raise GraphError(f"decode_attention: V cache {cache_v.shape} != {(H, C, hd)}")
+        for name, t in (("q", q), ("k", k), ("v", v)):
+            if t.n != H * hd:
+                raise GraphError(f"decode_attention: {name} has {t.n} elements, want {H * hd}")
+        dts = {t.dtype for t in (q, k, v, cache_kt, cache_v)}
+        if len(dts) != 1 or next(iter(dts)) not in (V.DT_F32, V.DT_F16, V.DT_BF16):
+            raise GraphError("decode_attention: q, k, v and the caches share one float dtype")
+        if pos.n != 1 or pos.dtype != V.DT_I32:
+            raise GraphError("decode_attention: pos is an i32 scalar")
+        if hd % 8 or hd > 256 or C % 8 or C > 0xFFFF:
+            raise GraphError("decode_attention: hd and C must be multiples of 8 (hd <= 256)")
+        dst = self._new((H, hd), q.dtype)
+        desc = self.add_aux([hd, k.buf, v.buf, pos.buf, V.f32_bits(scale)])
+        self.emit(V.Instr(V.OP_DECODE_ATTN, dst=dst.buf, a=q.buf, b=cache_kt.buf, n=H,
+                          imm=C, aux=desc, imm2=cache_v.buf,
+                          reads_hint=(cache_v.buf, k.buf, v.buf, pos.buf)))
+        return dst
+
     # ---- dynamic slices / gathers ------------------------------------------------
     def dynamic_slice(self, a: Tensor, starts, sizes) -> Tensor:
         a = self.materialize(a)

@@ -156,6 +156,8 @@ def n_tiles(task: V.Task, cfg: DeviceConfig) -> int:
         return max(1, task.p1 * task.p2)
     if top == V.TOP_GEMV:
         return max(1, task.p3) * -(-task.p1 // task.p4)
+    if top == V.TOP_DECODE_ATTN:
+        return max(1, task.p4)
     raise ScheduleError(f"n_tiles: unknown tile_op {top}")
 
 
@@ -270,6 +272,10 @@ def instr_to_task(ins: V.Instr, prog: V.VMProgram, cfg: DeviceConfig) -> V.Task:
     elif op == V.OP_FLASH_ATTN:
         t = V.Task(V.TOP_FLASH_ATTN, ins.dst, ins.a, ins.b, ins.imm2, ins.n,
                    ins.imm, ins.aux)
+    elif op == V.OP_DECODE_ATTN:
+        hd, kb, vb, posb, sbits = prog.aux[ins.aux:ins.aux + 5]
+        t = V.Task(V.TOP_DECODE_ATTN, ins.dst, ins.a, ins.b, ins.imm2, kb, vb,
+                   posb, ins.n, hd, ins.imm, sbits)
     elif op == V.OP_DOT:
         M, N, K, G = ins.n, ins.imm >> 16, ins.imm & 0xFFFF, max(1, ins.imm2)
         aview, bview, epi, epi_res = ins.aview, ins.bview, ins.epi, ins.epi_res
@@ -377,6 +383,8 @@ def _instr_reads(ins: V.Instr, prog: V.VMProgram) -> set:
         r = {ins.a}
     elif op == V.OP_FLASH_ATTN:
         r = {ins.a, ins.b, ins.imm2}
+    elif op == V.OP_DECODE_ATTN:
+        r = {ins.a, ins.b, ins.imm2} | set(prog.aux[ins.aux + 1:ins.aux + 4])
     elif op == V.OP_MAP_REGION:
         r = set(ins.region_inputs or _region_inputs_from_aux(ins, prog))
     elif op in (V.OP_DYNAMIC_SLICE, V.OP_DYNAMIC_UPDATE_SLICE, V.OP_GATHER_INDEX):
@@ -433,6 +441,9 @@ def task_cost(task: V.Task, cfg: DeviceConfig, prog: V.VMProgram) -> float:
         hd = prog.aux[task.p3 + 3] if task.p3 + 3 < len(prog.aux) else 128
         C = prog.aux[task.p3 + 2] if task.p3 + 2 < len(prog.aux) else T
         return 4.0 * H * T * C * hd / (_MFMA_TFLOPS * 1e6) + 1.0
+    if top == V.TOP_DECODE_ATTN:
+        # one CU per head streams the head's two cache slices (~100 GB/s)
+        return task.p4 * (2.0 * task.p5 * task.p6 * asz / 100e3 + 3.0)
     if top in (V.TOP_RED_SEG, V.TOP_SOFTMAX_SEG, V.TOP_LAYERNORM_SEG,
                V.TOP_ARGMAX_SEG):
         n = task.p0 * task.p1

@@ -37,7 +37,14 @@ which does not use them is byte-for-byte a reference program):
   reference rejects (python/pjrt_ocl/ops/reduce.py:165-168);
 * tile op ``TOP_GEMV`` (20): the scheduler's column-strip form of an ``OP_DOT``
   with at most 8 rows (decode-time matmuls); p0 M, p1 N, p2 K, p3 G, p4 strip
-  width, p6 epilogue + 1, p7 residual.
+  width, p6 epilogue + 1, p7 residual;
+* tensor opcode ``OP_DECODE_ATTN`` (68) / tile op ``TOP_DECODE_ATTN`` (21): one
+  decode step of attention per head, over a cache prefix of runtime length plus
+  the step's own key/value: ``out[h] = softmax(scale q[h] . [K^T[h, :, :pos],
+  k[h]]) [V[h, :pos]; v[h]]``.  Instr: dst out, a q, b K^T cache [H, hd, C],
+  n H, imm C, imm2 V cache [H, C, hd], aux -> [hd, k, v, pos buffer, scale
+  bits].  Task: p0 V, p1 k, p2 v, p3 pos, p4 H, p5 hd, p6 C, p7 scale bits;
+  one tile per head.  ``pos`` (i32 scalar) is clamped to [0, C].
 """
 from __future__ import annotations
 
@@ -126,7 +133,8 @@ OP_SCATTER_INDEX = 65
 # extensions (see module docstring)
 OP_LAYERNORM_AFFINE = 66
 OP_ARGMAX_SEG = 67
-OP_MAX = OP_ARGMAX_SEG
+OP_DECODE_ATTN = 68
+OP_MAX = OP_DECODE_ATTN
 
 REGION_OPS = frozenset({OP_WHILE, OP_IF, OP_FOR})
 
@@ -138,7 +146,8 @@ TOP_EW, TOP_MMA, TOP_GATHER, TOP_RED_PART, TOP_RED_COMB, TOP_IOTA_DIM, \
     TOP_SCATTER_INDEX = range(19)
 TOP_ARGMAX_SEG = 19          # extension
 TOP_GEMV = 20                # extension
-TOP_MAX = TOP_GEMV
+TOP_DECODE_ATTN = 21         # extension
+TOP_MAX = TOP_DECODE_ATTN
 
 # ---- EW subops (vm_common.cl:118-146) ------------------------------------------
 SUB_ADD, SUB_MUL, SUB_SUB, SUB_DIV, SUB_MAX, SUB_MIN, SUB_POW, SUB_COPY, \

@@ -477,6 +477,72 @@ def test_flash_attention_score_jump(dt, causal, T, C, target):
     np.testing.assert_allclose(got[0][:, qi], want[:, qi], rtol=0, atol=2e-2 * np.abs(want).max())
 
 
+@pytest.mark.parametrize("dt,H,hd,C,pos,jump", [
+    ("bf16", 12, 64, 640, 600, None),       # the decoder's shape
+    ("bf16", 12, 64, 640, 0, None),         # the step's own key only
+    ("f16", 3, 8, 16, 16, None),            # full cache
+    ("f32", 2, 24, 24, -1, None),           # clamped position; 3 threads per V row
+    ("f32", 1, 256, 1032, 1030, None),      # widest head, two key chunks
+    ("bf16", 2, 128, 2056, 2050, 1500),     # three chunks; a dominant key in the second
+    ("bf16", 2, 64, 640, 300, "new"),       # a dominant new key
+])
+def test_decode_attention(dt, H, hd, C, pos, jump):
+    """TOP_DECODE_ATTN against float64 math on the same (rounded) inputs: keys
+    are the cache prefix [0, pos) then the step's own key; chunks of 1024 keys
+    combine through the online softmax."""
+    rng = np.random.default_rng(2024 + hd + C)
+    q = rng.standard_normal((H, hd)).astype(np.float32)
+    k = rng.standard_normal((H, hd)).astype(np.float32)
+    v = rng.standard_normal((H, hd)).astype(np.float32)
+    ckt = rng.standard_normal((H, hd, C)).astype(np.float32)
+    cv = rng.standard_normal((H, C, hd)).astype(np.float32)
+    scale = 1.0 / np.sqrt(hd)
+    for h in range(H):
+        big = q[h] * (40.0 / (scale * float(q[h] @ q[h])))
+        if jump == "new":
+            k[h] = big
+        elif jump is not None:
+            ckt[h, :, jump] = big
+    if dt == "bf16":
+        q, k, v, ckt, cv = (vmref.bf16_to_f32(vmref.f32_to_bf16(t)) for t in (q, k, v, ckt, cv))
+    elif dt == "f16":
+        q, k, v, ckt, cv = (t.astype(np.float16).astype(np.float32) for t in (q, k, v, ckt, cv))
+    g = G.Graph()
+    Q, K, Vv = (g.input((H, hd), dt) for _ in range(3))
+    CK, CV = g.input((H, hd, C), dt), g.input((H, C, hd), dt)
+    POS = g.input((), "i32")
+    g.output(g.decode_attention(Q, K, Vv, CK, CV, POS, scale))
+    prog = g.build()
+    blob, _ = blob_for(prog)
+    assert any(tk.top == V.TOP_DECODE_ATTN for tk in vmref.parse(blob).tasks)
+    got, _ = run_both(blob, [q, k, v, ckt, cv, np.array(pos, np.int32)], oracle=None)
+    got = as_f32(got[0], V.DT_BY_NAME[dt]).astype(np.float64).reshape(H, hd)
+    want = vmref.decode_attention(q, ckt, cv, k, v, pos, scale)
+    tol = 1e-3 if dt == "f32" else 1e-2
+    err = np.abs(got - want).max() / max(1e-6, np.abs(want).max())
+    assert np.isfinite(got).all() and err <= tol, err
+
+
+def test_decode_attention_runs_twice_with_moving_position():
+    """The same loaded program at two positions (the position is read at run
+    time, nothing is cached between executions)."""
+    H, hd, C = 4, 64, 640
+    rng = np.random.default_rng(77)
+    arrs = [rng.standard_normal(sh).astype(np.float32) for sh in ((H, hd),) * 3 + ((H, hd, C), (H, C, hd))]
+    g = G.Graph()
+    ins = [g.input(a.shape) for a in arrs] + [g.input((), "i32")]
+    g.output(g.decode_attention(*ins, 0.125))
+    blob, _ = blob_for(g.build())
+    lp = runtime().load(blob)
+    try:
+        for pos in (511, 17):
+            got = np.asarray(lp(*arrs, np.array(pos, np.int32))[0], np.float64).reshape(H, hd)
+            want = vmref.decode_attention(arrs[0], arrs[3], arrs[4], arrs[1], arrs[2], pos, 0.125)
+            assert np.abs(got - want).max() <= 1e-3 * np.abs(want).max()
+    finally:
+        lp.close()
+
+
 # --- loader validation ----------------------------------------------------------------------------
 
 def test_loader_rejects_out_of_bounds_task():

@@ -393,6 +393,91 @@ def test_flash_attention_brute_force(causal):
     np.testing.assert_allclose(got, attention_loops(q, k, v, 0.5, causal), rtol=1e-5, atol=1e-6)
 
 
+def decode_attention_loops(q, Kt, Vc, k, v, pos, scale):
+    """Brute-force decode step with Python loops: keys are the cache columns
+    [0, p) then the step's own key, p = pos clamped to [0, C]."""
+    H, hd, C = Kt.shape
+    p = min(max(int(pos), 0), C)
+    out = np.zeros((H, hd))
+    for h in range(H):
+        keys = [[float(Kt[h, d, j]) for d in range(hd)] for j in range(p)] + [[float(x) for x in k[h]]]
+        vals = [[float(Vc[h, j, d]) for d in range(hd)] for j in range(p)] + [[float(x) for x in v[h]]]
+        s = [scale * sum(float(q[h, d]) * kj[d] for d in range(hd)) for kj in keys]
+        mx = max(s)
+        w = [math.exp(x - mx) for x in s]
+        z = sum(w)
+        for d in range(hd):
+            out[h, d] = sum(wj * vj[d] for wj, vj in zip(w, vals)) / z
+    return out
+
+
+def _decode_inputs(H=3, hd=8, C=16, seed=21):
+    rng = np.random.default_rng(seed)
+    return [rng.standard_normal(sh).astype(np.float32)
+            for sh in ((H, hd), (H, hd), (H, hd), (H, hd, C), (H, C, hd))]
+
+
+def _decode_graph(H, hd, C, scale, dt="f32"):
+    g = G.Graph()
+    Q, K, Vv = (g.input((H, hd), dt) for _ in range(3))
+    CK, CV = g.input((H, hd, C), dt), g.input((H, C, hd), dt)
+    POS = g.input((), "i32")
+    g.output(g.decode_attention(Q, K, Vv, CK, CV, POS, scale))
+    return g.build()
+
+
+@pytest.mark.parametrize("pos", [0, 1, 9, 16, -3, 40])
+def test_decode_attention_brute_force(pos):
+    """Extension op OP_DECODE_ATTN: cache prefix plus the step's own key/value,
+    pos clamped to [0, C] (16 = a full cache, -3 and 40 clamp)."""
+    q, k, v, ckt, cv = _decode_inputs()
+    args = [q, k, v, ckt, cv, np.array(pos, np.int32)]
+    (got,) = both(_decode_graph(3, 8, 16, 0.35), args)
+    np.testing.assert_allclose(got, decode_attention_loops(q, ckt, cv, k, v, pos, 0.35), rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("pos", [0, 5, 15])
+def test_decode_attention_equals_decomposed_chain(pos):
+    """The fused step equals the decomposed chain of pinned ops: cache update at
+    pos, then dot(q, K^T[:, :, :pos + 1]) * scale -> softmax -> dot(P, V[:, :pos + 1])."""
+    H, hd, C, scale = 3, 8, 16, 0.35
+    q, k, v, ckt, cv = _decode_inputs()
+    args = [q, k, v, ckt, cv, np.array(pos, np.int32)]
+    (fused,) = both(_decode_graph(H, hd, C, scale), args)
+    g = G.Graph()
+    Q, K, Vv = (g.input((H, hd)) for _ in range(3))
+    CK, CV = g.input((H, hd, C)), g.input((H, C, hd))
+    POS = g.input((), "i32")
+    zero = g.scalar(0, "i32")
+    ck, cvv = g.fill((H, hd, C), 0.0), g.fill((H, C, hd), 0.0)
+    g.copy_into(ck, CK)
+    g.copy_into(cvv, CV)
+    g.dynamic_update_slice(ck, g.reshape(K, (H, hd, 1)), [zero, zero, POS])
+    g.dynamic_update_slice(cvv, g.reshape(Vv, (H, 1, hd)), [zero, POS, zero])
+    s = g.dot(g.reshape(Q, (H, 1, hd)), g.slice(ck, (0, 0, 0), (H, hd, pos + 1)),
+              epilogue=[(V.SUB_AFFINE, 0, scale, 0.0)])
+    o = g.dot(g.softmax_last(s), g.slice(cvv, (0, 0, 0), (H, pos + 1, hd)))
+    g.output(o)
+    (chain,) = both(g.build(), args)
+    np.testing.assert_allclose(fused, chain.reshape(H, hd), rtol=1e-5, atol=1e-6)
+
+
+def test_planted_decode_new_key_is_caught(monkeypatch):
+    """An oracle that reads the cache's column pos instead of the step's own key
+    and value fails the brute-force check."""
+    def wrong(q, Kt, Vc, k, v, pos, scale):
+        C = Kt.shape[2]
+        p = min(max(int(pos), 0), C - 1)
+        s = np.einsum("hd,hdc->hc", q.astype(np.float64), Kt[:, :, :p + 1].astype(np.float64)) * scale
+        e = np.exp(s - s.max(-1, keepdims=True))
+        e /= e.sum(-1, keepdims=True)
+        return np.einsum("hc,hcd->hd", e, Vc[:, :p + 1].astype(np.float64))
+
+    monkeypatch.setattr(vmref, "decode_attention", wrong)
+    with pytest.raises(AssertionError):
+        test_decode_attention_brute_force(9)
+
+
 # --- data movement -----------------------------------------------------------------------------
 
 def test_gather_scatter_dyn_embedding_brute_force():

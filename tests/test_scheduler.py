@@ -258,3 +258,61 @@ def test_alias_rejects_unaligned_or_outside():
         g.alias(y, 3, (2,))                           # 6-byte offset
     with pytest.raises(G.GraphError):
         g.alias(y, 8, (4,))                           # past the end
+
+
+def test_decode_attention_task_and_cache_update_overlap():
+    """OP_DECODE_ATTN lowers to one TOP_DECODE_ATTN tile per head; the cache
+    update that follows it (write after read of the caches) starts the next
+    phase and shares it with the output projection, which reads neither cache."""
+    H, hd, C, D = 4, 16, 32, 64
+    g = G.Graph()
+    qkv = g.input((1, 3 * D), "bf16")
+    ck, cv = g.fill((H, hd, C), 0.0, "bf16"), g.fill((H, C, hd), 0.0, "bf16")
+    pos = g.fill((), 5, "i32")
+    zero = g.scalar(0, "i32")
+    w = g.input((D, D), "bf16")
+    q, k, v = (g.alias(qkv, s * D, (H, hd)) for s in range(3))
+    att = g.decode_attention(q, k, v, ck, cv, pos, 0.25)
+    g.dynamic_update_slice(ck, g.reshape(k, (H, hd, 1)), [zero, zero, pos])
+    g.dynamic_update_slice(cv, g.reshape(v, (H, 1, hd)), [zero, pos, zero])
+    g.output(g.dot(g.reshape(att, (1, D)), w))
+    prog = g.build()
+    sched = S.schedule_program(prog, S.DeviceConfig(nlanes=8))
+    da = [i for i, t in enumerate(sched.tasks) if t.tile_op == V.TOP_DECODE_ATTN]
+    assert len(da) == 1
+    t = sched.tasks[da[0]]
+    assert (t.p4, t.p5, t.p6) == (H, hd, C) and S.n_tiles(t, S.DeviceConfig(nlanes=8)) == H
+    ph = phases(sched)
+    at = next(i for i, p in enumerate(ph) if da[0] in p)
+    later = {sched.tasks[x].tile_op for x in ph[at + 1]}
+    assert V.TOP_DYN_SCATTER in later and (V.TOP_GEMV in later or V.TOP_MMA in later)
+
+
+def test_decode_attention_rejects_bad_shapes():
+    g = G.Graph()
+    q = g.input((2, 8))
+    pos = g.input((), "i32")
+    with pytest.raises(G.GraphError):      # C not a multiple of 8
+        g.decode_attention(q, q, q, g.input((2, 8, 12)), g.input((2, 12, 8)), pos, 1.0)
+    with pytest.raises(G.GraphError):      # V cache shape
+        g.decode_attention(q, q, q, g.input((2, 8, 16)), g.input((2, 8, 16)), pos, 1.0)
+    with pytest.raises(G.GraphError):      # mixed dtypes
+        g.decode_attention(q, q, q, g.input((2, 8, 16), "bf16"), g.input((2, 16, 8), "bf16"), pos, 1.0)
+    with pytest.raises(G.GraphError):      # pos must be i32
+        g.decode_attention(q, q, q, g.input((2, 8, 16)), g.input((2, 16, 8)), g.input(()), 1.0)
+
+
+def test_gpt_decode_phases_per_layer():
+    """The C5 decode body: 7 barrier-separated phases per layer (LN, QKV with
+    the attention-residual add, attention, cache update with the output
+    projection, LN, FC with the MLP-residual add, projection)."""
+    import dataclasses
+    from pjrt_amd import configs as CF
+    counts = {}
+    for layers in (1, 2):
+        c = dataclasses.replace(CF.C5, layers=layers, steps=4, vocab=512)
+        prog = CF.gpt_c5(c, trips=4)
+        fo = next(x for x in prog.instrs if x.op == V.OP_FOR)
+        sc = S._Scheduler(prog, S.DeviceConfig(nlanes=256))
+        counts[layers] = len(sc.levels(list(range(fo.n, fo.n + fo.imm))))
+    assert counts[2] - counts[1] == 7

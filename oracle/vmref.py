@@ -504,6 +504,16 @@ def decode_attention(q, Kt, Vc, k, v, pos, scale):
     return np.einsum("hc,hcd->hd", e, vals)
 
 
+def _round_to(y, dt):
+    """f32 values as stored in dtype dt and read back as f32."""
+    y = np.asarray(y, np.float32)
+    if dt == BF16:
+        return bf16_to_f32(f32_to_bf16(y))
+    if dt == F16:
+        return y.astype(np.float16).astype(np.float32)
+    return y
+
+
 def _epi_micro(kind, x, y, s, t):
     if kind in IS_BIN:
         return _float_bin(kind, x, y)
@@ -709,7 +719,13 @@ class TaskRunner:
         m = self.m
         M, N, K, G, CW = t.p[0], t.p[1], t.p[2], max(1, t.p[3]), t.p[4]
         ncb = -(-N // CW)
-        A = m.load_f(t.a, t.adt)[:G * M * K].reshape(G, M, K)
+        if t.p[5]:
+            # fused layernorm (extension): x is normalised while staged and
+            # rounded to the layernorm's output dtype, its result never stored
+            ln = m.p.tasks[t.p[5] - 1]
+            A = _round_to(self._ln_rows(ln, 0, M), ln.dt).reshape(1, M, K)
+        else:
+            A = m.load_f(t.a, t.adt)[:G * M * K].reshape(G, M, K)
         B = m.load_f(t.b, t.adt)[:G * K * N].reshape(G, K, N)
         res = m.load_f(t.p[7]) if t.p[6] else None
         have = m.load_f(t.dst, t.dt)[:G * M * N].reshape(G, M, N).copy()
@@ -852,11 +868,18 @@ class TaskRunner:
 
     # 12: layernorm rows (+ extension flags in p3)
     def top12(self, t, lo, hi):
-        n_out, seg, flags = t.p[0], t.p[1], t.p[3]
-        eps = float(_bits_f32(t.p[2]))
+        n_out, seg = t.p[0], t.p[1]
         r0, r1 = lo, min(hi, n_out)
         if r0 >= r1:
             return
+        y = self._ln_rows(t, r0, r1)
+        self.m.store_f(t.dst, slice(r0 * seg, r1 * seg), y.reshape(-1), t.dt)
+
+    def _ln_rows(self, t, r0, r1):
+        """Layernorm rows [r0, r1) of a LAYERNORM_SEG task in f32, before the
+        store's conversion to the task's output dtype."""
+        seg, flags = t.p[1], t.p[3]
+        eps = float(_bits_f32(t.p[2]))
         x = self.m.load_f(t.a, t.adt)[r0 * seg:r1 * seg].reshape(-1, seg)
         y = layernorm_core(x, eps, two_pass=bool(flags & 4))
         if flags & 1:
@@ -865,7 +888,7 @@ class TaskRunner:
             y = (y.astype(np.float64) * g + b).astype(np.float32)
         if flags & 2:
             y = gelu_f32(y)
-        self.m.store_f(t.dst, slice(r0 * seg, r1 * seg), y.reshape(-1), t.dt)
+        return y
 
     # 13: map region (region.cl:43-98)
     def top13(self, t, lo, hi):
@@ -1156,6 +1179,9 @@ def execute(data_or_prog, args, ew_ts: int = 4096, mma_t: int = 128):
 # --- schedule lane simulator (validator b) --------------------------------------------------
 
 def check_coverage(prog: Prog, ew_ts: int, mma_t: int) -> None:
+    """Every tile of every task runs exactly once, except the layernorm tasks a
+    GEMV stages as its prologue (task p5), which no lane runs."""
+    prologue = {t.p[5] - 1 for t in prog.tasks if t.top == 20 and t.p[5]}
     per = {}
     for s in prog.streams:
         for e in s:
@@ -1163,6 +1189,10 @@ def check_coverage(prog: Prog, ew_ts: int, mma_t: int) -> None:
                 continue
             per.setdefault(e[0], []).append((e[1], e[2]))
     for tid, t in enumerate(prog.tasks):
+        if tid in prologue:
+            if tid in per or t.top != 12:
+                raise AssertionError(f"task {tid}: a GEMV prologue must be a layernorm that no lane runs")
+            continue
         nt = _whole_tiles(t, ew_ts, mma_t)
         rs = sorted(per.get(tid, []))
         cur = 0

@@ -7,7 +7,10 @@
 // scratch, deterministic).
 //
 // Task: p0 M (<= kGemvMaxM), p1 N (multiple of 8), p2 K, p3 G, p4 CW (columns
-// per tile: 8 x a power of two, at most 256), p6 epilogue descriptor + 1, p7
+// per tile: 8 x a power of two, at most 256), p5 layernorm prologue (index + 1
+// of a LAYERNORM_SEG task over the M rows of K that no lane runs: each tile
+// normalises x while staging it, rounded to A's dtype as the layernorm's store
+// would, which saves the phase between the two), p6 epilogue descriptor + 1, p7
 // residual handle.  Operands contiguous row-major, A/B of one dtype (bf16 / f16 /
 // f32), f32 accumulation.
 //
@@ -18,6 +21,7 @@
 // through LDS.
 #pragma once
 #include "tile_mma.h"
+#include "tile_reduce.h"
 
 namespace vm {
 
@@ -66,6 +70,62 @@ VM_DEV void gemv_cvt(const typename GemvRaw<ADT>::T& r, float (&w)[8]) {
 }
 
 constexpr int kGemvU = 8;                 // rows per load chunk and thread
+
+// f32 value as stored in dtype DT and read back
+template <uint32_t DT>
+VM_DEV float gemv_round(float z) {
+  if constexpr (DT == DT_BF16) return bf16_to_f32(f32_to_bf16(z));
+  else if constexpr (DT == DT_F16) return f16_to_f32(f32_to_f16(z));
+  else return z;
+}
+
+// Stage the M x K rows of x normalised by the layernorm task `lti` (the
+// LAYERNORM_SEG semantics: mean, two-pass or one-pass variance per its flags,
+// rsqrt(var + eps), affine, GELU), rounded to DT, into xs.  Each thread keeps the
+// same columns in every pass, so the in-place update needs no extra barrier.
+template <uint32_t DT>
+VM_DEV void gemv_ln_stage(Args A, uint32_t lti, uint32_t M, uint32_t K, float* xs, float* red) {
+  const VM_K Task& L = task_of(A, lti);
+  const uint32_t flags = L.p[3];
+  const float eps = __uint_as_float(L.p[2]);
+  const uint32_t xdt = (L.tile_op >> 16) & 0xFF;
+  const bool affine = flags & LN_AFFINE, do_gelu = flags & LN_GELU, two_pass = flags & LN_TWO_PASS;
+  const gbyte* x = resolve(A, L.a);
+  const gbyte* gp = resolve(A, affine ? L.b : L.a);
+  const gbyte* bp = resolve(A, affine ? L.p[4] : L.a);
+  const float inv_n = 1.0f / float(K);
+  for (uint32_t m = 0; m < M; ++m)
+    for (uint32_t j = threadIdx.x; j < K; j += kBlock) xs[m * K + j] = load_f(x, xdt, uint64_t(m) * K + j);
+  for (uint32_t m = 0; m < M; ++m) {
+    float* row = xs + m * K;
+    float s = 0.0f, s2 = 0.0f;
+    for (uint32_t j = threadIdx.x; j < K; j += kBlock) {
+      const float v = row[j];
+      s += v;
+      s2 = fmaf(v, v, s2);
+    }
+    const float mean = block_reduce(s, OpSum(), red) * inv_n;
+    float var;
+    if (two_pass) {
+      float q = 0.0f;
+      for (uint32_t j = threadIdx.x; j < K; j += kBlock) {
+        const float dv = row[j] - mean;
+        q = fmaf(dv, dv, q);
+      }
+      var = block_reduce(q, OpSum(), red + kWaves) * inv_n;
+    } else {
+      var = block_reduce(s2, OpSum(), red + kWaves) * inv_n - mean * mean;
+    }
+    const float rstd = rsqrtf(var + eps);
+    const float shift = -mean * rstd;
+    for (uint32_t j = threadIdx.x; j < K; j += kBlock) {
+      float z = fmaf(row[j], rstd, shift);
+      if (affine) z = fmaf(z, load_f(gp, DT_F32, j), load_f(bp, DT_F32, j));
+      if (do_gelu) z = gelu(z);
+      row[j] = gemv_round<DT>(z);
+    }
+  }
+}
 
 template <uint32_t ADT>
 VM_DEV void gemv_issue(typename GemvRaw<ADT>::T (&raw)[kGemvU], const gbyte* b, uint32_t N, uint32_t K, uint32_t k,
@@ -118,7 +178,9 @@ VM_TILE void gemv_tile(Args A, uint32_t ti, uint32_t tile) {
   typename GemvRaw<ADT>::T r0[kGemvU], r1[kGemvU];
   gemv_issue<ADT>(r0, b, N, K, rp, RP, col);
   __syncthreads();                       // the previous user of the LDS is done
-  for (uint32_t i = threadIdx.x; i < M * K; i += kBlock) xs[i] = load_f(a, ADT, i);
+  if (t.p[5]) gemv_ln_stage<ADT>(A, t.p[5] - 1, M, K, xs, red);
+  else
+    for (uint32_t i = threadIdx.x; i < M * K; i += kBlock) xs[i] = load_f(a, ADT, i);
   __syncthreads();
 
   float acc[MM][8];

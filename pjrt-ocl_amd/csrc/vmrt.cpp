@@ -520,6 +520,14 @@ struct Checker {
           return fail(ti, "gemv x row does not fit the LDS");
         if (!has(t.a, G * M * K, adt) || !has(t.b, G * K * N, adt)) return fail(ti, "gemv operands");
         if (!has(t.dst, G * M * N, dt)) return fail(ti, "gemv result");
+        if (t.p[5]) {
+          const uint32_t li = t.p[5] - 1;
+          if (li >= P.tasks.size()) return fail(ti, "gemv layernorm prologue task");
+          const Task& L = P.tasks[li];
+          if ((L.tile_op & 0xFF) != TOP_LAYERNORM_SEG || L.p[0] != M || L.p[1] != K || G != 1 ||
+              ((L.tile_op >> 8) & 0xFF) != adt)
+            return fail(ti, "gemv layernorm prologue shape");
+        }
         if (t.p[6]) {
           const uint32_t e = t.p[6] - 1;
           if (!aux_ok(e, 1) || P.aux[e] < 0 || !aux_ok(e, 1 + 4 * int64_t(P.aux[e]))) return fail(ti, "epilogue");

@@ -61,7 +61,10 @@ class DeviceConfig:
     # Matmuls of at most 8 rows as column-strip TOP_GEMV tasks (extension), and
     # the narrowest strip width they may use.
     gemv: bool = True
-    gemv_min_strip: int = 8
+    gemv_min_strip: int = 16
+    # A layernorm whose only reader is a TOP_GEMV runs inside that GEMV's x
+    # staging (extension; saves the phase between them).
+    ln_gemv: bool = True
 
     @classmethod
     def from_env(cls, environ=None) -> "DeviceConfig":
@@ -91,7 +94,8 @@ class DeviceConfig:
                    fuse=env.get("PJRT_OCL_FUSE", "1") != "0",
                    mma_autotile=env.get("PJRT_AMD_MMA_AUTOTILE", "1") != "0",
                    gemv=env.get("PJRT_AMD_GEMV", "1") != "0",
-                   gemv_min_strip=max(8, min(256, geti("PJRT_AMD_GEMV_STRIP", 8))))
+                   gemv_min_strip=max(8, min(256, geti("PJRT_AMD_GEMV_STRIP", 16))),
+                   ln_gemv=env.get("PJRT_AMD_LN_GEMV", "1") != "0")
 
 
 # --- instruction -> task ------------------------------------------------------
@@ -169,13 +173,16 @@ _EPI_INLINE = {V.SUB_AFFINE, V.SUB_GELU, V.SUB_COPY, V.SUB_ADD, V.SUB_MUL, V.SUB
                V.SUB_MAX, V.SUB_MIN}
 
 
-def gemv_strip(N: int, G: int, nlanes: int, min_strip: int = 8) -> int:
+def gemv_strip(N: int, G: int, nlanes: int, min_strip: int = 16) -> int:
     """Columns per TOP_GEMV tile: the narrowest strip (min_strip, ... 256, powers
-    of two) that keeps the tile count within two per lane."""
+    of two) that gives no lane a second tile.  A tile's time is latency, not
+    bytes: measured on MI355X with K = 768, 16-column strips beat 8-column ones
+    (N = 2304: 9.2 against 15.3 us per one-phase launch, which gave lanes two
+    tiles) and the 32000-column LM head takes 128 (16.4 against 21.0 us at 64)."""
     cw = 8
     while cw < min_strip:
         cw *= 2
-    while cw < 256 and G * -(-N // cw) > 2 * nlanes:
+    while cw < 256 and G * -(-N // cw) > nlanes:
         cw *= 2
     return cw
 
@@ -192,6 +199,95 @@ def gemv_eligible(M, N, K, G, aview, bview, epi, adt, dt, prog) -> bool:
         if any(prog.aux[epi + 4 * k] not in _EPI_INLINE for k in range(nm)):
             return False
     return True
+
+
+def _dot_fields(ins: V.Instr, prog: V.VMProgram):
+    """(M, N, K, G, aview, bview, epi, epi_res) of an OP_DOT, the view /
+    epilogue fields taken from the in-memory instruction or its aux mirror."""
+    M, N, K, G = ins.n, ins.imm >> 16, ins.imm & 0xFFFF, max(1, ins.imm2)
+    aview, bview, epi, epi_res = ins.aview, ins.bview, ins.epi, ins.epi_res
+    if ins.aux and not (aview or bview or epi):
+        aview, bview, epi, epi_res = prog.aux[ins.aux:ins.aux + 4]
+    return M, N, K, G, aview, bview, epi, epi_res
+
+
+def _gemv_form(ins: V.Instr, prog: V.VMProgram, cfg: DeviceConfig) -> bool:
+    """An OP_DOT the scheduler maps to TOP_GEMV."""
+    M, N, K, G, aview, bview, epi, _ = _dot_fields(ins, prog)
+    if N == 1 and G == 1 and not aview and not bview and not epi:
+        return False                     # the reference's dot-mode segmented reduce
+    bufs = prog.buffers
+    return cfg.gemv and gemv_eligible(M, N, K, G, aview, bview, epi, bufs[ins.a].dtype,
+                                      bufs[ins.dst].dtype, prog)
+
+
+def _instr_lists(prog: V.VMProgram):
+    """Every instruction list of the program: the root list and each region's
+    sub-lists, as index ranges."""
+    out, todo = [], [range(prog.main_len)]
+    while todo:
+        r = todo.pop()
+        out.append(r)
+        for i in r:
+            ins = prog.instrs[i]
+            if ins.op == V.OP_FOR:
+                todo.append(range(ins.n, ins.n + ins.imm))
+            elif ins.op in (V.OP_WHILE, V.OP_IF):
+                todo += [range(ins.a, ins.a + ins.b), range(ins.n, ins.n + ins.imm)]
+    return out
+
+
+def ln_gemv_pairs(prog: V.VMProgram, cfg: DeviceConfig) -> dict:
+    """{dot index: layernorm index} for each OP_LAYERNORM_AFFINE whose result is
+    read by exactly one instruction, an OP_DOT mapped to TOP_GEMV with M = the
+    layernorm's rows and K = its row length, later in the same instruction list
+    with no write to the layernorm's inputs and no region in between.  The GEMV
+    then normalises x while staging it (task p5 = layernorm task + 1) and the
+    layernorm gets no tile of its own; its result buffer is never written."""
+    if not cfg.ln_gemv:
+        return {}
+    grp = overlap_groups(prog)
+    gsize: dict = {}
+    for g in grp:
+        gsize[g] = gsize.get(g, 0) + 1
+    readers: dict = {}
+    writers: dict = {}
+    for i, ins in enumerate(prog.instrs):
+        if ins.op in V.REGION_OPS or ins.op == V.OP_NOP:
+            continue
+        for b in instr_reads(ins, prog):
+            readers.setdefault(b, []).append(i)
+        for b in instr_writes(ins, prog):
+            writers.setdefault(b, []).append(i)
+    io = set(prog.inputs) | set(prog.outputs)
+    pairs = {}
+    for lst in _instr_lists(prog):
+        idx = list(lst)
+        for p, i in enumerate(idx):
+            ln = prog.instrs[i]
+            if ln.op != V.OP_LAYERNORM_AFFINE:
+                continue
+            h = ln.dst
+            gh = grp[h] if h < len(grp) else h
+            if h in io or gsize.get(gh, 1) != 1 or writers.get(gh, []) != [i]:
+                continue
+            rd = readers.get(gh, [])
+            if len(rd) != 1 or rd[0] not in lst:
+                continue
+            j = rd[0]
+            dot = prog.instrs[j]
+            if dot.op != V.OP_DOT or dot.a != h or j < i or not _gemv_form(dot, prog, cfg):
+                continue
+            M, N, K, G, aview, _, _, _ = _dot_fields(dot, prog)
+            if G != 1 or aview or M != ln.n or K != ln.imm:
+                continue
+            ins_reads = instr_reads(ln, prog)
+            between = idx[p + 1:idx.index(j)]
+            if any(prog.instrs[k].op in V.REGION_OPS or instr_writes(prog.instrs[k], prog) & ins_reads
+                   for k in between):
+                continue
+            pairs[j] = i
+    return pairs
 
 
 def instr_to_task(ins: V.Instr, prog: V.VMProgram, cfg: DeviceConfig) -> V.Task:
@@ -286,7 +382,7 @@ def instr_to_task(ins: V.Instr, prog: V.VMProgram, cfg: DeviceConfig) -> V.Task:
             # GEMV: one matrix row per tile through the segmented reduce in dot
             # mode (ops/dot.py:166-183).
             t = V.Task(V.TOP_RED_SEG, ins.dst, ins.a, ins.b, M, K, 0, 1)
-        elif cfg.gemv and gemv_eligible(M, N, K, G, aview, bview, epi, adt, dt, prog):
+        elif _gemv_form(ins, prog, cfg):
             t = V.Task(V.TOP_GEMV, ins.dst, ins.a, ins.b, M, N, K, G,
                        gemv_strip(N, G, cfg.nlanes, cfg.gemv_min_strip), 0, epi,
                        epi_res if epi else 0)
@@ -454,11 +550,18 @@ def task_cost(task: V.Task, cfg: DeviceConfig, prog: V.VMProgram) -> float:
 
 # --- phases ---------------------------------------------------------------------
 
-def _phases(prog, indices, tasks_of, fuse):
+def _phases(prog, indices, tasks_of, fuse, extra_reads=None):
     """Split ``indices`` (program order) into barrier-separated phases. A new
     phase starts when an instruction has a cross-lane dependency on a member
-    of the current phase (RAW, WAW or WAR through a shared buffer)."""
+    of the current phase (RAW, WAW or WAR through a shared buffer).
+    ``extra_reads``: {index: buffers} read beyond the instruction's own operands
+    (a GEMV staging a fused layernorm reads the layernorm's inputs)."""
     instrs = prog.instrs
+    extra_reads = extra_reads or {}
+
+    def reads(k):
+        r = instr_reads(instrs[k], prog)
+        return r | extra_reads[k] if k in extra_reads else r
     phases, cur = [], []
     readers: dict = {}
     writers: dict = {}
@@ -471,7 +574,7 @@ def _phases(prog, indices, tasks_of, fuse):
         wa, wb = instr_writes(a, prog), instr_writes(b, prog)
         if a.disjoint and a.disjoint == b.disjoint:
             wa, wb = wa - wb, wb - instr_writes(a, prog)
-        dep = (instr_reads(b, prog) & wa) or (wb & wa) or (instr_reads(a, prog) & wb)
+        dep = (reads(j) & wa) or (wb & wa) or (reads(i) & wb)
         if not dep:
             return False
         if not fuse:
@@ -482,7 +585,7 @@ def _phases(prog, indices, tasks_of, fuse):
     for j in indices:
         ins = instrs[j]
         cand = set()
-        for b in instr_reads(ins, prog):
+        for b in reads(j):
             cand.update(writers.get(b, ()))
         for b in instr_writes(ins, prog):
             cand.update(writers.get(b, ()))
@@ -493,7 +596,7 @@ def _phases(prog, indices, tasks_of, fuse):
             readers.clear()
             writers.clear()
         cur.append(j)
-        for b in instr_reads(ins, prog):
+        for b in reads(j):
             readers.setdefault(b, []).append(j)
         for b in instr_writes(ins, prog):
             writers.setdefault(b, []).append(j)
@@ -581,13 +684,21 @@ class _Scheduler:
         self.tasks: list = []
         self.task_of: dict = {}
         self.regions: list = []
+        # layernorms staged inside their GEMV: {dot index: layernorm index}
+        self.ln_pro = ln_gemv_pairs(prog, cfg)
+        self.ln_fused = set(self.ln_pro.values())
+        self.extra_reads = {j: instr_reads(prog.instrs[i], prog) for j, i in self.ln_pro.items()}
 
     def task_id(self, i: int) -> int:
         tid = self.task_of.get(i)
         if tid is None:
             tid = len(self.tasks)
             self.task_of[i] = tid
-            self.tasks.append(instr_to_task(self.prog.instrs[i], self.prog, self.cfg))
+            t = instr_to_task(self.prog.instrs[i], self.prog, self.cfg)
+            self.tasks.append(t)
+            if i in self.ln_pro:
+                # the layernorm's task is a descriptor only: no lane runs it
+                t.p5 = self.task_id(self.ln_pro[i]) + 1
         return tid
 
     def task(self, i: int) -> V.Task:
@@ -602,7 +713,7 @@ class _Scheduler:
 
         def flush():
             if seg:
-                for ph in _phases(self.prog, list(seg), self.task, self.cfg.fuse):
+                for ph in _phases(self.prog, list(seg), self.task, self.cfg.fuse, self.extra_reads):
                     out.append(("compute", ph))
                 seg.clear()
 
@@ -611,7 +722,7 @@ class _Scheduler:
             if op in V.REGION_OPS:
                 flush()
                 out.append(("region", i))
-            elif op != V.OP_NOP:
+            elif op != V.OP_NOP and i not in self.ln_fused:
                 seg.append(i)
         flush()
         return out

@@ -37,7 +37,9 @@ which does not use them is byte-for-byte a reference program):
   reference rejects (python/pjrt_ocl/ops/reduce.py:165-168);
 * tile op ``TOP_GEMV`` (20): the scheduler's column-strip form of an ``OP_DOT``
   with at most 8 rows (decode-time matmuls); p0 M, p1 N, p2 K, p3 G, p4 strip
-  width, p6 epilogue + 1, p7 residual;
+  width, p5 layernorm prologue (index + 1 of a ``LAYERNORM_SEG`` task that no
+  lane runs: the GEMV normalises its x rows while staging them), p6 epilogue +
+  1, p7 residual;
 * tensor opcode ``OP_DECODE_ATTN`` (68) / tile op ``TOP_DECODE_ATTN`` (21): one
   decode step of attention per head, over a cache prefix of runtime length plus
   the step's own key/value: ``out[h] = softmax(scale q[h] . [K^T[h, :, :pos],

@@ -543,6 +543,28 @@ def test_decode_attention_runs_twice_with_moving_position():
         lp.close()
 
 
+@pytest.mark.parametrize("dt,M,K,N,gelu", [("bf16", 1, 768, 2304, False), ("bf16", 3, 200, 96, True),
+                                           ("f16", 2, 512, 64, False), ("f32", 1, 300, 40, True)])
+def test_gemv_layernorm_prologue(dt, M, K, N, gelu):
+    """A layernorm read only by a skinny matmul runs inside the GEMV's x staging
+    (task p5): same result as the oracle (layernorm rounded to the matmul's
+    dtype, then the product) within the bf16 / f16 / f32 matmul bar."""
+    rng = np.random.default_rng(90 + K)
+    x = (rng.standard_normal((M, K)) * 2 + 0.5).astype(np.float32)
+    gam = rng.uniform(0.5, 1.5, K).astype(np.float32)
+    bet = rng.normal(0, 0.1, K).astype(np.float32)
+    w = rng.standard_normal((K, N)).astype(np.float32) / np.sqrt(K)
+    g = G.Graph()
+    X, GA, BE, W = g.input((M, K)), g.input((K,)), g.input((K,)), g.input((K, N), dt)
+    g.output(g.dot(g.layernorm(X, GA, BE, 1e-5, gelu=gelu, out_dtype=dt), W))
+    blob, _ = blob_for(g.build())
+    p = vmref.parse(blob)
+    assert any(tk.top == V.TOP_GEMV and tk.p[5] for tk in p.tasks)
+    got, want = run_both(blob, [x, gam, bet, w])
+    err = np.abs(got[0] - want[0]).max() / np.abs(want[0]).max()
+    assert err <= (1e-3 if dt == "f32" else 1e-2), err
+
+
 # --- loader validation ----------------------------------------------------------------------------
 
 def test_loader_rejects_out_of_bounds_task():

@@ -478,6 +478,34 @@ def test_planted_decode_new_key_is_caught(monkeypatch):
         test_decode_attention_brute_force(9)
 
 
+@pytest.mark.parametrize("M,gelu", [(1, False), (3, True)])
+def test_gemv_layernorm_prologue(M, gelu):
+    """A layernorm staged inside its GEMV (schedule-level fusion): the lane
+    simulator's result equals the tensor interpreter's, which stores the
+    layernorm result in bf16 and reads it back, and float64 math."""
+    rng = np.random.default_rng(31)
+    K, N = 96, 40
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    gam = rng.uniform(0.5, 1.5, K).astype(np.float32)
+    bet = rng.normal(0, 0.1, K).astype(np.float32)
+    w = vmref.bf16_to_f32(vmref.f32_to_bf16(rng.standard_normal((K, N)).astype(np.float32)))
+    g = G.Graph()
+    X, GA, BE, W = g.input((M, K)), g.input((K,)), g.input((K,)), g.input((K, N), "bf16")
+    g.output(g.dot(g.layernorm(X, GA, BE, 1e-5, gelu=gelu, out_dtype="bf16"), W))
+    prog = g.build()
+    cfg = S.DeviceConfig(nlanes=4, ew_ts=256, mma_t=64)
+    sched = S.schedule_program(prog, cfg)
+    assert any(t.tile_op == V.TOP_GEMV and t.p5 for t in sched.tasks)
+    (got,) = both(prog, [x, gam, bet, w], cfg)
+    mu = x.astype(np.float64).mean(1, keepdims=True)
+    var = ((x - mu) ** 2).mean(1, keepdims=True)
+    hn = (x - mu) / np.sqrt(var + 1e-5) * gam + bet
+    if gelu:
+        hn = 0.5 * hn * (1 + np.tanh(math.sqrt(2 / math.pi) * (hn + 0.044715 * hn ** 3)))
+    want = vmref.bf16_to_f32(vmref.f32_to_bf16(hn.astype(np.float32))).astype(np.float64) @ w
+    np.testing.assert_allclose(got, want, rtol=2e-2, atol=2e-2 * np.abs(want).max())
+
+
 # --- data movement -----------------------------------------------------------------------------
 
 def test_gather_scatter_dyn_embedding_brute_force():

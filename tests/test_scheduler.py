@@ -204,9 +204,11 @@ def test_gemv_epilogue_matches_tensor_semantics():
 
 
 def test_gemv_strips_cover_lanes():
-    for N, G_, want in [(2304, 1, 8), (32000, 1, 64), (768, 1, 8), (640, 12, 16), (64, 12, 8), (8, 1, 8)]:
+    for N, G_, want in [(2304, 1, 16), (32000, 1, 128), (768, 1, 16), (640, 12, 32), (64, 12, 16),
+                        (8, 1, 16), (4096, 16, 256)]:
         cw = S.gemv_strip(N, G_, 256)
-        assert cw == want and G_ * -(-N // cw) <= max(512, G_)
+        assert cw == want and G_ * -(-N // cw) <= max(256, G_)
+    assert S.gemv_strip(2304, 1, 256, min_strip=8) == 16 and S.gemv_strip(768, 1, 256, min_strip=8) == 8
 
 
 def test_gemv_lds_bound_falls_back_to_mma():
@@ -303,9 +305,10 @@ def test_decode_attention_rejects_bad_shapes():
 
 
 def test_gpt_decode_phases_per_layer():
-    """The C5 decode body: 7 barrier-separated phases per layer (LN, QKV with
-    the attention-residual add, attention, cache update with the output
-    projection, LN, FC with the MLP-residual add, projection)."""
+    """The C5 decode body: 5 barrier-separated phases per layer (QKV with its
+    layernorm staged inside and the attention-residual add, attention, cache
+    update with the output projection, FC with its layernorm and the
+    MLP-residual add, projection)."""
     import dataclasses
     from pjrt_amd import configs as CF
     counts = {}
@@ -315,4 +318,47 @@ def test_gpt_decode_phases_per_layer():
         fo = next(x for x in prog.instrs if x.op == V.OP_FOR)
         sc = S._Scheduler(prog, S.DeviceConfig(nlanes=256))
         counts[layers] = len(sc.levels(list(range(fo.n, fo.n + fo.imm))))
-    assert counts[2] - counts[1] == 7
+    assert counts[2] - counts[1] == 5
+
+
+def _ln_dot(extra=None):
+    g = G.Graph()
+    x = g.input((1, 64))
+    gam, bet = g.input((64,)), g.input((64,))
+    w = g.input((64, 32), "bf16")
+    h = g.layernorm(x, gam, bet, 1e-5, out_dtype="bf16")
+    if extra:
+        extra(g, x, h)
+    g.output(g.dot(h, w))
+    return g.build()
+
+
+def test_ln_gemv_prologue_fuses_single_reader():
+    """A layernorm read only by a GEMV runs inside it: the GEMV task's p5 names
+    the layernorm task, which no lane runs, and the program has one phase."""
+    prog = _ln_dot()
+    cfg = S.DeviceConfig(nlanes=8)
+    sched = S.schedule_program(prog, cfg)
+    gv = [t for t in sched.tasks if t.tile_op == V.TOP_GEMV]
+    assert len(gv) == 1 and gv[0].p5
+    ln = gv[0].p5 - 1
+    assert sched.tasks[ln].tile_op == V.TOP_LAYERNORM_SEG
+    assert all(e.task != ln for st in sched.lane_streams for e in st)
+    assert len(phases(sched)) == 1
+    off = S.schedule_program(prog, S.DeviceConfig(nlanes=8, ln_gemv=False))
+    assert len(phases(off)) == 2 and not any(t.p5 for t in off.tasks if t.tile_op == V.TOP_GEMV)
+
+
+@pytest.mark.parametrize("case", ["second_reader", "input_written", "output"])
+def test_ln_gemv_prologue_not_fused(case):
+    def second_reader(g, x, h):
+        g.output(g.convert(h, "f32"))
+
+    def input_written(g, x, h):
+        g.copy_into(x, g.add(x, x))
+
+    def output(g, x, h):
+        g.output(h)
+
+    prog = _ln_dot({"second_reader": second_reader, "input_written": input_written, "output": output}[case])
+    assert S.ln_gemv_pairs(prog, S.DeviceConfig(nlanes=8)) == {}

@@ -28,8 +28,9 @@ namespace vm {
 // Rows rp, rp + RP, ... of this thread's 8 columns.  Loads run in chunks of U rows
 // into two register buffers: chunk c+1 is in flight while chunk c is consumed.
 // Rows past K re-read row K - 1 and are not accumulated; col is always a valid
-// column group (callers clamp it), so no load sits behind a branch; xs rows past
-// M re-read row M - 1 (results unused).
+// column group (callers clamp it), so no load sits behind a branch (a load under
+// a lane-dependent branch makes the compiler wait for it before the join); xs
+// rows past M re-read row M - 1 (results unused).
 template <uint32_t ADT>
 struct GemvRaw {
   typedef v4u T;                          // 8 x 16-bit
@@ -69,7 +70,11 @@ VM_DEV void gemv_cvt(const typename GemvRaw<ADT>::T& r, float (&w)[8]) {
   }
 }
 
-constexpr int kGemvU = 8;                 // rows per load chunk and thread
+// Weight rows per load chunk and thread (two chunks in flight), and x elements
+// per thread staged from registers.
+template <uint32_t ADT>
+constexpr int gemv_u() { return 8; }
+constexpr int kGemvXU = 12;
 
 // f32 value as stored in dtype DT and read back
 template <uint32_t DT>
@@ -79,23 +84,44 @@ VM_DEV float gemv_round(float z) {
   else return z;
 }
 
-// Stage the M x K rows of x normalised by the layernorm task `lti` (the
+// The first kGemvXU * kBlock elements of x (flat index threadIdx.x + u kBlock) as
+// raw bits, all loads issued back to back and nothing converted yet, so that the
+// weight loads issued next are in flight before the first wait.  Indices past n
+// re-read element n - 1 (no load behind a branch); gemv_xcvt zeroes them.
+VM_DEV bool gemv_x_raw_ok(uint32_t dt) { return dt == DT_F32 || dt == DT_BF16 || dt == DT_F16; }
+VM_DEV void gemv_xraw(uint32_t (&r)[kGemvXU], const gbyte* src, uint32_t dt, uint32_t n) {
+  if (dt == DT_F32) {
+#pragma unroll
+    for (int u = 0; u < kGemvXU; ++u) r[u] = gcast<uint32_t>(src)[min(threadIdx.x + u * kBlock, n - 1)];
+  } else {
+#pragma unroll
+    for (int u = 0; u < kGemvXU; ++u) r[u] = gcast<uint16_t>(src)[min(threadIdx.x + u * kBlock, n - 1)];
+  }
+}
+VM_DEV void gemv_xcvt(const uint32_t (&r)[kGemvXU], float (&x)[kGemvXU], uint32_t dt, uint32_t n) {
+#pragma unroll
+  for (int u = 0; u < kGemvXU; ++u) {
+    const float v = dt == DT_F32 ? __uint_as_float(r[u]) : dt == DT_BF16 ? bf16_to_f32(uint16_t(r[u]))
+                                                                         : f16_to_f32(uint16_t(r[u]));
+    x[u] = threadIdx.x + u * kBlock < n ? v : 0.0f;
+  }
+}
+
+// Normalise the M x K rows staged in xs in place by the layernorm task L (the
 // LAYERNORM_SEG semantics: mean, two-pass or one-pass variance per its flags,
-// rsqrt(var + eps), affine, GELU), rounded to DT, into xs.  Each thread keeps the
-// same columns in every pass, so the in-place update needs no extra barrier.
+// rsqrt(var + eps), affine, GELU), rounded to DT as the layernorm's store would.
+// gv / bv: gamma / beta of columns threadIdx.x + u kBlock (K <= kGemvXU kBlock),
+// else read from memory.  Each thread keeps the same columns in every pass.
 template <uint32_t DT>
-VM_DEV void gemv_ln_stage(Args A, uint32_t lti, uint32_t M, uint32_t K, float* xs, float* red) {
-  const VM_K Task& L = task_of(A, lti);
+VM_DEV void gemv_ln_rows(Args A, const VM_K Task& L, uint32_t M, uint32_t K, float* xs, float* red,
+                         const float (&gv)[kGemvXU], const float (&bv)[kGemvXU]) {
   const uint32_t flags = L.p[3];
   const float eps = __uint_as_float(L.p[2]);
-  const uint32_t xdt = (L.tile_op >> 16) & 0xFF;
   const bool affine = flags & LN_AFFINE, do_gelu = flags & LN_GELU, two_pass = flags & LN_TWO_PASS;
-  const gbyte* x = resolve(A, L.a);
   const gbyte* gp = resolve(A, affine ? L.b : L.a);
   const gbyte* bp = resolve(A, affine ? L.p[4] : L.a);
+  const bool regs = K <= kGemvXU * kBlock;
   const float inv_n = 1.0f / float(K);
-  for (uint32_t m = 0; m < M; ++m)
-    for (uint32_t j = threadIdx.x; j < K; j += kBlock) xs[m * K + j] = load_f(x, xdt, uint64_t(m) * K + j);
   for (uint32_t m = 0; m < M; ++m) {
     float* row = xs + m * K;
     float s = 0.0f, s2 = 0.0f;
@@ -118,27 +144,40 @@ VM_DEV void gemv_ln_stage(Args A, uint32_t lti, uint32_t M, uint32_t K, float* x
     }
     const float rstd = rsqrtf(var + eps);
     const float shift = -mean * rstd;
-    for (uint32_t j = threadIdx.x; j < K; j += kBlock) {
-      float z = fmaf(row[j], rstd, shift);
-      if (affine) z = fmaf(z, load_f(gp, DT_F32, j), load_f(bp, DT_F32, j));
-      if (do_gelu) z = gelu(z);
-      row[j] = gemv_round<DT>(z);
+    if (regs) {
+#pragma unroll
+      for (int u = 0; u < kGemvXU; ++u) {
+        const uint32_t j = threadIdx.x + u * kBlock;
+        if (j < K) {
+          float z = fmaf(row[j], rstd, shift);
+          if (affine) z = fmaf(z, gv[u], bv[u]);
+          if (do_gelu) z = gelu(z);
+          row[j] = gemv_round<DT>(z);
+        }
+      }
+    } else {
+      for (uint32_t j = threadIdx.x; j < K; j += kBlock) {
+        float z = fmaf(row[j], rstd, shift);
+        if (affine) z = fmaf(z, load_f(gp, DT_F32, j), load_f(bp, DT_F32, j));
+        if (do_gelu) z = gelu(z);
+        row[j] = gemv_round<DT>(z);
+      }
     }
   }
 }
 
-template <uint32_t ADT>
-VM_DEV void gemv_issue(typename GemvRaw<ADT>::T (&raw)[kGemvU], const gbyte* b, uint32_t N, uint32_t K, uint32_t k,
+template <uint32_t ADT, int U>
+VM_DEV void gemv_issue(typename GemvRaw<ADT>::T (&raw)[U], const gbyte* b, uint32_t N, uint32_t K, uint32_t k,
                        uint32_t RP, uint32_t col) {
 #pragma unroll
-  for (int u = 0; u < kGemvU; ++u) raw[u] = gemv_ld<ADT>(b, uint64_t(min(k + u * RP, K - 1)) * N + col);
+  for (int u = 0; u < U; ++u) raw[u] = gemv_ld<ADT>(b, uint64_t(min(k + u * RP, K - 1)) * N + col);
 }
 
-template <uint32_t ADT, int MM>
-VM_DEV void gemv_consume(const typename GemvRaw<ADT>::T (&raw)[kGemvU], uint32_t M, uint32_t K, uint32_t k,
+template <uint32_t ADT, int U, int MM>
+VM_DEV void gemv_consume(const typename GemvRaw<ADT>::T (&raw)[U], uint32_t M, uint32_t K, uint32_t k,
                          uint32_t RP, const float* xs, float (&acc)[MM][8]) {
 #pragma unroll
-  for (int u = 0; u < kGemvU; ++u) {
+  for (int u = 0; u < U; ++u) {
     const uint32_t kk = k + u * RP;
     if (kk < K) {
       float w[8];
@@ -153,9 +192,14 @@ VM_DEV void gemv_consume(const typename GemvRaw<ADT>::T (&raw)[kGemvU], uint32_t
   }
 }
 
+// One tile.  Latency is its cost, so every global read it needs is issued
+// before the first wait: x (or the fused layernorm's input, gamma and beta),
+// the epilogue's residual values, then two weight chunks; later chunks are
+// issued as earlier ones are consumed.
 template <uint32_t ADT, int MM>
 VM_TILE void gemv_tile(Args A, uint32_t ti, uint32_t tile) {
   A = uargs(A);
+  constexpr int U = gemv_u<ADT>();
   const VM_K Task& t = task_of(A, ti);
   const uint32_t M = t.p[0], N = t.p[1], K = t.p[2], CW = t.p[4];
   const uint32_t ncb = (N + CW - 1) / CW;
@@ -170,32 +214,94 @@ VM_TILE void gemv_tile(Args A, uint32_t ti, uint32_t tile) {
   float* xs = reinterpret_cast<float*>(vm_smem);
   float* red = xs + ((M * K + 3) & ~3u);
   float* tmp = red + 2048 * M;
+  const uint32_t nx = M * K;
+
+  // x, or the fused layernorm's input with its gamma / beta, as raw bits
+  const bool lnp = t.p[5] != 0;
+  const VM_K Task& L = task_of(A, lnp ? t.p[5] - 1 : ti);
+  const gbyte* xsrc = lnp ? resolve(A, L.a) : a;
+  const uint32_t xdt = lnp ? (L.tile_op >> 16) & 0xFF : ADT;
+  const bool lnaff = lnp && (L.p[3] & LN_AFFINE);
+  const bool xreg = gemv_x_raw_ok(xdt);
+  uint32_t xr[kGemvXU], gr[kGemvXU], br[kGemvXU];
+  if (xreg) gemv_xraw(xr, xsrc, xdt, nx);
+  if (lnaff) {
+    gemv_xraw(gr, resolve(A, L.b), DT_F32, K);
+    gemv_xraw(br, resolve(A, L.p[4]), DT_F32, K);
+  }
+  // the epilogue's residual values of this thread's first output
+  const uint32_t epi = t.p[6];
+  const VM_K int32_t* e = aux_of(A) + (epi ? epi - 1 : 0);
+  const int nm = epi ? e[0] : 0;
+  const gbyte* res = epi ? resolve(A, t.p[7]) : nullptr;
+  bool src1 = false, src2 = false;
+  for (int k = 0; k < nm; ++k) {
+    src1 |= e[2 + 4 * k] == 1;
+    src2 |= e[2 + 4 * k] == 2;
+  }
+  const uint32_t outs = M * CW;
+  float ry1 = 0.0f, ry2 = 0.0f;
+  {
+    // clamped to a valid output so the loads sit behind no branch
+    const uint32_t o = min(uint32_t(threadIdx.x), outs - 1), m = o / CW, n = min(nb * CW + o % CW, N - 1);
+    if (src1) ry1 = gcast<float>(res)[(uint64_t(g) * M + m) * N + n];
+    if (src2) ry2 = gcast<float>(res)[n];
+  }
 
   const uint32_t cg = threadIdx.x % cgs, rp = threadIdx.x / cgs;
   // column groups past N (the last strip's tail) read the last group instead
   const uint32_t col = min(nb * CW + cg * 8, N - 8);
-  // the first weight chunk is in flight while x is staged
-  typename GemvRaw<ADT>::T r0[kGemvU], r1[kGemvU];
-  gemv_issue<ADT>(r0, b, N, K, rp, RP, col);
+  const uint32_t step = U * RP;
+  typename GemvRaw<ADT>::T r0[U], r1[U];
+  gemv_issue<ADT, U>(r0, b, N, K, rp, RP, col);
+  if (step < K) gemv_issue<ADT, U>(r1, b, N, K, step + rp, RP, col);
+
+  float xv[kGemvXU], gv[kGemvXU], bv[kGemvXU];
+  if (xreg) gemv_xcvt(xr, xv, xdt, nx);
+  if (lnaff) {
+    gemv_xcvt(gr, gv, DT_F32, K);
+    gemv_xcvt(br, bv, DT_F32, K);
+  }
   __syncthreads();                       // the previous user of the LDS is done
-  if (t.p[5]) gemv_ln_stage<ADT>(A, t.p[5] - 1, M, K, xs, red);
-  else
-    for (uint32_t i = threadIdx.x; i < M * K; i += kBlock) xs[i] = load_f(a, ADT, i);
+  if (xreg) {
+#pragma unroll
+    for (int u = 0; u < kGemvXU; ++u) {
+      const uint32_t i = threadIdx.x + u * kBlock;
+      if (i < nx) xs[i] = xv[u];
+    }
+  }
+  if (xreg) {
+    // rows longer than the register window: batches of kGemvXU loads in flight
+    for (uint32_t i0 = kGemvXU * kBlock; i0 < nx; i0 += kGemvXU * kBlock) {
+      gemv_xraw(xr, xsrc + uint64_t(i0) * (xdt == DT_F32 ? 4 : 2), xdt, nx - i0);
+      gemv_xcvt(xr, xv, xdt, nx - i0);
+#pragma unroll
+      for (int u = 0; u < kGemvXU; ++u) {
+        const uint32_t i = i0 + threadIdx.x + u * kBlock;
+        if (i < nx) xs[i] = xv[u];
+      }
+    }
+  } else {
+    for (uint32_t i = threadIdx.x; i < nx; i += kBlock) xs[i] = load_f(xsrc, xdt, i);
+  }
   __syncthreads();
+  if (lnp) {
+    gemv_ln_rows<ADT>(A, L, M, K, xs, red, gv, bv);
+    __syncthreads();
+  }
 
   float acc[MM][8];
 #pragma unroll
   for (int m = 0; m < MM; ++m)
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc[m][j] = 0.0f;
-  // uniform loop over chunk pairs; the prefetch is unconditional (clamped rows)
-  const uint32_t step = kGemvU * RP;
+  // uniform loop over chunk pairs, two chunks in flight
   for (uint32_t kb = 0; kb < K; kb += 2 * step) {
-    gemv_issue<ADT>(r1, b, N, K, kb + step + rp, RP, col);
-    gemv_consume<ADT, MM>(r0, M, K, kb + rp, RP, xs, acc);
+    gemv_consume<ADT, U, MM>(r0, M, K, kb + rp, RP, xs, acc);
+    if (kb + 2 * step < K) gemv_issue<ADT, U>(r0, b, N, K, kb + 2 * step + rp, RP, col);
     if (kb + step >= K) break;
-    gemv_issue<ADT>(r0, b, N, K, kb + 2 * step + rp, RP, col);
-    gemv_consume<ADT, MM>(r1, M, K, kb + step + rp, RP, xs, acc);
+    gemv_consume<ADT, U, MM>(r1, M, K, kb + step + rp, RP, xs, acc);
+    if (kb + 3 * step < K) gemv_issue<ADT, U>(r1, b, N, K, kb + 3 * step + rp, RP, col);
   }
 #pragma unroll
   for (int m = 0; m < MM; ++m)
@@ -206,7 +312,6 @@ VM_TILE void gemv_tile(Args A, uint32_t ti, uint32_t tile) {
 
   // Sum the RP row phases of each of the M * CW outputs in a fixed order: J
   // threads per output each add every J-th phase, then one thread adds the J.
-  const uint32_t outs = M * CW;
   const uint32_t J = outs >= kBlock ? 1u : kBlock / outs;
   for (uint32_t i = threadIdx.x; i < outs * J; i += kBlock) {
     const uint32_t o = i % outs, j = i / outs;
@@ -217,22 +322,19 @@ VM_TILE void gemv_tile(Args A, uint32_t ti, uint32_t tile) {
   __syncthreads();
 
   const uint32_t dt = (t.tile_op >> 8) & 0xFF;
-  const uint32_t epi = t.p[6];
   gbyte* d = resolve(A, t.dst);
-  const VM_K int32_t* e = aux_of(A) + (epi ? epi - 1 : 0);
-  const int nm = epi ? e[0] : 0;
-  const gbyte* res = epi ? resolve(A, t.p[7]) : nullptr;
   for (uint32_t o = threadIdx.x; o < outs; o += kBlock) {
     const uint32_t m = o / CW, n = nb * CW + o % CW;
     if (n >= N) continue;
     float x = 0.0f;
     for (uint32_t j = 0; j < J; ++j) x += tmp[j * outs + o];
     const uint64_t elem = (uint64_t(g) * M + m) * N + n;
+    const bool first = o == threadIdx.x;
     for (int k = 0; k < nm; ++k) {
       const uint32_t kind = uint32_t(e[1 + 4 * k]), src = uint32_t(e[2 + 4 * k]);
       float y = x;
-      if (src == 1) y = gcast<float>(res)[elem];
-      else if (src == 2) y = gcast<float>(res)[n];
+      if (src == 1) y = first ? ry1 : gcast<float>(res)[elem];
+      else if (src == 2) y = first ? ry2 : gcast<float>(res)[n];
       x = epi_inline(kind, x, y, __int_as_float(e[3 + 4 * k]), __int_as_float(e[4 + 4 * k]));
     }
     store_f(d, dt, elem, x);

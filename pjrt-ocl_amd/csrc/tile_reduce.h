@@ -813,12 +813,35 @@ VM_TILE void argmax_tiles(Args A, uint32_t ti, uint32_t lo, uint32_t hi) {
     const uint64_t base = uint64_t(o) * seg;
     float bv = -INFINITY;
     uint32_t bi = 0xFFFFFFFFu;
-    for (uint32_t j = threadIdx.x; j < seg; j += kBlock) {
-      const float v = load_f(a, adt, base + j);
+    auto take = [&](float v, uint32_t j) {
       if (bi == 0xFFFFFFFFu || amax_better(v, j, bv, bi)) {
         bv = v;
         bi = j;
       }
+    };
+    if (adt == DT_F32 && (seg & 3) == 0 && ((uintptr_t(a) & 15) == 0)) {
+      // f32 rows (logits): 16-byte loads, 16 of them in flight per thread; each
+      // thread still visits its elements in increasing index order
+      const VM_G v4f* row = (const VM_G v4f*)(a + base * 4);
+      const uint32_t n4 = seg >> 2;
+      constexpr int U = 16;
+      for (uint32_t q0 = threadIdx.x; q0 < n4; q0 += U * kBlock) {
+        v4f v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) v[u] = row[min(q0 + u * kBlock, n4 - 1)];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const uint32_t q = q0 + u * kBlock;
+          if (q < n4) {
+            take(v[u].x, 4 * q);
+            take(v[u].y, 4 * q + 1);
+            take(v[u].z, 4 * q + 2);
+            take(v[u].w, 4 * q + 3);
+          }
+        }
+      }
+    } else {
+      for (uint32_t j = threadIdx.x; j < seg; j += kBlock) take(load_f(a, adt, base + j), j);
     }
     lds_barrier();
     sv[threadIdx.x] = bv;

@@ -181,12 +181,18 @@ def test_integer_reductions_bit_exact(dt, kind):
         np.testing.assert_array_equal(gv, wv, err_msg=f"{dt} kind {kind} out {k}")
 
 
-def test_argmax_rows():
+@pytest.mark.parametrize("rows,seg", [(33, 513), (7, 516), (5, 32000)])
+def test_argmax_rows(rows, seg):
+    """First index of the row maximum, a NaN winning (its first index); f32 rows
+    of a multiple of 4 take the 16-byte-load path."""
     rng = np.random.default_rng(40)
-    a = rng.standard_normal((33, 513)).astype(np.float32)
+    a = rng.standard_normal((rows, seg)).astype(np.float32)
     a[3, 100] = a[3].max() + 1
     a[3, 200] = a[3, 100]          # tie: first index wins
-    a[5, 7] = np.nan
+    a[4, seg - 1] = a[4].max() + 1
+    a[4, seg // 2 + 1] = a[4, seg - 1]   # tie across threads' ranges
+    a[1, seg - 2] = np.nan
+    a[1, seg - 1] = np.nan
     g = G.Graph()
     x = g.input(a.shape)
     val, idx = g.argmax_last(x)

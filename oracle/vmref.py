@@ -936,12 +936,14 @@ class TaskRunner:
                     out[g, tile % T] = O[tile % T]
         self.m.store_f(t.dst, slice(0, H * T * hd), out.reshape(-1), t.dt)
 
-    # 21: decode-step attention, one head per tile (extension)
+    # 21: decode-step attention (extension): tile = head * S + split, p4 = H | S << 16;
+    # a head's result is complete once its last split has run
     def top21(self, t, lo, hi):
-        H, hd, C = t.p[4], t.p[5], t.p[6]
-        h0, h1 = lo, min(hi, H)
-        if h0 >= h1:
+        H, S, hd, C = t.p[4] & 0xFFFF, max(1, t.p[4] >> 16), t.p[5], t.p[6]
+        heads = [tile // S for tile in range(lo, min(hi, H * S)) if tile % S == S - 1]
+        if not heads:
             return
+        h0, h1 = heads[0], heads[-1] + 1
         ld = lambda bid, n: self.m.load_f(bid, t.adt)[:n]
         q = ld(t.a, H * hd).reshape(H, hd)
         Kt = ld(t.b, H * hd * C).reshape(H, hd, C)
@@ -1128,7 +1130,7 @@ def _whole_tiles(t: Task, ew_ts: int, mma_t: int) -> int:
     if t.top == 20:
         return max(1, p[3]) * -(-p[1] // p[4])
     if t.top == 21:
-        return max(1, p[4])
+        return max(1, (p[4] & 0xFFFF) * max(1, p[4] >> 16))
     raise NotImplementedError(t.top)
 
 

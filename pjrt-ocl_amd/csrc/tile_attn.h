@@ -112,7 +112,7 @@ VM_DEV void attn_block_mfma(Args A, uint32_t ti, uint32_t h, uint32_t row0, uint
   vhi = uni(vhi);
   typedef AttnLds<HD> L;
   const uint32_t T = P.T, C = P.C, dt = (t.tile_op >> 8) & 0xFF;
-  uint16_t* lds = reinterpret_cast<uint16_t*>(vm_smem);
+  uint16_t* lds = lds_ptr<uint16_t>();
   constexpr int KS = HD / 16;            // MFMA steps over hd for S
   constexpr int DB = HD / 32;            // 32-row d blocks of O^T
   const uint32_t lane = threadIdx.x & 63, wave = uni(threadIdx.x >> 6), g = lane >> 5;

@@ -15,28 +15,30 @@
 // key and value are read from where the projection wrote them, which lets the
 // cache update run after this op, beside the next matmul.
 //
+// A head's keys can be split S ways (tile = head * S + split): each split
+// streams its slice of the cache with its own CU and leaves its partial result
+// (running maximum, sum, unnormalised output) in the task's scratch; the split
+// that arrives last at the head's counter combines the S partials in split
+// order (deterministic whichever arrives last) and resets the counter.  One CU
+// moves only so many bytes per microsecond, so spreading a head over CUs is
+// what shortens the step.
+//
 // Task: a q, b K^T cache [H, hd, C], p0 V cache [H, C, hd], p1 k, p2 v, p3 pos
-// (i32 scalar, clamped to [0, C]), p4 H, p5 hd (multiple of 8, <= 256), p6 C
-// (multiple of 8), p7 scale bits.  One dtype (bf16 / f16 / f32) for every
-// operand and the output; f32 arithmetic.
+// (i32 scalar, clamped to [0, C]), p4 H | S << 16 (S <= 1: no split), p5 hd
+// (multiple of 8, <= 256), p6 C (multiple of 8), p7 scale bits.  One dtype
+// (bf16 / f16 / f32) for every operand and the output; f32 arithmetic.
+// Scratch (S > 1): [H * S][hd + 2] partials {max, sum, hd channels}, then H
+// arrival counters.
 #pragma once
 #include "tile_gemv.h"
 
 namespace vm {
 
-constexpr uint32_t kDecKeys = 1024;                 // keys per chunk: 128 octets of 8
-// LDS, in floats: q [256], reduction slots [16], chunk scores / probabilities
-// [1024], then the two score halves [2][1024], reused for the P.V partials
-constexpr uint32_t kDecQ = 0, kDecRed = 256, kDecS = 272, kDecPart = kDecS + kDecKeys;
-constexpr uint32_t kDecLdsBytes = (kDecPart + 2 * kDecKeys) * 4;
-
-VM_DEV float dec_block_max(float x, float* red) {
-  x = wave_max(x);
-  __syncthreads();
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = x;
-  __syncthreads();
-  return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-}
+constexpr uint32_t kDecKU = 8;                      // K / V 16-byte loads per thread at most
+// LDS, in floats: scores / probabilities [64], reduction slots [16], the P.V
+// partials [2048], their first-pass sums [256]
+constexpr uint32_t kDecS = 0, kDecRed = 64, kDecPart = 80, kDecTmp = kDecPart + 2048;
+constexpr uint32_t kDecLdsBytes = (kDecTmp + 256) * 4;
 
 VM_DEV float dec_block_sum(float x, float* red) {
   x = wave_sum(x);
@@ -47,162 +49,246 @@ VM_DEV float dec_block_sum(float x, float* red) {
 }
 
 template <uint32_t DT>
-VM_TILE void decode_attn_head(Args A, uint32_t ti, uint32_t h) {
+VM_DEV void dec_cvt8(const typename GemvRaw<DT>::T& r, float (&w)[8]) { gemv_cvt<DT>(r, w); }
+
+// One split of one head.  Every global read the tile needs is issued before
+// the first wait (the split's key range is fixed by C and S, not by pos): pos,
+// q, the step's own k and v, the split's K^T columns and V rows.  So the tile
+// pays one memory round trip, then the scores, the softmax and P.V come out of
+// registers, lane shuffles and LDS.
+template <uint32_t DT>
+VM_TILE void decode_attn_split(Args A, uint32_t ti, uint32_t tile) {
   A = uargs(A);
   const VM_K Task& t = task_of(A, ti);
   const uint32_t hd = t.p[5], C = t.p[6];
+  const uint32_t H = t.p[4] & 0xFFFF, S = max(1u, t.p[4] >> 16);
   const float scale = __uint_as_float(t.p[7]);
-  h = uni(h);
+  tile = uni(tile);
+  const uint32_t h = tile / S, split = tile % S;
   constexpr uint32_t esz = DT == DT_F32 ? 4 : 2;
-  constexpr int kU = DT == DT_F32 ? 8 : 16;          // loads per batch and thread
   typedef typename GemvRaw<DT>::T Raw;
   const gbyte* q = resolve(A, t.a) + uint64_t(h) * hd * esz;
   const gbyte* kt = resolve(A, t.b) + uint64_t(h) * hd * C * esz;
   const gbyte* vc = resolve(A, t.p[0]) + uint64_t(h) * C * hd * esz;
   const gbyte* kn = resolve(A, t.p[1]) + uint64_t(h) * hd * esz;
   const gbyte* vn = resolve(A, t.p[2]) + uint64_t(h) * hd * esz;
-  const int64_t praw = read_index(resolve(A, t.p[3]), false);
-  const uint32_t pos = uni(uint32_t(praw < 0 ? 0 : praw > int64_t(C) ? int64_t(C) : praw));
-  const uint32_t n = pos + 1;                        // keys, the step's own included
+  // the split's cache keys [k0, k0 + nk): whole octets (C is a multiple of 8)
+  const uint32_t per = ((C + S - 1) / S + 7) & ~7u;          // <= kDecSplitKeys (loader check)
+  const uint32_t k0 = min(split * per, C), nk = min(per, C - k0);
+  const uint32_t tid = threadIdx.x, lane = tid & 63;
 
-  float* lds = reinterpret_cast<float*>(vm_smem);
-  float* qs = lds + kDecQ;
-  float* red = lds + kDecRed;
-  float* sc = lds + kDecS;
-  float* part = lds + kDecPart;
-  const uint32_t tid = threadIdx.x;
-
-  __syncthreads();                                   // the previous user of the LDS is done
+  // ---- every read up front -----------------------------------------------------
+  const int32_t praw = __hip_atomic_load((const int32_t*)resolve(A, t.p[3]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // scores: thread (octet o = tid / 32, channel group dg = tid % 32) holds
+  // channels dg, dg + 32, ... of keys [k0 + 8 o, +8); octets past nk re-read
+  // the last one (discarded), channels past hd re-read hd - 1 (not accumulated)
+  const uint32_t o = tid >> 5, dg = tid & 31;
+  const uint32_t oc = nk ? min(o, nk / 8 - 1) : 0;
+  const uint32_t kcol = min(k0 + 8 * oc, C - 8);
+  const uint32_t dpt = (hd + 31) / 32;                        // <= kDecKU
+  Raw kr[kDecKU];
+  float qd[kDecKU];
+#pragma unroll
+  for (uint32_t u = 0; u < kDecKU; ++u)
+    if (u < dpt) {                                            // uniform: dpt is
+      const uint32_t d = min(dg + 32 * u, hd - 1);
+      kr[u] = gemv_ld<DT>(kt, uint64_t(d) * C + kcol);
+      qd[u] = load_f(q, DT, d);
+    }
+  // P.V: thread (cg = tid % cgs, rg = tid / cgs) holds channels [8 cg, +8) of
+  // rows rg, rg + rpp, ...; rows past nk re-read the last row (not accumulated)
+  const uint32_t cgs = hd / 8, rpp = kBlock / cgs;
+  const uint32_t cg = tid % cgs, rg = min(tid / cgs, rpp - 1);
+  const uint32_t vpt = (per + rpp - 1) / rpp;                 // <= kDecKU
+  Raw vr[kDecKU];
+#pragma unroll
+  for (uint32_t u = 0; u < kDecKU; ++u)
+    if (u < vpt) {
+      const uint32_t r = nk ? min(rg + rpp * u, nk - 1) : 0;
+      vr[u] = gemv_ld<DT>(vc, (uint64_t(min(k0 + r, C - 1)) * hd + cg * 8));
+    }
+  const Raw vnew = gemv_ld<DT>(vn, cg * 8);
   float qn = 0.0f;
+  if (tid < hd) qn = load_f(q, DT, tid) * load_f(kn, DT, tid);
+
+  float* lds = lds_ptr<float>();
+  float* sc = lds + kDecS;
+  float* red = lds + kDecRed;
+  float* part = lds + kDecPart;
+  float* tmp = lds + kDecTmp;
+  __syncthreads();                                   // the previous user of the LDS is done
+  const float s_new = dec_block_sum(qn, red) * scale;   // the step's own key
+  const uint32_t pos = uni(uint32_t(praw < 0 ? 0 : praw > int32_t(C) ? int32_t(C) : praw));
+
+  // ---- scores of the split's cache keys ---------------------------------------
+  float acc[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) acc[j] = 0.0f;
+#pragma unroll
+  for (uint32_t u = 0; u < kDecKU; ++u)
+    if (u < dpt && dg + 32 * u < hd) {
+      float w[8];
+      gemv_cvt<DT>(kr[u], w);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[j] = fmaf(qd[u], w[j], acc[j]);
+    }
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+    for (int msk = 16; msk >= 1; msk >>= 1) acc[j] += __shfl_xor(acc[j], msk, 64);
+  if (dg == 0 && 8 * o < nk)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) sc[8 * o + j] = acc[j] * scale;
+  __syncthreads();
+
+  // ---- softmax over the split's keys up to pos (wave 0) -----------------------
+  // key pos is the step's own (its cache column is not written yet)
+  float m = -INFINITY, l = 0.0f;
+  if (tid < 64) {
+    const uint32_t key = k0 + lane;
+    float sv = -INFINITY;
+    if (lane < nk && key <= pos) sv = key == pos ? s_new : sc[lane];
+    m = wave_max(sv);
+    const float p = sv == -INFINITY ? 0.0f : expf(sv - m);
+    l = wave_sum(p);
+    sc[lane] = p;
+    if (lane == 0) {
+      red[8] = m;
+      red[9] = l;
+    }
+  }
+  // the step's own key when it lies past the cache (pos == C) belongs to the
+  // last split
+  const bool own_extra = pos == C && split == S - 1;
+  __syncthreads();
+  m = red[8];
+  l = red[9];
+  float p_own = 0.0f;
+  if (own_extra) {                                   // one more key: rescale
+    const float mn = fmaxf(m, s_new);
+    const float a = m == -INFINITY ? 0.0f : expf(m - mn);
+    p_own = expf(s_new - mn);
+    l = l * a + p_own;
+    // the cache keys' probabilities are rescaled by a below
+    for (uint32_t j = tid; j < 64; j += kBlock) sc[j] *= a;
+    m = mn;
+    __syncthreads();
+  }
+
+  // ---- P.V ----------------------------------------------------------------------
+  float ov[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) ov[j] = 0.0f;
+  if (tid / cgs < rpp) {
+#pragma unroll
+    for (uint32_t u = 0; u < kDecKU; ++u) {
+      const uint32_t r = rg + rpp * u;
+      if (u < vpt && r < nk) {
+        float w[8];
+        gemv_cvt<DT>(k0 + r == pos ? vnew : vr[u], w);
+        const float p = sc[r];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) ov[j] = fmaf(p, w[j], ov[j]);
+      }
+    }
+    if (own_extra && rg == 0) {
+      float w[8];
+      gemv_cvt<DT>(vnew, w);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) ov[j] = fmaf(p_own, w[j], ov[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) part[rg * hd + cg * 8 + j] = ov[j];
+  }
+  __syncthreads();
+  // sum the rpp row groups in a fixed order: J threads per channel, then one
+  const uint32_t J = kBlock / hd;
+  {
+    const uint32_t c = tid % hd, jj = tid / hd;
+    if (jj < J) {
+      float v = 0.0f;
+      for (uint32_t r = jj; r < rpp; r += J) v += part[r * hd + c];
+      tmp[jj * hd + c] = v;
+    }
+  }
+  __syncthreads();
+  float oacc = 0.0f;
+  if (tid < hd)
+    for (uint32_t jj = 0; jj < J; ++jj) oacc += tmp[jj * hd + tid];
+
+  gbyte* out = resolve(A, t.dst) + uint64_t(h) * hd * esz;
+  if (S == 1) {
+    if (tid < hd) store_f(out, DT, tid, oacc / l);
+    return;
+  }
+  // split: publish the partial, count the arrival; the last split combines.
+  // Partials and counters move as agent-scope atomics, which go to memory past
+  // the XCD's L2, so no L2-wide write-back (release fence) is needed: the
+  // stores are complete (vmcnt) before the counter moves, and the combining
+  // split reads them back past its own L2.
+  uint32_t* sp = reinterpret_cast<uint32_t*>(A->scratch + A->task_scratch[ti]);
+  uint32_t* arrivals = sp + uint64_t(H) * S * (hd + 2);
+  uint32_t* mine = sp + uint64_t(h * S + split) * (hd + 2);
+  if (tid < hd) __hip_atomic_store(mine + 2 + tid, __float_as_uint(oacc), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (tid == 0) {
+    __hip_atomic_store(mine, __float_as_uint(m), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(mine + 1, __float_as_uint(l), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __builtin_amdgcn_s_waitcnt(0x0F70);                 // vmcnt(0): this thread's stores are done
+  __syncthreads();
+  uint32_t* flag = reinterpret_cast<uint32_t*>(red + 12);
+  if (tid == 0) {
+    const uint32_t before = __hip_atomic_fetch_add(arrivals + h, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const bool last = before == S - 1;
+    // reset for the next run of this task (ordered before it by a grid barrier)
+    if (last) __hip_atomic_store(arrivals + h, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *flag = last;
+  }
+  __syncthreads();
+  if (!*flag) return;
+  // combine in split order; every read issued in parallel
+  const uint32_t* hp = sp + uint64_t(h) * S * (hd + 2);
+  auto rd = [](const uint32_t* p) {
+    return __uint_as_float(__hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+  };
+  float* ms = part;                                  // [S] maxima, then weights
+  float* ls = part + kDecMaxSplits;                  // [S] sums
+  for (uint32_t k = tid; k < S; k += kBlock) {
+    ms[k] = rd(hp + k * (hd + 2));
+    ls[k] = rd(hp + k * (hd + 2) + 1);
+  }
+  __syncthreads();
+  float M = -INFINITY;
+  for (uint32_t k = 0; k < S; ++k) M = fmaxf(M, ms[k]);
+  __syncthreads();
+  for (uint32_t k = tid; k < S; k += kBlock) ms[k] = ms[k] == -INFINITY ? 0.0f : expf(ms[k] - M);
+  __syncthreads();
   if (tid < hd) {
-    const float qv = load_f(q, DT, tid);
-    qs[tid] = qv;
-    qn = qv * load_f(kn, DT, tid);
+    float L = 0.0f, O = 0.0f;
+    constexpr int B = 8;
+    for (uint32_t k0b = 0; k0b < S; k0b += B) {
+      float o8[B];
+#pragma unroll
+      for (int u = 0; u < B; ++u) o8[u] = rd(hp + min(k0b + u, S - 1) * (hd + 2) + 2 + tid);
+#pragma unroll
+      for (int u = 0; u < B; ++u)
+        if (k0b + u < S) {
+          L = fmaf(ls[k0b + u], ms[k0b + u], L);
+          O = fmaf(o8[u], ms[k0b + u], O);
+        }
+    }
+    store_f(out, DT, tid, O / L);
   }
-  const float s_new = dec_block_sum(qn, red) * scale;   // the step's own key (syncs: qs visible)
-
-  // score pass: thread (octet o, half hh) owns keys [8o, 8o + 8) of the chunk
-  // over channels [hh hd/2, (hh + 1) hd/2)
-  const uint32_t o = tid & 127, hh = tid >> 7;
-  const uint32_t dh = hd / 2, d0 = hh * dh, dend = d0 + dh;
-  // P.V pass: gsz threads per V row (8 channels each), R rows at a time
-  const uint32_t gsz = hd / 8, R = kBlock / gsz;
-  const uint32_t cgi = tid % gsz, rgi = tid / gsz;
-
-  float m = -INFINITY, l = 0.0f, oacc = 0.0f;
-  for (uint32_t c0 = 0; c0 < n; c0 += kDecKeys) {
-    const uint32_t cnt = min(kDecKeys, n - c0);
-    const uint32_t kb = c0 + 8 * o;
-    float acc[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) acc[j] = 0.0f;
-    if (kb < pos) {                                  // kb + 8 <= C: C is a multiple of 8
-      Raw ra[kU], rb[kU];
-      auto issue = [&](Raw (&r)[kU], uint32_t d) {
-#pragma unroll
-        for (int u = 0; u < kU; ++u) r[u] = gemv_ld<DT>(kt, uint64_t(min(d + u, dend - 1)) * C + kb);
-      };
-      auto consume = [&](const Raw (&r)[kU], uint32_t d) {
-#pragma unroll
-        for (int u = 0; u < kU; ++u)
-          if (d + u < dend) {
-            float w[8];
-            gemv_cvt<DT>(r[u], w);
-            const float qd = qs[d + u];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) acc[j] = fmaf(qd, w[j], acc[j]);
-          }
-      };
-      issue(ra, d0);
-      for (uint32_t d = d0;; d += 2 * kU) {
-        if (d + kU < dend) issue(rb, d + kU);
-        consume(ra, d);
-        if (d + kU >= dend) break;
-        if (d + 2 * kU < dend) issue(ra, d + 2 * kU);
-        consume(rb, d + kU);
-        if (d + 2 * kU >= dend) break;
-      }
-    }
-    *(v4f*)(part + hh * kDecKeys + 8 * o) = v4f{acc[0], acc[1], acc[2], acc[3]};
-    *(v4f*)(part + hh * kDecKeys + 8 * o + 4) = v4f{acc[4], acc[5], acc[6], acc[7]};
-    __syncthreads();
-
-    float mx = -INFINITY;
-    for (uint32_t j = tid; j < cnt; j += kBlock) {
-      const float s = c0 + j == pos ? s_new : (part[j] + part[kDecKeys + j]) * scale;
-      sc[j] = s;
-      mx = fmaxf(mx, s);
-    }
-    const float mnew = fmaxf(m, dec_block_max(mx, red));
-    const float alpha = expf(m - mnew);              // 0 on the first chunk
-    float ps = 0.0f;
-    for (uint32_t j = tid; j < cnt; j += kBlock) {
-      const float p = expf(sc[j] - mnew);
-      sc[j] = p;
-      ps += p;
-    }
-    l = l * alpha + dec_block_sum(ps, red);          // syncs: sc and part free / visible
-    m = mnew;
-
-    // P.V over the chunk's rows; rows past cnt re-read the chunk's last row and
-    // are not accumulated, so no load sits behind a branch
-    float pacc[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) pacc[j] = 0.0f;
-    if (rgi < R) {
-      auto vrow = [&](uint32_t r) -> const gbyte* {
-        const uint32_t key = c0 + min(r, cnt - 1);
-        return key == pos ? vn + cgi * 8 * esz : vc + (uint64_t(key) * hd + cgi * 8) * esz;
-      };
-      Raw va[kU], vb[kU];
-      auto issue = [&](Raw (&r)[kU], uint32_t r0) {
-#pragma unroll
-        for (int u = 0; u < kU; ++u) r[u] = gemv_ld<DT>(vrow(r0 + u * R), 0);
-      };
-      auto consume = [&](const Raw (&r)[kU], uint32_t r0) {
-#pragma unroll
-        for (int u = 0; u < kU; ++u)
-          if (r0 + u * R < cnt) {
-            float w[8];
-            gemv_cvt<DT>(r[u], w);
-            const float p = sc[r0 + u * R];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) pacc[j] = fmaf(p, w[j], pacc[j]);
-          }
-      };
-      const uint32_t step = kU * R;
-      issue(va, rgi);
-      for (uint32_t r = rgi;; r += 2 * step) {
-        if (r + step < cnt) issue(vb, r + step);
-        consume(va, r);
-        if (r + step >= cnt) break;
-        if (r + 2 * step < cnt) issue(va, r + 2 * step);
-        consume(vb, r + step);
-        if (r + 2 * step >= cnt) break;
-      }
-      *(v4f*)(part + rgi * hd + cgi * 8) = v4f{pacc[0], pacc[1], pacc[2], pacc[3]};
-      *(v4f*)(part + rgi * hd + cgi * 8 + 4) = v4f{pacc[4], pacc[5], pacc[6], pacc[7]};
-    }
-    __syncthreads();
-    if (tid < hd) {
-      float s = 0.0f;
-      for (uint32_t g = 0; g < R; ++g) s += part[g * hd + tid];
-      oacc = oacc * alpha + s;
-    }
-    __syncthreads();                                 // part / sc reused by the next chunk
-  }
-  if (tid < hd) store_f(resolve(A, t.dst) + uint64_t(h) * hd * esz, DT, tid, oacc / l);
 }
 
 VM_TILE void decode_attn_tiles(Args A, uint32_t ti, uint32_t lo, uint32_t hi) {
   A = uargs(A);
   const VM_K Task& t = task_of(A, ti);
   const uint32_t dt = (t.tile_op >> 8) & 0xFF;
-  hi = min(hi, max(1u, t.p[4]));
-  for (uint32_t h = lo; h < hi; ++h) {
-    if (dt == DT_BF16) decode_attn_head<DT_BF16>(A, ti, h);
-    else if (dt == DT_F16) decode_attn_head<DT_F16>(A, ti, h);
-    else decode_attn_head<DT_F32>(A, ti, h);
+  hi = min(hi, max(1u, (t.p[4] & 0xFFFF) * max(1u, t.p[4] >> 16)));
+  for (uint32_t tile = lo; tile < hi; ++tile) {
+    if (dt == DT_BF16) decode_attn_split<DT_BF16>(A, ti, tile);
+    else if (dt == DT_F16) decode_attn_split<DT_F16>(A, ti, tile);
+    else decode_attn_split<DT_F32>(A, ti, tile);
   }
 }
 

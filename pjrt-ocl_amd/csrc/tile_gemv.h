@@ -211,7 +211,7 @@ VM_TILE void gemv_tile(Args A, uint32_t ti, uint32_t tile) {
   const uint32_t cgs = CW / 8, RP = kBlock / cgs;
   // LDS: x [M][K], then the row-phase sums [RP][M][CW] (= 2048 M floats), then the
   // first-pass sums; the loader checks that M * K + 4096 M floats fit
-  float* xs = reinterpret_cast<float*>(vm_smem);
+  float* xs = lds_ptr<float>();
   float* red = xs + ((M * K + 3) & ~3u);
   float* tmp = red + 2048 * M;
   const uint32_t nx = M * K;

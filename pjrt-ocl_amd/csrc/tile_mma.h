@@ -209,7 +209,7 @@ template <int T, bool BF16>
 VM_TILE void mma_tile16(Args A, const MmaDesc* Dp, uint32_t tile) {
   A = uargs(A);
   const MmaDesc D = load_desc(Dp);
-  uint16_t* lds = reinterpret_cast<uint16_t*>(vm_smem);
+  uint16_t* lds = lds_ptr<uint16_t>();
   using C = MmaCfg<T>;
   uint32_t g, m0, n0;
   tile_origin(D, uni(tile), T, &g, &m0, &n0);
@@ -393,7 +393,7 @@ VM_DEV float epi_inline(uint32_t kind, float x, float y, float s, float t) {
 template <bool F32>
 VM_DEV void store_fast(Args A, const MmaDesc& D, const f32x16 (&acc)[4][4], uint32_t g, uint32_t m0, uint32_t n0) {
   constexpr int LD = 256 + 4;
-  float* st = reinterpret_cast<float*>(vm_smem);
+  float* st = lds_ptr<float>();
   const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const uint32_t wm = wave >> 1, wn = wave & 1;
   const uint64_t tile0 = (uint64_t(g) * D.M + m0) * D.N + n0;
@@ -447,7 +447,7 @@ template <bool BF16>
 VM_TILE void mma_tile16_fast(Args A, const MmaDesc* Dp, uint32_t tile) {
   A = uargs(A);
   const MmaDesc D = load_desc(Dp);
-  uint16_t* lds = reinterpret_cast<uint16_t*>(vm_smem);
+  uint16_t* lds = lds_ptr<uint16_t>();
   uint32_t g, m0, n0;
   fast_origin(D, uni(tile), &g, &m0, &n0);
   const uint32_t K = D.K, N = D.N;
@@ -607,7 +607,7 @@ template <int T>
 VM_TILE void mma_tile32(Args A, const MmaDesc* Dp, uint32_t tile) {
   A = uargs(A);
   const MmaDesc D = load_desc(Dp);
-  float* lds = reinterpret_cast<float*>(vm_smem);
+  float* lds = lds_ptr<float>();
   using C = MmaCfg<T>;
   uint32_t g, m0, n0;
   tile_origin(D, uni(tile), T, &g, &m0, &n0);

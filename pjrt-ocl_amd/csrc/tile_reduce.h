@@ -21,7 +21,7 @@ VM_DEV void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-VM_DEV float* lds_f32() { return reinterpret_cast<float*>(vm_smem); }
+VM_DEV float* lds_f32() { return lds_ptr<float>(); }
 
 template <class Op>
 VM_DEV float block_reduce(float x, Op op, float* red) {
@@ -79,7 +79,7 @@ VM_DEV T ired(uint32_t kind, bool uns, T a, T b) {
 // Block reduction of an integer value through an LDS tree (exact).
 template <typename T, typename U>
 VM_DEV T block_ireduce(T v, uint32_t kind, bool uns) {
-  T* tree = reinterpret_cast<T*>(vm_smem);
+  T* tree = lds_ptr<T>();
   lds_barrier();
   tree[threadIdx.x] = v;
   lds_barrier();
@@ -515,7 +515,7 @@ VM_TILE void ln_rows_fast(Args A, uint32_t ti, uint32_t r0, uint32_t r1) {
   L.d = resolve(A, t.dst);
   L.lane = threadIdx.x & 63;
   const uint32_t wave = uni(threadIdx.x >> 6);       // wave-uniform: scalar loop control
-  v4f* lg = reinterpret_cast<v4f*>(vm_smem);
+  v4f* lg = lds_ptr<v4f>();
   v4f* lb = lg + L.nv4;
   {
     const VM_G v4f* g4 = (const VM_G v4f*)gcast<float>(resolve(A, affine ? t.b : t.a));
@@ -550,7 +550,7 @@ VM_TILE void ln_rows_wave(Args A, uint32_t ti, uint32_t r0, uint32_t r1) {
   const bool affine = flags & LN_AFFINE, do_gelu = flags & LN_GELU, two_pass = flags & LN_TWO_PASS;
   const uint32_t nv4 = seg >> 2;
   const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  v4f* lg = reinterpret_cast<v4f*>(vm_smem);
+  v4f* lg = lds_ptr<v4f>();
   v4f* lb = lg + nv4;
   if (affine) {
     const VM_G v4f* g4 = (const VM_G v4f*)gcast<float>(resolve(A, t.b));

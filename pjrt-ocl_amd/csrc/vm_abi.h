@@ -59,6 +59,9 @@ constexpr uint32_t FLAG_NONE = 0xFFFFFFFFu;
 // (vm_common.cl:41-45).  Ports are caller-owned device buffers bound per execute.
 constexpr uint32_t PORT_BIT = 0x80000000u;
 
+// TOP_DECODE_ATTN: key splits per head at most, cache keys per split at most.
+constexpr uint32_t kDecMaxSplits = 1024;
+constexpr uint32_t kDecSplitKeys = 64;
 // TOP_GEMV: rows (M) per task at most.
 constexpr uint32_t kGemvMaxM = 8;
 constexpr int kMaxPorts = 256;          // power of two: handles mask the port index
@@ -115,6 +118,8 @@ struct VmArgs {
   uint32_t mma_t;           // default MMA output tile edge (PJRT_OCL_MMA_T)
   uint32_t timeout_ticks;   // barrier wait limit in s_memrealtime ticks (100 MHz)
   uint64_t* stats;          // profiling counters (null: off), see kStat*
+  uint8_t* scratch;         // loader-owned scratch, zeroed at load (split partials, arrival counters)
+  const uint32_t* task_scratch;   // per task: byte offset of its scratch region
   uint8_t* ports[kMaxPorts];
 };
 

@@ -31,6 +31,20 @@ typedef const VM_K VmArgs* Args;
 // address it as LDS directly.
 extern __shared__ __align__(16) uint8_t vm_smem[];
 
+// Base of the dynamic LDS block, read once into a scalar register.  In the tile
+// functions (not the kernel itself) the compiler finds the block through the
+// kernel's dynamic-LDS offset table; that table read is a global load which,
+// under register pressure, it repeats at every use inside a loop, each with a
+// full memory wait.  An empty asm that owns the value in an SGPR makes it opaque,
+// so it is kept (or spilled) instead of re-derived.
+template <typename T>
+VM_DEV T* lds_ptr() {
+  typedef __attribute__((address_space(3))) uint8_t lds_u8;
+  uint32_t off = uint32_t(reinterpret_cast<uintptr_t>((lds_u8*)vm_smem));
+  asm("" : "+s"(off));
+  return (T*)(lds_u8*)(uintptr_t)off;
+}
+
 VM_DEV uint32_t uni(uint32_t x) { return __builtin_amdgcn_readfirstlane(x); }
 
 // A pointer argument of a non-inlined function arrives in VGPRs; make it

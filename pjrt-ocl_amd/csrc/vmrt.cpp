@@ -324,7 +324,7 @@ struct Checker {
         return std::max<uint64_t>(1, t.p[0]);
       case TOP_FLASH_ATTN: return std::max<uint64_t>(1, uint64_t(t.p[1]) * t.p[2]);
       case TOP_GEMV: return t.p[4] ? std::max<uint64_t>(1, t.p[3]) * cdiv(t.p[1], t.p[4]) : 0;
-      case TOP_DECODE_ATTN: return std::max<uint64_t>(1, t.p[4]);
+      case TOP_DECODE_ATTN: return std::max<uint64_t>(1, uint64_t(t.p[4] & 0xFFFF) * std::max<uint32_t>(1, t.p[4] >> 16));
       default: return 0;
     }
   }
@@ -543,9 +543,12 @@ struct Checker {
         return true;
       }
       case TOP_DECODE_ATTN: {
-        const uint64_t H = t.p[4], hd = t.p[5], C = t.p[6];
+        const uint64_t H = t.p[4] & 0xFFFF, S = t.p[4] >> 16, hd = t.p[5], C = t.p[6];
         if (dt != adt || (adt != DT_F32 && adt != DT_BF16 && adt != DT_F16)) return fail(ti, "decode attention dtype");
-        if (H < 1 || hd < 8 || hd > 256 || hd % 8 || C < 8 || C % 8) return fail(ti, "decode attention shape");
+        if (H < 1 || hd < 8 || hd > 256 || hd % 8 || C < 8 || C % 8 || S > kDecMaxSplits)
+          return fail(ti, "decode attention shape");
+        if (((C + std::max<uint64_t>(S, 1) - 1) / std::max<uint64_t>(S, 1) + 7) / 8 * 8 > kDecSplitKeys)
+          return fail(ti, "decode attention: more than 64 cache keys per split");
         if (!has(t.a, H * hd, adt) || !has(t.p[1], H * hd, adt) || !has(t.p[2], H * hd, adt))
           return fail(ti, "decode attention q / k / v");
         if (!has(t.b, H * hd * C, adt) || !has(t.p[0], H * C * hd, adt)) return fail(ti, "decode attention caches");
@@ -624,6 +627,9 @@ struct vmrt_program {
   uint32_t* ctl = nullptr;
   uint64_t* stats = nullptr;                  // profiling counters (PJRT_AMD_PROFILE=1)
   size_t stats_words = 0;
+  uint8_t* scratch = nullptr;                 // split partials + arrival counters, zeroed at load
+  uint64_t scratch_bytes = 0;
+  uint32_t* task_scratch = nullptr;           // per task: byte offset of its scratch region
   std::vector<int> input_port, output_port;   // -1 = arena copy
   std::vector<uint32_t> in_bytes, out_bytes;
   VmArgs args{};
@@ -712,9 +718,11 @@ int vmrt_device_info_get(vmrt_runtime* rt, vmrt_device_info* out) {
 static void free_program_memory(vmrt_program* p) {
   for (void* q : {static_cast<void*>(p->arena), static_cast<void*>(p->aux), static_cast<void*>(p->tasks),
                   static_cast<void*>(p->entries), static_cast<void*>(p->lanes), static_cast<void*>(p->ctl),
-                  static_cast<void*>(p->stats)})
+                  static_cast<void*>(p->stats), static_cast<void*>(p->scratch), static_cast<void*>(p->task_scratch)})
     if (q) hipFree(q);
   p->stats = nullptr;
+  p->scratch = nullptr;
+  p->task_scratch = nullptr;
   p->arena = nullptr;
   p->aux = nullptr;
   p->tasks = nullptr;
@@ -729,6 +737,17 @@ void vmrt_unload(vmrt_program* p) {
   hipStreamSynchronize(p->rt->stream);
   free_program_memory(p);
   delete p;
+}
+
+// Scratch bytes a task needs (0: none): a split decode attention keeps one
+// partial (running max, sum, hd channels) per split and head, and one arrival
+// counter per head.
+static uint64_t task_scratch_bytes(const Task& t) {
+  if ((t.tile_op & 0xFF) == TOP_DECODE_ATTN && (t.p[4] >> 16) > 1) {
+    const uint64_t H = t.p[4] & 0xFFFF, S = t.p[4] >> 16, hd = t.p[5];
+    return (H * S * (hd + 2) + H) * 4;
+  }
+  return 0;
 }
 
 int vmrt_load(vmrt_runtime* rt, const void* bytes, size_t len, uint32_t ew_ts, uint32_t mma_t, vmrt_program** out,
@@ -853,6 +872,16 @@ int vmrt_load(vmrt_runtime* rt, const void* bytes, size_t len, uint32_t ew_ts, u
       e.pad = w | (fl ? 0x100u : 0u);
     }
   }
+  // each task that needs scratch gets its own region (tasks of one phase run at once)
+  std::vector<uint32_t> task_scratch(tasks.size(), 0);
+  for (size_t i = 0; i < tasks.size(); ++i) {
+    const uint64_t nb = task_scratch_bytes(tasks[i]);
+    if (!nb) continue;
+    task_scratch[i] = uint32_t(lp->scratch_bytes);
+    lp->scratch_bytes += (nb + 255) & ~uint64_t(255);
+    if (lp->scratch_bytes > 0xFFFFFFFFull)
+      return set_err(err, errlen, VMRT_RESOURCE_EXHAUSTED, "LoadedProgram: task scratch exceeds 4 GiB");
+  }
   for (size_t i = 0; i < P.inputs.size(); ++i) lp->in_bytes.push_back(uint32_t(P.buffers[P.inputs[i]].size));
   for (size_t i = 0; i < P.outputs.size(); ++i) lp->out_bytes.push_back(uint32_t(P.buffers[P.outputs[i]].size));
 
@@ -877,6 +906,10 @@ int vmrt_load(vmrt_runtime* rt, const void* bytes, size_t len, uint32_t ew_ts, u
   if (e == hipSuccess) e = up(reinterpret_cast<void**>(&lp->lanes), P.lanes.data(), P.lanes.size() * sizeof(LaneSpan));
   if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&lp->ctl), BAR_WORDS * 4);
   if (e == hipSuccess) e = hipMemset(lp->ctl, 0, BAR_WORDS * 4);
+  if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&lp->scratch), std::max<uint64_t>(lp->scratch_bytes, 256));
+  if (e == hipSuccess) e = hipMemset(lp->scratch, 0, std::max<uint64_t>(lp->scratch_bytes, 256));
+  if (e == hipSuccess)
+    e = up(reinterpret_cast<void**>(&lp->task_scratch), task_scratch.data(), task_scratch.size() * 4);
   if (const char* prof = std::getenv("PJRT_AMD_PROFILE"); e == hipSuccess && prof && std::atoi(prof) != 0) {
     lp->stats_words = kStatTask + 4 * tasks.size();
     e = hipMalloc(reinterpret_cast<void**>(&lp->stats), lp->stats_words * 8);
@@ -902,6 +935,8 @@ int vmrt_load(vmrt_runtime* rt, const void* bytes, size_t len, uint32_t ew_ts, u
   a.mma_t = lp->mma_t;
   a.timeout_ticks = rt->timeout_ticks;
   a.stats = lp->stats;
+  a.scratch = lp->scratch;
+  a.task_scratch = lp->task_scratch;
   for (int k = 0; k < kMaxPorts; ++k) a.ports[k] = lp->arena;   // unbound ports point at the arena
   *out = lp.release();
   return VMRT_OK;
@@ -967,6 +1002,8 @@ static int check_status(vmrt_program* p, char* err, size_t errlen) {
   if (e != hipSuccess) return set_err(err, errlen, VMRT_INTERNAL, "status read: " + hip_msg(e));
   if (st[BAR_ERROR] == VM_OK) return VMRT_OK;
   hipMemset(p->ctl, 0, BAR_WORDS * 4);
+  // an aborted launch can leave arrival counters part-way
+  if (p->scratch) hipMemset(p->scratch, 0, std::max<uint64_t>(p->scratch_bytes, 256));
   const char* what = st[BAR_ERROR] == VM_ERR_BARRIER_TIMEOUT ? "grid barrier timed out (lanes not co-resident, "
                                                                 "or non-uniform control across lanes)"
                      : st[BAR_ERROR] == VM_ERR_FRAME_DEPTH ? "control frame stack overflow"

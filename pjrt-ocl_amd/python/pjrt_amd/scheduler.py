@@ -161,7 +161,7 @@ def n_tiles(task: V.Task, cfg: DeviceConfig) -> int:
     if top == V.TOP_GEMV:
         return max(1, task.p3) * -(-task.p1 // task.p4)
     if top == V.TOP_DECODE_ATTN:
-        return max(1, task.p4)
+        return max(1, (task.p4 & 0xFFFF) * max(1, task.p4 >> 16))
     raise ScheduleError(f"n_tiles: unknown tile_op {top}")
 
 
@@ -199,6 +199,14 @@ def gemv_eligible(M, N, K, G, aview, bview, epi, adt, dt, prog) -> bool:
         if any(prog.aux[epi + 4 * k] not in _EPI_INLINE for k in range(nm)):
             return False
     return True
+
+
+def decode_splits(H: int, C: int, cfg: DeviceConfig) -> int:
+    """Key splits per head of a decode attention: one per 64 cache keys (the
+    tile kernel's register window), whatever the lane count.  A split's reads
+    are all issued before its first wait, so a tile costs about one memory
+    round trip; one CU streaming a 640-key head took ~19 us."""
+    return max(1, -(-C // 64))
 
 
 def _dot_fields(ins: V.Instr, prog: V.VMProgram):
@@ -370,8 +378,9 @@ def instr_to_task(ins: V.Instr, prog: V.VMProgram, cfg: DeviceConfig) -> V.Task:
                    ins.imm, ins.aux)
     elif op == V.OP_DECODE_ATTN:
         hd, kb, vb, posb, sbits = prog.aux[ins.aux:ins.aux + 5]
+        S = decode_splits(ins.n, ins.imm, cfg)
         t = V.Task(V.TOP_DECODE_ATTN, ins.dst, ins.a, ins.b, ins.imm2, kb, vb,
-                   posb, ins.n, hd, ins.imm, sbits)
+                   posb, ins.n | (S << 16), hd, ins.imm, sbits)
     elif op == V.OP_DOT:
         M, N, K, G = ins.n, ins.imm >> 16, ins.imm & 0xFFFF, max(1, ins.imm2)
         aview, bview, epi, epi_res = ins.aview, ins.bview, ins.epi, ins.epi_res
@@ -538,8 +547,9 @@ def task_cost(task: V.Task, cfg: DeviceConfig, prog: V.VMProgram) -> float:
         C = prog.aux[task.p3 + 2] if task.p3 + 2 < len(prog.aux) else T
         return 4.0 * H * T * C * hd / (_MFMA_TFLOPS * 1e6) + 1.0
     if top == V.TOP_DECODE_ATTN:
-        # one CU per head streams the head's two cache slices (~100 GB/s)
-        return task.p4 * (2.0 * task.p5 * task.p6 * asz / 100e3 + 3.0)
+        # each tile streams its share of a head's two cache slices (~15 GB/s per CU)
+        H, S = task.p4 & 0xFFFF, max(1, task.p4 >> 16)
+        return H * S * (2.0 * task.p5 * task.p6 * asz / S / 15e3 + 3.0)
     if top in (V.TOP_RED_SEG, V.TOP_SOFTMAX_SEG, V.TOP_LAYERNORM_SEG,
                V.TOP_ARGMAX_SEG):
         n = task.p0 * task.p1

@@ -488,14 +488,15 @@ def test_flash_attention_score_jump(dt, causal, T, C, target):
     ("bf16", 12, 64, 640, 0, None),         # the step's own key only
     ("f16", 3, 8, 16, 16, None),            # full cache
     ("f32", 2, 24, 24, -1, None),           # clamped position; 3 threads per V row
-    ("f32", 1, 256, 1032, 1030, None),      # widest head, two key chunks
-    ("bf16", 2, 128, 2056, 2050, 1500),     # three chunks; a dominant key in the second
+    ("f32", 1, 256, 1032, 1030, None),      # widest head, 17 splits
+    ("bf16", 2, 128, 2056, 2050, 1500),     # 33 splits; a dominant key in an early one
     ("bf16", 2, 64, 640, 300, "new"),       # a dominant new key
+    ("bf16", 4, 64, 640, 640, "new"),       # position past the cache: the step's key joins the last split
 ])
 def test_decode_attention(dt, H, hd, C, pos, jump):
     """TOP_DECODE_ATTN against float64 math on the same (rounded) inputs: keys
-    are the cache prefix [0, pos) then the step's own key; chunks of 1024 keys
-    combine through the online softmax."""
+    are the cache prefix [0, pos) then the step's own key; splits of 64 cache
+    keys combine their partial softmax results."""
     rng = np.random.default_rng(2024 + hd + C)
     q = rng.standard_normal((H, hd)).astype(np.float32)
     k = rng.standard_normal((H, hd)).astype(np.float32)
@@ -519,14 +520,18 @@ def test_decode_attention(dt, H, hd, C, pos, jump):
     POS = g.input((), "i32")
     g.output(g.decode_attention(Q, K, Vv, CK, CV, POS, scale))
     prog = g.build()
-    blob, _ = blob_for(prog)
-    assert any(tk.top == V.TOP_DECODE_ATTN for tk in vmref.parse(blob).tasks)
-    got, _ = run_both(blob, [q, k, v, ckt, cv, np.array(pos, np.int32)], oracle=None)
-    got = as_f32(got[0], V.DT_BY_NAME[dt]).astype(np.float64).reshape(H, hd)
     want = vmref.decode_attention(q, ckt, cv, k, v, pos, scale)
     tol = 1e-3 if dt == "f32" else 1e-2
-    err = np.abs(got - want).max() / max(1e-6, np.abs(want).max())
-    assert np.isfinite(got).all() and err <= tol, err
+    # keys split over CUs, 64 per split; a few lanes run several tiles each
+    for nlanes in (None, 7):
+        blob, _ = blob_for(prog, nlanes=nlanes)
+        tk = next(tk for tk in vmref.parse(blob).tasks if tk.top == V.TOP_DECODE_ATTN)
+        assert tk.p[4] >> 16 == -(-C // 64), tk.p[4]
+        for _ in range(2):              # the arrival counters reset themselves
+            got, _ = run_both(blob, [q, k, v, ckt, cv, np.array(pos, np.int32)], oracle=None)
+            got = as_f32(got[0], V.DT_BY_NAME[dt]).astype(np.float64).reshape(H, hd)
+            err = np.abs(got - want).max() / max(1e-6, np.abs(want).max())
+            assert np.isfinite(got).all() and err <= tol, (nlanes, err)
 
 
 def test_decode_attention_runs_twice_with_moving_position():

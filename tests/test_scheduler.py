@@ -283,7 +283,8 @@ def test_decode_attention_task_and_cache_update_overlap():
     da = [i for i, t in enumerate(sched.tasks) if t.tile_op == V.TOP_DECODE_ATTN]
     assert len(da) == 1
     t = sched.tasks[da[0]]
-    assert (t.p4, t.p5, t.p6) == (H, hd, C) and S.n_tiles(t, S.DeviceConfig(nlanes=8)) == H
+    assert (t.p4 & 0xFFFF, t.p5, t.p6) == (H, hd, C)
+    assert S.n_tiles(t, S.DeviceConfig(nlanes=8)) == H * max(1, t.p4 >> 16)
     ph = phases(sched)
     at = next(i for i, p in enumerate(ph) if da[0] in p)
     later = {sched.tasks[x].tile_op for x in ph[at + 1]}
@@ -362,3 +363,11 @@ def test_ln_gemv_prologue_not_fused(case):
 
     prog = _ln_dot({"second_reader": second_reader, "input_written": input_written, "output": output}[case])
     assert S.ln_gemv_pairs(prog, S.DeviceConfig(nlanes=8)) == {}
+
+
+def test_decode_splits():
+    cfg = S.DeviceConfig(nlanes=256)
+    assert S.decode_splits(12, 640, cfg) == 10          # 64 keys each
+    assert S.decode_splits(12, 4096, cfg) == 64
+    assert S.decode_splits(300, 72, cfg) == 2
+    assert S.decode_splits(2, 16, cfg) == 1

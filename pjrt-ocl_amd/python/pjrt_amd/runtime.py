@@ -196,7 +196,10 @@ class Runtime:
 
     # ---- scheduling contract (PJRT_OCL_NLANES / _EW_TS / _MMA_T) ----
     def scheduler_config(self, **overrides) -> S.DeviceConfig:
-        cfg = S.DeviceConfig(nlanes=self.info["n_lanes"], ew_ts=self.info["ew_ts"], mma_t=self.info["mma_t"])
+        """The scheduler's knobs from the environment (DeviceConfig.from_env),
+        with the lane count and tile sizes this runtime advertises."""
+        cfg = S.DeviceConfig.from_env()
+        cfg.nlanes, cfg.ew_ts, cfg.mma_t = self.info["n_lanes"], self.info["ew_ts"], self.info["mma_t"]
         for k, v in overrides.items():
             setattr(cfg, k, v)
         return cfg

@@ -1001,12 +1001,14 @@ class TaskRunner:
         dtn = {1: BOOL, 2: BF16, 4: U32, 8: I64}[SIZE[t.dt]]
         self.m.view(t.dst, dtn)[a0:a1] = self.m.view(t.a, dtn)[off]
 
-    # 19: argmax over the last axis (extension)
+    # 19: argmax over the last axis (extension); tile = row * S + split with
+    # S = p3 (a row's result is complete once its last split has run)
     def top19(self, t, lo, hi):
-        n_out, seg = t.p[0], t.p[1]
-        r0, r1 = lo, min(hi, n_out)
-        if r0 >= r1:
+        n_out, seg, S = t.p[0], t.p[1], max(1, t.p[3])
+        rows = [tile // S for tile in range(lo, min(hi, n_out * S)) if tile % S == S - 1]
+        if not rows:
             return
+        r0, r1 = rows[0], rows[-1] + 1
         x = self.m.load_f(t.a, t.adt)[r0 * seg:r1 * seg].reshape(-1, seg)
         nan = np.isnan(x)
         idx = np.where(nan.any(1), nan.argmax(1), np.nanargmax(np.where(nan, -np.inf, x), 1))
@@ -1123,8 +1125,10 @@ def _whole_tiles(t: Task, ew_ts: int, mma_t: int) -> int:
         return max(1, -(-p[0] // p[1]))
     if t.top == 4:
         return 1
-    if t.top in (10, 11, 12, 19):
+    if t.top in (10, 11, 12):
         return max(1, p[0])
+    if t.top == 19:
+        return max(1, p[0]) * max(1, p[3])
     if t.top == 14:
         return max(1, p[1] * p[2])
     if t.top == 20:

@@ -790,7 +790,13 @@ VM_TILE void softmax_tiles(Args A, uint32_t ti, uint32_t lo, uint32_t hi) {
 }
 
 // ARGMAX_SEG: dst = first index of the row maximum (a NaN wins: its first index),
-// b = that value (a's dtype).  p0 n_out, p1 seg.
+// b = that value (a's dtype).  p0 n_out, p1 seg, p3 S: a row's elements split S
+// ways (tile = row * S + split; S <= 1: one tile per row).  Each split finds its
+// best (value, index); the split that arrives last at the row's counter in the
+// task's scratch combines the S candidates (the order is total, so the result
+// does not depend on which split is last) and resets the counter.  Candidates
+// and counters are agent-scope atomics, which go to memory past the XCD's L2.
+// Scratch (S > 1): [n_out * S] {value bits, index}, then n_out counters.
 VM_DEV bool amax_better(float v, uint32_t i, float bv, uint32_t bi) {
   const bool vn = v != v, bn = bv != bv;
   if (vn != bn) return vn;
@@ -798,73 +804,133 @@ VM_DEV bool amax_better(float v, uint32_t i, float bv, uint32_t bi) {
   if (v != bv) return v > bv;
   return i < bi;
 }
+
+// Best (value, index) of elements [j0, j1) of a row over the block; the result
+// is in sv[0] / si[0] (index 0xFFFFFFFF: no element).
+VM_DEV void amax_block(const gbyte* a, uint32_t adt, uint64_t base, uint32_t j0, uint32_t j1, float* sv,
+                       uint32_t* si) {
+  float bv = -INFINITY;
+  uint32_t bi = 0xFFFFFFFFu;
+  auto take = [&](float v, uint32_t j) {
+    if (bi == 0xFFFFFFFFu || amax_better(v, j, bv, bi)) {
+      bv = v;
+      bi = j;
+    }
+  };
+  if (adt == DT_F32 && ((j0 | j1) & 3) == 0 && (((uintptr_t(a) + base * 4) & 15) == 0)) {
+    // f32 rows (logits): 16-byte loads, 16 of them in flight per thread; each
+    // thread still visits its elements in increasing index order
+    const VM_G v4f* row = (const VM_G v4f*)(a + base * 4);
+    const uint32_t q0b = j0 >> 2, n4 = j1 >> 2;
+    constexpr int U = 16;
+    for (uint32_t q0 = q0b + threadIdx.x; q0 < n4; q0 += U * kBlock) {
+      v4f v[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) v[u] = row[min(q0 + u * kBlock, n4 - 1)];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const uint32_t q = q0 + u * kBlock;
+        if (q < n4) {
+          take(v[u].x, 4 * q);
+          take(v[u].y, 4 * q + 1);
+          take(v[u].z, 4 * q + 2);
+          take(v[u].w, 4 * q + 3);
+        }
+      }
+    }
+  } else {
+    for (uint32_t j = j0 + threadIdx.x; j < j1; j += kBlock) take(load_f(a, adt, base + j), j);
+  }
+  lds_barrier();
+  sv[threadIdx.x] = bv;
+  si[threadIdx.x] = bi;
+  lds_barrier();
+  for (int s = kBlock / 2; s > 0; s >>= 1) {
+    if (int(threadIdx.x) < s) {
+      const float v2 = sv[threadIdx.x + s];
+      const uint32_t i2 = si[threadIdx.x + s];
+      if (i2 != 0xFFFFFFFFu && (si[threadIdx.x] == 0xFFFFFFFFu || amax_better(v2, i2, sv[threadIdx.x], si[threadIdx.x]))) {
+        sv[threadIdx.x] = v2;
+        si[threadIdx.x] = i2;
+      }
+    }
+    lds_barrier();
+  }
+}
+
+VM_DEV void amax_store(gbyte* di, gbyte* dv, uint32_t dt, uint32_t adt, uint32_t o, float v, uint32_t i) {
+  const uint32_t idx = i == 0xFFFFFFFFu ? 0u : i;
+  if (dt == DT_I64) gcast<int64_t>(di)[o] = idx;
+  else gcast<uint32_t>(di)[o] = idx;
+  store_f(dv, adt, o, i == 0xFFFFFFFFu ? -INFINITY : v);
+}
+
 VM_TILE void argmax_tiles(Args A, uint32_t ti, uint32_t lo, uint32_t hi) {
   A = uargs(A);
   const VM_K Task& t = task_of(A, ti);
-  const uint32_t n_out = t.p[0], seg = t.p[1];
+  const uint32_t n_out = t.p[0], seg = t.p[1], S = max(1u, t.p[3]);
   const uint32_t dt = (t.tile_op >> 8) & 0xFF, adt = (t.tile_op >> 16) & 0xFF;
   const gbyte* a = resolve(A, t.a);
   gbyte* di = resolve(A, t.dst);
   gbyte* dv = resolve(A, t.b);
   float* sv = lds_f32();
   uint32_t* si = reinterpret_cast<uint32_t*>(sv + kBlock);
-  hi = min(hi, n_out);
-  for (uint32_t o = lo; o < hi; ++o) {
-    const uint64_t base = uint64_t(o) * seg;
-    float bv = -INFINITY;
-    uint32_t bi = 0xFFFFFFFFu;
-    auto take = [&](float v, uint32_t j) {
-      if (bi == 0xFFFFFFFFu || amax_better(v, j, bv, bi)) {
-        bv = v;
-        bi = j;
+  uint32_t* flag = si + kBlock;
+  // split length: whole 16-byte runs
+  const uint32_t per = ((seg + S - 1) / S + 3) & ~3u;
+  hi = min(hi, n_out * S);
+  for (uint32_t tile = lo; tile < hi; ++tile) {
+    const uint32_t o = tile / S, split = tile % S;
+    const uint32_t j0 = min(split * per, seg), j1 = min(seg, j0 + per);
+    amax_block(a, adt, uint64_t(o) * seg, j0, j1, sv, si);
+    if (S == 1) {
+      if (threadIdx.x == 0) amax_store(di, dv, dt, adt, o, sv[0], si[0]);
+      continue;
+    }
+    uint32_t* sp = reinterpret_cast<uint32_t*>(A->scratch + A->task_scratch[ti]);
+    uint32_t* arrivals = sp + 2ull * n_out * S;
+    if (threadIdx.x == 0) {
+      uint32_t* mine = sp + 2ull * (uint64_t(o) * S + split);
+      __hip_atomic_store(mine, __float_as_uint(sv[0]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(mine + 1, si[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __builtin_amdgcn_s_waitcnt(0x0F70);             // vmcnt(0): the candidate is in memory
+      const uint32_t before = __hip_atomic_fetch_add(arrivals + o, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const bool last = before == S - 1;
+      if (last) __hip_atomic_store(arrivals + o, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      *flag = last;
+    }
+    lds_barrier();
+    if (*flag) {
+      // candidate k by thread k, then the same tree as above
+      float bv = -INFINITY;
+      uint32_t bi = 0xFFFFFFFFu;
+      for (uint32_t k = threadIdx.x; k < S; k += kBlock) {
+        const uint32_t* c = sp + 2ull * (uint64_t(o) * S + k);
+        const float v = __uint_as_float(__hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+        const uint32_t i = __hip_atomic_load(c + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (i != 0xFFFFFFFFu && (bi == 0xFFFFFFFFu || amax_better(v, i, bv, bi))) {
+          bv = v;
+          bi = i;
+        }
       }
-    };
-    if (adt == DT_F32 && (seg & 3) == 0 && ((uintptr_t(a) & 15) == 0)) {
-      // f32 rows (logits): 16-byte loads, 16 of them in flight per thread; each
-      // thread still visits its elements in increasing index order
-      const VM_G v4f* row = (const VM_G v4f*)(a + base * 4);
-      const uint32_t n4 = seg >> 2;
-      constexpr int U = 16;
-      for (uint32_t q0 = threadIdx.x; q0 < n4; q0 += U * kBlock) {
-        v4f v[U];
-#pragma unroll
-        for (int u = 0; u < U; ++u) v[u] = row[min(q0 + u * kBlock, n4 - 1)];
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-          const uint32_t q = q0 + u * kBlock;
-          if (q < n4) {
-            take(v[u].x, 4 * q);
-            take(v[u].y, 4 * q + 1);
-            take(v[u].z, 4 * q + 2);
-            take(v[u].w, 4 * q + 3);
+      sv[threadIdx.x] = bv;
+      si[threadIdx.x] = bi;
+      lds_barrier();
+      for (int s = kBlock / 2; s > 0; s >>= 1) {
+        if (int(threadIdx.x) < s) {
+          const float v2 = sv[threadIdx.x + s];
+          const uint32_t i2 = si[threadIdx.x + s];
+          if (i2 != 0xFFFFFFFFu &&
+              (si[threadIdx.x] == 0xFFFFFFFFu || amax_better(v2, i2, sv[threadIdx.x], si[threadIdx.x]))) {
+            sv[threadIdx.x] = v2;
+            si[threadIdx.x] = i2;
           }
         }
+        lds_barrier();
       }
-    } else {
-      for (uint32_t j = threadIdx.x; j < seg; j += kBlock) take(load_f(a, adt, base + j), j);
+      if (threadIdx.x == 0) amax_store(di, dv, dt, adt, o, sv[0], si[0]);
     }
-    lds_barrier();
-    sv[threadIdx.x] = bv;
-    si[threadIdx.x] = bi;
-    lds_barrier();
-    for (int s = kBlock / 2; s > 0; s >>= 1) {
-      if (int(threadIdx.x) < s) {
-        const float v2 = sv[threadIdx.x + s];
-        const uint32_t i2 = si[threadIdx.x + s];
-        if (i2 != 0xFFFFFFFFu &&
-            (si[threadIdx.x] == 0xFFFFFFFFu || amax_better(v2, i2, sv[threadIdx.x], si[threadIdx.x]))) {
-          sv[threadIdx.x] = v2;
-          si[threadIdx.x] = i2;
-        }
-      }
-      lds_barrier();
-    }
-    if (threadIdx.x == 0) {
-      const uint32_t idx = si[0] == 0xFFFFFFFFu ? 0u : si[0];
-      if (dt == DT_I64) gcast<int64_t>(di)[o] = idx;
-      else gcast<uint32_t>(di)[o] = idx;
-      store_f(dv, adt, o, si[0] == 0xFFFFFFFFu ? -INFINITY : sv[0]);
-    }
+    lds_barrier();                                    // flag / sv reused by the next tile
   }
 }
 

@@ -62,6 +62,8 @@ constexpr uint32_t PORT_BIT = 0x80000000u;
 // TOP_DECODE_ATTN: key splits per head at most, cache keys per split at most.
 constexpr uint32_t kDecMaxSplits = 1024;
 constexpr uint32_t kDecSplitKeys = 64;
+// TOP_ARGMAX_SEG: splits per row at most.
+constexpr uint32_t kArgmaxMaxSplits = 256;
 // TOP_GEMV: rows (M) per task at most.
 constexpr uint32_t kGemvMaxM = 8;
 constexpr int kMaxPorts = 256;          // power of two: handles mask the port index

@@ -320,8 +320,9 @@ struct Checker {
       }
       case TOP_RED_PART: return t.p[1] ? std::max<uint64_t>(1, cdiv(t.p[0], t.p[1])) : 1;
       case TOP_RED_COMB: return 1;
-      case TOP_RED_SEG: case TOP_SOFTMAX_SEG: case TOP_LAYERNORM_SEG: case TOP_ARGMAX_SEG:
+      case TOP_RED_SEG: case TOP_SOFTMAX_SEG: case TOP_LAYERNORM_SEG:
         return std::max<uint64_t>(1, t.p[0]);
+      case TOP_ARGMAX_SEG: return std::max<uint64_t>(1, uint64_t(t.p[0]) * std::max<uint32_t>(1, t.p[3]));
       case TOP_FLASH_ATTN: return std::max<uint64_t>(1, uint64_t(t.p[1]) * t.p[2]);
       case TOP_GEMV: return t.p[4] ? std::max<uint64_t>(1, t.p[3]) * cdiv(t.p[1], t.p[4]) : 0;
       case TOP_DECODE_ATTN: return std::max<uint64_t>(1, uint64_t(t.p[4] & 0xFFFF) * std::max<uint32_t>(1, t.p[4] >> 16));
@@ -461,6 +462,7 @@ struct Checker {
       case TOP_ARGMAX_SEG: {
         const uint64_t n_out = t.p[0], seg = t.p[1];
         if (dt != DT_I32 && dt != DT_U32 && dt != DT_I64) return fail(ti, "argmax index dtype");
+        if (t.p[3] > kArgmaxMaxSplits) return fail(ti, "argmax splits");
         return (has(t.a, n_out * seg, adt) && has(t.dst, n_out, dt) && has(t.b, n_out, adt)) ||
                fail(ti, "argmax operands");
       }
@@ -743,6 +745,7 @@ void vmrt_unload(vmrt_program* p) {
 // partial (running max, sum, hd channels) per split and head, and one arrival
 // counter per head.
 static uint64_t task_scratch_bytes(const Task& t) {
+  if ((t.tile_op & 0xFF) == TOP_ARGMAX_SEG && t.p[3] > 1) return (2ull * t.p[0] * t.p[3] + t.p[0]) * 4;
   if ((t.tile_op & 0xFF) == TOP_DECODE_ATTN && (t.p[4] >> 16) > 1) {
     const uint64_t H = t.p[4] & 0xFFFF, S = t.p[4] >> 16, hd = t.p[5];
     return (H * S * (hd + 2) + H) * 4;

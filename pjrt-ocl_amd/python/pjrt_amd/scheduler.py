@@ -153,9 +153,10 @@ def n_tiles(task: V.Task, cfg: DeviceConfig) -> int:
         return max(1, math.ceil(task.p0 / task.p1)) if task.p1 else 1
     if top == V.TOP_RED_COMB:
         return 1
-    if top in (V.TOP_RED_SEG, V.TOP_SOFTMAX_SEG, V.TOP_LAYERNORM_SEG,
-               V.TOP_ARGMAX_SEG):
+    if top in (V.TOP_RED_SEG, V.TOP_SOFTMAX_SEG, V.TOP_LAYERNORM_SEG):
         return max(1, task.p0)
+    if top == V.TOP_ARGMAX_SEG:
+        return max(1, task.p0) * max(1, task.p3)
     if top == V.TOP_FLASH_ATTN:
         return max(1, task.p1 * task.p2)
     if top == V.TOP_GEMV:
@@ -199,6 +200,15 @@ def gemv_eligible(M, N, K, G, aview, bview, epi, adt, dt, prog) -> bool:
         if any(prog.aux[epi + 4 * k] not in _EPI_INLINE for k in range(nm)):
             return False
     return True
+
+
+def argmax_splits(n_out: int, seg: int, cfg: DeviceConfig) -> int:
+    """Splits per row of an argmax (p3): rows of 8192 elements or more are cut
+    into runs of about 4096 on separate CUs (one 32000-element row took ~21 us
+    on one CU), as long as every split has a lane."""
+    if seg < 8192 or n_out <= 0:
+        return 1
+    return max(1, min(-(-seg // 4096), cfg.nlanes // n_out, 256))
 
 
 def decode_splits(H: int, C: int, cfg: DeviceConfig) -> int:
@@ -367,7 +377,7 @@ def instr_to_task(ins: V.Instr, prog: V.VMProgram, cfg: DeviceConfig) -> V.Task:
     elif op == V.OP_ARGMAX_SEG:
         # dst = index output, b = value output (may alias a scratch), p2 = kind
         t = V.Task(V.TOP_ARGMAX_SEG, ins.dst, ins.a, ins.b, ins.n, ins.imm,
-                   ins.imm2)
+                   ins.imm2, argmax_splits(ins.n, ins.imm, cfg))
     elif op == V.OP_MAP_REGION:
         inp = list(ins.region_inputs) or _region_inputs_from_aux(ins, prog)
         f = [inp[k] if k < len(inp) else inp[0] for k in range(8)]

@@ -184,7 +184,8 @@ def test_integer_reductions_bit_exact(dt, kind):
 @pytest.mark.parametrize("rows,seg", [(33, 513), (7, 516), (5, 32000)])
 def test_argmax_rows(rows, seg):
     """First index of the row maximum, a NaN winning (its first index); f32 rows
-    of a multiple of 4 take the 16-byte-load path."""
+    of a multiple of 4 take the 16-byte-load path; rows of 8192 or more are split
+    over CUs and combined by the last split."""
     rng = np.random.default_rng(40)
     a = rng.standard_normal((rows, seg)).astype(np.float32)
     a[3, 100] = a[3].max() + 1
@@ -197,9 +198,13 @@ def test_argmax_rows(rows, seg):
     x = g.input(a.shape)
     val, idx = g.argmax_last(x)
     g.output(val, idx)
-    got, want = run_both(g.build(), [a])
-    np.testing.assert_array_equal(got[1], want[1])
-    np.testing.assert_array_equal(got[0].view(np.uint32), want[0].view(np.uint32))
+    blob, _ = blob_for(g.build())
+    splits = next(tk.p[3] for tk in vmref.parse(blob).tasks if tk.top == V.TOP_ARGMAX_SEG)
+    assert (splits > 1) == (seg >= 8192), splits
+    for _ in range(2):                  # split rows: the arrival counters reset themselves
+        got, want = run_both(blob, [a])
+        np.testing.assert_array_equal(got[1], want[1])
+        np.testing.assert_array_equal(got[0].view(np.uint32), want[0].view(np.uint32))
 
 
 @pytest.mark.parametrize("seg", [96, 768, 1000, 4096, 8192])

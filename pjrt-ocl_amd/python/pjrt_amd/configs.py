@@ -174,16 +174,18 @@ def gpt_c5(c: GptConfig = C5, emit_logits: bool = False, trips: int | None = Non
     first = g.fill((1,), 0, "i32")
     g.copy_into(first, tok)
 
-    # ---- greedy decode: one token per trip; carries token, position, step
+    # ---- greedy decode: one token per trip; carries the token and its position
     cur = g.fill((1,), 0, "i32")
     g.copy_into(cur, tok)
     pos = g.fill((), T, "i32")
-    step = g.fill((), 0, "i32")
     out = g.fill((c.steps,), 0, "i32")
 
     g.begin()
-    x = g.add(g.convert(g.take_rows(P["wte"], cur), "f32"),
-              g.convert(g.dynamic_slice(P["wpe"], [pos, zero], [1, D]), "f32"))
+    # both embedding rows are gathered in one phase, converted and added in the next
+    tok_row = g.take_rows(P["wte"], cur)
+    pos_row = g.dynamic_slice(P["wpe"], [pos, zero], [1, D])
+    step = g.add(pos, g.scalar(-T, "i32"))               # this trip's output slot
+    x = g.add(g.convert(tok_row, "f32"), g.convert(pos_row, "f32"))
     for l in range(c.layers):
         h = g.layernorm(x, P[f"h{l}.ln1_g"], P[f"h{l}.ln1_b"], c.eps, out_dtype="bf16")
         qkv = g.dot(h, P[f"h{l}.w_qkv"], out_dtype="bf16", residual=P[f"h{l}.b_qkv"],
@@ -200,10 +202,11 @@ def gpt_c5(c: GptConfig = C5, emit_logits: bool = False, trips: int | None = Non
                   epilogue=[(V.SUB_ADD, 1, 0.0, 0.0)])
         x = mlp_block(x, l, 1)
     nxt = head(x, g.add(step, one))
+    # the slot comes from `step`, not `pos`, so that the position moves on in
+    # the same phase
     g.dynamic_update_slice(out, nxt, [step])
     g.copy_into(cur, nxt)
     g.copy_into(pos, g.add(pos, one))
-    g.copy_into(step, g.add(step, one))
     body = g.end()
     g.for_loop(c.steps if trips is None else trips, body)
     g.output(first, out)

@@ -210,9 +210,11 @@ VM_DEV void grid_barrier_init(Args A) {
   __syncthreads();
 }
 
-VM_DEV bool barrier_timed_out(Args A, uint64_t t0) {
+// Every poll checks the clock; only every 32nd also reads the error word (a
+// memory round trip that would otherwise double the latency of each poll).
+VM_DEV bool barrier_timed_out(Args A, uint64_t t0, uint32_t poll) {
   uint32_t* ctl = A->ctl;
-  if (__hip_atomic_load(&ctl[BAR_ERROR], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) return true;
+  if ((poll & 31) == 31 && __hip_atomic_load(&ctl[BAR_ERROR], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) return true;
   if (__builtin_amdgcn_s_memrealtime() - t0 > A->timeout_ticks) {
     uint32_t expect = 0;
     __hip_atomic_compare_exchange_strong(&ctl[BAR_ERROR], &expect, uint32_t(VM_ERR_BARRIER_TIMEOUT), __ATOMIC_RELAXED,
@@ -230,13 +232,13 @@ VM_DEV bool grid_barrier(Args A) {
   const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
   if (blockIdx.x == 0) {
     if (threadIdx.x == 0) s_ok = 1;
-    for (;;) {
+    for (uint32_t poll = 0;; ++poll) {
       bool mine = true;
       for (uint32_t l = threadIdx.x + 1; l < A->n_lanes; l += kBlock)
         if (int32_t(__hip_atomic_load(&ctl[BAR_FLAGS + l], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - epoch) < 0)
           mine = false;
       if (__syncthreads_and(mine)) break;
-      if (threadIdx.x == 0 && barrier_timed_out(A, t0)) s_ok = 0;
+      if (threadIdx.x == 0 && barrier_timed_out(A, t0, poll)) s_ok = 0;
       __syncthreads();
       if (!s_ok) break;
       __builtin_amdgcn_s_sleep(1);
@@ -248,8 +250,9 @@ VM_DEV bool grid_barrier(Args A) {
   } else if (threadIdx.x == 0) {
     uint32_t ok = 1;
     __hip_atomic_store(&ctl[BAR_FLAGS + blockIdx.x], epoch, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
-    while (int32_t(__hip_atomic_load(&ctl[BAR_GEN], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - epoch) < 0) {
-      if (barrier_timed_out(A, t0)) {
+    for (uint32_t poll = 0;
+         int32_t(__hip_atomic_load(&ctl[BAR_GEN], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - epoch) < 0; ++poll) {
+      if (barrier_timed_out(A, t0, poll)) {
         ok = 0;
         break;
       }

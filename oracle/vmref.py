@@ -868,9 +868,16 @@ class TaskRunner:
 
     # 12: layernorm rows (+ extension flags in p3)
     def top12(self, t, lo, hi):
-        n_out, seg = t.p[0], t.p[1]
+        n_out, seg, c = t.p[0], t.p[1], t.p[5]
         r0, r1 = lo, min(hi, n_out)
         if r0 >= r1:
+            return
+        if c:
+            # row interleave (extension p5): logical row i is (i % c) * (n_out / c) + i / c
+            for i in range(r0, r1):
+                r = (i % c) * (n_out // c) + i // c
+                y = self._ln_rows(t, r, r + 1)
+                self.m.store_f(t.dst, slice(r * seg, (r + 1) * seg), y.reshape(-1), t.dt)
             return
         y = self._ln_rows(t, r0, r1)
         self.m.store_f(t.dst, slice(r0 * seg, r1 * seg), y.reshape(-1), t.dt)

@@ -380,6 +380,7 @@ struct LnRow {                 // per-row constants of one layernorm task
   const v4f* lg;
   const v4f* lb;
   uint32_t seg, nv4, lane;
+  uint32_t ichunk, istride;      // row interleave: row i -> (i % ichunk) * istride + i / ichunk
   float eps, inv_n;
   bool two_pass;
 };
@@ -391,6 +392,7 @@ struct LnRow {                 // per-row constants of one layernorm task
 template <int NV, bool IN_BF16, bool FULL>
 VM_DEV void ln_load(typename RowFmt<IN_BF16>::Raw (&buf)[NV], const LnRow& L, uint32_t r) {
   typedef typename RowFmt<IN_BF16>::Raw Raw;
+  r = (r % L.ichunk) * L.istride + r / L.ichunk;
   const VM_G Raw* rp = (const VM_G Raw*)(L.a + uint64_t(r) * L.seg * (IN_BF16 ? 2 : 4));
 #pragma unroll
   for (int k = 0; k < NV; ++k) buf[k] = rp[FULL ? L.lane + 64 * k : min(L.lane + 64 * k, L.nv4 - 1)];
@@ -427,6 +429,7 @@ VM_DEV void ln_process(const typename RowFmt<IN_BF16>::Raw (&buf)[NV], const LnR
   }
   const float rstd = rsqrtf(var + L.eps);
   const float shift = -mean * rstd;
+  r = (r % L.ichunk) * L.istride + r / L.ichunk;
   gbyte* rowd = L.d + uint64_t(r) * L.seg * (OUT_BF16 ? 2 : 4);
 #pragma unroll
   for (int k = 0; k < NV; ++k) {
@@ -514,6 +517,9 @@ VM_TILE void ln_rows_fast(Args A, uint32_t ti, uint32_t r0, uint32_t r1) {
   L.a = resolve(A, t.a);
   L.d = resolve(A, t.dst);
   L.lane = threadIdx.x & 63;
+  // p5: row interleave (0: none; the loader checks that it divides n_out)
+  L.ichunk = t.p[5] ? t.p[5] : 0xFFFFFFFFu;
+  L.istride = t.p[5] ? t.p[0] / t.p[5] : 1u;
   const uint32_t wave = uni(threadIdx.x >> 6);       // wave-uniform: scalar loop control
   v4f* lg = lds_ptr<v4f>();
   v4f* lb = lg + L.nv4;
@@ -680,6 +686,14 @@ VM_DEV bool row_vec_ok(uint32_t seg, const gbyte* a, const gbyte* d, uint32_t ad
   return fmt && (seg & 3) == 0 && seg <= 8 * 4 * kBlock && ((uintptr_t(a) | uintptr_t(d)) & 15) == 0;
 }
 
+VM_DEV void layernorm_rows(Args A, uint32_t ti, uint32_t lo, uint32_t hi);
+
+// LAYERNORM_SEG tiles [lo, hi).  Task p5 (scheduler, extension): the lanes'
+// rows interleaved -- logical row i is row (i % p5) * (n_out / p5) + i / p5, so
+// that at any moment the lanes stream neighbouring rows of the input (C2,
+// alternating runs on one MI355X: 38.7 against 39.6 us).  The streaming row
+// kernel applies it per row;
+// the other row kernels take the rows one by one.
 VM_TILE void layernorm_tiles(Args A, uint32_t ti, uint32_t lo, uint32_t hi) {
   A = uargs(A);
   const VM_K Task& t = task_of(A, ti);
@@ -687,6 +701,27 @@ VM_TILE void layernorm_tiles(Args A, uint32_t ti, uint32_t lo, uint32_t hi) {
   const uint32_t dt = (t.tile_op >> 8) & 0xFF, adt = (t.tile_op >> 16) & 0xFF;
   hi = min(hi, n_out);
   if (lo >= hi) return;
+  bool ok = row_vec_ok(seg, resolve(A, t.a), resolve(A, t.dst), adt, dt);
+  if (ok && (t.p[3] & LN_AFFINE)) ok = ((uintptr_t(resolve(A, t.b)) | uintptr_t(resolve(A, t.p[4]))) & 15) == 0;
+  const uint32_t nv4 = seg >> 2;
+  const bool fast = ok && (adt == DT_F32 || adt == DT_BF16) && (dt == DT_F32 || dt == DT_BF16) && nv4 <= 16 * 64;
+  if (t.p[5] && !fast) {
+    const uint32_t c = t.p[5], stride = n_out / c;
+    for (uint32_t i = lo; i < hi; ++i) {
+      const uint32_t r = (i % c) * stride + i / c;
+      layernorm_rows(A, ti, r, r + 1);
+    }
+    return;
+  }
+  layernorm_rows(A, ti, lo, hi);
+}
+
+// Rows [lo, hi) of a LAYERNORM_SEG task through the fitting row kernel (rows
+// taken as they are, except the streaming kernel, which applies p5 itself).
+VM_DEV void layernorm_rows(Args A, uint32_t ti, uint32_t lo, uint32_t hi) {
+  const VM_K Task& t = task_of(A, ti);
+  const uint32_t seg = t.p[1];
+  const uint32_t dt = (t.tile_op >> 8) & 0xFF, adt = (t.tile_op >> 16) & 0xFF;
   bool ok = row_vec_ok(seg, resolve(A, t.a), resolve(A, t.dst), adt, dt);
   if (ok && (t.p[3] & LN_AFFINE)) ok = ((uintptr_t(resolve(A, t.b)) | uintptr_t(resolve(A, t.p[4]))) & 15) == 0;
   if (!ok) return ln_rows_generic(A, ti, lo, hi);

@@ -457,6 +457,8 @@ struct Checker {
         if (top == TOP_LAYERNORM_SEG && (t.p[3] & LN_AFFINE) &&
             !(has(t.b, t.p[1], DT_F32) && has(t.p[4], t.p[1], DT_F32)))
           return fail(ti, "layernorm gamma/beta");
+        if (top == TOP_LAYERNORM_SEG && t.p[5] && t.p[0] % t.p[5])
+          return fail(ti, "layernorm row interleave must divide the row count");
         return true;
       }
       case TOP_ARGMAX_SEG: {

@@ -237,6 +237,26 @@ def test_fused_layernorm_affine_gelu(in_dt, out_dt):
     assert_rel(as_f32(got[0], odt), as_f32(want[0], odt), BF16_ULP if out_dt == "bf16" else 1e-5, 1e-5, "ln")
 
 
+@pytest.mark.parametrize("d,in_dt", [(100, "f32"), (6000, "f32"), (768, "f16"), (768, "f32")])
+def test_layernorm_row_interleave(d, in_dt):
+    """Rows a multiple of the lane count: the scheduler interleaves the lanes'
+    rows (task p5) and every row kernel (streaming, per-wave, per-block,
+    generic) honours it."""
+    rng = np.random.default_rng(1003)
+    rows = 2 * runtime().info["n_lanes"]
+    x_np = rng.standard_normal((rows, d)).astype(np.float32)
+    gamma = rng.uniform(0.5, 1.5, d).astype(np.float32)
+    beta = (rng.standard_normal(d) * 0.1).astype(np.float32)
+    g = G.Graph()
+    x = g.input((rows, d), in_dt)
+    ga, be = g.input((d,)), g.input((d,))
+    g.output(g.layernorm(x, ga, be, 1e-5, gelu=True, out_dtype="bf16"))
+    blob, _ = blob_for(g.build())
+    assert any(tk.top == V.TOP_LAYERNORM_SEG and tk.p[5] == 2 for tk in vmref.parse(blob).tasks)
+    got, want = run_both(blob, [x_np, gamma, beta])
+    assert_rel(as_f32(got[0], V.DT_BF16), as_f32(want[0], V.DT_BF16), BF16_ULP, 1e-5, "ln")
+
+
 def test_config2_full_size_layernorm_gelu_bf16():
     """Config 2 at its real shape [8192, 4096] (seed 1002)."""
     rng = np.random.default_rng(1002)

@@ -371,3 +371,22 @@ def test_decode_splits():
     assert S.decode_splits(12, 4096, cfg) == 64
     assert S.decode_splits(300, 72, cfg) == 2
     assert S.decode_splits(2, 16, cfg) == 1
+
+
+def test_layernorm_row_interleave():
+    """LAYERNORM_SEG p5: set when the rows are a multiple of the lanes; the
+    lane simulator (which applies it) still equals the tensor interpreter."""
+    assert S.row_interleave(8192, S.DeviceConfig(nlanes=256)) == 32
+    assert S.row_interleave(8191, S.DeviceConfig(nlanes=256)) == 0
+    assert S.row_interleave(256, S.DeviceConfig(nlanes=256)) == 0
+    g = G.Graph()
+    x = g.input((32, 24))
+    ga, be = g.input((24,)), g.input((24,))
+    g.output(g.layernorm(x, ga, be, 1e-5, gelu=True))
+    prog = g.build()
+    blob = V.serialize(prog, S.schedule_program(prog, S.DeviceConfig(nlanes=4)))
+    assert any(t.top == V.TOP_LAYERNORM_SEG and t.p[5] == 8 for t in vmref.parse(blob).tasks)
+    rng = np.random.default_rng(3)
+    args = [rng.standard_normal((32, 24)).astype(np.float32), rng.uniform(0.5, 1.5, 24).astype(np.float32),
+            rng.normal(0, 0.1, 24).astype(np.float32)]
+    np.testing.assert_array_equal(vmref.execute_schedule(blob, args)[0], vmref.execute(blob, args)[0])

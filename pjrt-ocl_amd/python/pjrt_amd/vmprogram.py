@@ -30,11 +30,15 @@ which does not use them is byte-for-byte a reference program):
 
 * tensor opcode ``OP_LAYERNORM_AFFINE`` (66) and the ``LAYERNORM_SEG`` task
   flags in ``p3`` (affine gamma/beta, tanh-GELU epilogue, output convert);
+  ``LAYERNORM_SEG`` p5: row interleave c (logical row i is row
+  (i % c) * (n / c) + i / c; 0 = none);
 * ``MMA`` task ``p3`` bits 24..27 select a per-task output tile edge
   (0 = the runtime default advertised as PJRT_OCL_MMA_T);
 * tensor opcode ``OP_ARGMAX_SEG`` (67) / tile op ``TOP_ARGMAX_SEG`` (19):
   the variadic (value, index) reduce that ``jnp.argmax`` lowers to, which the
-  reference rejects (python/pjrt_ocl/ops/reduce.py:165-168);
+  reference rejects (python/pjrt_ocl/ops/reduce.py:165-168); task p3 S splits
+  a row over S tiles (tile = row * S + split) combined by the last split
+  through the task's scratch;
 * tile op ``TOP_GEMV`` (20): the scheduler's column-strip form of an ``OP_DOT``
   with at most 8 rows (decode-time matmuls); p0 M, p1 N, p2 K, p3 G, p4 strip
   width, p5 layernorm prologue (index + 1 of a ``LAYERNORM_SEG`` task that no
@@ -45,8 +49,15 @@ which does not use them is byte-for-byte a reference program):
   the step's own key/value: ``out[h] = softmax(scale q[h] . [K^T[h, :, :pos],
   k[h]]) [V[h, :pos]; v[h]]``.  Instr: dst out, a q, b K^T cache [H, hd, C],
   n H, imm C, imm2 V cache [H, C, hd], aux -> [hd, k, v, pos buffer, scale
-  bits].  Task: p0 V, p1 k, p2 v, p3 pos, p4 H, p5 hd, p6 C, p7 scale bits;
-  one tile per head.  ``pos`` (i32 scalar) is clamped to [0, C].
+  bits].  Task: p0 V, p1 k, p2 v, p3 pos, p4 H | S << 16, p5 hd, p6 C, p7
+  scale bits; tile = head * S + split, each split at most 64 cache keys,
+  combined by the last split through the task's scratch.  ``pos`` (i32
+  scalar) is clamped to [0, C].
+
+Task scratch: the loader gives each task that needs it (a split decode
+attention or argmax) its own zeroed region of device memory; the last split of
+a head / row resets its arrival counter, so the region is zero again for the
+next run.
 """
 from __future__ import annotations
 

@@ -804,7 +804,10 @@ class _Scheduler:
             units.append(([self.task_id(i)], n_tiles(t, self.cfg),
                           task_cost(t, self.cfg, self.prog),
                           _tile_quantum(t, self.cfg, self.prog),
-                          t.tile_op == V.TOP_FLASH_ATTN))
+                          # neighbouring strips share weight lines (a 16-column
+                          # bf16 strip is a quarter of a 128-byte line): on one
+                          # XCD they share its L2 (C5: 1014 -> 1036 tokens/s)
+                          t.tile_op in (V.TOP_FLASH_ATTN, V.TOP_GEMV)))
         for comp in self.chains(maps):
             tids = [self.task_id(i) for i in comp]
             t0 = self.tasks[tids[0]]

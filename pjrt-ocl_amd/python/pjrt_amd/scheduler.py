@@ -61,7 +61,7 @@ class DeviceConfig:
     # Matmuls of at most 8 rows as column-strip TOP_GEMV tasks (extension), and
     # the narrowest strip width they may use.
     gemv: bool = True
-    gemv_min_strip: int = 16
+    gemv_min_strip: int = 8
     # A layernorm whose only reader is a TOP_GEMV runs inside that GEMV's x
     # staging (extension; saves the phase between them).
     ln_gemv: bool = True
@@ -97,7 +97,7 @@ class DeviceConfig:
                    fuse=env.get("PJRT_OCL_FUSE", "1") != "0",
                    mma_autotile=env.get("PJRT_AMD_MMA_AUTOTILE", "1") != "0",
                    gemv=env.get("PJRT_AMD_GEMV", "1") != "0",
-                   gemv_min_strip=max(8, min(256, geti("PJRT_AMD_GEMV_STRIP", 16))),
+                   gemv_min_strip=max(8, min(256, geti("PJRT_AMD_GEMV_STRIP", 8))),
                    ln_gemv=env.get("PJRT_AMD_LN_GEMV", "1") != "0",
                    idle_master=env.get("PJRT_AMD_IDLE_MASTER", "1") != "0")
 
@@ -178,12 +178,15 @@ _EPI_INLINE = {V.SUB_AFFINE, V.SUB_GELU, V.SUB_COPY, V.SUB_ADD, V.SUB_MUL, V.SUB
                V.SUB_MAX, V.SUB_MIN}
 
 
-def gemv_strip(N: int, G: int, nlanes: int, min_strip: int = 16) -> int:
+def gemv_strip(N: int, G: int, nlanes: int, min_strip: int = 8) -> int:
     """Columns per TOP_GEMV tile: the narrowest strip (min_strip, ... 256, powers
     of two) that gives no lane a second tile.  A tile's time is latency, not
-    bytes: measured on MI355X with K = 768, 16-column strips beat 8-column ones
-    (N = 2304: 9.2 against 15.3 us per one-phase launch, which gave lanes two
-    tiles) and the 32000-column LM head takes 128 (16.4 against 21.0 us at 64)."""
+    bytes: measured on MI355X with K = 768, a strip width that gave lanes two
+    tiles cost a whole tile (N = 2304: 9.2 against 15.3 us per one-phase
+    launch), and the 32000-column LM head takes 128 (16.4 against 21.0 us at
+    64).  Within one tile per lane the narrowest strip wins in the decoder
+    (C5, strips XCD-grouped: 1042 against 1035 tokens/s with 8 against 16
+    columns for N = 768)."""
     cw = 8
     while cw < min_strip:
         cw *= 2

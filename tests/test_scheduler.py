@@ -204,11 +204,11 @@ def test_gemv_epilogue_matches_tensor_semantics():
 
 
 def test_gemv_strips_cover_lanes():
-    for N, G_, want in [(2304, 1, 16), (32000, 1, 128), (768, 1, 16), (640, 12, 32), (64, 12, 16),
-                        (8, 1, 16), (4096, 16, 256)]:
+    for N, G_, want in [(2304, 1, 16), (32000, 1, 128), (768, 1, 8), (640, 12, 32), (64, 12, 8),
+                        (8, 1, 8), (4096, 16, 256)]:
         cw = S.gemv_strip(N, G_, 256)
         assert cw == want and G_ * -(-N // cw) <= max(256, G_)
-    assert S.gemv_strip(2304, 1, 256, min_strip=8) == 16 and S.gemv_strip(768, 1, 256, min_strip=8) == 8
+    assert S.gemv_strip(768, 1, 256, min_strip=16) == 16 and S.gemv_strip(3072, 1, 256, min_strip=16) == 16
 
 
 def test_gemv_lds_bound_falls_back_to_mma():

@@ -451,10 +451,12 @@ VM_DEV void ln_process(const typename RowFmt<IN_BF16>::Raw (&buf)[NV], const LnR
         z.w = gelu(z.w);
       }
       if (FULL || L.lane + 64 * k < L.nv4) {
+        // streaming stores: the rows are not read again by this launch (C2,
+        // alternating runs: 38.2 against 38.7 us; streaming loads were slower)
         if constexpr (OUT_BF16)
-          ((VM_G v2u*)rowd)[q] = v2u_make(pack_bf16x2(z.x, z.y), pack_bf16x2(z.z, z.w));
+          __builtin_nontemporal_store(v2u_make(pack_bf16x2(z.x, z.y), pack_bf16x2(z.z, z.w)), &((VM_G v2u*)rowd)[q]);
         else
-          ((VM_G v4f*)rowd)[q] = z;
+          __builtin_nontemporal_store(z, &((VM_G v4f*)rowd)[q]);
       }
     }
   }

@@ -75,8 +75,11 @@ enum : uint32_t {
   BAR_ERROR = 2,      // nonzero: a lane aborted (see VmError)
   BAR_ERRINFO = 3,    // lane / detail of the first error
   BAR_FLAGS = 64,     // [kMaxLanes] arrival epochs, one word per lane
-  BAR_WORDS = BAR_FLAGS + kMaxLanes
+  BAR_XGEN = BAR_FLAGS + kMaxLanes,   // [kXcds] copies of the release epoch, one cache line apart
+  BAR_WORDS = BAR_XGEN + 8 * 32
 };
+// XCDs per device: workgroup i of a launch is dispatched to XCD i % kXcds.
+constexpr uint32_t kXcds = 8;
 // Profiling counters (100 MHz ticks of s_memrealtime): [0] lane-time in grid
 // barriers, [1] lane-barriers; task i at kStatTask + 4 i: lane-time summed over
 // its entries, longest single entry, entry count.

@@ -194,9 +194,10 @@ VM_DEV float wave_max(float x) { return wave_reduce(x, OpMax()); }
 // lanes: the previous launch ended with every lane past its last barrier).  A lane
 // arrives by storing the epoch into its own word ctl[BAR_FLAGS + lane] with
 // release semantics -- a plain store to a private word, so arrivals never queue
-// on one atomic -- then spins until ctl[BAR_GEN] reaches the epoch.  Lane 0 is the
-// master: its 256 threads poll the other lanes' words until all have reached the
-// epoch and then publish it in ctl[BAR_GEN].  The release before each arrival and
+// on one atomic -- then spins until its XCD's copy of the release epoch reaches the
+// epoch.  Lane 0 is the master: its 256 threads poll the other lanes' words until
+// all have reached the epoch and then publish it in one word per XCD (so each
+// polled line is shared by one XCD's lanes only) and in ctl[BAR_GEN].  The release before each arrival and
 // the acquire after the wait make every lane's writes before the barrier visible
 // to every lane after it across the XCDs' L2s (the reference's device-scope fence
 // pair, vm_common.cl:231-300).  Every wait gives up after `timeout_ticks` of the
@@ -243,15 +244,17 @@ VM_DEV bool grid_barrier(Args A) {
       if (!s_ok) break;
       __builtin_amdgcn_s_sleep(1);
     }
-    if (threadIdx.x == 0 && s_ok) {
+    if (threadIdx.x < kXcds && s_ok) {
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-      __hip_atomic_store(&ctl[BAR_GEN], epoch, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(&ctl[BAR_XGEN + 32 * threadIdx.x], epoch, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+      if (threadIdx.x == 0) __hip_atomic_store(&ctl[BAR_GEN], epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   } else if (threadIdx.x == 0) {
     uint32_t ok = 1;
+    const uint32_t* gen = &ctl[BAR_XGEN + 32 * (blockIdx.x % kXcds)];
     __hip_atomic_store(&ctl[BAR_FLAGS + blockIdx.x], epoch, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
     for (uint32_t poll = 0;
-         int32_t(__hip_atomic_load(&ctl[BAR_GEN], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - epoch) < 0; ++poll) {
+         int32_t(__hip_atomic_load(gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - epoch) < 0; ++poll) {
       if (barrier_timed_out(A, t0, poll)) {
         ok = 0;
         break;

@@ -68,6 +68,9 @@ class DeviceConfig:
     # Phases that leave lanes idle keep lane 0, the grid barrier's master, idle
     # too, so it polls the arrivals while the others compute.
     idle_master: bool = True
+    # A program may run on half the lanes when the work model below says the
+    # saved per-phase overhead outweighs the halved bandwidth (extension).
+    fit_lanes: bool = True
 
     @classmethod
     def from_env(cls, environ=None) -> "DeviceConfig":
@@ -99,7 +102,8 @@ class DeviceConfig:
                    gemv=env.get("PJRT_AMD_GEMV", "1") != "0",
                    gemv_min_strip=max(8, min(256, geti("PJRT_AMD_GEMV_STRIP", 8))),
                    ln_gemv=env.get("PJRT_AMD_LN_GEMV", "1") != "0",
-                   idle_master=env.get("PJRT_AMD_IDLE_MASTER", "1") != "0")
+                   idle_master=env.get("PJRT_AMD_IDLE_MASTER", "1") != "0",
+                   fit_lanes=env.get("PJRT_AMD_FIT_LANES", "1") != "0")
 
 
 # --- instruction -> task ------------------------------------------------------
@@ -587,6 +591,54 @@ def task_cost(task: V.Task, cfg: DeviceConfig, prog: V.VMProgram) -> float:
     return n * (asz * 2 + dsz) / (_HBM_GBS * 1e3) + 0.3
 
 
+# Work model of lane_fit: chip rates split evenly over 256 CUs, one tile's
+# latency, and the grid barrier's cost (base + per lane).
+_LANE_GBS = 8000.0 / 256
+_LANE_TFLOPS = {V.DT_F32: 150.0 / 256}
+_LANE_TFLOPS_MMA = 2500.0 / 256
+_TILE_US = 2.0
+_BAR_US = 2.3
+_BAR_US_PER_LANE = 1.8 / 128
+
+
+def task_work(task: V.Task, prog: V.VMProgram) -> tuple:
+    """(HBM bytes, flops) one task moves and computes, algorithmically."""
+    dsz = V.DT_SIZE.get(task.dtype, 4)
+    asz = V.DT_SIZE.get(task.adtype, 4)
+    top = task.tile_op
+    if top == V.TOP_MMA:
+        M, N, K, G = task.p0, task.p1, task.p2, max(1, task.p3 & 0xFFFFFF)
+        return (M * K + K * N) * G * asz + M * N * G * dsz, 2.0 * M * N * K * G
+    if top == V.TOP_GEMV:
+        M, N, K, G = task.p0, task.p1, task.p2, max(1, task.p3)
+        return (K * N + M * K) * G * asz + M * N * G * dsz, 2.0 * M * N * K * G
+    if top == V.TOP_FLASH_ATTN:
+        H, T = task.p1, task.p2
+        hd = prog.aux[task.p3 + 3] if task.p3 + 3 < len(prog.aux) else 128
+        C = prog.aux[task.p3 + 2] if task.p3 + 2 < len(prog.aux) else T
+        return 2 * H * C * hd * asz, 4.0 * H * T * C * hd
+    if top == V.TOP_DECODE_ATTN:
+        return 2 * (task.p4 & 0xFFFF) * task.p5 * task.p6 * asz, 0.0
+    if top in (V.TOP_RED_SEG, V.TOP_SOFTMAX_SEG, V.TOP_LAYERNORM_SEG, V.TOP_ARGMAX_SEG):
+        return task.p0 * task.p1 * (asz + (dsz if top != V.TOP_RED_SEG else 0)), 0.0
+    n = max(task.p0, task.p1) if top != V.TOP_EW else task.p1
+    return n * (asz * 2 + dsz), 0.0
+
+
+def phase_us(tasks: list, n_lanes: int, cfg: DeviceConfig, prog: V.VMProgram) -> float:
+    """Estimated microseconds of one phase on ``n_lanes`` lanes."""
+    byts = flops = 0.0
+    tiles = 0
+    for t in tasks:
+        b, f = task_work(t, prog)
+        rate = _LANE_TFLOPS_MMA if t.adtype != V.DT_F32 else _LANE_TFLOPS[V.DT_F32]
+        byts += b
+        flops += f / rate
+        tiles += n_tiles(t, cfg)
+    rounds = -(-tiles // n_lanes) if tiles else 0
+    return rounds * _TILE_US + max(byts / (n_lanes * _LANE_GBS * 1e3), flops / (n_lanes * 1e6))
+
+
 # --- phases ---------------------------------------------------------------------
 
 def _phases(prog, indices, tasks_of, fuse, extra_reads=None):
@@ -720,6 +772,7 @@ class _Region:
     first: list             # WHILE: cond, FOR: [], IF: then
     second: list            # WHILE/FOR: body, IF: else
     op: int
+    weight: float = 1.0     # executions per launch (FOR trips, nested)
 
 
 class _Scheduler:
@@ -735,6 +788,9 @@ class _Scheduler:
         self.ln_pro = ln_gemv_pairs(prog, cfg)
         self.ln_fused = set(self.ln_pro.values())
         self.extra_reads = {j: instr_reads(prog.instrs[i], prog) for j, i in self.ln_pro.items()}
+        # estimated microseconds per launch (work model of lane_fit)
+        self.weight = 1.0
+        self.est = 0.0
 
     def task_id(self, i: int) -> int:
         tid = self.task_of.get(i)
@@ -754,6 +810,7 @@ class _Scheduler:
     def barrier(self):
         for s in self.lanes:
             s.append(V.barrier_entry())
+        self.est += self.weight * (_BAR_US + _BAR_US_PER_LANE * self.n)
 
     def levels(self, indices):
         out, seg = [], []
@@ -818,6 +875,8 @@ class _Scheduler:
             units.append((tids, n_tiles(t0, self.cfg), cost, 1))
         for lane, e in pack_units(units, self.n, self.cfg.idle_master):
             self.lanes[lane].append(e)
+        self.est += self.weight * phase_us([self.task(i) for i in indices if i not in self.ln_fused],
+                                           self.n, self.cfg, self.prog)
 
     def schedule_range(self, indices, trailing_barrier: bool):
         lv = self.levels(indices)
@@ -846,9 +905,11 @@ class _Scheduler:
         else:
             first = list(range(ins.a, ins.a + ins.b))
             second = list(range(ins.n, ins.n + ins.imm))
-        self.regions.append(_Region(ents, first, second, ins.op))
+        w = self.weight * (max(1, ins.b) if ins.op == V.OP_FOR else 1)
+        self.regions.append(_Region(ents, first, second, ins.op, w))
 
     def schedule_region(self, r: _Region):
+        self.weight = r.weight
         s0 = [len(s) for s in self.lanes]
         if r.op != V.OP_FOR:
             self.schedule_range(r.first, trailing_barrier=False)
@@ -865,8 +926,28 @@ class _Scheduler:
                 e.wait_flag, e.wait_count = s1[lane], s2[lane] - s1[lane]
 
 
-def schedule_program(prog: V.VMProgram, cfg: DeviceConfig | None = None) -> V.Schedule:
-    cfg = cfg or DeviceConfig.from_env()
+def lane_fit(prog: V.VMProgram, cfg: DeviceConfig) -> int:
+    """Lane count to schedule ``prog`` on (extension): the advertised count, or
+    half of it when the work model estimates the launch faster there.  A phase
+    of bytes B and flops F costs max(B / (L bw), F / (L flops)) per lane share
+    plus one tile latency per round of tiles, and each grid barrier a per-lane
+    overhead fitted to the decode loop (C5, one FOR trip per token: 935 us per
+    token on 256 lanes, 845 on 128 -- the saved barrier time is larger than
+    the halved bandwidth of its 240 MB).  Bandwidth- and MFMA-bound programs
+    (C2-C4) keep every lane."""
+    n = cfg.nlanes
+    if not cfg.fit_lanes or n < 128 or n % 16:
+        return n
+    best, best_us = n, None
+    for lanes in (n, n // 2):
+        c = dataclasses.replace(cfg, nlanes=lanes, fit_lanes=False)
+        sc = _schedule(prog, c)
+        if best_us is None or sc.est < best_us:
+            best, best_us = lanes, sc.est
+    return best
+
+
+def _schedule(prog: V.VMProgram, cfg: DeviceConfig) -> _Scheduler:
     sc = _Scheduler(prog, cfg)
     # No barrier after the last root level: nothing reads it before the launch
     # completes, so a one-phase program needs no grid barrier at all.
@@ -876,7 +957,16 @@ def schedule_program(prog: V.VMProgram, cfg: DeviceConfig | None = None) -> V.Sc
     root_lens = [len(s) for s in sc.lanes]
     while sc.regions:
         sc.schedule_region(sc.regions.pop(0))
-    return V.Schedule(cfg.nlanes, sc.tasks, sc.lanes, root_lens)
+    sc.root_lens = root_lens
+    return sc
+
+
+def schedule_program(prog: V.VMProgram, cfg: DeviceConfig | None = None) -> V.Schedule:
+    cfg = cfg or DeviceConfig.from_env()
+    if cfg.fit_lanes:
+        cfg = dataclasses.replace(cfg, nlanes=lane_fit(prog, cfg), fit_lanes=False)
+    sc = _schedule(prog, cfg)
+    return V.Schedule(cfg.nlanes, sc.tasks, sc.lanes, sc.root_lens)
 
 
 def schedule_bytes(prog: V.VMProgram, cfg: DeviceConfig | None = None) -> bytes:

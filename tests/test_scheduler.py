@@ -390,3 +390,29 @@ def test_layernorm_row_interleave():
     args = [rng.standard_normal((32, 24)).astype(np.float32), rng.uniform(0.5, 1.5, 24).astype(np.float32),
             rng.normal(0, 0.1, 24).astype(np.float32)]
     np.testing.assert_array_equal(vmref.execute_schedule(blob, args)[0], vmref.execute(blob, args)[0])
+
+
+def test_lane_fit():
+    """A program of many small phases (the decode loop) runs on half the
+    lanes; bandwidth- and MFMA-bound programs keep every lane."""
+    import dataclasses
+    from pjrt_amd import configs as CF
+    cfg = S.DeviceConfig(nlanes=256)
+    dec = CF.gpt_c5(dataclasses.replace(CF.C5, layers=2, steps=8))
+    assert S.lane_fit(dec, cfg) == 128
+    assert S.schedule_program(dec, cfg).n_lanes == 128
+    assert S.schedule_program(dec, dataclasses.replace(cfg, fit_lanes=False)).n_lanes == 256
+    assert S.lane_fit(dec, S.DeviceConfig(nlanes=7)) == 7
+    g = G.Graph()
+    x = g.input((8192, 4096))
+    ga, be = g.input((4096,)), g.input((4096,))
+    g.output(g.layernorm(x, ga, be, 1e-5, gelu=True, out_dtype="bf16"))
+    assert S.lane_fit(g.build(), cfg) == 256
+    g = G.Graph()
+    a, b = g.input((4096, 4096), "bf16"), g.input((4096, 4096), "bf16")
+    g.output(g.dot(a, b))
+    assert S.lane_fit(g.build(), cfg) == 256
+    # the FOR body's phases count once per trip
+    one = S._schedule(dec, dataclasses.replace(cfg, fit_lanes=False)).est
+    dec16 = CF.gpt_c5(dataclasses.replace(CF.C5, layers=2, steps=16))
+    assert S._schedule(dec16, dataclasses.replace(cfg, fit_lanes=False)).est > 1.5 * one

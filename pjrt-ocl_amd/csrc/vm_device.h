@@ -204,11 +204,15 @@ VM_DEV float wave_max(float x) { return wave_reduce(x, OpMax()); }
 // 100 MHz constant clock, so a broken schedule ends the launch with an error
 // instead of hanging.  Returns false when the launch must abort.
 __shared__ uint32_t vm_bar_epoch;      // epoch of this lane's last barrier
+__shared__ uint32_t vm_bar_ready;      // vm_bar_epoch is set (this lane passed a barrier)
 
+// The launch's base epoch is read at the lane's first barrier, not here: until
+// this lane has arrived there, lane 0 cannot advance ctl[BAR_GEN], so the read
+// still sees the base -- and a program without barriers never waits on it
+// (the read is a memory round trip ahead of every lane's first tile).
 VM_DEV void grid_barrier_init(Args A) {
-  if (threadIdx.x == 0)
-    vm_bar_epoch = __hip_atomic_load(&A->ctl[BAR_GEN], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  __syncthreads();
+  (void)A;
+  if (threadIdx.x == 0) vm_bar_ready = 0;   // read after grid_barrier's first block sync
 }
 
 // Every poll checks the clock; only every 32nd also reads the error word (a
@@ -229,6 +233,11 @@ VM_DEV bool grid_barrier(Args A) {
   __shared__ uint32_t s_ok;
   __syncthreads();
   uint32_t* ctl = A->ctl;
+  if (!vm_bar_ready) {       // block-uniform: vm_bar_ready changes only after the last sync below
+    if (threadIdx.x == 0)
+      vm_bar_epoch = __hip_atomic_load(&ctl[BAR_GEN], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+  }
   const uint32_t epoch = vm_bar_epoch + 1;
   const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
   if (blockIdx.x == 0) {
@@ -265,7 +274,10 @@ VM_DEV bool grid_barrier(Args A) {
     s_ok = ok;
   }
   __syncthreads();
-  if (threadIdx.x == 0) vm_bar_epoch = epoch;   // read again only after the next barrier's block sync
+  if (threadIdx.x == 0) {        // read again only after the next barrier's block sync
+    vm_bar_epoch = epoch;
+    vm_bar_ready = 1;
+  }
   return s_ok != 0;
 }
 

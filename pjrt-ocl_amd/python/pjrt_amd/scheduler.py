@@ -61,13 +61,13 @@ class DeviceConfig:
     # Matmuls of at most 8 rows as column-strip TOP_GEMV tasks (extension), and
     # the narrowest strip width they may use.
     gemv: bool = True
-    gemv_min_strip: int = 8
+    gemv_min_strip: int = 0          # 0: by lane count (gemv_strip_floor)
     # A layernorm whose only reader is a TOP_GEMV runs inside that GEMV's x
     # staging (extension; saves the phase between them).
     ln_gemv: bool = True
     # Phases that leave lanes idle keep lane 0, the grid barrier's master, idle
     # too, so it polls the arrivals while the others compute.
-    idle_master: bool = True
+    idle_master: bool | None = None  # None: by lane count (master_idle)
     # A program may run on half the lanes when the work model below says the
     # saved per-phase overhead outweighs the halved bandwidth (extension).
     fit_lanes: bool = True
@@ -100,9 +100,9 @@ class DeviceConfig:
                    fuse=env.get("PJRT_OCL_FUSE", "1") != "0",
                    mma_autotile=env.get("PJRT_AMD_MMA_AUTOTILE", "1") != "0",
                    gemv=env.get("PJRT_AMD_GEMV", "1") != "0",
-                   gemv_min_strip=max(8, min(256, geti("PJRT_AMD_GEMV_STRIP", 8))),
+                   gemv_min_strip=max(0, min(256, geti("PJRT_AMD_GEMV_STRIP", 0))),
                    ln_gemv=env.get("PJRT_AMD_LN_GEMV", "1") != "0",
-                   idle_master=env.get("PJRT_AMD_IDLE_MASTER", "1") != "0",
+                   idle_master=(env["PJRT_AMD_IDLE_MASTER"] != "0") if env.get("PJRT_AMD_IDLE_MASTER") else None,
                    fit_lanes=env.get("PJRT_AMD_FIT_LANES", "1") != "0")
 
 
@@ -180,6 +180,22 @@ GEMV_MAX_M = 8
 GEMV_LDS_FLOATS = 147456 // 4   # the kernel's LDS: x rows + row-phase sums
 _EPI_INLINE = {V.SUB_AFFINE, V.SUB_GELU, V.SUB_COPY, V.SUB_ADD, V.SUB_MUL, V.SUB_SUB, V.SUB_DIV,
                V.SUB_MAX, V.SUB_MIN}
+
+
+# Defaults that depend on the lane count, measured on the decode loop (C5,
+# alternating runs): on 256 lanes 8-column strips and an idle lane 0 were
+# faster (1035 -> 1042 and 1006 -> 1015 tokens/s); on 128 lanes 16-column
+# strips with lane 0 taking tiles are (1178 -> 1197).
+def gemv_strip_floor(cfg) -> int:
+    """Narrowest GEMV strip the scheduler may use."""
+    if cfg.gemv_min_strip:
+        return max(8, cfg.gemv_min_strip)
+    return 8 if cfg.nlanes > 128 else 16
+
+
+def master_idle(cfg) -> bool:
+    """Whether phases that leave lanes idle keep lane 0 idle too."""
+    return cfg.idle_master if cfg.idle_master is not None else cfg.nlanes > 128
 
 
 def gemv_strip(N: int, G: int, nlanes: int, min_strip: int = 8) -> int:
@@ -426,7 +442,7 @@ def instr_to_task(ins: V.Instr, prog: V.VMProgram, cfg: DeviceConfig) -> V.Task:
             t = V.Task(V.TOP_RED_SEG, ins.dst, ins.a, ins.b, M, K, 0, 1)
         elif _gemv_form(ins, prog, cfg):
             t = V.Task(V.TOP_GEMV, ins.dst, ins.a, ins.b, M, N, K, G,
-                       gemv_strip(N, G, cfg.nlanes, cfg.gemv_min_strip), 0, epi,
+                       gemv_strip(N, G, cfg.nlanes, gemv_strip_floor(cfg)), 0, epi,
                        epi_res if epi else 0)
         else:
             code = V.MMA_TILE_CODES.get(ins.mma_tile, 0)
@@ -873,7 +889,7 @@ class _Scheduler:
             t0 = self.tasks[tids[0]]
             cost = sum(task_cost(self.tasks[t], self.cfg, self.prog) for t in tids)
             units.append((tids, n_tiles(t0, self.cfg), cost, 1))
-        for lane, e in pack_units(units, self.n, self.cfg.idle_master):
+        for lane, e in pack_units(units, self.n, master_idle(self.cfg)):
             self.lanes[lane].append(e)
         self.est += self.weight * phase_us([self.task(i) for i in indices if i not in self.ln_fused],
                                            self.n, self.cfg, self.prog)

@@ -416,3 +416,18 @@ def test_lane_fit():
     one = S._schedule(dec, dataclasses.replace(cfg, fit_lanes=False)).est
     dec16 = CF.gpt_c5(dataclasses.replace(CF.C5, layers=2, steps=16))
     assert S._schedule(dec16, dataclasses.replace(cfg, fit_lanes=False)).est > 1.5 * one
+
+
+def test_lane_count_defaults():
+    """Strip floor and idle master follow the lane count unless set."""
+    assert S.gemv_strip_floor(S.DeviceConfig(nlanes=256)) == 8
+    assert S.gemv_strip_floor(S.DeviceConfig(nlanes=128)) == 16
+    assert S.gemv_strip_floor(S.DeviceConfig(nlanes=128, gemv_min_strip=8)) == 8
+    assert S.gemv_strip_floor(S.DeviceConfig(nlanes=256, gemv_min_strip=3)) == 8
+    assert S.master_idle(S.DeviceConfig(nlanes=256)) is True
+    assert S.master_idle(S.DeviceConfig(nlanes=128)) is False
+    assert S.master_idle(S.DeviceConfig(nlanes=128, idle_master=True)) is True
+    env = S.DeviceConfig.from_env({"PJRT_AMD_GEMV_STRIP": "8", "PJRT_AMD_IDLE_MASTER": "1"})
+    assert env.gemv_min_strip == 8 and env.idle_master is True
+    env = S.DeviceConfig.from_env({})
+    assert env.gemv_min_strip == 0 and env.idle_master is None

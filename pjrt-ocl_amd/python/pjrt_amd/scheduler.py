@@ -951,16 +951,21 @@ def lane_fit(prog: V.VMProgram, cfg: DeviceConfig) -> int:
     token on 256 lanes, 845 on 128 -- the saved barrier time is larger than
     the halved bandwidth of its 240 MB).  Bandwidth- and MFMA-bound programs
     (C2-C4) keep every lane."""
+    return _fit(prog, cfg)[0]
+
+
+def _fit(prog: V.VMProgram, cfg: DeviceConfig):
+    """(lanes, schedule) of lane_fit; the schedule is None when only one lane
+    count was a candidate."""
     n = cfg.nlanes
     if not cfg.fit_lanes or n < 128 or n % 16:
-        return n
-    best, best_us = n, None
+        return n, None
+    best, best_sc = n, None
     for lanes in (n, n // 2):
-        c = dataclasses.replace(cfg, nlanes=lanes, fit_lanes=False)
-        sc = _schedule(prog, c)
-        if best_us is None or sc.est < best_us:
-            best, best_us = lanes, sc.est
-    return best
+        sc = _schedule(prog, dataclasses.replace(cfg, nlanes=lanes, fit_lanes=False))
+        if best_sc is None or sc.est < best_sc.est:
+            best, best_sc = lanes, sc
+    return best, best_sc
 
 
 def _schedule(prog: V.VMProgram, cfg: DeviceConfig) -> _Scheduler:
@@ -979,10 +984,10 @@ def _schedule(prog: V.VMProgram, cfg: DeviceConfig) -> _Scheduler:
 
 def schedule_program(prog: V.VMProgram, cfg: DeviceConfig | None = None) -> V.Schedule:
     cfg = cfg or DeviceConfig.from_env()
-    if cfg.fit_lanes:
-        cfg = dataclasses.replace(cfg, nlanes=lane_fit(prog, cfg), fit_lanes=False)
-    sc = _schedule(prog, cfg)
-    return V.Schedule(cfg.nlanes, sc.tasks, sc.lanes, sc.root_lens)
+    lanes, sc = _fit(prog, cfg)
+    if sc is None:
+        sc = _schedule(prog, dataclasses.replace(cfg, nlanes=lanes, fit_lanes=False))
+    return V.Schedule(lanes, sc.tasks, sc.lanes, sc.root_lens)
 
 
 def schedule_bytes(prog: V.VMProgram, cfg: DeviceConfig | None = None) -> bytes:

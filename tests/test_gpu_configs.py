@@ -13,7 +13,7 @@ import sys
 import numpy as np
 import pytest
 
-from gpu_util import assert_rel, blob_for, run_both, runtime
+from gpu_util import assert_rel, blob_for, run_both, run_gpu, runtime
 from oracle import vmref
 from pjrt_amd import configs as CF
 
@@ -77,3 +77,23 @@ def test_gpt_c5_full_program_deterministic():
         np.testing.assert_array_equal(x, y)
     toks = np.concatenate(a)
     assert toks.shape == (CF.C5.steps + 1,) and toks.min() >= 0 and toks.max() < CF.C5.vocab
+
+
+def test_gpt_c5_lane_fit_matches_every_lane():
+    """The decode program scheduled on half the lanes (lane_fit, with its
+    lane-count defaults) gives the tokens of the same program on every lane
+    (16 steps: with fewer, the prefill dominates and every lane is kept)."""
+    c = dataclasses.replace(CF.C5, steps=16)
+    prog = CF.gpt_c5(c, emit_logits=True)
+    args = CF.gpt_inputs(c)
+    fit, _ = blob_for(prog)
+    full, _ = blob_for(prog, fit_lanes=False)
+    lanes = vmref.parse(fit).n_lanes, vmref.parse(full).n_lanes
+    print(f"[gpu] lane fit: {lanes[0]} lanes against {lanes[1]}", file=sys.stderr, flush=True)
+    if runtime().info["n_lanes"] >= 128:
+        assert lanes[0] == lanes[1] // 2
+    got = run_gpu(fit, args)
+    want = run_gpu(full, args)
+    # the strip width, and with it the summation order of the bf16 GEMVs,
+    # differs between the two schedules: the bf16 decoder tolerance applies
+    assert check_decoder(got, want, 5e-3) >= 4

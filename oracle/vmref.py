@@ -749,6 +749,8 @@ class TaskRunner:
                 y = res[:M * N * (g + 1)].reshape(-1, M, N)[g, r0:r1, c0:c1]
             elif src == 2:
                 y = np.broadcast_to(res[c0:c1], v.shape)
+            elif src == 3:          # this build's constant operand: y = s
+                y = np.full(v.shape, np.float32(s), np.float32)
             else:
                 y = v
             v = np.asarray(_epi_micro(kind, v, y, np.float32(s), np.float32(tt)), np.float32)

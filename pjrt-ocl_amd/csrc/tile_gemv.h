@@ -335,6 +335,7 @@ VM_TILE void gemv_tile(Args A, uint32_t ti, uint32_t tile) {
       float y = x;
       if (src == 1) y = first ? ry1 : gcast<float>(res)[elem];
       else if (src == 2) y = first ? ry2 : gcast<float>(res)[n];
+      else if (src == 3) y = __int_as_float(e[3 + 4 * k]);     // constant operand s (extension)
       x = epi_inline(kind, x, y, __int_as_float(e[3 + 4 * k]), __int_as_float(e[4 + 4 * k]));
     }
     store_f(d, dt, elem, x);

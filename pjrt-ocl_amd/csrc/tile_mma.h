@@ -49,6 +49,7 @@ VM_TILE float apply_epilogue(Args A, uint32_t epi, const gbyte* res, uint64_t el
     float y = v;
     if (src == 1) y = gcast<float>(res)[elem];
     else if (src == 2) y = gcast<float>(res)[col];
+    else if (src == 3) y = s;          // constant operand (extension: relu as max(v, 0))
     v = micro(kind, v, y, s, t);
   }
   return v;
@@ -427,6 +428,7 @@ VM_DEV void store_fast(Args A, const MmaDesc& D, const f32x16 (&acc)[4][4], uint
         v4f y = x;
         if (src == 1) y = *(const VM_G v4f*)(D.res + (tile0 + off) * 4);
         else if (src == 2) y = *(const VM_G v4f*)(D.res + (uint64_t(n0) + c) * 4);
+        else if (src == 3) y = v4f{s, s, s, s};
         x.x = epi_inline(kind, x.x, y.x, s, t);
         x.y = epi_inline(kind, x.y, y.y, s, t);
         x.z = epi_inline(kind, x.z, y.z, s, t);

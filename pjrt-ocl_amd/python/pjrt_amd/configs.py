@@ -33,10 +33,9 @@ def mlp_c1(batch=256, d_in=128, d_hidden=512, d_out=64):
     x = g.input((batch, d_in))
     w1, b1 = g.input((d_in, d_hidden)), g.input((d_hidden,))
     w2, b2 = g.input((d_hidden, d_out)), g.input((d_out,))
-    # bias per column, then relu as max(h, 0): the epilogue's binary ops take the
-    # per-column operand, so relu is the elementwise max against a zero splat
-    h = g.dot(x, w1, epilogue=[(V.SUB_ADD, 2, 0.0, 0.0)], residual=b1)
-    h = g.maximum(h, g.fill((batch, d_hidden), 0.0))
+    # bias per column, then relu as max(h, 0) against the epilogue's constant
+    # operand (src 3), in the matmul's store: no phase of its own
+    h = g.dot(x, w1, epilogue=[(V.SUB_ADD, 2, 0.0, 0.0), (V.SUB_MAX, 3, 0.0, 0.0)], residual=b1)
     y = g.dot(h, w2, epilogue=[(V.SUB_ADD, 2, 0.0, 0.0)], residual=b2)
     g.output(y)
     return g.build()

@@ -415,7 +415,8 @@ class Graph:
         """C[G,M,N] = A[G,M,K] @ B[G,K,N]; leading dims of a 2-D-weight matmul
         fold into M.  ``a``/``b`` may be views (folded transposes).  The
         epilogue is a list of (kind, src, s, t) micro-ops applied before the
-        store (src 0: unary, 1: residual per element, 2: residual per column)."""
+        store (src 0: unary, 1: residual per element, 2: residual per column,
+        3: the constant s -- this build's extension, e.g. relu as (MAX, 3, 0, 0))."""
         if len(b.shape) == 2:
             G = 1
             K = a.shape[-1]

@@ -58,6 +58,9 @@ Task scratch: the loader gives each task that needs it (a split decode
 attention or argmax) its own zeroed region of device memory; the last split of
 a head / row resets its arrival counter, so the region is zero again for the
 next run.
+
+Matmul epilogue source 3: a micro-op (kind, 3, s, t) takes the constant s as
+its operand, e.g. relu as (SUB_MAX, 3, 0, 0) in the matmul's store.
 """
 from __future__ import annotations
 

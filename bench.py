@@ -64,14 +64,17 @@ def c2_inputs():
     return x, gamma, beta
 
 
-def time_program(rt, lp, dev_in, dev_out, steps, warmup, min_warm_s=0.3):
+def time_program(rt, lp, dev_in, dev_out, steps, warmup, min_warm_s=0.3, sets=None):
     """Warm up (at least `warmup` executions and `min_warm_s` seconds, so the GPU
     clocks have ramped up), then time exactly `steps` back-to-back executions:
-    wall clock around the whole region and HIP events on the launch stream."""
+    wall clock around the whole region and HIP events on the launch stream.
+    `sets`, a list of (inputs, outputs), rotates the buffers step by step (a
+    working set larger than the 256 MB memory-side cache: a cold-cache rate)."""
+    sets = sets or [(dev_in, dev_out)]
     t_warm = time.perf_counter()
     n = 0
     while n < warmup or time.perf_counter() - t_warm < min_warm_s:
-        lp.enqueue(dev_in, dev_out)
+        lp.enqueue(*sets[n % len(sets)])
         n += 1
         if n % 8 == 0:
             rt.synchronize()
@@ -81,8 +84,8 @@ def time_program(rt, lp, dev_in, dev_out, steps, warmup, min_warm_s=0.3):
     rt.synchronize()
     t0 = time.perf_counter()
     e0.record()
-    for _ in range(steps):
-        lp.enqueue(dev_in, dev_out)
+    for i in range(steps):
+        lp.enqueue(*sets[i % len(sets)])
     e1.record()
     rt.synchronize()
     wall = time.perf_counter() - t0
@@ -99,14 +102,56 @@ def load_traffic(name):
         return None
 
 
-def cpu_baseline_c2(x, gamma, beta, budget_s=10.0):
-    """The reference's CPU engine path for config 2 (decomposed phases), restated in
-    C (oracle/refcpu.c), on the host cores, over the full workload."""
+def cpu_info():
+    """Host threads the CPU baseline uses and the host's CPU model.  The GPU box
+    gives one GPU's job a share of 16 host cores (its OMP_NUM_THREADS), whatever
+    nproc reports, so the baseline uses min(16, available cores)."""
+    avail = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    share = int(os.environ.get("OMP_NUM_THREADS", "16") or 16)
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return max(1, min(avail, share, 16)), os.cpu_count() or 1, model
+
+
+def time_cpu(call, budget_s=10.0, min_round_s=0.1, min_rounds=5):
+    """Median seconds per call: one warm-up call, then rounds of adaptive length
+    (at least `min_round_s` each), at least `min_rounds` of them and as many more
+    as fit `budget_s` (the reference's tools/bench_cpu.py:35-50 methodology)."""
+    t0 = time.perf_counter()
+    call()
+    per = max(time.perf_counter() - t0, 1e-6)
+    reps = max(1, int(math.ceil(min_round_s / per)))
+    rounds, t_start = [], time.perf_counter()
+    while len(rounds) < min_rounds or (time.perf_counter() - t_start < budget_s and len(rounds) < 50):
+        t = time.perf_counter()
+        for _ in range(reps):
+            call()
+        rounds.append((time.perf_counter() - t) / reps)
+    return float(np.median(rounds)), len(rounds), reps
+
+
+def _refcpu():
     lib = ctypes.CDLL(os.path.join(ROOT, "oracle", "librefcpu.so"))
     lib.refcpu_ln_gelu_bf16.restype = ctypes.c_int
     lib.refcpu_ln_gelu_bf16.argtypes = [ctypes.c_void_p] * 4 + [ctypes.c_int64, ctypes.c_int64, ctypes.c_float,
                                                                ctypes.c_void_p, ctypes.c_int]
-    cores = min(16, os.cpu_count() or 1)
+    lib.refcpu_mlp_f32.restype = ctypes.c_int
+    lib.refcpu_mlp_f32.argtypes = [ctypes.c_void_p] * 7 + [ctypes.c_int64] * 4 + [ctypes.c_int]
+    return lib
+
+
+def cpu_baseline_c2(x, gamma, beta, budget_s=10.0):
+    """The reference's CPU engine path for config 2 (decomposed phases), restated in
+    C (oracle/refcpu.c), on the host cores, over the full workload."""
+    lib = _refcpu()
+    cores, nproc, model = cpu_info()
     out = np.empty((C2_ROWS, C2_D), np.uint16)
     scratch = np.empty(2 * C2_ROWS * C2_D + 2 * C2_ROWS, np.float32)
 
@@ -114,18 +159,35 @@ def cpu_baseline_c2(x, gamma, beta, budget_s=10.0):
         lib.refcpu_ln_gelu_bf16(x.ctypes.data, gamma.ctypes.data, beta.ctypes.data, out.ctypes.data, C2_ROWS, C2_D,
                                 1e-5, scratch.ctypes.data, cores)
 
-    call()
-    n, t0 = 0, time.perf_counter()
-    while True:
-        call()
-        n += 1
-        if time.perf_counter() - t0 >= budget_s or n >= 200:
-            break
-    dt = (time.perf_counter() - t0) / n
+    dt, rounds, reps = time_cpu(call, budget_s)
     return {"value": round(C2_BYTES / dt / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
-            "sample": f"full config-2 workload [8192,4096], {n} timed calls after 1 warm-up, "
-                      f"{dt * 1e3:.1f} ms/call; C restatement of the reference's decomposed CPU-engine phases "
-                      f"(oracle/refcpu.c)"}, out
+            "nproc": nproc, "cpu_model": model,
+            "sample": f"full config-2 workload [8192,4096]; median of {rounds} rounds of {reps} call(s) after a "
+                      f"warm-up call, {dt * 1e3:.1f} ms/call; C restatement of the reference's decomposed "
+                      f"CPU-engine phases (oracle/refcpu.c)"}, out
+
+
+def cpu_baseline_c1(args, budget_s=3.0):
+    """Config 1 on the reference's CPU path (its configs[0] names the PoCL CPU
+    path): two SGEMM phases plus bias / relu phases (oracle/refcpu.c)."""
+    lib = _refcpu()
+    cores, nproc, model = cpu_info()
+    x, w1, b1, w2, b2 = args
+    M, D = x.shape
+    H, O = w1.shape[1], w2.shape[1]
+    y = np.empty((M, O), np.float32)
+    h = np.empty((M, H), np.float32)
+
+    def call():
+        lib.refcpu_mlp_f32(x.ctypes.data, w1.ctypes.data, b1.ctypes.data, w2.ctypes.data, b2.ctypes.data,
+                           y.ctypes.data, h.ctypes.data, M, D, H, O, cores)
+
+    dt, rounds, reps = time_cpu(call, budget_s)
+    flops = 2.0 * M * D * H + 2.0 * M * H * O
+    return {"value": round(flops / dt / 1e9, 3), "unit": "GFLOP/s", "cores": cores, "kind": "port",
+            "nproc": nproc, "cpu_model": model, "ms_per_forward": round(dt * 1e3, 4),
+            "sample": f"full config-1 forward; median of {rounds} rounds of {reps} call(s); C restatement of the "
+                      f"reference's CPU-engine SGEMM + elementwise phases (oracle/refcpu.c)"}, y
 
 
 def bench_c2(rt, steps, warmup, with_cpu):
@@ -136,6 +198,14 @@ def bench_c2(rt, steps, warmup, with_cpu):
     dev_out = lp.alloc_outputs()
     ms_step, ms_kernel = time_program(rt, lp, dev_in, dev_out, steps, warmup)
     got = dev_out[0].to_host(np.uint16, (C2_ROWS, C2_D))
+    # cold: three input/output sets (3 x 192 MiB) in rotation, more than the
+    # 256 MB memory-side cache holds, so every step's reads come from HBM
+    extra_sets = [([rt.to_device(x), dev_in[1], dev_in[2]], lp.alloc_outputs()) for _ in range(2)]
+    sets = [(dev_in, dev_out)] + extra_sets
+    cold_step, cold_kernel = time_program(rt, lp, None, None, steps, warmup, sets=sets)
+    for ins, outs in extra_sets:
+        for b in [ins[0]] + outs:
+            b.free()
     # spot check against float64 math on a slice of rows
     rows = slice(0, 256)
     x64 = x[rows].astype(np.float64)
@@ -153,6 +223,7 @@ def bench_c2(rt, steps, warmup, with_cpu):
                       (got.astype(np.uint32) << 16).view(np.float32).astype(np.float64))
         cpu["max_abs_diff_vs_gpu"] = float(diff.max())
     achieved = C2_BYTES / (ms_kernel * 1e-3) / 1e9
+    cold_achieved = C2_BYTES / (cold_kernel * 1e-3) / 1e9
     traffic = load_traffic("c2")
     res = {
         "value": C2_BYTES / (ms_step * 1e-3) / 1e9, "unit": "GB/s", "ms_per_step": ms_step,
@@ -160,6 +231,10 @@ def bench_c2(rt, steps, warmup, with_cpu):
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic.get("bytes_per_launch") if traffic else None},
+        "cold": {"sets": len(sets), "working_set_bytes": len(sets) * (C2_ROWS * C2_D * 6),
+                 "value": round(C2_BYTES / (cold_step * 1e-3) / 1e9, 2), "ms_per_step": round(cold_step, 5),
+                 "kernel_ms": round(cold_kernel, 5), "achieved": round(cold_achieved, 2),
+                 "frac": round(cold_achieved / HBM_PEAK_GBS, 4)},
         "cpu_baseline": cpu, "max_rel_err_first_256_rows": err,
     }
     for b in dev_in + dev_out:
@@ -237,8 +312,9 @@ def bench_attention(rt, steps, warmup, B=4, H=16, S=2048, D=128):
             "max_rel_err_2_heads": max(errs)}
 
 
-def bench_c1(rt, steps):
-    """Config 1: the f32 two-layer MLP forward, on the GPU."""
+def bench_c1(rt, steps, with_cpu=False):
+    """Config 1: the f32 two-layer MLP forward, on the GPU,
+    beside the reference's CPU path for it (the path configs[0] names)."""
     from pjrt_amd import configs as CF
     args = CF.mlp_c1_inputs()
     lp = rt.compile(CF.mlp_c1())
@@ -253,9 +329,14 @@ def bench_c1(rt, steps):
     for b in dev_in + dev_out:
         b.free()
     lp.close()
-    return {"workload": "C1 f32 MLP x[256,128] @ W1[128,512] + b1, relu, @ W2[512,64] + b2",
-            "ms_per_step": ms_step, "kernel_ms": ms_kernel,
-            "gflops": round(flops / (ms_kernel * 1e-3) / 1e9, 2), "max_rel_err": err}
+    res = {"workload": "C1 f32 MLP x[256,128] @ W1[128,512] + b1, relu, @ W2[512,64] + b2",
+           "ms_per_step": ms_step, "kernel_ms": ms_kernel,
+           "gflops": round(flops / (ms_kernel * 1e-3) / 1e9, 2), "max_rel_err": err}
+    if with_cpu:
+        cpu, ycpu = cpu_baseline_c1(args)
+        cpu["max_rel_diff_vs_gpu"] = float(np.abs(ycpu - y).max() / np.abs(y).max())
+        res["cpu_baseline"] = cpu
+    return res
 
 
 def bench_c5(rt, reps=3):
@@ -329,7 +410,11 @@ def main():
         raise SystemExit("bench.py measures one GPU: this build has no multi-GPU path "
                          "(each GPU would run its own shard of the same megakernel; see DESIGN.md)")
     from pjrt_amd.runtime import Runtime
-    rt = Runtime(device=0)
+    with Runtime(device=0) as rt:      # closed (programs first) before interpreter exit
+        run(args, rt)
+
+
+def run(args, rt):
     log(f"device {rt.info['name']} {rt.info['arch']} lanes={rt.info['n_lanes']}")
     wl = set(args.workloads.split(","))
     extra = {}
@@ -342,7 +427,7 @@ def main():
         extra["c4"] = bench_attention(rt, max(5, args.steps // 5), 2)
     if "c1" in wl:
         log("C1")
-        extra["c1"] = bench_c1(rt, max(5, args.steps))
+        extra["c1"] = bench_c1(rt, max(5, args.steps), not args.no_cpu)
     if "c5" in wl:
         log("C5")
         extra["c5"] = bench_c5(rt)
@@ -360,7 +445,8 @@ def main():
         "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
         "config": {"workload": "C2 fused layernorm(eps=1e-5, gamma/beta) + tanh-GELU + f32->bf16 on x[8192,4096] f32",
                    "rows": C2_ROWS, "d": C2_D, "bytes_per_step": C2_BYTES, "kernel_ms": round(c2["kernel_ms"], 5)},
-        "roofline": c2["roofline"], "cpu_baseline": c2["cpu_baseline"], "extra": extra,
+        "roofline": c2["roofline"], "cpu_baseline": c2["cpu_baseline"], "cold_cache": c2["cold"],
+        "extra": extra,
     }
     print(json.dumps(line), flush=True)
 

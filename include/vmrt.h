@@ -65,7 +65,10 @@ void vmrt_default_options(vmrt_options* opts);
  * Replaces OclRuntime::Create (runtime.h:120-135; runtime.cc:255-662). */
 int vmrt_create(const vmrt_options* opts, vmrt_runtime** out, char* err, size_t errlen);
 
-/* Replaces OclRuntime::~OclRuntime. */
+/* Replaces OclRuntime::~OclRuntime.  Waits for the device, then unloads every
+ * program still loaded on this runtime (a program borrows its runtime's device,
+ * stream and mutex, runtime.h:365): their handles are invalid afterwards and must
+ * not be passed to vmrt_unload or any other call. */
 void vmrt_destroy(vmrt_runtime* rt);
 
 /* Device parameters the lowering must schedule for: these are the values the
@@ -81,7 +84,8 @@ int vmrt_device_info_get(vmrt_runtime* rt, vmrt_device_info* out);
 int vmrt_load(vmrt_runtime* rt, const void* bytes, size_t len, uint32_t ew_ts, uint32_t mma_t,
               vmrt_program** out, char* err, size_t errlen);
 
-/* Replaces LoadedProgram::~LoadedProgram (runtime.cc:1076-1086). */
+/* Replaces LoadedProgram::~LoadedProgram (runtime.cc:1076-1086).  Waits for the
+ * program's last launch first. */
 void vmrt_unload(vmrt_program* prog);
 
 /* Program signature (executable metadata the PJRT layer reports,
@@ -104,7 +108,9 @@ int vmrt_execute(vmrt_program* prog, const void* const* inputs, size_t n_inputs,
 int vmrt_enqueue(vmrt_program* prog, const void* const* inputs, size_t n_inputs, void* const* outputs,
                  size_t n_outputs, void* stream, char* err, size_t errlen);
 
-/* Wait for the runtime's stream, then read and clear the program's VM status
+/* Wait for the program's last launch (on whichever stream it was enqueued:
+ * vmrt_execute / vmrt_enqueue record a completion event after it), then read and
+ * clear the program's VM status
  * word (barrier time-out, frame overflow).  Extension of the reference, whose
  * clFinish error path only reports an OpenCL code (runtime.cc:2185-2189). */
 int vmrt_program_status(vmrt_program* prog, char* err, size_t errlen);

@@ -17,7 +17,9 @@
  *     runs them (runtime.cc:1483-2105), work split over the host cores like PoCL's
  *     one-work-item work-groups (runtime.cc:620-622);
  *   - f32 matmul: a cache-blocked SGEMM standing in for the packed mm2p kernel
- *     (vm_main.cl:419-518), row panels split over the cores.
+ *     (vm_main.cl:419-518), row panels split over the cores;
+ *   - config 1, the f32 MLP: two SGEMM phases with the bias adds and the relu
+ *     as elementwise phases between them.
  *
  * Parity of these routines is checked by tests/test_refcpu.py against the numpy
  * oracle; they exist to be timed, not to define semantics.
@@ -113,6 +115,23 @@ int refcpu_sgemm(const float* A, const float* B, float* C, int64_t M, int64_t N,
       }
     }
   }
+  return 0;
+}
+
+/* Config 1, the f32 MLP y = relu(x W1 + b1) W2 + b2, as the reference's CPU engine
+ * runs it: each matmul phase peeled to the packed SGEMM (runtime.cc:1698-1800),
+ * the bias adds and the relu as elementwise phases over the result.  `h` holds
+ * M * H floats. */
+int refcpu_mlp_f32(const float* x, const float* w1, const float* b1, const float* w2, const float* b2, float* y,
+                   float* h, int64_t M, int64_t D, int64_t H, int64_t O, int threads) {
+  refcpu_sgemm(x, w1, h, M, H, D, threads);
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < M * H; ++i) h[i] += b1[i % H];
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < M * H; ++i) h[i] = h[i] > 0.0f ? h[i] : 0.0f;
+  refcpu_sgemm(h, w2, y, M, O, H, threads);
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < M * O; ++i) y[i] += b2[i % O];
   return 0;
 }
 

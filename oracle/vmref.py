@@ -83,8 +83,13 @@ def bf16_to_f32(b):
 
 def f32_to_bf16(x):
     """RNE f32 -> bf16 bits; NaN stays NaN (quiet bit set)."""
-    u = np.ascontiguousarray(x, np.float32).view(np.uint32).astype(np.uint64)
-    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    u = np.ascontiguousarray(x, np.float32).view(np.uint32)
+    # u32 sums that wrap (negative NaN patterns only) lose only the bit the
+    # 16-bit cast drops; NaNs are replaced below anyway
+    r = (u >> 16) & np.uint32(1)
+    r += u
+    r += np.uint32(0x7FFF)
+    r = (r >> 16).astype(np.uint16)
     nan = (u & 0x7FFFFFFF) > 0x7F800000
     if np.any(nan):
         r = np.where(nan, ((u >> 16) | 0x40).astype(np.uint16), r)

@@ -221,10 +221,11 @@ VM_TILE void decode_attn_split(Args A, uint32_t ti, uint32_t tile) {
     return;
   }
   // split: publish the partial, count the arrival; the last split combines.
-  // Partials and counters move as agent-scope atomics, which go to memory past
-  // the XCD's L2, so no L2-wide write-back (release fence) is needed: the
-  // stores are complete (vmcnt) before the counter moves, and the combining
-  // split reads them back past its own L2.
+  // The partials are agent-scope atomic stores; the workgroup barrier orders
+  // every thread's stores before thread 0's arrival, an agent-scope
+  // acquire-release read-modify-write: its release publishes this workgroup's
+  // partials to the other XCDs, its acquire (observed by the last arriver)
+  // makes every earlier split's partials visible before the combine reads them.
   uint32_t* sp = reinterpret_cast<uint32_t*>(A->scratch + A->task_scratch[ti]);
   uint32_t* arrivals = sp + uint64_t(H) * S * (hd + 2);
   uint32_t* mine = sp + uint64_t(h * S + split) * (hd + 2);
@@ -237,7 +238,7 @@ VM_TILE void decode_attn_split(Args A, uint32_t ti, uint32_t tile) {
   __syncthreads();
   uint32_t* flag = reinterpret_cast<uint32_t*>(red + 12);
   if (tid == 0) {
-    const uint32_t before = __hip_atomic_fetch_add(arrivals + h, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t before = __hip_atomic_fetch_add(arrivals + h, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
     const bool last = before == S - 1;
     // reset for the next run of this task (ordered before it by a grid barrier)
     if (last) __hip_atomic_store(arrivals + h, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

@@ -931,7 +931,9 @@ VM_TILE void argmax_tiles(Args A, uint32_t ti, uint32_t lo, uint32_t hi) {
       __hip_atomic_store(mine, __float_as_uint(sv[0]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       __hip_atomic_store(mine + 1, si[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       __builtin_amdgcn_s_waitcnt(0x0F70);             // vmcnt(0): the candidate is in memory
-      const uint32_t before = __hip_atomic_fetch_add(arrivals + o, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      // acquire-release at agent scope: publishes this split's candidate, and the
+      // last arriver sees every other split's before it combines
+      const uint32_t before = __hip_atomic_fetch_add(arrivals + o, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
       const bool last = before == S - 1;
       if (last) __hip_atomic_store(arrivals + o, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       *flag = last;

@@ -507,7 +507,13 @@ struct Checker {
           const uint32_t e = t.p[6] - 1;
           if (!aux_ok(e, 1) || P.aux[e] < 0 || !aux_ok(e, 1 + 4 * int64_t(P.aux[e]))) return fail(ti, "epilogue");
           for (int k = 0; k < P.aux[e]; ++k) {
-            const int32_t src = P.aux[e + 2 + 4 * k];
+            const int32_t kind = P.aux[e + 1 + 4 * k], src = P.aux[e + 2 + 4 * k];
+            // float micro-ops of the store epilogue (mma.cl:67-96): binary, unary,
+            // affine and GELU; operand 0 self, 1 residual, 2 column, 3 constant s
+            const bool kind_ok = (kind >= SUB_ADD && kind <= SUB_SIGN) || (kind >= SUB_ATAN2 && kind <= SUB_ROUND) ||
+                                 kind == SUB_AFFINE || kind == SUB_GELU;
+            if (!kind_ok) return fail(ti, "matmul epilogue kind");
+            if (src < 0 || src > 3) return fail(ti, "matmul epilogue operand source");
             if (src == 1 && !has(t.p[7], G * M * N, DT_F32)) return fail(ti, "epilogue residual");
             if (src == 2 && !has(t.p[7], N, DT_F32)) return fail(ti, "epilogue bias");
           }
@@ -540,6 +546,7 @@ struct Checker {
             if (!(kind == SUB_AFFINE || kind == SUB_GELU || kind == SUB_COPY || (kind >= 0 && kind <= SUB_DIV) ||
                   kind == SUB_MAX || kind == SUB_MIN))
               return fail(ti, "gemv epilogue kind");
+            if (src < 0 || src > 3) return fail(ti, "gemv epilogue operand source");
             if (src == 1 && !has(t.p[7], G * M * N, DT_F32)) return fail(ti, "epilogue residual");
             if (src == 2 && !has(t.p[7], N, DT_F32)) return fail(ti, "epilogue bias");
           }
@@ -617,6 +624,7 @@ struct vmrt_runtime {
   uint32_t timeout_ticks = 0;
   std::mutex mu;     // serialises execute / transfers (runtime.h:233, 301)
   Pool pool;
+  std::set<vmrt_program*> programs;   // loaded and not yet unloaded (guarded by mu)
 };
 
 struct vmrt_program {
@@ -636,6 +644,7 @@ struct vmrt_program {
   uint32_t* task_scratch = nullptr;           // per task: byte offset of its scratch region
   std::vector<int> input_port, output_port;   // -1 = arena copy
   std::vector<uint32_t> in_bytes, out_bytes;
+  hipEvent_t done = nullptr;                  // recorded after each launch on its stream
   VmArgs args{};
 };
 
@@ -705,10 +714,22 @@ int vmrt_create(const vmrt_options* opts, vmrt_runtime** out, char* err, size_t 
   return VMRT_OK;
 }
 
+static void free_program_memory(vmrt_program* p);
+
 void vmrt_destroy(vmrt_runtime* rt) {
   if (!rt) return;
   hipSetDevice(rt->device);
-  hipStreamSynchronize(rt->stream);
+  hipDeviceSynchronize();   // programs may have been enqueued on caller streams
+  {
+    // programs still loaded are unloaded with their runtime: they borrow its
+    // device, stream and mutex (runtime.h:365), so none may outlive it
+    std::lock_guard<std::mutex> g(rt->mu);
+    for (vmrt_program* p : rt->programs) {
+      free_program_memory(p);
+      delete p;
+    }
+    rt->programs.clear();
+  }
   hipStreamDestroy(rt->stream);
   delete rt;
 }
@@ -720,6 +741,8 @@ int vmrt_device_info_get(vmrt_runtime* rt, vmrt_device_info* out) {
 }
 
 static void free_program_memory(vmrt_program* p) {
+  if (p->done) hipEventDestroy(p->done);
+  p->done = nullptr;
   for (void* q : {static_cast<void*>(p->arena), static_cast<void*>(p->aux), static_cast<void*>(p->tasks),
                   static_cast<void*>(p->entries), static_cast<void*>(p->lanes), static_cast<void*>(p->ctl),
                   static_cast<void*>(p->stats), static_cast<void*>(p->scratch), static_cast<void*>(p->task_scratch)})
@@ -737,8 +760,12 @@ static void free_program_memory(vmrt_program* p) {
 
 void vmrt_unload(vmrt_program* p) {
   if (!p) return;
-  hipSetDevice(p->rt->device);
-  hipStreamSynchronize(p->rt->stream);
+  vmrt_runtime* rt = p->rt;
+  std::lock_guard<std::mutex> g(rt->mu);
+  if (!rt->programs.erase(p)) return;   // not a live program of this runtime
+  hipSetDevice(rt->device);
+  if (p->done) hipEventSynchronize(p->done);
+  hipStreamSynchronize(rt->stream);
   free_program_memory(p);
   delete p;
 }
@@ -915,6 +942,7 @@ int vmrt_load(vmrt_runtime* rt, const void* bytes, size_t len, uint32_t ew_ts, u
   if (e == hipSuccess) e = hipMemset(lp->scratch, 0, std::max<uint64_t>(lp->scratch_bytes, 256));
   if (e == hipSuccess)
     e = up(reinterpret_cast<void**>(&lp->task_scratch), task_scratch.data(), task_scratch.size() * 4);
+  if (e == hipSuccess) e = hipEventCreateWithFlags(&lp->done, hipEventDisableTiming);
   if (const char* prof = std::getenv("PJRT_AMD_PROFILE"); e == hipSuccess && prof && std::atoi(prof) != 0) {
     lp->stats_words = kStatTask + 4 * tasks.size();
     e = hipMalloc(reinterpret_cast<void**>(&lp->stats), lp->stats_words * 8);
@@ -943,6 +971,7 @@ int vmrt_load(vmrt_runtime* rt, const void* bytes, size_t len, uint32_t ew_ts, u
   a.scratch = lp->scratch;
   a.task_scratch = lp->task_scratch;
   for (int k = 0; k < kMaxPorts; ++k) a.ports[k] = lp->arena;   // unbound ports point at the arena
+  rt->programs.insert(lp.get());
   *out = lp.release();
   return VMRT_OK;
 }
@@ -998,6 +1027,8 @@ static int enqueue_locked(vmrt_program* p, const void* const* inputs, size_t n_i
       if (e != hipSuccess) return set_err(err, errlen, VMRT_INTERNAL, "output copy: " + hip_msg(e));
     }
   }
+  e = hipEventRecord(p->done, s);
+  if (e != hipSuccess) return set_err(err, errlen, VMRT_INTERNAL, "completion event: " + hip_msg(e));
   return VMRT_OK;
 }
 
@@ -1042,7 +1073,8 @@ int vmrt_program_status(vmrt_program* p, char* err, size_t errlen) {
   if (!p) return set_err(err, errlen, VMRT_INVALID_ARGUMENT, "null program");
   std::lock_guard<std::mutex> g(p->rt->mu);
   hipSetDevice(p->rt->device);
-  hipError_t e = hipDeviceSynchronize();
+  // the last launch of this program, on whichever stream it was enqueued
+  hipError_t e = hipEventSynchronize(p->done);
   if (e != hipSuccess) return set_err(err, errlen, VMRT_INTERNAL, "synchronize: " + hip_msg(e));
   return check_status(p, err, errlen);
 }

@@ -17,7 +17,9 @@ constructing a Runtime raises.
 from __future__ import annotations
 
 import ctypes
+import sys
 import threading
+import weakref
 
 import numpy as np
 
@@ -160,14 +162,17 @@ class DeviceBuffer:
             self.rt.h2d(self.ptr, arr.ctypes.data, self.nbytes)
 
     def free(self) -> None:
-        if self.ptr:
+        if self.ptr and self.rt._h:
             self.rt._lib.vmrt_free(self.rt._h, _VP(self.ptr))
-            self.ptr = 0
+        self.ptr = 0          # after Runtime.close the pool has already released it
 
     def __del__(self):
+        # no native call while the interpreter shuts down: the HIP runtime's own
+        # exit handlers (and a profiler's) may already have run
+        if sys.is_finalizing():
+            return
         try:
-            if self.ptr and self.rt._h:
-                self.free()
+            self.free()
         except Exception:
             pass
 
@@ -188,6 +193,7 @@ class Runtime:
         err = ctypes.create_string_buffer(_ERRLEN)
         _check(self._lib.vmrt_create(ctypes.byref(opts), ctypes.byref(h), err, _ERRLEN), err)
         self._h = h
+        self._programs = weakref.WeakSet()      # live LoadedPrograms
         info = _DeviceInfo()
         self._lib.vmrt_device_info_get(self._h, ctypes.byref(info))
         self.info = {k: getattr(info, k) for k, _ in _DeviceInfo._fields_}
@@ -215,11 +221,28 @@ class Runtime:
         return int(self._lib.vmrt_stream(self._h) or 0)
 
     def close(self) -> None:
+        """Unload every live program, then release the device (vmrt_destroy,
+        which also returns the pool's memory).  Programs and buffers of a closed
+        runtime are dead: their close/free do nothing, execute raises."""
         if getattr(self, "_h", None):
+            for lp in list(self._programs):
+                lp.close()
             self._lib.vmrt_destroy(self._h)
             self._h = None
 
+    @property
+    def closed(self) -> bool:
+        return not getattr(self, "_h", None)
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
     def __del__(self):
+        if sys.is_finalizing():
+            return
         try:
             self.close()
         except Exception:
@@ -267,6 +290,7 @@ class Runtime:
                                    err, _ERRLEN), err)
         lp = LoadedProgram(self, p)
         lp._blob = blob
+        self._programs.add(lp)
         return lp
 
     def compile(self, prog: V.VMProgram, **cfg_overrides) -> "LoadedProgram":
@@ -299,6 +323,8 @@ class Event:
         return float(ms.value)
 
     def __del__(self):
+        if sys.is_finalizing():
+            return
         try:
             self.rt._lib.vmrt_event_destroy(self._e)
         except Exception:
@@ -339,15 +365,22 @@ class LoadedProgram:
         return IOSpec(dt.value, nbytes.value, tuple(int(dims[k]) for k in range(rank.value)))
 
     def close(self) -> None:
-        if getattr(self, "_h", None):
-            self.rt._lib.vmrt_unload(self._h)
-            self._h = None
+        h, self._h = getattr(self, "_h", None), None
+        if h and not self.rt.closed:        # a closed runtime has unloaded it already
+            self.rt._lib.vmrt_unload(h)
 
     def __del__(self):
+        if sys.is_finalizing():
+            return
         try:
             self.close()
         except Exception:
             pass
+
+    def _live(self):
+        if not getattr(self, "_h", None) or self.rt.closed:
+            raise VmrtError(FAILED_PRECONDITION, "program is closed (or its runtime is)")
+        return self._h
 
     def _arrays(self, inputs, outputs):
         if len(inputs) != len(self.inputs):
@@ -367,20 +400,20 @@ class LoadedProgram:
             outputs = self.alloc_outputs()
         ins, outs = self._arrays(inputs, outputs)
         err = ctypes.create_string_buffer(_ERRLEN)
-        _check(self.rt._lib.vmrt_execute(self._h, ins, len(inputs), outs, len(outputs), err, _ERRLEN), err)
+        _check(self.rt._lib.vmrt_execute(self._live(), ins, len(inputs), outs, len(outputs), err, _ERRLEN), err)
         return outputs
 
     def enqueue(self, inputs, outputs, stream: int | None = None) -> None:
         """Launch without waiting (on `stream`, default the runtime's)."""
         ins, outs = self._arrays(inputs, outputs)
         err = ctypes.create_string_buffer(_ERRLEN)
-        _check(self.rt._lib.vmrt_enqueue(self._h, ins, len(inputs), outs, len(outputs), _VP(stream or 0), err,
+        _check(self.rt._lib.vmrt_enqueue(self._live(), ins, len(inputs), outs, len(outputs), _VP(stream or 0), err,
                                          _ERRLEN), err)
 
     def status(self) -> None:
         """Synchronize and raise if the VM aborted (barrier time-out etc.)."""
         err = ctypes.create_string_buffer(_ERRLEN)
-        _check(self.rt._lib.vmrt_program_status(self._h, err, _ERRLEN), err)
+        _check(self.rt._lib.vmrt_program_status(self._live(), err, _ERRLEN), err)
 
     def profile(self, reset: bool = True) -> dict:
         """Per-task device time since the last reset (the program must have been
@@ -390,13 +423,14 @@ class LoadedProgram:
         words = 4 + 4 * n_tasks
         buf = (ctypes.c_uint64 * words)()
         err = ctypes.create_string_buffer(_ERRLEN)
-        _check(self.rt._lib.vmrt_program_profile(self._h, buf, words, int(reset), err, _ERRLEN), err)
+        _check(self.rt._lib.vmrt_program_profile(self._live(), buf, words, int(reset), err, _ERRLEN), err)
         v = np.frombuffer(buf, np.uint64).astype(np.float64)
         return {"barrier_us": v[0] / 100.0, "barriers": int(v[1]),
                 "tasks": [(i, v[4 + 4 * i] / 100.0, v[5 + 4 * i] / 100.0, int(v[6 + 4 * i])) for i in range(n_tasks)]}
 
     def __call__(self, *args):
         """Host convenience: numpy arrays in, numpy arrays out."""
+        self._live()
         if len(args) != len(self.inputs):
             raise VmrtError(INVALID_ARGUMENT, f"expected {len(self.inputs)} inputs, got {len(args)}")
         dev_in = []

@@ -94,8 +94,14 @@ FLOAT_DTYPES = frozenset({DT_F32, DT_F64, DT_F16, DT_BF16})
 def f32_to_bf16(x) -> np.ndarray:
     """Round-to-nearest-even f32 -> bf16 bit pattern (uint16), the rule the
     device uses: (u + 0x7fff + ((u >> 16) & 1)) >> 16 (vm_common.cl:66-70)."""
-    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
-    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32)
+    # u32 arithmetic: a sum that wraps past 2^32 (negative NaN patterns only)
+    # loses just the bit that the cast to 16 bits drops anyway
+    r = (u >> 16) & np.uint32(1)
+    r += u
+    r += np.uint32(0x7FFF)
+    r >>= 16
+    return r.astype(np.uint16)
 
 
 def bf16_to_f32(b) -> np.ndarray:

@@ -63,12 +63,26 @@ UN = ["copy", "neg", "exp", "log", "sqrt", "rsqrt", "tanh", "abs", "floor", "cei
       "expm1", "cbrt", "sin", "cos", "tan", "rint", "round", "gelu"]
 
 
+@pytest.mark.parametrize("signed", [False, True])
 @pytest.mark.parametrize("dt", ["f32", "bf16"])
 @pytest.mark.parametrize("n", [1, 1000, 70001])
-def test_ew_float_ops(dt, n):
+def test_ew_float_ops(dt, n, signed):
+    """Every float EW op; the signed variant draws negative operands and integer
+    exponents too, so remainder's sign-of-dividend rule (C fmod), pow of negative
+    bases and the NaN domains of log / sqrt / rsqrt are compared (NaN == NaN)."""
     rng = np.random.default_rng(11)
-    a = (np.abs(rng.standard_normal(n)) + 0.25).astype(np.float32)
-    b = (np.abs(rng.standard_normal(n)) + 0.5).astype(np.float32)
+    if signed:
+        a = (rng.standard_normal(n) * 3.0).astype(np.float32)
+        b = (rng.standard_normal(n) * 2.0).astype(np.float32)
+        b[::3] = rng.integers(-4, 5, b[::3].size).astype(np.float32)
+        a[a == 0] = -1.5
+        b[b == 0] = 2.0
+        if n >= 8:
+            a[:8] = [-5, 5, -5, 5, -6, -2, -2, -8]
+            b[:8] = [3, -3, -3, 3, 3, 3, 2, 0.5]
+    else:
+        a = (np.abs(rng.standard_normal(n)) + 0.25).astype(np.float32)
+        b = (np.abs(rng.standard_normal(n)) + 0.5).astype(np.float32)
     g = G.Graph()
     x, y = g.input((n,), dt), g.input((n,), dt)
     outs = [getattr(g, op)(x, y) for op in BIN] + [g.unary(op, x) for op in UN]
@@ -626,3 +640,22 @@ def test_loader_rejects_more_lanes_than_resident():
     blob = V.serialize(g.build(), S.schedule_program(g.build(), S.DeviceConfig(nlanes=4096, ew_ts=256)))
     with pytest.raises(VmrtError):
         runtime().load(blob, ew_ts=256)
+
+
+def test_runtime_close_with_live_program():
+    """Closing a runtime unloads its live programs first; the program object
+    then makes no native call and raises on use (a second Runtime, so the
+    session's stays open)."""
+    from pjrt_amd.runtime import Runtime, VmrtError
+    rt = Runtime(device=0)
+    g = G.Graph()
+    x = g.input((1000,))
+    g.output(g.add(x, x))
+    lp = rt.compile(g.build())
+    (y,) = lp(np.arange(1000, dtype=np.float32))
+    np.testing.assert_array_equal(y, 2 * np.arange(1000, dtype=np.float32))
+    rt.close()
+    with pytest.raises(VmrtError):
+        lp(np.arange(1000, dtype=np.float32))
+    lp.close()
+    del lp

@@ -48,3 +48,53 @@ def test_binding_loads_without_a_device():
     except FileNotFoundError:
         pytest.skip("libvmrt.so not built")
     assert lib.vmrt_version()
+
+
+class _FakeLib:
+    """Records native calls; stands in for libvmrt.so to test the host-side
+    ownership rules without a device."""
+
+    def __init__(self):
+        self.calls = []
+
+    def __getattr__(self, name):
+        def fn(*args):
+            self.calls.append(name)
+            return 0
+        return fn
+
+
+def _fake_runtime():
+    import weakref
+    from pjrt_amd import runtime
+    rt = object.__new__(runtime.Runtime)
+    rt._lib = _FakeLib()
+    rt._h = 1234
+    rt._programs = weakref.WeakSet()
+    lp = object.__new__(runtime.LoadedProgram)
+    lp.rt, lp._h = rt, 5678
+    rt._programs.add(lp)
+    return rt, lp
+
+
+def test_closing_the_runtime_closes_its_programs_first():
+    rt, lp = _fake_runtime()
+    rt.close()
+    assert rt._lib.calls == ["vmrt_unload", "vmrt_destroy"]
+    lp.close()                        # already unloaded: no second native call
+    del lp
+    assert rt._lib.calls == ["vmrt_unload", "vmrt_destroy"]
+
+
+def test_program_of_a_closed_runtime_makes_no_native_call():
+    from pjrt_amd import runtime
+    rt, lp = _fake_runtime()
+    rt._programs.discard(lp)          # a program the runtime no longer tracks
+    rt.close()
+    assert rt._lib.calls == ["vmrt_destroy"]
+    lp.close()
+    with pytest.raises(runtime.VmrtError):
+        lp.status()
+    buf = runtime.DeviceBuffer(rt, 42, 16)
+    buf.free()
+    assert rt._lib.calls == ["vmrt_destroy"] and buf.ptr == 0

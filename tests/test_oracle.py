@@ -106,6 +106,75 @@ def test_ew_unary_f32_closed_form(name):
     np.testing.assert_allclose(got, UN[name](a.astype(np.float64)), rtol=2e-6, atol=1e-6)
 
 
+def _math_pow(a, b):
+    """C pow semantics from Python's math module (an implementation independent of
+    numpy): a negative base with a non-integer exponent is NaN, 0 ** negative is
+    +inf (ew.cl:19-50 maps pow onto the device libm's pow)."""
+    try:
+        return math.pow(a, b)
+    except ValueError:
+        return math.nan
+    except ZeroDivisionError:
+        return math.inf
+    except OverflowError:
+        return math.copysign(math.inf, a) if (b == int(b) and int(b) % 2 and a < 0) else math.inf
+
+
+def _signed_operands():
+    rng = np.random.default_rng(17)
+    a = (rng.standard_normal(600) * 3.0).astype(np.float32)
+    b = (rng.standard_normal(600) * 2.0).astype(np.float32)
+    b[::3] = rng.integers(-4, 5, b[::3].size).astype(np.float32)   # integer exponents
+    b[b == 0] = 2.0
+    a[a == 0] = -1.5
+    # fixed cases: remainder takes the dividend's sign; pow of negative bases
+    fa = np.array([-5, 5, -5, 5, -0.0, -6, 7.5, -7.5, -2, -2, -8, 0.5, -3], np.float32)
+    fb = np.array([3, -3, -3, 3, 3, 3, 2, 2, 3, 2, 1 / 3, -1, 0.5], np.float32)
+    return np.concatenate([fa, a]), np.concatenate([fb, b]), fa.size
+
+
+def test_ew_remainder_sign_of_dividend():
+    """remainder is C fmod: the result takes the dividend's sign (ew.cl:27):
+    -5 % 3 = -2, 5 % -3 = 2, -0.0 % 3 = -0.0, -6 % 3 = -0.0; checked against
+    math.fmod element by element, signs of zeros included."""
+    a, b, nf = _signed_operands()
+    g = G.Graph()
+    x, y = g.input(a.shape), g.input(b.shape)
+    g.output(g.remainder(x, y))
+    (got,) = both(g.build(), [a, b])
+    want = np.array([math.fmod(float(p), float(q)) for p, q in zip(a, b)])
+    assert got[:4].tolist() == [-2.0, 2.0, -2.0, 2.0]
+    assert math.copysign(1, got[4]) == -1 and math.copysign(1, got[5]) == -1
+    np.testing.assert_allclose(got, want, rtol=1e-6, atol=0)
+    assert np.array_equal(np.signbit(got), np.signbit(want.astype(np.float32)))
+
+
+def test_ew_pow_signed_bases():
+    """pow over signed bases and integer / fractional exponents against
+    math.pow: (-2)^3 = -8, (-2)^2 = 4, (-8)^(1/3) = NaN, 0.5^-1 = 2, (-3)^0.5 = NaN."""
+    a, b, nf = _signed_operands()
+    g = G.Graph()
+    x, y = g.input(a.shape), g.input(b.shape)
+    g.output(g.pow(x, y))
+    (got,) = both(g.build(), [a, b])
+    want = np.array([_math_pow(float(p), float(q)) for p, q in zip(a, b)])
+    assert got[8] == -8.0 and got[9] == 4.0 and np.isnan(got[10]) and got[11] == 2.0 and np.isnan(got[12])
+    nan_g, nan_w = np.isnan(got), np.isnan(want)
+    assert np.array_equal(nan_g, nan_w)
+    np.testing.assert_allclose(got[~nan_g], want[~nan_w], rtol=2e-6, atol=0)
+
+
+def test_ew_tan_closed_form():
+    """tan against math.tan over (-pi/2, pi/2) and a few periods out."""
+    x = np.concatenate([np.linspace(-1.5, 1.5, 301), np.linspace(-20, 20, 173)]).astype(np.float32)
+    g = G.Graph()
+    a = g.input(x.shape)
+    g.output(g.unary("tan", a))
+    (got,) = both(g.build(), [x])
+    want = np.array([math.tan(float(v)) for v in x])
+    np.testing.assert_allclose(got, want, rtol=4e-6, atol=1e-7)
+
+
 def test_rounding_modes_exact():
     a = np.array([0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 0.49999997], np.float32)
     g = G.Graph()
@@ -343,6 +412,49 @@ def test_dot_views_batch_and_epilogue():
     (got,) = both(g.build(), [a, bt, res])
     want = (np.einsum("gmk,gnk->gmn", a, bt) * 2 + 1) + res
     np.testing.assert_array_equal(got, want)
+
+
+@pytest.mark.parametrize("M", [40, 3])
+def test_dot_epilogue_constant_operand(M):
+    """Epilogue source 3 (the operand is the constant s): bias, then
+    min(., 6), then max(., 0.5) with t = 7 -- a clamp to [0.5, 6] written out
+    by hand.  Taking t for the operand would give max(., 7) and fail.  M = 3
+    schedules the skinny-matmul (GEMV) tile, M = 40 the MMA tile."""
+    rng = np.random.default_rng(15)
+    K, N = 24, 37
+    a = rng.integers(-3, 4, (M, K)).astype(np.float32)
+    b = rng.integers(-3, 4, (K, N)).astype(np.float32)
+    bias = rng.integers(-4, 5, N).astype(np.float32)
+    g = G.Graph()
+    x, y, bb = g.input(a.shape), g.input(b.shape), g.input(bias.shape)
+    g.output(g.dot(x, y, residual=bb, epilogue=[(V.SUB_ADD, 2, 0.0, 0.0), (V.SUB_MIN, 3, 6.0, 0.0),
+                                                (V.SUB_MAX, 3, 0.5, 7.0)]))
+    (got,) = both(g.build(), [a, b, bias])
+    want = [[min(max(sum(int(a[i, k]) * int(b[k, j]) for k in range(K)) + int(bias[j]), 0.5), 6.0)
+             if sum(int(a[i, k]) * int(b[k, j]) for k in range(K)) + int(bias[j]) < 6.0 else 6.0
+             for j in range(N)] for i in range(M)]
+    np.testing.assert_array_equal(got, np.array(want, np.float32))
+
+
+def test_planted_epilogue_constant_is_caught(monkeypatch):
+    orig = vmref.TaskRunner._epilogue
+
+    def wrong(self, t, v, g, r0, r1, c0, c1, M, N, res):
+        aux = list(self.m.p.aux)
+        off = t.p[6] - 1
+        for k in range(aux[off]):          # use t where the constant operand is s
+            if aux[off + 2 + 4 * k] == 3:
+                aux[off + 3 + 4 * k] = aux[off + 4 + 4 * k]
+        saved = self.m.p.aux
+        self.m.p.aux = aux
+        try:
+            return orig(self, t, v, g, r0, r1, c0, c1, M, N, res)
+        finally:
+            self.m.p.aux = saved
+
+    monkeypatch.setattr(vmref.TaskRunner, "_epilogue", wrong)
+    with pytest.raises(AssertionError):
+        test_dot_epilogue_constant_operand(40)
 
 
 def test_gemv_dot_mode():
@@ -594,6 +706,34 @@ def test_planted_causal_offset_is_caught(monkeypatch):
     with pytest.raises(AssertionError):
         test_flash_attention_brute_force(True)
     monkeypatch.setattr(vmref, "attention", orig)
+
+
+@pytest.mark.parametrize("sub,wrong_fn,pin", [
+    (26, np.remainder, "test_ew_remainder_sign_of_dividend"),    # sign of the divisor
+    (6, lambda x, y: np.power(np.abs(x), y), "test_ew_pow_signed_bases"),
+    (32, None, "test_ew_tan_closed_form"),
+])
+def test_planted_float_op_is_caught(monkeypatch, sub, wrong_fn, pin):
+    """A wrong remainder (np.remainder: sign of the divisor), a pow that drops the
+    base's sign, and a tan that is really sin/cos of a shifted angle each fail
+    their pin."""
+    orig_bin, orig_un = vmref._float_bin, vmref._float_un
+    if sub == 32:
+        def wrong_un(s, x):
+            if s == 32:
+                with np.errstate(all="ignore"):
+                    return (np.sin(x) / np.cos(x + np.float32(1e-3))).astype(x.dtype)
+            return orig_un(s, x)
+        monkeypatch.setattr(vmref, "_float_un", wrong_un)
+    else:
+        def wrong_bin(s, x, y):
+            if s == sub:
+                with np.errstate(all="ignore"):
+                    return wrong_fn(x, y).astype(x.dtype)
+            return orig_bin(s, x, y)
+        monkeypatch.setattr(vmref, "_float_bin", wrong_bin)
+    with pytest.raises(AssertionError):
+        globals()[pin]()
 
 
 def test_planted_shift_mask_is_caught(monkeypatch):

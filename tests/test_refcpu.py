@@ -72,3 +72,15 @@ def test_bf16_formula_matches_numpy_oracle(lib):
     want = ((u.astype(np.uint64) + 0x7FFF + ((u.astype(np.uint64) >> 16) & 1)) >> 16).astype(np.uint16)
     assert np.array_equal(got[~nan], want[~nan])
     assert np.all(((got[nan] & 0x7F80) == 0x7F80) & ((got[nan] & 0x7F) != 0))
+
+
+def test_mlp_f32_matches_numpy(lib):
+    lib.refcpu_mlp_f32.argtypes = [ctypes.c_void_p] * 7 + [ctypes.c_int64] * 4 + [ctypes.c_int]
+    from pjrt_amd import configs as CF
+    x, w1, b1, w2, b2 = CF.mlp_c1_inputs(batch=40, d_in=24, d_hidden=56, d_out=12)
+    y = np.empty((40, 12), np.float32)
+    h = np.empty((40, 56), np.float32)
+    lib.refcpu_mlp_f32(x.ctypes.data, w1.ctypes.data, b1.ctypes.data, w2.ctypes.data, b2.ctypes.data,
+                       y.ctypes.data, h.ctypes.data, 40, 24, 56, 12, 3)
+    want = np.maximum(x.astype(np.float64) @ w1 + b1, 0) @ w2 + b2
+    np.testing.assert_allclose(y, want, rtol=1e-4, atol=1e-5)

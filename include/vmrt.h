@@ -108,6 +108,22 @@ int vmrt_execute(vmrt_program* prog, const void* const* inputs, size_t n_inputs,
 int vmrt_enqueue(vmrt_program* prog, const void* const* inputs, size_t n_inputs, void* const* outputs,
                  size_t n_outputs, void* stream, char* err, size_t errlen);
 
+/* Parse, validate and run a VMProgram v3 blob once, synchronously, without
+ * allocating: no hipMalloc / hipFree and no allocating library routine.  No
+ * counterpart in the reference: it is for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  The program's arena, side tables, barrier words and task
+ * scratch live in a static device array of 64 MiB per GPU, reserved when the
+ * library loads and held until the process ends; a program needing more is
+ * rejected with VMRT_RESOURCE_EXHAUSTED.  Inputs and outputs are the caller's
+ * device buffers, as for vmrt_execute (same results).  Every call on one GPU
+ * shares that GPU's array and clears what must start at zero; calls through one
+ * runtime serialise on its mutex, while overlapping calls on one GPU through
+ * different runtimes race. */
+int vmrt_run_noalloc(vmrt_runtime* rt, const void* bytes, size_t len, uint32_t ew_ts, uint32_t mma_t,
+                     const void* const* inputs, size_t n_inputs, void* const* outputs, size_t n_outputs, char* err,
+                     size_t errlen);
+
 /* Wait for the program's last launch (on whichever stream it was enqueued:
  * vmrt_execute / vmrt_enqueue record a completion event after it), then read and
  * clear the program's VM status

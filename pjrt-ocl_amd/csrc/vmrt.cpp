@@ -617,6 +617,17 @@ struct Pool {
 
 }  // namespace
 
+// ---- device memory of the allocation-free entry point (vmrt_run_noalloc) ----
+// One array per GPU, reserved when the library's code object loads and held
+// until the process ends.  Host code never uses the name `scratch` as an
+// address: hipGetSymbolAddress gives each device's own copy, kept in
+// g_scratch_dev at vmrt_create.
+constexpr size_t kNoAllocBytes = size_t(64) << 20;
+static __device__ __align__(256) uint8_t scratch[kNoAllocBytes];
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static uint8_t* g_scratch_dev[kMaxDevices];
+
 struct vmrt_runtime {
   int device = 0;
   hipStream_t stream = nullptr;
@@ -666,6 +677,15 @@ int vmrt_create(const vmrt_options* opts, vmrt_runtime** out, char* err, size_t 
   if (e != hipSuccess || ndev == 0) return set_err(err, errlen, VMRT_NOT_FOUND, "no HIP device: " + hip_msg(e));
   if (o.device < 0 || o.device >= ndev) return set_err(err, errlen, VMRT_NOT_FOUND, fmt("device %d not present", o.device));
   if ((e = hipSetDevice(o.device)) != hipSuccess) return set_err(err, errlen, VMRT_INTERNAL, hip_msg(e));
+  if (o.device < kMaxDevices) {
+    std::lock_guard<std::mutex> g(g_scratch_mu);
+    if (!g_scratch_dev[o.device]) {
+      void* ptr = nullptr;
+      if ((e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch))) != hipSuccess || !ptr)
+        return set_err(err, errlen, VMRT_INTERNAL, "device address of the static scratch array: " + hip_msg(e));
+      g_scratch_dev[o.device] = static_cast<uint8_t*>(ptr);
+    }
+  }
   hipDeviceProp_t prop;
   if ((e = hipGetDeviceProperties(&prop, o.device)) != hipSuccess) return set_err(err, errlen, VMRT_INTERNAL, hip_msg(e));
   if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
@@ -782,10 +802,18 @@ static uint64_t task_scratch_bytes(const Task& t) {
   return 0;
 }
 
-int vmrt_load(vmrt_runtime* rt, const void* bytes, size_t len, uint32_t ew_ts, uint32_t mma_t, vmrt_program** out,
-              char* err, size_t errlen) {
-  if (!rt || !bytes || !out) return set_err(err, errlen, VMRT_INVALID_ARGUMENT, "null argument");
-  auto lp = std::make_unique<vmrt_program>();
+// Host half of a load: parse, validate, choose ports, patch buffer ids to handles
+// and lay out the task scratch.  Fills lp (program, tile sizes, ports, I/O sizes,
+// scratch size) and the patched tables in `pr`; touches no device memory.
+struct Prepared {
+  std::vector<Task> tasks;
+  std::vector<int32_t> aux;
+  std::vector<Entry> entries;
+  std::vector<uint32_t> task_scratch;
+};
+
+static int prepare_program(vmrt_runtime* rt, vmrt_program* lp, const void* bytes, size_t len, uint32_t ew_ts,
+                           uint32_t mma_t, Prepared* pr, char* err, size_t errlen) {
   lp->rt = rt;
   std::string msg;
   if (!parse_program(static_cast<const uint8_t*>(bytes), len, &lp->prog, &msg))
@@ -861,7 +889,8 @@ int vmrt_load(vmrt_runtime* rt, const void* bytes, size_t len, uint32_t ew_ts, u
   };
 
   // ---- patch tasks (runtime.cc:826-875) ----
-  std::vector<Task> tasks = P.tasks;
+  std::vector<Task>& tasks = pr->tasks;
+  tasks = P.tasks;
   for (Task& t : tasks) {
     const uint32_t top = t.tile_op & 0xFF;
     const Task orig = t;
@@ -881,7 +910,8 @@ int vmrt_load(vmrt_runtime* rt, const void* bytes, size_t len, uint32_t ew_ts, u
       for (int k = 0; k < 4; ++k) t.p[k] = handle(orig.p[k]);
   }
   // ---- patch aux: runtime start-scalar / index-buffer locations (runtime.cc:883-924) ----
-  std::vector<int32_t> aux = P.aux;
+  std::vector<int32_t>& aux = pr->aux;
+  aux = P.aux;
   for (const Task& t : P.tasks) {
     const uint32_t top = t.tile_op & 0xFF;
     const uint32_t x = t.p[0];
@@ -893,7 +923,8 @@ int vmrt_load(vmrt_runtime* rt, const void* bytes, size_t len, uint32_t ew_ts, u
     }
   }
   // ---- patch control entries: cond buffer -> handle, pad -> cond format ----
-  std::vector<Entry> entries = P.entries;
+  std::vector<Entry>& entries = pr->entries;
+  entries = P.entries;
   for (Entry& e : entries) {
     if (e.task == ENT_WHILE || e.task == ENT_IF) {
       const Buffer& b = P.buffers[e.signal_flag];
@@ -905,7 +936,8 @@ int vmrt_load(vmrt_runtime* rt, const void* bytes, size_t len, uint32_t ew_ts, u
     }
   }
   // each task that needs scratch gets its own region (tasks of one phase run at once)
-  std::vector<uint32_t> task_scratch(tasks.size(), 0);
+  std::vector<uint32_t>& task_scratch = pr->task_scratch;
+  task_scratch.assign(tasks.size(), 0);
   for (size_t i = 0; i < tasks.size(); ++i) {
     const uint64_t nb = task_scratch_bytes(tasks[i]);
     if (!nb) continue;
@@ -916,6 +948,22 @@ int vmrt_load(vmrt_runtime* rt, const void* bytes, size_t len, uint32_t ew_ts, u
   }
   for (size_t i = 0; i < P.inputs.size(); ++i) lp->in_bytes.push_back(uint32_t(P.buffers[P.inputs[i]].size));
   for (size_t i = 0; i < P.outputs.size(); ++i) lp->out_bytes.push_back(uint32_t(P.buffers[P.outputs[i]].size));
+
+  return VMRT_OK;
+}
+
+int vmrt_load(vmrt_runtime* rt, const void* bytes, size_t len, uint32_t ew_ts, uint32_t mma_t, vmrt_program** out,
+              char* err, size_t errlen) {
+  if (!rt || !bytes || !out) return set_err(err, errlen, VMRT_INVALID_ARGUMENT, "null argument");
+  auto lp = std::make_unique<vmrt_program>();
+  Prepared pr;
+  if (int rc = prepare_program(rt, lp.get(), bytes, len, ew_ts, mma_t, &pr, err, errlen)) return rc;
+  const Program& P = lp->prog;
+  const uint32_t n_lanes = uint32_t(P.lanes.size());
+  const std::vector<Task>& tasks = pr.tasks;
+  const std::vector<int32_t>& aux = pr.aux;
+  const std::vector<Entry>& entries = pr.entries;
+  const std::vector<uint32_t>& task_scratch = pr.task_scratch;
 
   // ---- device memory ----
   std::lock_guard<std::mutex> g(rt->mu);
@@ -1027,8 +1075,10 @@ static int enqueue_locked(vmrt_program* p, const void* const* inputs, size_t n_i
       if (e != hipSuccess) return set_err(err, errlen, VMRT_INTERNAL, "output copy: " + hip_msg(e));
     }
   }
-  e = hipEventRecord(p->done, s);
-  if (e != hipSuccess) return set_err(err, errlen, VMRT_INTERNAL, "completion event: " + hip_msg(e));
+  if (p->done) {
+    e = hipEventRecord(p->done, s);
+    if (e != hipSuccess) return set_err(err, errlen, VMRT_INTERNAL, "completion event: " + hip_msg(e));
+  }
   return VMRT_OK;
 }
 
@@ -1067,6 +1117,82 @@ int vmrt_execute(vmrt_program* p, const void* const* inputs, size_t n_in, void* 
   hipError_t e = hipStreamSynchronize(p->rt->stream);
   if (e != hipSuccess) return set_err(err, errlen, VMRT_INTERNAL, "VM execution: " + hip_msg(e));
   return check_status(p, err, errlen);
+}
+
+int vmrt_run_noalloc(vmrt_runtime* rt, const void* bytes, size_t len, uint32_t ew_ts, uint32_t mma_t,
+                     const void* const* inputs, size_t n_in, void* const* outputs, size_t n_out, char* err,
+                     size_t errlen) {
+  if (!rt || !bytes) return set_err(err, errlen, VMRT_INVALID_ARGUMENT, "null argument");
+  vmrt_program lp;
+  Prepared pr;
+  if (int rc = prepare_program(rt, &lp, bytes, len, ew_ts, mma_t, &pr, err, errlen)) return rc;
+  const Program& P = lp.prog;
+  // layout in the device's array: control words, task-scratch table, task
+  // scratch, aux, tasks, entries, lane table, arena (each 256-byte aligned)
+  size_t off = 0;
+  auto place = [&](size_t n) {
+    const size_t at = off;
+    off += (std::max<size_t>(n, 64) + 255) & ~size_t(255);
+    return at;
+  };
+  const size_t o_ctl = place(BAR_WORDS * 4);
+  const size_t o_tsc = place(pr.task_scratch.size() * 4);
+  const size_t o_scr = place(lp.scratch_bytes);
+  const size_t o_aux = place(pr.aux.size() * 4);
+  const size_t o_tasks = place(pr.tasks.size() * sizeof(Task));
+  const size_t o_ent = place(pr.entries.size() * sizeof(Entry));
+  const size_t o_lanes = place(P.lanes.size() * sizeof(LaneSpan));
+  const size_t arena_n = size_t(P.arena_bytes) + 64;
+  const size_t o_arena = place(arena_n);
+  if (off > kNoAllocBytes)
+    return set_err(err, errlen, VMRT_RESOURCE_EXHAUSTED,
+                   fmt("vmrt_run_noalloc: the program needs %zu bytes of device memory (arena %llu, tables and "
+                       "scratch); the allocation-free entry point holds at most %zu",
+                       off, (unsigned long long)P.arena_bytes, kNoAllocBytes));
+  std::lock_guard<std::mutex> g(rt->mu);
+  hipSetDevice(rt->device);
+  uint8_t* base = rt->device < kMaxDevices ? g_scratch_dev[rt->device] : nullptr;
+  if (!base) return set_err(err, errlen, VMRT_FAILED_PRECONDITION, "no static scratch array on this device");
+  hipStream_t s = rt->stream;
+  // the array keeps the previous call's contents: clear what must start at zero
+  // (barrier words, split counters and partials, the arena as vmrt_load leaves it)
+  hipError_t e = hipMemsetAsync(base + o_ctl, 0, BAR_WORDS * 4, s);
+  if (e == hipSuccess) e = hipMemsetAsync(base + o_scr, 0, std::max<uint64_t>(lp.scratch_bytes, 64), s);
+  if (e == hipSuccess) e = hipMemsetAsync(base + o_arena, 0, arena_n, s);
+  auto up = [&](size_t at, const void* src, size_t n) {
+    if (e == hipSuccess && n) e = hipMemcpyAsync(base + at, src, n, hipMemcpyHostToDevice, s);
+  };
+  up(o_tsc, pr.task_scratch.data(), pr.task_scratch.size() * 4);
+  up(o_aux, pr.aux.data(), pr.aux.size() * 4);
+  up(o_tasks, pr.tasks.data(), pr.tasks.size() * sizeof(Task));
+  up(o_ent, pr.entries.data(), pr.entries.size() * sizeof(Entry));
+  up(o_lanes, P.lanes.data(), P.lanes.size() * sizeof(LaneSpan));
+  for (auto& c : P.consts) up(o_arena + P.buffers[c.first].off, c.second.data(), c.second.size());
+  if (e != hipSuccess) return set_err(err, errlen, VMRT_INTERNAL, "vmrt_run_noalloc upload: " + hip_msg(e));
+  lp.arena = base + o_arena;
+  lp.ctl = reinterpret_cast<uint32_t*>(base + o_ctl);
+  lp.scratch = base + o_scr;
+  VmArgs& a = lp.args;
+  a.arena = lp.arena;
+  a.aux = reinterpret_cast<const int32_t*>(base + o_aux);
+  a.tasks = reinterpret_cast<const Task*>(base + o_tasks);
+  a.entries = reinterpret_cast<const Entry*>(base + o_ent);
+  a.lanes = reinterpret_cast<const LaneSpan*>(base + o_lanes);
+  a.ctl = lp.ctl;
+  a.n_lanes = uint32_t(P.lanes.size());
+  a.ew_ts = lp.ew_ts;
+  a.mma_t = lp.mma_t;
+  a.timeout_ticks = rt->timeout_ticks;
+  a.stats = nullptr;
+  a.scratch = lp.scratch;
+  a.task_scratch = reinterpret_cast<const uint32_t*>(base + o_tsc);
+  for (int k = 0; k < kMaxPorts; ++k) a.ports[k] = lp.arena;
+  int rc = enqueue_locked(&lp, inputs, n_in, outputs, n_out, s, err, errlen);
+  // the host tables above stay alive until the copies and the launch are done
+  e = hipStreamSynchronize(s);
+  if (rc != VMRT_OK) return rc;
+  if (e != hipSuccess) return set_err(err, errlen, VMRT_INTERNAL, "VM execution: " + hip_msg(e));
+  return check_status(&lp, err, errlen);
 }
 
 int vmrt_program_status(vmrt_program* p, char* err, size_t errlen) {

@@ -81,6 +81,8 @@ SIGNATURES = {
     "vmrt_execute": (ctypes.c_int, [_VP, ctypes.POINTER(_VP), _SZ, ctypes.POINTER(_VP), _SZ, _CP, _SZ]),
     "vmrt_enqueue": (ctypes.c_int, [_VP, ctypes.POINTER(_VP), _SZ, ctypes.POINTER(_VP), _SZ, _VP, _CP, _SZ]),
     "vmrt_program_status": (ctypes.c_int, [_VP, _CP, _SZ]),
+    "vmrt_run_noalloc": (ctypes.c_int, [_VP, _VP, _SZ, _U32, _U32, ctypes.POINTER(_VP), _SZ, ctypes.POINTER(_VP),
+                                        _SZ, _CP, _SZ]),
     "vmrt_program_profile": (ctypes.c_int, [_VP, ctypes.POINTER(ctypes.c_uint64), _SZ, ctypes.c_int, _CP, _SZ]),
     "vmrt_alloc": (ctypes.c_int, [_VP, _SZ, ctypes.POINTER(_VP), _CP, _SZ]),
     "vmrt_free": (ctypes.c_int, [_VP, _VP]),
@@ -292,6 +294,18 @@ class Runtime:
         lp._blob = blob
         self._programs.add(lp)
         return lp
+
+    def run_noalloc(self, blob: bytes, inputs, outputs, ew_ts: int = 0, mma_t: int = 0) -> None:
+        """Run a program once on device buffers without allocating device memory
+        (vmrt_run_noalloc: the program lives in the library's static 64 MiB
+        array; synchronous)."""
+        blob = bytes(blob)
+        buf = ctypes.create_string_buffer(blob, len(blob))
+        ins = (_VP * max(1, len(inputs)))(*[_ptr_of(x) for x in inputs])
+        outs = (_VP * max(1, len(outputs)))(*[_ptr_of(x) for x in outputs])
+        err = ctypes.create_string_buffer(_ERRLEN)
+        _check(self._lib.vmrt_run_noalloc(self._h, ctypes.cast(buf, _VP), len(blob), ew_ts, mma_t, ins, len(inputs),
+                                          outs, len(outputs), err, _ERRLEN), err)
 
     def compile(self, prog: V.VMProgram, **cfg_overrides) -> "LoadedProgram":
         """Schedule a tensor program for this device and load it."""

@@ -657,6 +657,24 @@ def phase_us(tasks: list, n_lanes: int, cfg: DeviceConfig, prog: V.VMProgram) ->
 
 # --- phases ---------------------------------------------------------------------
 
+_VIEW_BIN = frozenset({V.OP_ADD_F32, V.OP_MUL_F32, V.OP_SUB_F32, V.OP_DIV_F32, V.OP_MAX_F32,
+                       V.OP_MIN_F32, V.OP_POW_F32, V.OP_ATAN2_F32, V.OP_REMAINDER_F32})
+
+
+def viewed_reads(ins: V.Instr) -> set:
+    """Buffers a float elementwise instruction reads through a strided view
+    (operand a's view in imm, b's in imm2 for the binary ops)."""
+    out = set()
+    if ins.op in _VIEW_BIN:
+        if ins.imm:
+            out.add(ins.a)
+        if ins.imm2:
+            out.add(ins.b)
+    elif ins.op in _UN_SUB and ins.op != V.OP_AFFINE_F32 and ins.imm:
+        out.add(ins.a)
+    return out
+
+
 def _phases(prog, indices, tasks_of, fuse, extra_reads=None):
     """Split ``indices`` (program order) into barrier-separated phases. A new
     phase starts when an instruction has a cross-lane dependency on a member
@@ -686,8 +704,13 @@ def _phases(prog, indices, tasks_of, fuse, extra_reads=None):
             return False
         if not fuse:
             return True
-        # lane-local: both elementwise over the same count, no shared writes
-        return not (is_map(i) and is_map(j) and a.n == b.n and wa.isdisjoint(wb))
+        # lane-local: both elementwise over the same count, no shared writes,
+        # and no dependency through a strided view (a viewed operand reads
+        # elements of other tiles, which other lanes produce or still read)
+        if not (is_map(i) and is_map(j) and a.n == b.n and wa.isdisjoint(wb)):
+            return True
+        grp = overlap_groups(prog)
+        return bool(({grp[x] for x in viewed_reads(b)} & wa) or ({grp[x] for x in viewed_reads(a)} & wb))
 
     for j in indices:
         ins = instrs[j]

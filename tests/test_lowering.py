@@ -1,0 +1,279 @@
+"""The StableHLO front end (pjrt_amd.mlir + lowering + passes), on the CPU oracle.
+
+Each program (tests/hlo_programs.py, MLIR text in the form JAX prints) is
+lowered twice -- with the fusion passes and without them -- and both programs
+are executed by the oracle; the results must agree with each other and with a
+float64 numpy statement of the JAX function.  The fused program must contain the
+fused op the pass is for, so a pass that silently stops matching fails here.
+"Parity unpinned": the exact StableHLO a given JAX version emits for these
+functions is not pinned (no jax in this image); the texts follow JAX's
+documented lowering rules."""
+import math
+
+import numpy as np
+import pytest
+
+import hlo_programs as H
+from oracle import vmref
+from pjrt_amd import lowering as L
+from pjrt_amd import mlir as M
+from pjrt_amd import passes
+from pjrt_amd import scheduler as S
+from pjrt_amd import vmprogram as V
+
+CFG = S.DeviceConfig(nlanes=8, ew_ts=256, mma_t=64)
+
+
+def run(prog, args, cfg=CFG):
+    blob = V.serialize(prog, S.schedule_program(prog, cfg))
+    out = vmref.execute(blob, args, ew_ts=cfg.ew_ts, mma_t=cfg.mma_t)
+    sched = vmref.execute_schedule(blob, args, ew_ts=cfg.ew_ts, mma_t=cfg.mma_t)
+    for a, b in zip(out, sched):
+        np.testing.assert_array_equal(a, b)
+    return out
+
+
+def both(text, args):
+    fused = L.lower_text(text)
+    plain = L.lower_text(text, fuse=False)
+    return fused, run(fused, args), run(plain, args)
+
+
+def live_ops(prog):
+    return [i.op for i in prog.instrs if i.op != V.OP_NOP]
+
+
+def bf16(x):
+    return vmref.bf16_to_f32(vmref.f32_to_bf16(np.asarray(x, np.float32)))
+
+
+# --- the reader ------------------------------------------------------------------------------
+
+def test_reader_pretty_and_generic_forms():
+    m = M.parse_module(H.mlp(4, 3, 5, 2))
+    assert set(m.funcs) == {"main", "relu"}
+    main = m.main
+    assert [a.type.shape for a in main.args] == [(4, 3), (3, 5), (5,), (5, 2), (2,)]
+    assert [o.name for o in main.body.ops][:3] == ["stablehlo.dot_general", "stablehlo.broadcast_in_dim",
+                                                   "stablehlo.add"]
+    dn = main.body.ops[0].attr("dot_dimension_numbers").fields
+    assert dn["lhs_contracting_dimensions"] == [1] and dn["rhs_contracting_dimensions"] == [0]
+    g = M.parse_module(H.generic_chain(64))
+    ops = g.main.body.ops
+    assert ops[1].attr("value").array().tolist() == 2.0
+    assert M.attr_ints(ops[5].attr("permutation")) == [1, 0]
+
+
+def test_reader_dense_forms():
+    t = M.TensorType((2, 2), "f32")
+    assert M.dense_to_numpy("[[1.0, 2.0], [3.0, 4.0]]", t).tolist() == [[1, 2], [3, 4]]
+    assert M.dense_to_numpy('"0x0000803F000000400000404000008040"', t).tolist() == [[1, 2], [3, 4]]
+    assert M.dense_to_numpy("0xFF800000", M.TensorType((), "f32")) == -np.inf
+    assert M.dense_to_numpy("true", M.TensorType((3,), "i1")).tolist() == [True] * 3
+    assert M.dense_to_numpy("-7", M.TensorType((), "i32")) == -7
+
+
+def test_reader_rejects_malformed_text():
+    with pytest.raises(L.LoweringError):
+        L.lower_text("module { func.func public @main(%arg0: tensor<4xf32>) -> tensor<4xf32> { %0 = ")
+    with pytest.raises(L.LoweringError):
+        L.lower_text(H.mlp().replace("stablehlo.maximum", "stablehlo.frobnicate"))
+
+
+# --- configs as JAX programs --------------------------------------------------------------------
+
+def test_mlp_config1_epilogue_fusion():
+    """Config 1: bias and relu run in the first matmul's store (epilogue sources
+    2 and 3), the second bias in the second's: two instructions."""
+    rng = np.random.default_rng(1001)
+    x = rng.standard_normal((16, 8)).astype(np.float32)
+    w1 = (rng.standard_normal((8, 32)) / math.sqrt(8)).astype(np.float32)
+    b1 = np.full(32, 0.01, np.float32)
+    w2 = (rng.standard_normal((32, 4)) / math.sqrt(32)).astype(np.float32)
+    b2 = rng.standard_normal(4).astype(np.float32)
+    prog, (got,), (plain,) = both(H.mlp(16, 8, 32, 4), [x, w1, b1, w2, b2])
+    assert live_ops(prog) == [V.OP_DOT, V.OP_DOT]
+    want = np.maximum(x.astype(np.float64) @ w1 + b1, 0) @ w2 + b2
+    np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(got, plain, rtol=1e-6, atol=1e-7)
+
+
+@pytest.mark.parametrize("rows,d", [(8, 64), (16, 4096)])
+def test_layernorm_gelu_convert_config2_one_row_op(rows, d):
+    """Config 2: the decomposed layernorm (reduce / broadcast / divide / rsqrt),
+    gamma / beta, tanh-GELU and the bf16 convert become ONE row op -- the
+    reference's fusion stops at seg <= 1024 (lowering.py:1553) and never takes
+    the affine, GELU or convert."""
+    rng = np.random.default_rng(1002)
+    x = rng.standard_normal((rows, d)).astype(np.float32)
+    g = rng.uniform(0.5, 1.5, d).astype(np.float32)
+    b = (rng.standard_normal(d) * 0.1).astype(np.float32)
+    prog, (got,), (plain,) = both(H.ln_gelu(rows, d), [x, g, b])
+    assert live_ops(prog) == [V.OP_LAYERNORM_AFFINE]
+    ln = next(i for i in prog.instrs if i.op == V.OP_LAYERNORM_AFFINE)
+    assert prog.aux[ln.aux] == V.LN_AFFINE | V.LN_GELU | V.LN_TWO_PASS
+    assert prog.buffers[ln.dst].dtype == V.DT_BF16
+    x64 = x.astype(np.float64)
+    mu = x64.mean(1, keepdims=True)
+    z = (x64 - mu) / np.sqrt(((x64 - mu) ** 2).mean(1, keepdims=True) + 1e-5) * g + b
+    want = 0.5 * z * (1 + np.tanh(0.7978845608 * (z + 0.044715 * z ** 3)))
+    gf, pf = vmref.bf16_to_f32(got).astype(np.float64), vmref.bf16_to_f32(plain).astype(np.float64)
+    assert np.all(np.abs(gf - want) <= 2.0 ** -7 * np.abs(want) + 1e-6)
+    assert np.all(np.abs(gf - pf) <= 2.0 ** -7 * np.abs(pf) + 1e-6)
+    # arena: input, gamma, beta, output and the constants, no intermediates
+    assert prog.arena_bytes < rows * d * 6 + 3 * d * 4 + 4096
+
+
+@pytest.mark.parametrize("dt,out", [("bf16", "f32"), ("f32", "f32"), ("bf16", "bf16")])
+def test_dot_general_dtypes(dt, out):
+    """dot_general with bf16 operands and f32 accumulation; a bf16 result is
+    honoured (the reference always produces f32, ops/dot.py:158)."""
+    rng = np.random.default_rng(1003)
+    a = rng.integers(-3, 4, (64, 32)).astype(np.float32)
+    b = rng.integers(-3, 4, (32, 48)).astype(np.float32)
+    prog, (got,), _ = both(H.matmul(64, 32, 48, dt, out), [a, b])
+    assert live_ops(prog) == [V.OP_DOT]
+    want = a.astype(np.float64) @ b
+    if out == "bf16":
+        np.testing.assert_array_equal(got, vmref.f32_to_bf16(want.astype(np.float32)))
+    else:
+        np.testing.assert_array_equal(got, want)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_attention_config4_becomes_flash_attention(causal):
+    """Config 4's shape of program (bf16 Q/K/V, f32 scores, optional causal mask
+    by iota compare, softmax, bf16 P): one OP_FLASH_ATTN with the causal flag,
+    K read through the plain transpose view the MFMA kernel takes, within the
+    bf16 attention tolerance of float64 math and of the unfused program."""
+    B, Hh, T, D = 1, 2, 32, 16
+    rng = np.random.default_rng(1004)
+    q, k, v = (bf16(rng.standard_normal((B, Hh, T, D))) for _ in range(3))
+    prog, (got,), (plain,) = both(H.attention(B, Hh, T, D, causal=causal), [q, k, v])
+    assert live_ops(prog) == [V.OP_FLASH_ATTN]
+    fa = next(i for i in prog.instrs if i.op == V.OP_FLASH_ATTN)
+    G, Mq, C, hd, sbits, cflag, qv, kv, vv = prog.aux[fa.aux:fa.aux + 9]
+    assert (G, Mq, C, hd, cflag, qv, vv) == (B * Hh, T, T, D, int(causal), 0, 0)
+    assert prog.aux[kv - 1:kv + 7] == [3, G, hd, C, C * hd, 1, hd, 0]
+    assert abs(V.bits_f32(sbits) - D ** -0.5) < 1e-7
+    s = np.einsum("bhqd,bhkd->bhqk", q.astype(np.float64), k) * D ** -0.5
+    if causal:
+        s = np.where(np.tril(np.ones((T, T), bool)), s, -np.inf)
+    p = np.exp(s - s.max(-1, keepdims=True))
+    p /= p.sum(-1, keepdims=True)
+    want = p @ v
+    gf, pf = vmref.bf16_to_f32(got), vmref.bf16_to_f32(plain)
+    assert np.abs(gf - want).max() <= 1e-2 * np.abs(want).max()
+    assert np.abs(gf - pf).max() <= 1e-2 * np.abs(pf).max()
+
+
+def test_argmax_variadic_reduce():
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal((4, 1000)).astype(np.float32)
+    x[1, [10, 700]] = 9.0                          # a tie: the first index wins
+    prog, (val, idx), _ = both(H.argmax_rows(4, 1000), [x])
+    assert live_ops(prog) == [V.OP_ARGMAX_SEG]
+    assert idx.tolist() == np.argmax(x, 1).tolist() and idx[1] == 10
+    np.testing.assert_array_equal(val, x.max(1))
+
+
+# --- control flow (reference tests/_while_e2e_body.py closed forms) ---------------------------------
+
+def test_fori_loop_unrolled_and_composed():
+    """fori_loop(0, 5, a + 3) from 2 -> 17: unrolled, then the five affines
+    compose into one."""
+    prog, (got,), (plain,) = both(H.fori_add(5), [np.float32(2.0)])
+    assert float(got) == 17.0 and float(plain) == 17.0
+    assert live_ops(prog) == [V.OP_AFFINE_F32]
+
+
+def test_fori_loop_as_for_when_large(monkeypatch):
+    """A counted loop beyond the unroll limits becomes OP_FOR (one barrier per
+    trip), its carry updated in place."""
+    monkeypatch.setenv("PJRT_OCL_WHILE", "for")
+    x = np.arange(1000, dtype=np.float32)
+    prog, (got,), _ = both(H.fori_add(100, 1000), [x])
+    np.testing.assert_array_equal(got, x + 300)
+    ops = live_ops(prog)
+    assert V.OP_FOR in ops and ops.count(V.OP_COPY_F32) <= 1
+
+
+def test_while_data_dependent():
+    """while v < 1000: (i + 1, 2 v) from (0, 1) -> (10, 1024): OP_WHILE with a
+    cond sub-list."""
+    prog, (i, v), _ = both(H.while_double(), [np.float32(1.0)])
+    assert int(i) == 10 and float(v) == 1024.0
+    assert V.OP_WHILE in live_ops(prog)
+
+
+@pytest.mark.parametrize("mode", ["unroll", "for"])
+def test_scan_stacking_dynamic_update_slice(mode, monkeypatch):
+    """scan-style stacking ys[i] = x * (i + 1) through dynamic_update_slice: as
+    OP_FOR the update writes the carry in place (no per-trip copy of ys)."""
+    monkeypatch.setenv("PJRT_OCL_WHILE", mode)
+    x = np.array([1, 2, 3, 4], np.float32)
+    prog, (got,), _ = both(H.scan_stack(6, 4), [x])
+    np.testing.assert_array_equal(got, np.outer(np.arange(1, 7), x))
+    if mode == "for":
+        body = [i for i in prog.instrs if i.op == V.OP_DYNAMIC_UPDATE_SLICE]
+        assert body and not any(i.op == V.OP_GATHER_STRIDED for i in prog.instrs[prog.main_len:])
+
+
+def test_generic_form_chain_fuses_into_a_region():
+    x = np.linspace(-2, 2, 64, dtype=np.float32).reshape(8, 8)
+    prog, (got,), (plain,) = both(H.generic_chain(64), [x])
+    np.testing.assert_allclose(got, (np.exp(x.astype(np.float64)) * 2 - x).T, rtol=2e-6)
+    np.testing.assert_allclose(got, plain, rtol=1e-6)
+
+
+# --- the passes on their own ------------------------------------------------------------------------
+
+def test_reuse_arena_packs_a_chain():
+    """Twelve dependent steps sin(transpose(x)) over 64 KiB tensors (each step
+    reads across lanes, so each is a phase of its own): the bump layout needs one
+    slot per value, the liveness packing a few."""
+    t = "tensor<128x128xf32>"
+    steps = "\n".join(f"    %t{k} = stablehlo.transpose %{k}, dims = [1, 0] : ({t}) -> {t}\n"
+                      f"    %{k + 1} = stablehlo.sine %t{k} : {t}" for k in range(12))
+    text = f"""
+func.func public @main(%0: {t}) -> {t} {{
+{steps}
+    return %12 : {t}
+}}"""
+    for fuse in (False, True):
+        prog = L.lower_text(text, fuse=fuse)
+        bump = sum(max(64, b.size_bytes) for b in prog.buffers if b.size_bytes)
+        assert prog.arena_bytes <= 5 * 65536 < bump
+        x = np.linspace(-1, 1, 128 * 128, dtype=np.float32).reshape(128, 128)
+        (got,) = run(prog, [x])
+        want = x.astype(np.float64)
+        for _ in range(12):
+            want = np.sin(want.T)
+        np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-6)
+
+
+def test_reuse_arena_on_the_hand_built_decoder():
+    """The liveness packing applied to the config-5 decoder built by hand
+    (aliases move with their parent buffer): a smaller arena, the same tokens."""
+    from pjrt_amd import configs as CF
+    c = CF.GptConfig(layers=2, d=64, heads=2, mlp=128, vocab=97, prompt=8, steps=4)
+    args = CF.gpt_inputs(c, seed=5)
+    prog = CF.gpt_c5(c, emit_logits=True)
+    before = prog.arena_bytes
+    want = run(prog, args)
+    prog2 = CF.gpt_c5(c, emit_logits=True)
+    passes.reuse_arena(prog2, CFG)
+    assert prog2.arena_bytes < before
+    for a, b in zip(run(prog2, args), want):
+        np.testing.assert_array_equal(a, b)
+
+
+def test_planted_pass_mistake_is_caught(monkeypatch):
+    """A GELU fusion that matched the cubic coefficient loosely (0.04715) would
+    fuse a different function; the exact-constant gate must refuse, leaving the
+    decomposed chain (whose result then still equals numpy)."""
+    text = H.ln_gelu(8, 64).replace("4.471500e-02", "4.715000e-02")
+    prog = L.lower_text(text)
+    assert V.OP_GELU not in live_ops(prog)
+    ln = [i for i in prog.instrs if i.op == V.OP_LAYERNORM_AFFINE]
+    assert ln and not prog.aux[ln[0].aux] & V.LN_GELU

@@ -431,3 +431,26 @@ def test_lane_count_defaults():
     assert env.gemv_min_strip == 8 and env.idle_master is True
     env = S.DeviceConfig.from_env({})
     assert env.gemv_min_strip == 0 and env.idle_master is None
+
+
+def test_viewed_operand_is_a_cross_lane_dependency():
+    """y = 2 x, then z = transpose(y) + w with the transpose folded into z's
+    operand view: same element count, but z's tile t reads y elements other lanes
+    write, so a barrier must separate them.  The oracle's lane simulator runs the
+    lanes forward and in reverse and catches the race if it is scheduled
+    lane-local."""
+    n = 64
+    g = G.Graph()
+    x, w = g.input((n, n)), g.input((n, n))
+    y = g.affine(x, 2.0, 0.0)
+    z = g.add(g.transpose_view(y, (1, 0)), w)
+    g.output(z)
+    prog = g.build()
+    cfg = S.DeviceConfig(nlanes=4, ew_ts=256, mma_t=64)
+    blob = V.serialize(prog, S.schedule_program(prog, cfg))
+    sched = vmref.parse(blob)
+    assert sum(e[0] == V.ENT_BARRIER for e in sched.streams[0]) >= 1
+    rng = np.random.default_rng(3)
+    xv, wv = rng.standard_normal((n, n)).astype(np.float32), rng.standard_normal((n, n)).astype(np.float32)
+    (got,) = vmref.execute_schedule(blob, [xv, wv], ew_ts=256, mma_t=64)
+    np.testing.assert_array_equal(got, (2 * xv).T + wv)

@@ -98,3 +98,13 @@ def test_program_of_a_closed_runtime_makes_no_native_call():
     buf = runtime.DeviceBuffer(rt, 42, 16)
     buf.free()
     assert rt._lib.calls == ["vmrt_destroy"] and buf.ptr == 0
+
+
+def test_plugin_library_exports_the_declared_entry_point():
+    text = re.sub(r"/\*.*?\*/", "", open(os.path.join(ROOT, "include", "pjrt_amd.h")).read(), flags=re.S)
+    names = set(re.findall(r"\b(GetPjrtApi)\s*\(", text))
+    path = os.path.join(ROOT, "pjrt-ocl_amd", "python", "pjrt_amd", "libpjrt_amd.so")
+    if not os.path.isfile(path):
+        pytest.skip("libpjrt_amd.so not built")
+    lib = ctypes.CDLL(path)
+    assert names == {"GetPjrtApi"} and all(hasattr(lib, n) for n in names)

@@ -124,9 +124,9 @@ int vmrt_run_noalloc(vmrt_runtime* rt, const void* bytes, size_t len, uint32_t e
                      const void* const* inputs, size_t n_inputs, void* const* outputs, size_t n_outputs, char* err,
                      size_t errlen);
 
-/* Wait for the program's last launch (on whichever stream it was enqueued:
- * vmrt_execute / vmrt_enqueue record a completion event after it), then read and
- * clear the program's VM status
+/* Wait for the stream of the program's latest launch (the runtime's, or the
+ * stream given to vmrt_enqueue, which must still exist), then read and clear
+ * the program's VM status
  * word (barrier time-out, frame overflow).  Extension of the reference, whose
  * clFinish error path only reports an OpenCL code (runtime.cc:2185-2189). */
 int vmrt_program_status(vmrt_program* prog, char* err, size_t errlen);

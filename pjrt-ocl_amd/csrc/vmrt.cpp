@@ -655,7 +655,8 @@ struct vmrt_program {
   uint32_t* task_scratch = nullptr;           // per task: byte offset of its scratch region
   std::vector<int> input_port, output_port;   // -1 = arena copy
   std::vector<uint32_t> in_bytes, out_bytes;
-  hipEvent_t done = nullptr;                  // recorded after each launch on its stream
+  hipStream_t last_stream = nullptr;          // the stream of the latest launch (null: none yet)
+  bool launched = false;
   VmArgs args{};
 };
 
@@ -761,8 +762,6 @@ int vmrt_device_info_get(vmrt_runtime* rt, vmrt_device_info* out) {
 }
 
 static void free_program_memory(vmrt_program* p) {
-  if (p->done) hipEventDestroy(p->done);
-  p->done = nullptr;
   for (void* q : {static_cast<void*>(p->arena), static_cast<void*>(p->aux), static_cast<void*>(p->tasks),
                   static_cast<void*>(p->entries), static_cast<void*>(p->lanes), static_cast<void*>(p->ctl),
                   static_cast<void*>(p->stats), static_cast<void*>(p->scratch), static_cast<void*>(p->task_scratch)})
@@ -784,8 +783,9 @@ void vmrt_unload(vmrt_program* p) {
   std::lock_guard<std::mutex> g(rt->mu);
   if (!rt->programs.erase(p)) return;   // not a live program of this runtime
   hipSetDevice(rt->device);
-  if (p->done) hipEventSynchronize(p->done);
-  hipStreamSynchronize(rt->stream);
+  // the program may have been enqueued on a caller's stream that no longer
+  // exists: wait for the whole device before its memory is released
+  if (p->launched) hipDeviceSynchronize();
   free_program_memory(p);
   delete p;
 }
@@ -990,7 +990,6 @@ int vmrt_load(vmrt_runtime* rt, const void* bytes, size_t len, uint32_t ew_ts, u
   if (e == hipSuccess) e = hipMemset(lp->scratch, 0, std::max<uint64_t>(lp->scratch_bytes, 256));
   if (e == hipSuccess)
     e = up(reinterpret_cast<void**>(&lp->task_scratch), task_scratch.data(), task_scratch.size() * 4);
-  if (e == hipSuccess) e = hipEventCreateWithFlags(&lp->done, hipEventDisableTiming);
   if (const char* prof = std::getenv("PJRT_AMD_PROFILE"); e == hipSuccess && prof && std::atoi(prof) != 0) {
     lp->stats_words = kStatTask + 4 * tasks.size();
     e = hipMalloc(reinterpret_cast<void**>(&lp->stats), lp->stats_words * 8);
@@ -1075,10 +1074,10 @@ static int enqueue_locked(vmrt_program* p, const void* const* inputs, size_t n_i
       if (e != hipSuccess) return set_err(err, errlen, VMRT_INTERNAL, "output copy: " + hip_msg(e));
     }
   }
-  if (p->done) {
-    e = hipEventRecord(p->done, s);
-    if (e != hipSuccess) return set_err(err, errlen, VMRT_INTERNAL, "completion event: " + hip_msg(e));
-  }
+  // no per-launch event: a command between back-to-back launches costs
+  // microseconds of gap; status waits on the launch's stream instead
+  p->last_stream = s;
+  p->launched = true;
   return VMRT_OK;
 }
 
@@ -1200,7 +1199,7 @@ int vmrt_program_status(vmrt_program* p, char* err, size_t errlen) {
   std::lock_guard<std::mutex> g(p->rt->mu);
   hipSetDevice(p->rt->device);
   // the last launch of this program, on whichever stream it was enqueued
-  hipError_t e = hipEventSynchronize(p->done);
+  hipError_t e = p->launched ? hipStreamSynchronize(p->last_stream) : hipSuccess;
   if (e != hipSuccess) return set_err(err, errlen, VMRT_INTERNAL, "synchronize: " + hip_msg(e));
   return check_status(p, err, errlen);
 }

@@ -166,6 +166,18 @@ int vmrt_event_record(vmrt_runtime* rt, void* event, void* stream);
 int vmrt_event_elapsed_ms(void* start, void* stop, float* ms);
 void vmrt_event_destroy(void* event);
 
+/* Measure the scheduler's cost table on this device and write it as one JSON
+ * object into `json` (cap bytes): per-tile microseconds of the elementwise,
+ * matmul, reduce and gather tile ops on one lane ("ew_tile_us", "mma_tile_us",
+ * "reduce_tile_us", "gather_tile_us", the reference's keys), and the terms of
+ * this build's phase model: "tile_us" (a tile's latency), "lane_gbs" (per-lane
+ * streaming GB/s with every lane streaming), "barrier_us" and
+ * "barrier_us_per_lane" (the grid barrier's cost at L lanes is
+ * barrier_us + barrier_us_per_lane * L), "lane_mma_tflops".  Takes tens of
+ * milliseconds.  Replaces OclRuntime::CalibrateCosts (runtime.cc:2433-2517;
+ * the table the lowering reads through PJRT_OCL_COST_TABLE, plugin.cc:770-780). */
+int vmrt_calibrate(vmrt_runtime* rt, char* json, size_t cap, char* err, size_t errlen);
+
 /* Library version string. */
 const char* vmrt_version(void);
 

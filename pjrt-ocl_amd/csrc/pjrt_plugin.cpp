@@ -21,6 +21,7 @@
 #include <poll.h>
 #include <signal.h>
 #include <spawn.h>
+#include <sys/stat.h>
 #include <sys/wait.h>
 #include <time.h>
 #include <unistd.h>
@@ -130,13 +131,14 @@ class LowerService {
 
   // status: the one-shot exit code (0 ok, 2 unsupported, 3 internal); payload:
   // v3 bytes or the JSON error.  false = the service itself failed.
-  bool compile(const char* code, size_t n, const vmrt_device_info& dev, uint32_t* status, std::string* payload,
-               std::string* err) {
+  bool compile(const char* code, size_t n, const vmrt_device_info& dev, const std::string& costs, uint32_t* status,
+               std::string* payload, std::string* err) {
     if (!start(err)) return false;
-    uint32_t head[4] = {dev.n_lanes, dev.ew_ts, dev.mma_t, 0};
+    uint32_t head[4] = {dev.n_lanes, dev.ew_ts, dev.mma_t, uint32_t(costs.size())};
     uint64_t len = n;
     std::string req(reinterpret_cast<const char*>(head), sizeof head);
     req.append(reinterpret_cast<const char*>(&len), 8);
+    req.append(costs);
     req.append(code, n);
     std::string resp_head;
     if (!transfer(req, &resp_head, 16, err)) return restart_fail(err);
@@ -266,6 +268,7 @@ struct PJRT_Client {
   PJRT_Memory* memory_list[1] = {&memory};
   LowerService lower;
   std::string version;
+  std::string costs;     // the cost table handed to the lowering (JSON), or empty
   std::mutex compile_mu;
   ~PJRT_Client() {
     lower.stop();
@@ -375,6 +378,60 @@ std::string option_string(const PJRT_Client_Create_Args* a, const char* key) {
   return {};
 }
 
+std::string fingerprint(const std::string& bytes) {
+  uint64_t h = 1469598103934665603ull;   // FNV-1a, 64 bit
+  for (unsigned char ch : bytes) h = (h ^ ch) * 1099511628211ull;
+  char buf[17];
+  std::snprintf(buf, sizeof buf, "%016llx", static_cast<unsigned long long>(h));
+  return buf;
+}
+
+std::string read_file(const std::string& path) {
+  std::string out;
+  if (std::FILE* f = std::fopen(path.c_str(), "rb")) {
+    char buf[4096];
+    size_t n;
+    while ((n = std::fread(buf, 1, sizeof buf, f)) > 0) out.append(buf, n);
+    std::fclose(f);
+  }
+  return out;
+}
+
+// The cost table for the lowering (runtime.cc:2433-2517): PJRT_OCL_COST_TABLE
+// (a path) when set; else measured by vmrt_calibrate once per device and
+// library version and cached as
+// ${PJRT_OCL_CACHE_DIR:-${XDG_CACHE_HOME:-$HOME/.cache}/pjrt_amd}/costs-<key>.json;
+// PJRT_OCL_CALIBRATE=0 turns measuring off (the model's built-in constants
+// then), =1 re-measures.
+std::string cost_table(vmrt_runtime* rt, const vmrt_device_info& info) {
+  if (const char* p = std::getenv("PJRT_OCL_COST_TABLE"); p && *p) return read_file(p);
+  const char* cal = std::getenv("PJRT_OCL_CALIBRATE");
+  if (cal && !std::strcmp(cal, "0")) return {};
+  std::string dir;
+  if (const char* d = std::getenv("PJRT_OCL_CACHE_DIR"); d && *d) dir = d;
+  else if (const char* x = std::getenv("XDG_CACHE_HOME"); x && *x) dir = std::string(x) + "/pjrt_amd";
+  else if (const char* h = std::getenv("HOME"); h && *h) dir = std::string(h) + "/.cache/pjrt_amd";
+  const std::string key = fingerprint(std::string(info.name) + "|" + info.arch + "|" + vmrt_version() + "|" +
+                                      std::to_string(info.n_lanes) + "|" + std::to_string(info.ew_ts) + "|" +
+                                      std::to_string(info.mma_t));
+  const std::string path = dir.empty() ? std::string() : dir + "/costs-" + key + ".json";
+  if (!path.empty() && !(cal && !std::strcmp(cal, "1"))) {
+    std::string cached = read_file(path);
+    if (!cached.empty()) return cached;
+  }
+  char json[4096], e[1024];
+  if (vmrt_calibrate(rt, json, sizeof json, e, sizeof e) != VMRT_OK) return {};
+  if (!path.empty()) {
+    for (size_t k = 1; k <= dir.size(); ++k)   // mkdir -p, one component at a time
+      if (k == dir.size() || dir[k] == '/') mkdir(dir.substr(0, k).c_str(), 0755);
+    if (std::FILE* f = std::fopen(path.c_str(), "wb")) {
+      std::fputs(json, f);
+      std::fclose(f);
+    }
+  }
+  return json;
+}
+
 PJRT_Error* Client_Create(PJRT_Client_Create_Args* a) {
   auto c = std::make_unique<PJRT_Client>();
   c->lower.python = option_string(a, "python_exe");
@@ -396,6 +453,7 @@ PJRT_Error* Client_Create(PJRT_Client_Create_Args* a) {
   if (int rc = vmrt_create(&o, &c->rt, e, sizeof e)) return from_vmrt(rc, e, "device");
   vmrt_device_info_get(c->rt, &c->info);
   c->version = vmrt_version();
+  c->costs = cost_table(c->rt, c->info);
   PJRT_Device& d = c->device;
   d.client = c.get();
   d.memory = &c->memory;
@@ -473,13 +531,6 @@ PJRT_Error* Client_DefaultDeviceAssignment(PJRT_Client_DefaultDeviceAssignment_A
   return nullptr;
 }
 
-std::string fingerprint(const std::string& bytes) {
-  uint64_t h = 1469598103934665603ull;   // FNV-1a, 64 bit
-  for (unsigned char ch : bytes) h = (h ^ ch) * 1099511628211ull;
-  char buf[17];
-  std::snprintf(buf, sizeof buf, "%016llx", static_cast<unsigned long long>(h));
-  return buf;
-}
 
 PJRT_Error* Client_Compile(PJRT_Client_Compile_Args* a) {
   PJRT_Client* c = a->client;
@@ -491,7 +542,7 @@ PJRT_Error* Client_Compile(PJRT_Client_Compile_Args* a) {
   std::string payload, err;
   {
     std::lock_guard<std::mutex> g(c->compile_mu);
-    if (!c->lower.compile(prog->code, prog->code_size, c->info, &status, &payload, &err))
+    if (!c->lower.compile(prog->code, prog->code_size, c->info, c->costs, &status, &payload, &err))
       return make_error(PJRT_Error_Code_INTERNAL, "lowering service: " + err);
   }
   if (status == 2) return make_error(PJRT_Error_Code_UNIMPLEMENTED, "unsupported program: " + payload);

@@ -21,7 +21,8 @@ service process when its client is created and sends it one request per
 compile on stdin, so no process is forked per compile.  Frames are
 little-endian:
 
-    request   u32 n_lanes, u32 ew_ts, u32 mma_t, u32 pad, u64 length, program bytes
+    request   u32 n_lanes, u32 ew_ts, u32 mma_t, u32 cost_length, u64 length,
+              the cost table (cost_length bytes of JSON, vmrt_calibrate's), program bytes
     response  u32 status (the one-shot exit code), u32 pad, u64 length, payload
               (v3 bytes when status is 0, else the JSON error)
 
@@ -82,13 +83,16 @@ def serve(inp=None, out=None) -> int:
     _, scheduler = _package()
     while True:
         try:
-            lanes, ew_ts, mma_t, _, n = _REQ.unpack(_read_exact(inp, _REQ.size))
+            lanes, ew_ts, mma_t, cost_n, n = _REQ.unpack(_read_exact(inp, _REQ.size))
         except EOFError:
             return EXIT_OK
         if n == _END:
             return EXIT_OK
+        costs = _read_exact(inp, cost_n).decode(errors="replace") if cost_n else ""
         program = _read_exact(inp, n)
         cfg = scheduler.DeviceConfig.from_env()
+        if costs:
+            cfg.costs = scheduler.load_cost_table(costs)
         if lanes:
             cfg.nlanes = lanes
         if ew_ts:

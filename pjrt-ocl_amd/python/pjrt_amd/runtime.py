@@ -90,6 +90,7 @@ SIGNATURES = {
     "vmrt_d2h": (ctypes.c_int, [_VP, _VP, _VP, _SZ, _CP, _SZ]),
     "vmrt_d2d": (ctypes.c_int, [_VP, _VP, _VP, _SZ, _CP, _SZ]),
     "vmrt_synchronize": (ctypes.c_int, [_VP, _CP, _SZ]),
+    "vmrt_calibrate": (ctypes.c_int, [_VP, _CP, _SZ, _CP, _SZ]),
     "vmrt_stream": (_VP, [_VP]),
     "vmrt_event_create": (ctypes.c_int, [_VP, ctypes.POINTER(_VP)]),
     "vmrt_event_record": (ctypes.c_int, [_VP, _VP, _VP]),
@@ -278,6 +279,16 @@ class Runtime:
     def synchronize(self) -> None:
         err = ctypes.create_string_buffer(_ERRLEN)
         _check(self._lib.vmrt_synchronize(self._h, err, _ERRLEN), err)
+
+    def calibrate(self) -> dict:
+        """The measured cost table (vmrt_calibrate) as a dict; the scheduler
+        takes it as DeviceConfig.costs (or as the JSON file PJRT_OCL_COST_TABLE
+        names)."""
+        import json
+        buf = ctypes.create_string_buffer(4096)
+        err = ctypes.create_string_buffer(_ERRLEN)
+        _check(self._lib.vmrt_calibrate(self._h, buf, 4096, err, _ERRLEN), err)
+        return json.loads(buf.value.decode())
 
     def event(self) -> "Event":
         return Event(self)

@@ -42,6 +42,24 @@ _COST_KEYS = {
     V.TOP_GATHER: "gather_tile_us", V.TOP_GATHER_INDEX: "gather_tile_us",
     V.TOP_RED_PART: "reduce_tile_us", V.TOP_RED_COMB: "reduce_tile_us",
 }
+# terms of the phase work model a measured cost table may set (vmrt_calibrate)
+_MODEL_KEYS = ("tile_us", "lane_gbs", "lane_mma_tflops", "barrier_us", "barrier_us_per_lane")
+
+
+def load_cost_table(spec: str) -> dict:
+    """A cost table from PJRT_OCL_COST_TABLE: a JSON file path (the reference's
+    form, runtime.cc:2500-2515) or the JSON object itself; unknown keys and
+    unreadable tables are ignored (unit costs then)."""
+    try:
+        if spec.lstrip().startswith("{"):
+            raw = json.loads(spec)
+        else:
+            with open(spec) as f:
+                raw = json.load(f)
+        keys = set(_COST_KEYS.values()) | set(_MODEL_KEYS)
+        return {k: float(raw[k]) for k in keys if k in raw and float(raw[k]) > 0}
+    except (OSError, ValueError, TypeError):
+        return {}
 
 
 class ScheduleError(NotImplementedError):
@@ -83,16 +101,8 @@ class DeviceConfig:
                 v = default
             return v
 
-        costs = {}
-        path = env.get("PJRT_OCL_COST_TABLE", "")
-        if path:
-            try:
-                with open(path) as f:
-                    raw = json.load(f)
-                costs = {k: float(raw[k]) for k in set(_COST_KEYS.values())
-                         if k in raw}
-            except (OSError, ValueError, TypeError):
-                costs = {}
+        spec = env.get("PJRT_OCL_COST_TABLE", "")
+        costs = load_cost_table(spec) if spec else {}
         return cls(nlanes=max(1, min(4096, geti("PJRT_OCL_NLANES", DEFAULT_NLANES))),
                    ew_ts=max(64, geti("PJRT_OCL_EW_TS", DEFAULT_EW_TS)),
                    mma_t=geti("PJRT_OCL_MMA_T", DEFAULT_MMA_T),
@@ -641,18 +651,28 @@ def task_work(task: V.Task, prog: V.VMProgram) -> tuple:
     return n * (asz * 2 + dsz), 0.0
 
 
+def model_terms(cfg: DeviceConfig) -> tuple:
+    """(tile latency us, per-lane GB/s, per-lane MFMA TFLOP/s, barrier us, barrier
+    us per lane): measured values from the cost table, else the constants above
+    (fitted on one MI355X)."""
+    c = cfg.costs
+    return (c.get("tile_us", _TILE_US), c.get("lane_gbs", _LANE_GBS), c.get("lane_mma_tflops", _LANE_TFLOPS_MMA),
+            c.get("barrier_us", _BAR_US), c.get("barrier_us_per_lane", _BAR_US_PER_LANE))
+
+
 def phase_us(tasks: list, n_lanes: int, cfg: DeviceConfig, prog: V.VMProgram) -> float:
     """Estimated microseconds of one phase on ``n_lanes`` lanes."""
+    tile_us, lane_gbs, lane_mma, _, _ = model_terms(cfg)
     byts = flops = 0.0
     tiles = 0
     for t in tasks:
         b, f = task_work(t, prog)
-        rate = _LANE_TFLOPS_MMA if t.adtype != V.DT_F32 else _LANE_TFLOPS[V.DT_F32]
+        rate = lane_mma if t.adtype != V.DT_F32 else _LANE_TFLOPS[V.DT_F32]
         byts += b
         flops += f / rate
         tiles += n_tiles(t, cfg)
     rounds = -(-tiles // n_lanes) if tiles else 0
-    return rounds * _TILE_US + max(byts / (n_lanes * _LANE_GBS * 1e3), flops / (n_lanes * 1e6))
+    return rounds * tile_us + max(byts / (n_lanes * lane_gbs * 1e3), flops / (n_lanes * 1e6))
 
 
 # --- phases ---------------------------------------------------------------------
@@ -849,7 +869,8 @@ class _Scheduler:
     def barrier(self):
         for s in self.lanes:
             s.append(V.barrier_entry())
-        self.est += self.weight * (_BAR_US + _BAR_US_PER_LANE * self.n)
+        _, _, _, bar, bar_lane = model_terms(self.cfg)
+        self.est += self.weight * (bar + bar_lane * self.n)
 
     def levels(self, indices):
         out, seg = [], []

@@ -7,6 +7,9 @@ attention rel 1e-3 (f32) / 1e-2 (bf16) against float64; bf16 outputs of f32 math
 within one bf16 ulp of the oracle's rounding (the device's f32 result and the
 oracle's float64 one can straddle a bf16 rounding boundary); one ulp is at most
 2^-7 of the value."""
+import dataclasses
+import sys
+
 import numpy as np
 import pytest
 
@@ -659,3 +662,28 @@ def test_runtime_close_with_live_program():
         lp(np.arange(1000, dtype=np.float32))
     lp.close()
     del lp
+
+
+def test_calibrate_cost_table():
+    """vmrt_calibrate measures the reference's four per-tile costs and this
+    build's phase-model terms; all positive and of plausible size, and a program
+    scheduled with them runs and matches the oracle."""
+    import json
+    from pjrt_amd import scheduler as S
+    rt = runtime()
+    costs = rt.calibrate()
+    print(f"[gpu] cost table {json.dumps(costs)}", file=sys.stderr, flush=True)
+    for k in ("ew_tile_us", "mma_tile_us", "reduce_tile_us", "gather_tile_us", "tile_us", "barrier_us",
+              "lane_gbs", "lane_mma_tflops"):
+        assert costs[k] > 0, k
+    assert costs["tile_us"] < 50 and costs["barrier_us"] < 50 and 1 < costs["lane_gbs"] < 200
+    cfg = S.DeviceConfig.from_env({"PJRT_OCL_COST_TABLE": json.dumps(costs)})
+    assert S.model_terms(cfg)[0] == costs["tile_us"]
+    g = G.Graph()
+    x = g.input((70000,))
+    g.output(g.unary("exp", g.add(x, x)))
+    blob = V.serialize(g.build(), S.schedule_program(g.build(), dataclasses.replace(
+        cfg, nlanes=rt.info["n_lanes"], ew_ts=4096, mma_t=128)))
+    a = np.linspace(-2, 2, 70000, dtype=np.float32)
+    got, want = run_both(blob, [a])
+    assert_rel(got[0], want[0], 4e-6, 1e-6, "calibrated schedule")

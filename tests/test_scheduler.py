@@ -454,3 +454,37 @@ def test_viewed_operand_is_a_cross_lane_dependency():
     xv, wv = rng.standard_normal((n, n)).astype(np.float32), rng.standard_normal((n, n)).astype(np.float32)
     (got,) = vmref.execute_schedule(blob, [xv, wv], ew_ts=256, mma_t=64)
     np.testing.assert_array_equal(got, (2 * xv).T + wv)
+
+
+def test_cost_table_forms_and_model_terms(tmp_path):
+    """PJRT_OCL_COST_TABLE as a file path (the reference's form) or inline JSON;
+    the measured terms replace the work model's constants, unknown keys and
+    non-positive values are ignored."""
+    table = {"ew_tile_us": 2.5, "tile_us": 1.25, "lane_gbs": 20.0, "barrier_us": 3.0,
+             "barrier_us_per_lane": 0.01, "lane_mma_tflops": 8.0, "bogus": 1.0, "gather_tile_us": -1}
+    p = tmp_path / "costs.json"
+    p.write_text(json.dumps(table))
+    for spec in (str(p), json.dumps(table)):
+        cfg = S.DeviceConfig.from_env({"PJRT_OCL_COST_TABLE": spec})
+        assert cfg.costs == {k: v for k, v in table.items() if k not in ("bogus", "gather_tile_us")}
+        assert S.model_terms(cfg) == (1.25, 20.0, 8.0, 3.0, 0.01)
+    assert S.DeviceConfig.from_env({"PJRT_OCL_COST_TABLE": "/nonexistent.json"}).costs == {}
+
+
+def test_lane_fit_follows_the_measured_barrier_cost():
+    """A barrier-heavy program (a FOR loop of one small EW per trip) moves to
+    half the lanes when barriers cost more per lane, and stays when they cost
+    nothing."""
+    g = G.Graph()
+    x = g.input((4096,))
+    a = g.fill((4096,), 0.0)
+    g.copy_into(a, x)
+    g.begin()
+    g.copy_into(a, g.add(a, g.broadcast_view(g.scalar(1.0), (4096,), ())))
+    g.for_loop(64, g.end())
+    g.output(a)
+    prog = g.build()
+    cheap = S.DeviceConfig(nlanes=256, costs={"barrier_us": 0.01, "barrier_us_per_lane": 0.0})
+    dear = S.DeviceConfig(nlanes=256, costs={"barrier_us": 1.0, "barrier_us_per_lane": 0.5})
+    assert S.lane_fit(prog, cheap) == 256
+    assert S.lane_fit(prog, dear) == 128

@@ -376,6 +376,72 @@ def bench_c5(rt, reps=3):
                          "frac": round(achieved / HBM_PEAK_GBS, 4), "bytes_per_token": int(bytes_tok)}}
 
 
+def profile_c5(rt, steps=16):
+    """--device-profile: where a C5 decode step spends its time, from the
+    runtime's per-task device counters (the runtime is created with
+    PJRT_AMD_PROFILE=1).  The per-step figures are the difference between the
+    decoder with `steps` loop trips and the same program with none, divided by
+    `steps`: the grid barriers each lane passes and its average wait in them,
+    and per tile op the entries, the mean time of one entry and the lane-time."""
+    import dataclasses
+    from pjrt_amd import configs as CF
+    from pjrt_amd import scheduler as S
+    from pjrt_amd import vmprogram as V
+    c = dataclasses.replace(CF.C5, steps=steps)
+    args = CF.gpt_inputs(c)
+    dev_in = [rt.to_device(a) for a in args]
+    res = {}
+    for trips in (0, steps):
+        prog = CF.gpt_c5(c, trips=trips)
+        sched = S.schedule_program(prog, rt.scheduler_config())
+        lp = rt.load(V.serialize(prog, sched))
+        outs = lp.alloc_outputs()
+        lp.execute(dev_in, outs)
+        lp.profile(reset=True)
+        e0, e1 = rt.event(), rt.event()
+        e0.record()
+        lp.execute(dev_in, outs)
+        e1.record()
+        rt.synchronize()
+        res[trips] = (e0.elapsed_ms(e1), lp.profile(), sched)
+        for b in outs:
+            b.free()
+        lp.close()
+    for b in dev_in:
+        b.free()
+    names = {v: k for k, v in vars(V).items() if k.startswith("TOP_") and k != "TOP_MAX"}
+    (ms0, pr0, _), (ms1, pr1, sched) = res[0], res[steps]
+    lanes = sched.n_lanes
+    per_step_us = (ms1 - ms0) * 1e3 / steps
+    bar_n = (pr1["barriers"] - pr0["barriers"]) / lanes / steps
+    bar_us = (pr1["barrier_us"] - pr0["barrier_us"]) / lanes / steps
+    print(f"C5 decode step on {lanes} lanes: {per_step_us:.1f} us per step (events), "
+          f"{bar_n:.1f} grid barriers per step, average lane wait in them {bar_us:.1f} us per step "
+          f"({bar_us / max(bar_n, 1):.2f} us per barrier)")
+    base = {i: (tot, cnt) for i, tot, _, cnt in pr0["tasks"]}
+    by_op, rows = {}, []
+    for i, tot, mx, cnt in pr1["tasks"]:
+        t0, c0 = base.get(i, (0.0, 0))
+        n = (cnt - c0) / steps
+        if n <= 0:
+            continue
+        lane_us = (tot - t0) / steps
+        t = sched.tasks[i]
+        op = names.get(t.tile_op & 0xFF, str(t.tile_op & 0xFF))
+        e = by_op.setdefault(op, [0.0, 0.0, 0])
+        e[0] += n
+        e[1] += lane_us
+        e[2] += 1
+        rows.append((lane_us, i, op, n, lane_us / n, mx))
+    print(f"{'tile op':18s} {'tasks':>5s} {'entries/step':>12s} {'us/entry':>9s} {'lane-us/step':>12s} "
+          f"{'us/step (/lanes)':>16s}")
+    for op, (n, us, k) in sorted(by_op.items(), key=lambda kv: -kv[1][1]):
+        print(f"{op:18s} {k:5d} {n:12.1f} {us / n:9.2f} {us:12.1f} {us / lanes:16.2f}")
+    print("heaviest tasks: task, op, entries/step, us/entry, max us/entry, lane-us/step")
+    for lane_us, i, op, n, avg, mx in sorted(rows, reverse=True)[:24]:
+        print(f"{i:5d} {op:18s} {n:8.1f} {avg:9.2f} {mx:9.2f} {lane_us:10.1f}")
+
+
 def bench_copy(rt, steps, nbytes=128 << 20):
     """A plain device-to-device copy of known size (the runtime's hipMemcpyAsync):
     the calibration kernel for the FETCH_SIZE / WRITE_SIZE counters."""
@@ -402,6 +468,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workloads", default="c1,c2,c3,c4,c5")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--device-profile", action="store_true",
+                    help="profiling aid: print the per-task device profile of the C5 decode step and exit")
     ap.add_argument("--skip-c2", action="store_true",
                     help="profiling aid: run only the --workloads extras and print them as one JSON line "
                          "(no headline C2 measurement)")
@@ -409,9 +477,14 @@ def main():
     if args.gpus != 1:
         raise SystemExit("bench.py measures one GPU: this build has no multi-GPU path "
                          "(each GPU would run its own shard of the same megakernel; see DESIGN.md)")
+    if args.device_profile:
+        os.environ["PJRT_AMD_PROFILE"] = "1"       # read when the runtime is created
     from pjrt_amd.runtime import Runtime
     with Runtime(device=0) as rt:      # closed (programs first) before interpreter exit
-        run(args, rt)
+        if args.device_profile:
+            profile_c5(rt)
+        else:
+            run(args, rt)
 
 
 def run(args, rt):

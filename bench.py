@@ -312,6 +312,73 @@ def bench_attention(rt, steps, warmup, B=4, H=16, S=2048, D=128):
             "max_rel_err_2_heads": max(errs)}
 
 
+def bench_lowered(rt, steps):
+    """The drop-in path: configs 1-4 as the StableHLO text a JAX program lowers
+    to (pjrt_amd.stablehlo_configs), through the lowering and its fusion passes
+    (what the plugin's Compile runs), timed beside the hand-built program of the
+    same config on the same inputs.  Reports both kernel times, their ratio,
+    the lowered program's tile ops and the largest difference between the two
+    outputs."""
+    from pjrt_amd import configs as CF
+    from pjrt_amd import graph as G
+    from pjrt_amd import lowering as L
+    from pjrt_amd import stablehlo_configs as H
+    from pjrt_amd import vmprogram as V
+    rng = np.random.default_rng(1005)
+
+    def bf16(shape):
+        return V.f32_to_bf16((rng.standard_normal(shape) * 0.125).astype(np.float32))
+
+    def hand_c3():
+        g = G.Graph()
+        x, y = g.input((4096, 4096), "bf16"), g.input((4096, 4096), "bf16")
+        g.output(g.dot(x, y))
+        return g.build()
+
+    def hand_c4():
+        g = G.Graph()
+        shape = (64, 2048, 128)
+        q, k, v = (g.input(shape, "bf16") for _ in range(3))
+        g.output(g.flash_attention(q, k, v, 1.0 / math.sqrt(128), True, out_dtype="bf16"))
+        return g.build()
+
+    x2, g2, b2 = c2_inputs()
+    cases = {
+        "c1": (H.mlp(), CF.mlp_c1(), list(CF.mlp_c1_inputs())),
+        "c2": (H.ln_gelu(C2_ROWS, C2_D), build_c2(), [x2, g2, b2]),
+        "c3_bf16": (H.matmul(4096, 4096, 4096, "bf16", "f32"), hand_c3(), [bf16((4096, 4096)), bf16((4096, 4096))]),
+        "c4": (H.attention(4, 16, 2048, 128, "bf16", True), hand_c4(), [bf16((4, 16, 2048, 128)) for _ in range(3)]),
+    }
+    names = {v: k for k, v in vars(V).items() if k.startswith("TOP_") and k != "TOP_MAX"}
+    out = {}
+    for name, (text, hand, args) in cases.items():
+        t0 = time.perf_counter()
+        low = L.lower_text(text)
+        lower_s = time.perf_counter() - t0
+        res = {}
+        for kind, prog, reuse in (("lowered", low, False), ("hand_built", hand, True)):
+            lp = rt.compile(prog, arena_reuse=reuse)
+            dev_in = [rt.to_device(a) for a in args]
+            dev_out = lp.alloc_outputs()
+            _, ms = time_program(rt, lp, dev_in, dev_out, steps, 3, min_warm_s=0.1)
+            spec = lp.outputs[0]
+            res[kind] = (ms, dev_out[0].to_host(spec.np_dtype, spec.shape))
+            for b in dev_in + dev_out:
+                b.free()
+            lp.close()
+        (ml, ol), (mh, oh) = res["lowered"], res["hand_built"]
+        f = (lambda a: V.bf16_to_f32(a).astype(np.float64)) if ol.dtype == np.uint16 else (lambda a: a.astype(np.float64))
+        diff = float(np.abs(f(ol).reshape(-1) - f(oh).reshape(-1)).max())
+        from pjrt_amd import scheduler as S
+        ops = sorted({names.get(t.tile_op, str(t.tile_op)) for t in
+                      S.schedule_program(low, rt.scheduler_config()).tasks})
+        out[name] = {"lowered_kernel_ms": round(ml, 5), "hand_built_kernel_ms": round(mh, 5),
+                     "lowered_over_hand_built": round(ml / mh, 3), "lower_s": round(lower_s, 2),
+                     "lowered_tile_ops": ops, "max_abs_diff_vs_hand_built": diff}
+        log(f"lowered {name}: {ml * 1e3:.1f} us vs hand-built {mh * 1e3:.1f} us ({', '.join(ops)})")
+    return out
+
+
 def bench_c1(rt, steps, with_cpu=False):
     """Config 1: the f32 two-layer MLP forward, on the GPU,
     beside the reference's CPU path for it (the path configs[0] names)."""
@@ -466,7 +533,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workloads", default="c1,c2,c3,c4,c5")
+    ap.add_argument("--workloads", default="c1,c2,c3,c4,c5,lowered")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--device-profile", action="store_true",
                     help="profiling aid: print the per-task device profile of the C5 decode step and exit")
@@ -504,6 +571,9 @@ def run(args, rt):
     if "c5" in wl:
         log("C5")
         extra["c5"] = bench_c5(rt)
+    if "lowered" in wl:
+        log("lowered")
+        extra["lowered"] = bench_lowered(rt, max(5, args.steps // 5))
     if "copy" in wl:
         log("copy")
         extra["copy"] = bench_copy(rt, max(5, args.steps // 5))

@@ -267,7 +267,8 @@ class Lowerer:
         if c is not None and c.size == 1 and x.dtype == V.DT_F32:
             self.sbcast[op.results[0]] = float(c.reshape(-1)[0])
         if c is not None and c.size == 1:
-            self.cval[op.results[0]] = np.full(shape, c.reshape(-1)[0], c.dtype)
+            # a read-only view with zero strides: a splat of any size costs nothing
+            self.cval[op.results[0]] = np.broadcast_to(c.reshape(()), shape)
         if G._prod(shape) == x.n and list(dims) == sorted(dims):
             # adds or drops only size-1 axes: a reshape, no data movement
             self.bind(op.results[0], self.g.reshape(x, shape))
@@ -279,7 +280,8 @@ class Lowerer:
         shape = op.results[0].type.shape
         c = self.cval.get(op.operands[0])
         if c is not None:
-            self.cval[op.results[0]] = c.reshape(shape)
+            splat = c.ndim and not any(c.strides)
+            self.cval[op.results[0]] = np.broadcast_to(c[(0,) * c.ndim], shape) if splat else c.reshape(shape)
             if c.size == 1 and x.dtype == V.DT_F32 and op.operands[0] in self.sbcast:
                 self.sbcast[op.results[0]] = self.sbcast[op.operands[0]]
         self.bind(op.results[0], self.g.reshape(x, shape))

@@ -1191,8 +1191,10 @@ def reuse_arena(prog: V.VMProgram, cfg=None) -> None:
         hi[b] = end
     for b, _ in prog.consts:
         lo[b], hi[b] = 0, end
-    # alias groups (arena-overlapping buffers of the bump layout) move as one
-    group = S.overlap_groups(prog)
+    # alias groups (arena-overlapping buffers of the bump layout) move as one;
+    # the scheduler keeps ordering by them, not by the packed overlaps
+    group = list(S.overlap_groups(prog))
+    prog.alias_groups = group
     members = {}
     for b in range(nb):
         members.setdefault(group[b], []).append(b)
@@ -1223,10 +1225,13 @@ def reuse_arena(prog: V.VMProgram, cfg=None) -> None:
         arena_end = max(arena_end, off + size_a)
         for m in mem:
             new_off[m] = off + bufs[m].arena_byte_offset - base
+    # buffers no instruction touches (intermediates a fusion replaced) keep no
+    # arena bytes at all
     for root, mem, base, size, l, h in units:
         if h < 0:
             for m in mem:
-                new_off[m] = bufs[m].arena_byte_offset - base
+                new_off[m] = 0
+                bufs[m].size_bytes = 0
     for b in range(nb):
         bufs[b].arena_byte_offset = new_off[b]
         arena_end = max(arena_end, new_off[b] + bufs[b].size_bytes)

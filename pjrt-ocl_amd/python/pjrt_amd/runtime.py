@@ -17,6 +17,7 @@ constructing a Runtime raises.
 from __future__ import annotations
 
 import ctypes
+import dataclasses
 import sys
 import threading
 import weakref
@@ -318,9 +319,16 @@ class Runtime:
         _check(self._lib.vmrt_run_noalloc(self._h, ctypes.cast(buf, _VP), len(blob), ew_ts, mma_t, ins, len(inputs),
                                           outs, len(outputs), err, _ERRLEN), err)
 
-    def compile(self, prog: V.VMProgram, **cfg_overrides) -> "LoadedProgram":
-        """Schedule a tensor program for this device and load it."""
+    def compile(self, prog: V.VMProgram, arena_reuse: bool = True, **cfg_overrides) -> "LoadedProgram":
+        """Schedule a tensor program for this device and load it.  With
+        `arena_reuse` the buffers of a copy of the program are first packed by
+        liveness (passes.reuse_arena, as the lowering does); `prog` itself is
+        left as it is."""
         cfg = self.scheduler_config(**cfg_overrides)
+        if arena_reuse:
+            from . import passes
+            prog = dataclasses.replace(prog, buffers=[dataclasses.replace(b) for b in prog.buffers])
+            passes.reuse_arena(prog, cfg)
         blob = V.serialize(prog, S.schedule_program(prog, cfg))
         return self.load(blob, ew_ts=cfg.ew_ts, mma_t=cfg.mma_t)
 

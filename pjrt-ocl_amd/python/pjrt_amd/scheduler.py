@@ -487,8 +487,14 @@ def _region_inputs_from_aux(ins: V.Instr, prog: V.VMProgram) -> list:
 def overlap_groups(prog: V.VMProgram) -> list:
     """Buffer id -> the lowest id of its group of arena-overlapping buffers, so
     that accesses to aliasing buffers (a contiguous slice kept as a buffer of its
-    own) are ordered like accesses to one buffer."""
+    own) are ordered like accesses to one buffer.  A program whose arena was
+    packed by liveness carries the groups of its layout before packing
+    (``alias_groups``): buffers the packing placed on the same bytes are
+    separated by a grid barrier by construction, not ordered as one buffer."""
     bufs = prog.buffers
+    alias = getattr(prog, "alias_groups", None)
+    if alias is not None and len(alias) == len(bufs):
+        return alias
     cached = getattr(prog, "_overlap_groups", None)
     if cached is not None and len(cached) == len(bufs):
         return cached

@@ -328,6 +328,12 @@ class VMProgram:
     main_len: int
     aux: list = dataclasses.field(default_factory=list)
     schedule: Schedule | None = None
+    # Buffer id -> lowest id of its group of true aliases (views of the same
+    # data), kept by passes.reuse_arena from the layout before packing: after
+    # packing, buffers with disjoint lifetimes share bytes too, and ordering
+    # those like one buffer would serialise unrelated work.  Not serialized;
+    # None: groups follow arena overlap.
+    alias_groups: list | None = dataclasses.field(default=None, compare=False, repr=False)
 
 
 def _pad8(out: bytearray) -> None:

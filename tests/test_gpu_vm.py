@@ -274,6 +274,29 @@ def test_layernorm_row_interleave(d, in_dt):
     assert_rel(as_f32(got[0], V.DT_BF16), as_f32(want[0], V.DT_BF16), BF16_ULP, 1e-5, "ln")
 
 
+@pytest.mark.parametrize("d", [1024, 2048, 4096])
+@pytest.mark.parametrize("out_dt,gelu", [("bf16", True), ("f32", False)])
+@pytest.mark.parametrize("per_lane", [1, 9])
+def test_layernorm_streamed_rows(d, out_dt, gelu, per_lane):
+    """f32 rows of 1024 / 2048 / 4096 through the streaming row kernel (three
+    or two rotating register buffers per wave): lanes with a few rows (some
+    waves with none) and with nine and a ragged tail (several buffer rotations,
+    the prefetch re-reading the last row past the end), against the oracle."""
+    rng = np.random.default_rng(1004 + d + per_lane)
+    lanes = runtime().info["n_lanes"]
+    rows = per_lane * lanes + 5
+    x_np = (rng.standard_normal((rows, d)) * 1.5 + 0.25).astype(np.float32)
+    gamma = rng.uniform(0.5, 1.5, d).astype(np.float32)
+    beta = (rng.standard_normal(d) * 0.1).astype(np.float32)
+    g = G.Graph()
+    x = g.input((rows, d))
+    ga, be = g.input((d,)), g.input((d,))
+    g.output(g.layernorm(x, ga, be, 1e-5, gelu=gelu, out_dtype=out_dt))
+    got, want = run_both(g.build(), [x_np, gamma, beta])
+    odt = V.DT_BY_NAME[out_dt]
+    assert_rel(as_f32(got[0], odt), as_f32(want[0], odt), BF16_ULP if out_dt == "bf16" else 1e-5, 1e-5, "ln")
+
+
 def test_config2_full_size_layernorm_gelu_bf16():
     """Config 2 at its real shape [8192, 4096] (seed 1002)."""
     rng = np.random.default_rng(1002)
@@ -444,6 +467,55 @@ def test_gemv_epilogue_bf16_out():
     got, want = run_both(g.build(), [a, b, bias, res], oracle="tensor")
     assert_rel(as_f32(got[0], V.DT_BF16), as_f32(want[0], V.DT_BF16), BF16_ULP, 1e-6, "gemv gelu bf16")
     assert_rel(got[1], want[1], 1e-5, 1e-5, "gemv affine + residual")
+
+
+def _gemv_chain(dt, M, seed):
+    """x -> three skinny matmuls in a row (each a phase after a grid barrier) ->
+    a fourth against weights the program rewrites first.  Integer operands in
+    {-1, 0, 1} and K <= 16 keep every value exact in bf16."""
+    rng = np.random.default_rng(seed)
+    x = rng.integers(-1, 2, (M, 16)).astype(np.float32)
+    ws = [rng.integers(-1, 2, s).astype(np.float32) for s in ((16, 64), (64, 16), (16, 128))]
+    w4 = rng.integers(-1, 2, (128, 40)).astype(np.float32)
+    g = G.Graph()
+    xi = g.input(x.shape, dt)
+    wi = [g.input(w.shape, dt) for w in ws]
+    w4i = g.input(w4.shape, dt)
+    h = xi
+    for w in wi:
+        h = g.dot(h, w, out_dtype=dt)
+    zero = g.const(np.zeros((), np.int32))
+    g.dynamic_update_slice(w4i, g.slice(h, (0, 0), (1, 40)), [zero, zero])
+    g.output(h, g.dot(h, w4i))
+    want_h = x.astype(np.float64)
+    for w in ws:
+        want_h = want_h @ w
+    w4b = w4.astype(np.float64).copy()
+    w4b[0, :] = want_h[0, :40]
+    return g.build(), [x] + ws + [w4], want_h, want_h @ w4b
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
+@pytest.mark.parametrize("M", [1, 3])
+@pytest.mark.parametrize("nlanes", [3, None])
+def test_gemv_chain_across_barriers(dt, M, nlanes):
+    """Skinny matmuls in a row, each a phase of its own after a grid barrier,
+    then one against weights the program rewrites first (the matmul must see
+    the rewrite): exact results, twice in a row, on 3 lanes and on the
+    device's lanes."""
+    prog, args, want_h, want_o = _gemv_chain(dt, M, 90 + M)
+    blob, _ = blob_for(prog, nlanes=nlanes)
+    assert sum(t.tile_op == V.TOP_GEMV for t in V.parse(blob).schedule.tasks) == 4
+    print(f"[gpu] case: gemv chain {dt} M={M} lanes={V.parse(blob).schedule.n_lanes}", file=sys.stderr, flush=True)
+    lp = runtime().load(blob)
+    f64 = (lambda a: as_f32(a, V.DT_BF16).astype(np.float64)) if dt == "bf16" else (lambda a: np.asarray(a, np.float64))
+    try:
+        for _ in range(2):
+            h, o = lp(*args)
+            np.testing.assert_array_equal(f64(h), want_h)
+            np.testing.assert_array_equal(np.asarray(o, np.float64), want_o)
+    finally:
+        lp.close()
 
 
 def test_dot_views_batch_epilogue():

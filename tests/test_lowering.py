@@ -268,6 +268,37 @@ def test_reuse_arena_on_the_hand_built_decoder():
         np.testing.assert_array_equal(a, b)
 
 
+def _barriers(prog, cfg):
+    sched = S.schedule_program(prog, cfg)
+    return sum(e.task == V.ENT_BARRIER for e in sched.lane_streams[0])
+
+
+def test_reuse_arena_keeps_the_schedule():
+    """Buffers the packing places on the same bytes have disjoint lifetimes; the
+    scheduler orders accesses by the true alias groups of the layout before
+    packing, so the packed decoder gets the same barriers as the unpacked one
+    (ordering every byte-sharing buffer as one, transitively, had doubled the
+    decode step's barriers), and a buffer no instruction touches keeps no
+    bytes."""
+    from pjrt_amd import configs as CF
+    c = CF.GptConfig(layers=2, d=64, heads=2, mlp=128, vocab=97, prompt=8, steps=4)
+    cfg = S.DeviceConfig(nlanes=16)
+    prog = CF.gpt_c5(c)
+    prog2 = CF.gpt_c5(c)
+    passes.reuse_arena(prog2, cfg)
+    assert prog2.arena_bytes < prog.arena_bytes
+    assert _barriers(prog2, cfg) == _barriers(prog, cfg)
+    # the same program with its alias groups dropped (groups from the packed overlaps)
+    prog3 = CF.gpt_c5(c)
+    passes.reuse_arena(prog3, cfg)
+    prog3.alias_groups = None
+    assert _barriers(prog3, cfg) > _barriers(prog, cfg)
+    # the lowered attention: the decomposed score matrices the fusion replaced take no arena
+    low = L.lower_text(H.attention(1, 2, 256, 64))
+    io = sum(low.buffers[b].size_bytes for b in low.inputs + low.outputs)
+    assert low.arena_bytes <= io + 64 * len(low.buffers)
+
+
 def test_planted_pass_mistake_is_caught(monkeypatch):
     """A GELU fusion that matched the cubic coefficient loosely (0.04715) would
     fuse a different function; the exact-constant gate must refuse, leaving the

@@ -653,9 +653,105 @@ VM_TILE void mma_tile32(Args A, const MmaDesc* Dp, uint32_t tile) {
   store_acc<T>(A, D, acc, g, m0, n0);
 }
 
+// ---- f32 fast path ---------------------------------------------------------------
+// 256 x 256 tiles of f32 operands (M, N multiples of 256, K of 16, no views,
+// 16-byte aligned): the wave split, accumulator layout (4 x 4 blocks of 32 x 32
+// per wave, in AGPRs) and store of the 16-bit fast path, with
+// v_mfma_f32_32x32x2_f32.  K goes in slabs of 16 through double-buffered LDS:
+//   A [m][k], row stride 20 floats: the 16 lanes of one 16-byte LDS read step
+//     read 16 consecutive rows at the same k, 80 bytes apart, which covers the 64
+//     banks once; a lane reads the 4 k values of 4 consecutive k steps with one
+//     ds_read_b128 per block;
+//   B [k][n], row stride 260: a lane reads one value per block and k step; the
+//     two half-waves read rows k and k + 8, whose banks are 32 apart.
+// Lanes 0-31 take k = kk and lanes 32-63 k = 8 + kk of the slab at k step kk,
+// the assignment of mma_tile32, so the two paths sum in the same order.  The
+// next slab's global loads are issued before the slab's MFMAs and written to
+// the idle buffer after them; a k step's B values are read while the previous
+// step's MFMAs run.
+constexpr int kF32BK = 16, kF32LdA = 20, kF32LdB = 256 + 4;
+constexpr int kF32A = 256 * kF32LdA, kF32Buf = kF32A + kF32BK * kF32LdB;
+constexpr int kF32FastLdsBytes = 2 * kF32Buf * 4;
+
+struct F32Stage {
+  // A: 256 rows x 16 k as 1024 chunks of 4 (thread t: row t / 4 + 64 j, k 4 (t % 4));
+  // B: 16 k x 256 n as 1024 chunks (thread t: k t / 64 + 4 j, n 4 (t % 64))
+  v4f ra[4], rb[4];
+  VM_DEV void load(const gbyte* a, const gbyte* b, uint32_t K, uint32_t N) {
+    const uint32_t t = threadIdx.x;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) ra[j] = *(const VM_G v4f*)(a + (uint64_t(t / 4 + 64 * j) * K + (t % 4) * 4) * 4);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) rb[j] = *(const VM_G v4f*)(b + (uint64_t(t / 64 + 4 * j) * N + (t % 64) * 4) * 4);
+  }
+  VM_DEV void store(float* s) const {
+    const uint32_t t = threadIdx.x;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) *reinterpret_cast<v4f*>(s + (t / 4 + 64 * j) * kF32LdA + (t % 4) * 4) = ra[j];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) *reinterpret_cast<v4f*>(s + kF32A + (t / 64 + 4 * j) * kF32LdB + (t % 64) * 4) = rb[j];
+  }
+};
+
+VM_TILE void mma_tile32_fast(Args A, const MmaDesc* Dp, uint32_t tile) {
+  A = uargs(A);
+  const MmaDesc D = load_desc(Dp);
+  float* lds = lds_ptr<float>();
+  uint32_t g, m0, n0;
+  fast_origin(D, uni(tile), &g, &m0, &n0);
+  const uint32_t K = D.K, N = D.N;
+  const gbyte* a = D.a + (uint64_t(g) * D.M + m0) * K * 4;        // A[g, m0, 0]
+  const gbyte* b = D.b + (uint64_t(g) * K * N + n0) * 4;           // B[g, 0, n0]
+  const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint32_t wm = wave >> 1, wn = wave & 1;
+  f32x16 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
+  const uint32_t nk = K / kF32BK;
+  F32Stage st;
+  st.load(a, b, K, N);
+  __syncthreads();                      // the previous user of the LDS is done
+  st.store(lds);
+  __syncthreads();
+  const uint32_t fa = (wm * 128 + (lane & 31)) * kF32LdA + (lane >> 5) * 8;
+  const uint32_t fb = kF32A + (lane >> 5) * 8 * kF32LdB + wn * 128 + (lane & 31);
+  for (uint32_t ks = 0; ks < nk; ++ks) {
+    const float* cur = lds + (ks & 1) * kF32Buf;
+    if (ks + 1 < nk) st.load(a + uint64_t(ks + 1) * kF32BK * 4, b + uint64_t(ks + 1) * kF32BK * N * 4, K, N);
+    float bfr[2][4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) bfr[0][j] = cur[fb + j * 32];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      v4f af[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) af[i] = *reinterpret_cast<const v4f*>(cur + fa + i * 32 * kF32LdA + q * 4);
+#pragma unroll
+      for (int kq = 0; kq < 4; ++kq) {
+        const int kk = 4 * q + kq, p = kk & 1;
+        if (kk + 1 < 8)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) bfr[p ^ 1][j] = cur[fb + (kk + 1) * kF32LdB + j * 32];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i][kq], bfr[p][j], acc[i][j], 0, 0, 0);
+      }
+    }
+    if (ks + 1 < nk) st.store(lds + ((ks + 1) & 1) * kF32Buf);
+    __syncthreads();
+  }
+  if (D.dt == DT_F32) store_fast<true>(A, D, acc, g, m0, n0);
+  else store_fast<false>(A, D, acc, g, m0, n0);
+}
+
 // LDS bytes the matmul tile op needs at its largest tile.
 constexpr int kMmaLdsBytes0 = Lds16<256>::kBytes > Lds32<256>::kBytes ? Lds16<256>::kBytes : Lds32<256>::kBytes;
-constexpr int kMmaLdsBytes = kFastLdsBytes > kMmaLdsBytes0 ? kFastLdsBytes : kMmaLdsBytes0;
+constexpr int kMmaLdsBytes1 = kFastLdsBytes > kMmaLdsBytes0 ? kFastLdsBytes : kMmaLdsBytes0;
+constexpr int kMmaLdsBytes = kF32FastLdsBytes > kMmaLdsBytes1 ? kF32FastLdsBytes : kMmaLdsBytes1;
 
 VM_TILE void mma_tiles(Args A, uint32_t ti, uint32_t lo, uint32_t hi) {
   A = uargs(A);
@@ -683,8 +779,13 @@ VM_TILE void mma_tiles(Args A, uint32_t ti, uint32_t lo, uint32_t hi) {
   const bool fast = h16 && T == 256 && !D.av && !D.bv && D.M % 256 == 0 && D.N % 256 == 0 && D.K % kFBK == 0 &&
                     D.N < (1u << 22) && ((uintptr_t(D.a) | uintptr_t(D.b)) & 15) == 0 &&
                     (D.dt == DT_F32 || D.dt == DT_BF16 || D.dt == DT_F16) && epi_inline_ok(A, D.epi);
+  const bool fast32 = D.adt == DT_F32 && T == 256 && !D.av && !D.bv && D.M % 256 == 0 && D.N % 256 == 0 &&
+                      D.K % kF32BK == 0 && D.N < (1u << 22) && ((uintptr_t(D.a) | uintptr_t(D.b)) & 15) == 0 &&
+                      (D.dt == DT_F32 || D.dt == DT_BF16 || D.dt == DT_F16) && epi_inline_ok(A, D.epi);
   for (uint32_t tile = lo; tile < hi; ++tile) {
-    if (fast) {
+    if (fast32) {
+      mma_tile32_fast(A, &D, tile);
+    } else if (fast) {
       if (bf) mma_tile16_fast<true>(A, &D, tile);
       else mma_tile16_fast<false>(A, &D, tile);
     } else if (h16) {

@@ -383,12 +383,12 @@ def test_dot_random_tolerance_and_tiles(dt, rtol):
         assert err <= rtol, (tile, err)
 
 
-@pytest.mark.parametrize("dt", ["bf16", "f16"])
+@pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
 @pytest.mark.parametrize("Gb,M,K,N", [(1, 512, 320, 768), (1, 1024, 128, 2048), (2, 256, 192, 1024)])
 def test_dot_fast_path_exact(dt, Gb, M, K, N):
-    """256 x 256 output tiles with K slabs of 64 (the MFMA fast path; 1024 x 2048
-    also takes the XCD tile swizzle, Gb=2 the batch offsets): integer-valued
-    operands give the exact f32 result."""
+    """256 x 256 output tiles (the MFMA fast paths: 16-bit operands in K slabs of
+    64, f32 in slabs of 16; 1024 x 2048 also takes the XCD tile swizzle, Gb=2 the
+    batch offsets): integer-valued operands give the exact f32 result."""
     rng = np.random.default_rng(72)
     a = rng.integers(-3, 4, (Gb, M, K)).astype(np.float32)
     b = rng.integers(-3, 4, (Gb, K, N)).astype(np.float32)
@@ -399,20 +399,22 @@ def test_dot_fast_path_exact(dt, Gb, M, K, N):
     np.testing.assert_array_equal(got[0], np.matmul(a.astype(np.float64), b.astype(np.float64)))
 
 
-def test_dot_fast_path_epilogue_bf16_out():
-    """Fast path with a fused store epilogue (affine, + residual, GELU) and a bf16
-    output, against the oracle within one bf16 ulp."""
+@pytest.mark.parametrize("in_dt,out_dt", [("bf16", "bf16"), ("f32", "f32"), ("f32", "bf16")])
+def test_dot_fast_path_epilogue(in_dt, out_dt):
+    """Fast paths with a fused store epilogue (affine, + residual, GELU), against
+    the oracle (one bf16 ulp for a bf16 output, rel 1e-5 for f32)."""
     rng = np.random.default_rng(73)
     M, K, N = 512, 256, 512
     a = rng.integers(-2, 3, (M, K)).astype(np.float32)
     b = rng.integers(-2, 3, (K, N)).astype(np.float32)
     res = (rng.standard_normal((M, N)) * 2).astype(np.float32)
     g = G.Graph()
-    x, y, r = g.input(a.shape, "bf16"), g.input(b.shape, "bf16"), g.input(res.shape)
-    g.output(g.dot(x, y, out_dtype="bf16", tile=256, residual=r,
+    x, y, r = g.input(a.shape, in_dt), g.input(b.shape, in_dt), g.input(res.shape)
+    g.output(g.dot(x, y, out_dtype=out_dt, tile=256, residual=r,
                    epilogue=[(V.SUB_AFFINE, 0, 0.125, -0.5), (V.SUB_ADD, 1, 0.0, 0.0), (V.SUB_GELU, 0, 0.0, 0.0)]))
     got, want = run_both(g.build(), [a, b, res], oracle="tensor")
-    assert_rel(as_f32(got[0], V.DT_BF16), as_f32(want[0], V.DT_BF16), BF16_ULP, 1e-6, "fast epilogue")
+    odt = V.DT_BY_NAME[out_dt]
+    assert_rel(as_f32(got[0], odt), as_f32(want[0], odt), BF16_ULP if out_dt == "bf16" else 1e-5, 1e-6, "fast epilogue")
 
 
 def test_dot_fast_path_random_bf16():

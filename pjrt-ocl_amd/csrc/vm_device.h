@@ -229,7 +229,16 @@ VM_DEV bool barrier_timed_out(Args A, uint64_t t0, uint32_t poll) {
   return false;
 }
 
-VM_DEV bool grid_barrier(Args A) {
+// `pre` runs on every thread of the lane once its arrival is published and
+// before it waits (on lane 0, the master, after the release): work that does
+// not depend on the phase before, such as warming the scalar cache with the
+// next entry's task records, then overlaps the wait.
+struct NoPre {
+  VM_DEV void operator()() const {}
+};
+
+template <typename Pre>
+VM_DEV bool grid_barrier(Args A, Pre&& pre) {
   __shared__ uint32_t s_ok;
   __syncthreads();
   uint32_t* ctl = A->ctl;
@@ -258,20 +267,25 @@ VM_DEV bool grid_barrier(Args A) {
       __hip_atomic_store(&ctl[BAR_XGEN + 32 * threadIdx.x], epoch, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
       if (threadIdx.x == 0) __hip_atomic_store(&ctl[BAR_GEN], epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-  } else if (threadIdx.x == 0) {
-    uint32_t ok = 1;
-    const uint32_t* gen = &ctl[BAR_XGEN + 32 * (blockIdx.x % kXcds)];
-    __hip_atomic_store(&ctl[BAR_FLAGS + blockIdx.x], epoch, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
-    for (uint32_t poll = 0;
-         int32_t(__hip_atomic_load(gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - epoch) < 0; ++poll) {
-      if (barrier_timed_out(A, t0, poll)) {
-        ok = 0;
-        break;
+    pre();
+  } else {
+    if (threadIdx.x == 0)
+      __hip_atomic_store(&ctl[BAR_FLAGS + blockIdx.x], epoch, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+    pre();
+    if (threadIdx.x == 0) {
+      uint32_t ok = 1;
+      const uint32_t* gen = &ctl[BAR_XGEN + 32 * (blockIdx.x % kXcds)];
+      for (uint32_t poll = 0;
+           int32_t(__hip_atomic_load(gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - epoch) < 0; ++poll) {
+        if (barrier_timed_out(A, t0, poll)) {
+          ok = 0;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(1);
       }
-      __builtin_amdgcn_s_sleep(1);
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+      s_ok = ok;
     }
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    s_ok = ok;
   }
   __syncthreads();
   if (threadIdx.x == 0) {        // read again only after the next barrier's block sync
@@ -280,6 +294,8 @@ VM_DEV bool grid_barrier(Args A) {
   }
   return s_ok != 0;
 }
+
+VM_DEV bool grid_barrier(Args A) { return grid_barrier(A, NoPre()); }
 
 // Record an error from a lane (first error wins) so the host can report it.
 VM_DEV void raise_error(Args A, uint32_t code, uint32_t info) {

@@ -56,11 +56,35 @@ VM_DEV void exec_tiles(Args A, uint32_t ti, uint32_t lo, uint32_t hi) {
   }
 }
 
-// grid_barrier, with the lane's wait added to the profiling counters when on
-VM_DEV bool timed_barrier(Args A) {
-  if (!A->stats) return grid_barrier(A);
+// Scalar-cache warm-up for the entry after a barrier: the entry, its task record
+// and, for a GEMV, the fused layernorm's task record and the epilogue words --
+// the dependent scalar loads a tile starts with.  Run between the lane's
+// arrival and its wait, so the loads (about a microsecond of dependent misses
+// after each barrier) overlap the wait instead of following it.  The values are
+// kept live (an empty asm) so the loads are issued, then dropped.
+VM_DEV void warm_entry(Args A, const VM_K Entry* ents, uint32_t i, uint32_t end) {
+  if (i >= end) return;
+  const Entry e = load_entry(ents + i);
+  asm volatile("" ::"s"(e.tile_hi));
+  if (e.task >= ENT_FOR) return;                          // a control entry
+  const VM_K Task& t = task_of(A, e.task);
+  const uint32_t top = t.tile_op, p5 = t.p[5], p6 = t.p[6];
+  asm volatile("" ::"s"(t.dst), "s"(t.a), "s"(t.b), "s"(t.p[0]), "s"(t.p[4]), "s"(t.p[7]));
+  if ((top & 0xFF) != TOP_GEMV) return;
+  if (p5) {
+    const VM_K Task& L = task_of(A, p5 - 1);
+    asm volatile("" ::"s"(L.a), "s"(L.b), "s"(L.p[3]), "s"(L.p[4]));
+  }
+  if (p6) asm volatile("" ::"s"(aux_of(A)[p6 - 1]));   // the epilogue's count word (checked at load)
+}
+
+// grid_barrier, with the lane's wait added to the profiling counters when on;
+// the entry at `next` (when inside [.., end)) is warmed while the lane waits
+VM_DEV bool timed_barrier(Args A, const VM_K Entry* ents, uint32_t next, uint32_t end) {
+  auto pre = [&] { warm_entry(A, ents, next, end); };
+  if (!A->stats) return grid_barrier(A, pre);
   const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
-  const bool ok = grid_barrier(A);
+  const bool ok = grid_barrier(A, pre);
   if (threadIdx.x == 0) {
     __hip_atomic_fetch_add(A->stats, __builtin_amdgcn_s_memrealtime() - t0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __hip_atomic_fetch_add(A->stats + 1, uint64_t(1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -96,7 +120,9 @@ __global__ __launch_bounds__(kBlock, 1) void vm_main(VmArgs args) {
         continue;
       }
       // loop bodies end with a grid barrier that publishes the carries
-      if (!timed_barrier(A)) return;
+      // (warming a FOR body's first entry when another trip follows)
+      const bool again = w.task == ENT_FOR && f_phase[sp] > 1;
+      if (!timed_barrier(A, ents, again ? w.tile_lo : 0u, again ? w.tile_lo + w.tile_hi : 0u)) return;
       pub = false;
       if (w.task == ENT_FOR) {
         if (--f_phase[sp] != 0) {
@@ -128,7 +154,7 @@ __global__ __launch_bounds__(kBlock, 1) void vm_main(VmArgs args) {
     const uint32_t epc = f_pc[sp];
     const Entry en = load_entry(ents + epc);
     if (en.task == ENT_BARRIER) {
-      if (!timed_barrier(A)) return;
+      if (!timed_barrier(A, ents, epc + 1, f_end[sp])) return;
       pub = false;
       ++f_pc[sp];
       continue;

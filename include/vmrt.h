@@ -31,6 +31,7 @@ enum {
   VMRT_FAILED_PRECONDITION = 9,
   VMRT_UNIMPLEMENTED = 12,
   VMRT_INTERNAL = 13,
+  VMRT_UNAVAILABLE = 14,
 };
 
 typedef struct vmrt_runtime vmrt_runtime;
@@ -165,6 +166,14 @@ int vmrt_event_create(vmrt_runtime* rt, void** event);
 int vmrt_event_record(vmrt_runtime* rt, void* event, void* stream);
 int vmrt_event_elapsed_ms(void* start, void* stop, float* ms);
 void vmrt_event_destroy(void* event);
+
+/* Completion of the work recorded before `event`: vmrt_event_query returns
+ * VMRT_OK once it has completed and VMRT_UNAVAILABLE while it has not;
+ * vmrt_event_synchronize waits for it.  VMRT_INTERNAL on a HIP error.  With
+ * vmrt_enqueue these give the asynchronous execution the reference's events
+ * stand for (plugin.cc:175-184, where every event is born complete). */
+int vmrt_event_query(void* event);
+int vmrt_event_synchronize(void* event);
 
 /* Measure the scheduler's cost table on this device and write it as one JSON
  * object into `json` (cap bytes): per-tile microseconds of the elementwise,

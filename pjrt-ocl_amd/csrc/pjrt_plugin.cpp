@@ -5,7 +5,15 @@
 // The table carries PJRT 0.112 (plugin.cc:997-999).  What this plugin does:
 //   * one client, one device (HIP device 0), one memory of kind "device";
 //   * buffers are pool-owned HIP device memory (vmrt_alloc), filled and read
-//     back synchronously, so every event is born ready (plugin.cc:175-184);
+//     back synchronously;
+//   * Execute is asynchronous: the program is launched on the runtime's stream
+//     (vmrt_enqueue) and a HIP event recorded after it is the Execute's
+//     completion event and its outputs' ready event, whose error is the VM
+//     status word read once the event completes (a barrier time-out, say).
+//     Everything runs on the one stream, so later launches and copies are
+//     ordered after it and pool memory may be reused at once.  OnReady
+//     callbacks of pending events run on one waiter thread per client.  (The
+//     reference's events are born complete, plugin.cc:175-184.);
 //   * Compile hands the StableHLO program to the Python lowering service and
 //     loads the VMProgram v3 bytes it returns (plugin.cc:748-819); the service
 //     runs as one child process per client, started at Client_Create, with
@@ -27,12 +35,15 @@
 #include <unistd.h>
 
 #include <cerrno>
+#include <condition_variable>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <deque>
 #include <memory>
 #include <mutex>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "../../include/vmrt.h"
@@ -46,7 +57,10 @@ struct PJRT_Error {
   std::string message;
 };
 
-struct PJRT_Event {};   // every event is complete when it is handed out
+namespace {
+struct ExecState;
+class Waiter;
+}  // namespace
 
 struct PJRT_DeviceDescription {
   int id = 0;
@@ -270,10 +284,8 @@ struct PJRT_Client {
   std::string version;
   std::string costs;     // the cost table handed to the lowering (JSON), or empty
   std::mutex compile_mu;
-  ~PJRT_Client() {
-    lower.stop();
-    if (rt) vmrt_destroy(rt);
-  }
+  std::unique_ptr<Waiter> waiter;      // runs OnReady callbacks of pending events
+  ~PJRT_Client();
 };
 
 struct PJRT_Buffer {
@@ -283,6 +295,7 @@ struct PJRT_Buffer {
   PJRT_Buffer_Type type = PJRT_Buffer_Type_INVALID;
   std::vector<int64_t> dims;
   bool deleted = false;
+  std::shared_ptr<ExecState> ready;    // the Execute that produced it (null: ready)
   void release() {
     if (ptr && client && client->rt) vmrt_free(client->rt, ptr);
     ptr = nullptr;
@@ -309,6 +322,120 @@ struct Program {
   }
 };
 }  // namespace
+
+namespace {
+// Completion of one Execute: a HIP event recorded after the launch on the
+// runtime's stream, and the program whose VM status word is read (and cleared)
+// once the event has completed.  Shared by the Execute's completion event and
+// the ready events of its outputs.
+struct ExecState {
+  void* ev = nullptr;
+  std::shared_ptr<Program> prog;
+  Waiter* waiter = nullptr;
+  std::mutex mu;
+  bool done = false;
+  PJRT_Error_Code code = PJRT_Error_Code_OK;
+  std::string message;
+  ~ExecState() {
+    if (ev) vmrt_event_destroy(ev);
+  }
+  void finish_locked(int rc) {
+    if (done) return;
+    done = true;
+    if (rc != VMRT_OK) {
+      code = PJRT_Error_Code_INTERNAL;
+      message = "execute: waiting for the device failed";
+      return;
+    }
+    char e[1024];
+    if (int st = vmrt_program_status(prog->prog, e, sizeof e)) {
+      code = static_cast<PJRT_Error_Code>(st);
+      message = std::string("execute: ") + e;
+    }
+  }
+  bool ready() {
+    std::lock_guard<std::mutex> g(mu);
+    if (done) return true;
+    const int rc = vmrt_event_query(ev);
+    if (rc == VMRT_UNAVAILABLE) return false;
+    finish_locked(rc);
+    return true;
+  }
+  void wait() {
+    {
+      std::lock_guard<std::mutex> g(mu);
+      if (done) return;
+    }
+    const int rc = vmrt_event_synchronize(ev);
+    std::lock_guard<std::mutex> g(mu);
+    finish_locked(rc);
+  }
+  // a new error object for the outcome (null: success); call once done
+  PJRT_Error* error() {
+    std::lock_guard<std::mutex> g(mu);
+    return code == PJRT_Error_Code_OK ? nullptr : new PJRT_Error{code, message};
+  }
+};
+
+// One thread per client that waits for pending events and runs their OnReady
+// callbacks in the order they were registered; it drains its queue before the
+// client goes.
+class Waiter {
+ public:
+  Waiter() : th_([this] { run(); }) {}
+  ~Waiter() {
+    {
+      std::lock_guard<std::mutex> g(mu_);
+      stop_ = true;
+    }
+    cv_.notify_all();
+    th_.join();
+  }
+  void post(std::shared_ptr<ExecState> s, PJRT_Event_OnReadyCallback cb, void* arg) {
+    {
+      std::lock_guard<std::mutex> g(mu_);
+      q_.push_back(Item{std::move(s), cb, arg});
+    }
+    cv_.notify_one();
+  }
+
+ private:
+  struct Item {
+    std::shared_ptr<ExecState> s;
+    PJRT_Event_OnReadyCallback cb;
+    void* arg;
+  };
+  void run() {
+    for (;;) {
+      Item it;
+      {
+        std::unique_lock<std::mutex> lk(mu_);
+        cv_.wait(lk, [&] { return stop_ || !q_.empty(); });
+        if (q_.empty()) return;
+        it = std::move(q_.front());
+        q_.pop_front();
+      }
+      it.s->wait();
+      it.cb(it.s->error(), it.arg);
+    }
+  }
+  std::mutex mu_;
+  std::condition_variable cv_;
+  std::deque<Item> q_;
+  bool stop_ = false;
+  std::thread th_;
+};
+}  // namespace
+
+PJRT_Client::~PJRT_Client() {
+  waiter.reset();             // pending callbacks run first
+  lower.stop();
+  if (rt) vmrt_destroy(rt);
+}
+
+struct PJRT_Event {
+  std::shared_ptr<ExecState> s;   // null: complete, no error
+};
 
 struct PJRT_Executable {
   std::shared_ptr<Program> p;
@@ -359,13 +486,27 @@ PJRT_Error* Event_Destroy(PJRT_Event_Destroy_Args* a) {
   return nullptr;
 }
 PJRT_Error* Event_IsReady(PJRT_Event_IsReady_Args* a) {
-  a->is_ready = true;
+  a->is_ready = !a->event->s || a->event->s->ready();
   return nullptr;
 }
-PJRT_Error* Event_Error(PJRT_Event_Error_Args*) { return nullptr; }
-PJRT_Error* Event_Await(PJRT_Event_Await_Args*) { return nullptr; }
+PJRT_Error* Event_Error(PJRT_Event_Error_Args* a) {
+  if (!a->event->s) return nullptr;
+  a->event->s->wait();            // the API expects a ready event; waiting keeps a premature call correct
+  return a->event->s->error();
+}
+PJRT_Error* Event_Await(PJRT_Event_Await_Args* a) {
+  if (!a->event->s) return nullptr;
+  a->event->s->wait();
+  return a->event->s->error();
+}
 PJRT_Error* Event_OnReady(PJRT_Event_OnReady_Args* a) {
-  a->callback(nullptr, a->user_arg);
+  const std::shared_ptr<ExecState>& s = a->event->s;
+  if (!s || s->ready() || !s->waiter) {
+    if (s) s->wait();
+    a->callback(s ? s->error() : nullptr, a->user_arg);
+  } else {
+    s->waiter->post(s, a->callback, a->user_arg);
+  }
   return nullptr;
 }
 
@@ -452,6 +593,7 @@ PJRT_Error* Client_Create(PJRT_Client_Create_Args* a) {
   char e[1024];
   if (int rc = vmrt_create(&o, &c->rt, e, sizeof e)) return from_vmrt(rc, e, "device");
   vmrt_device_info_get(c->rt, &c->info);
+  c->waiter = std::make_unique<Waiter>();
   c->version = vmrt_version();
   c->costs = cost_table(c->rt, c->info);
   PJRT_Device& d = c->device;
@@ -607,7 +749,7 @@ PJRT_Error* Client_BufferFromHostBuffer(PJRT_Client_BufferFromHostBuffer_Args* a
       b->release();
       return from_vmrt(rc, e, "host to device");
     }
-  a->done_with_host_buffer = new PJRT_Event;   // the copy above is complete
+  a->done_with_host_buffer = new PJRT_Event{};   // the copy above is complete
   a->buffer = b.release();
   return nullptr;
 }
@@ -826,12 +968,23 @@ PJRT_Error* LE_Execute(PJRT_LoadedExecutable_Execute_Args* a) {
     optr.push_back(b->ptr);
     outs.push_back(std::move(b));
   }
-  if (int rc = vmrt_execute(p.prog, ins.data(), ins.size(), optr.data(), optr.size(), e, sizeof e)) {
+  auto st = std::make_shared<ExecState>();
+  st->prog = ex->p;
+  st->waiter = c->waiter.get();
+  if (vmrt_event_create(c->rt, &st->ev) != VMRT_OK) {
+    for (auto& o : outs) o->release();
+    return make_error(PJRT_Error_Code_INTERNAL, "execute: event create failed");
+  }
+  if (int rc = vmrt_enqueue(p.prog, ins.data(), ins.size(), optr.data(), optr.size(), nullptr, e, sizeof e)) {
     for (auto& o : outs) o->release();
     return from_vmrt(rc, e, "execute");
   }
-  for (size_t i = 0; i < outs.size(); ++i) a->output_lists[0][i] = outs[i].release();
-  if (a->device_complete_events) a->device_complete_events[0] = new PJRT_Event;
+  if (vmrt_event_record(c->rt, st->ev, nullptr) != VMRT_OK) st->wait();   // no event: complete it now
+  for (size_t i = 0; i < outs.size(); ++i) {
+    outs[i]->ready = st;
+    a->output_lists[0][i] = outs[i].release();
+  }
+  if (a->device_complete_events) a->device_complete_events[0] = new PJRT_Event{st};
   return nullptr;
 }
 
@@ -886,10 +1039,14 @@ PJRT_Error* Buf_ToHostBuffer(PJRT_Buffer_ToHostBuffer_Args* a) {
   if (a->dst_size < b->bytes)
     return make_error(PJRT_Error_Code_INVALID_ARGUMENT, "destination of " + std::to_string(a->dst_size) +
                                                             " bytes for a " + std::to_string(b->bytes) + "-byte buffer");
+  if (b->ready) {                // the producing Execute's outcome comes first
+    b->ready->wait();
+    if (PJRT_Error* err = b->ready->error()) return err;
+  }
   char e[1024];
   if (b->bytes)
     if (int rc = vmrt_d2h(b->client->rt, a->dst, b->ptr, b->bytes, e, sizeof e)) return from_vmrt(rc, e, "device to host");
-  a->event = new PJRT_Event;
+  a->event = new PJRT_Event{};
   return nullptr;
 }
 PJRT_Error* Buf_IsOnCpu(PJRT_Buffer_IsOnCpu_Args* a) {
@@ -897,7 +1054,7 @@ PJRT_Error* Buf_IsOnCpu(PJRT_Buffer_IsOnCpu_Args* a) {
   return nullptr;
 }
 PJRT_Error* Buf_ReadyEvent(PJRT_Buffer_ReadyEvent_Args* a) {
-  a->event = new PJRT_Event;
+  a->event = new PJRT_Event{a->buffer->ready};
   return nullptr;
 }
 PJRT_Error* Buf_UnsafePointer(PJRT_Buffer_UnsafePointer_Args* a) {

@@ -1291,4 +1291,15 @@ void vmrt_event_destroy(void* event) {
   if (event) (void)hipEventDestroy(static_cast<hipEvent_t>(event));
 }
 
+int vmrt_event_query(void* event) {
+  if (!event) return VMRT_INVALID_ARGUMENT;
+  const hipError_t e = hipEventQuery(static_cast<hipEvent_t>(event));
+  return e == hipSuccess ? VMRT_OK : e == hipErrorNotReady ? VMRT_UNAVAILABLE : VMRT_INTERNAL;
+}
+
+int vmrt_event_synchronize(void* event) {
+  if (!event) return VMRT_INVALID_ARGUMENT;
+  return hipEventSynchronize(static_cast<hipEvent_t>(event)) == hipSuccess ? VMRT_OK : VMRT_INTERNAL;
+}
+
 }  // extern "C"

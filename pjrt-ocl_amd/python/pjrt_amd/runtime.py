@@ -35,9 +35,10 @@ RESOURCE_EXHAUSTED = 8
 FAILED_PRECONDITION = 9
 UNIMPLEMENTED = 12
 INTERNAL = 13
+UNAVAILABLE = 14
 CODE_NAMES = {OK: "OK", INVALID_ARGUMENT: "INVALID_ARGUMENT", NOT_FOUND: "NOT_FOUND",
               RESOURCE_EXHAUSTED: "RESOURCE_EXHAUSTED", FAILED_PRECONDITION: "FAILED_PRECONDITION",
-              UNIMPLEMENTED: "UNIMPLEMENTED", INTERNAL: "INTERNAL"}
+              UNIMPLEMENTED: "UNIMPLEMENTED", INTERNAL: "INTERNAL", UNAVAILABLE: "UNAVAILABLE"}
 
 
 class VmrtError(RuntimeError):
@@ -97,6 +98,8 @@ SIGNATURES = {
     "vmrt_event_record": (ctypes.c_int, [_VP, _VP, _VP]),
     "vmrt_event_elapsed_ms": (ctypes.c_int, [_VP, _VP, ctypes.POINTER(ctypes.c_float)]),
     "vmrt_event_destroy": (None, [_VP]),
+    "vmrt_event_query": (ctypes.c_int, [_VP]),
+    "vmrt_event_synchronize": (ctypes.c_int, [_VP]),
 }
 
 _lib = None
@@ -347,6 +350,18 @@ class Event:
         rc = self.rt._lib.vmrt_event_record(self.rt._h, self._e, _VP(stream or 0))
         if rc != OK:
             raise VmrtError(rc, "event record")
+
+    def query(self) -> bool:
+        """Whether the work recorded before the event has completed."""
+        rc = self.rt._lib.vmrt_event_query(self._e)
+        if rc not in (OK, UNAVAILABLE):
+            raise VmrtError(rc, "event query")
+        return rc == OK
+
+    def synchronize(self) -> None:
+        rc = self.rt._lib.vmrt_event_synchronize(self._e)
+        if rc != OK:
+            raise VmrtError(rc, "event synchronize")
 
     def elapsed_ms(self, stop: "Event") -> float:
         ms = ctypes.c_float()

@@ -79,6 +79,10 @@ BufOne = _args("BufOne", [("buffer", VP)])
 BufType = _args("BufType", [("buffer", VP), ("type", C.c_int)])
 BufDims = _args("BufDims", [("buffer", VP), ("dims", C.POINTER(C.c_int64)), ("num_dims", SZ)])
 EventOne = _args("EventOne", [("event", VP)])
+EventReady = _args("EventReady", [("event", VP), ("is_ready", C.c_bool)])
+OnReadyCb = C.CFUNCTYPE(None, VP, VP)
+EventOnReady = _args("EventOnReady", [("event", VP), ("callback", OnReadyCb), ("user_arg", VP)])
+BufEvent = _args("BufEvent", [("buffer", VP), ("event", VP)])
 ExeOne = _args("ExeOne", [("executable", VP)])
 ExeCount = _args("ExeCount", [("executable", VP), ("count", SZ)])
 GetExe = _args("GetExe", [("loaded", VP), ("executable", VP)])
@@ -198,7 +202,9 @@ class Plugin:
         self.call("PJRT_Executable_Destroy", ExeOne(executable=e))
         return n
 
-    def execute(self, loaded, buffers):
+    def execute(self, loaded, buffers, keep_event=False):
+        """Output buffers of one Execute; with keep_event also its device
+        completion event (the caller destroys it)."""
         n_out = self.num_outputs(loaded)
         args = (VP * max(1, len(buffers)))(*buffers)
         arg_lists = (VP * 1)(C.cast(args, VP))
@@ -208,9 +214,34 @@ class Plugin:
         a = Execute(executable=loaded, argument_lists=C.cast(arg_lists, VP), num_devices=1, num_args=len(buffers),
                     output_lists=C.cast(out_lists, VP), events=C.cast(events, VP))
         self.call("PJRT_LoadedExecutable_Execute", a)
+        if keep_event:
+            return [outs[k] for k in range(n_out)], events[0]
         if events[0]:
             self.call("PJRT_Event_Destroy", EventOne(event=events[0]))
         return [outs[k] for k in range(n_out)]
+
+    # events
+    def is_ready(self, ev) -> bool:
+        return bool(self.call("PJRT_Event_IsReady", EventReady(event=ev)).is_ready)
+
+    def await_event(self, ev) -> None:
+        self.call("PJRT_Event_Await", EventOne(event=ev))
+
+    def on_ready(self, ev, fn):
+        """Register fn(error_or_None) and return the ctypes callback (keep it alive)."""
+        def cb(err, _arg):
+            fn(self.error_info(err) if err else None)
+            if err:
+                self.destroy_error(err)
+        c = OnReadyCb(cb)
+        self.call("PJRT_Event_OnReady", EventOnReady(event=ev, callback=c, user_arg=None))
+        return c
+
+    def destroy_event(self, ev) -> None:
+        self.call("PJRT_Event_Destroy", EventOne(event=ev))
+
+    def ready_event(self, buf):
+        return self.call("PJRT_Buffer_ReadyEvent", BufEvent(buffer=buf)).event
 
     def destroy_executable(self, loaded):
         self.call("PJRT_LoadedExecutable_Destroy", ExeOne(executable=loaded))

@@ -211,3 +211,50 @@ def test_client_compile_execute_fused_programs():
         assert e.value.code == 12 and "cholesky" in e.value.message
     finally:
         p.destroy_client(client)
+
+
+@pytest.mark.gpu
+def test_execute_is_asynchronous_with_real_events():
+    """Execute returns once the program is launched: its completion event and its
+    outputs' ready events complete with the launch (IsReady, Await, OnReady on
+    the client's waiter thread), later launches and copies are ordered after it
+    on the one stream, and results read back after two back-to-back Executes
+    are both right."""
+    import threading
+    p = plugin()
+    client = p.create_client(sys.executable, P.LOWER_SERVICE)
+    try:
+        rng = np.random.default_rng(2024)
+        a = rng.standard_normal((1024, 1024)).astype(np.float32)
+        b = rng.standard_normal((1024, 1024)).astype(np.float32)
+        exe = p.compile(client, H.matmul(1024, 1024, 1024, "f32", "f32"))
+        bufs = [p.to_device(client, x) for x in (a, b)]
+        print("[gpu] pjrt: async executes", file=sys.stderr, flush=True)
+        (o1,), e1 = p.execute(exe, bufs, keep_event=True)
+        (o2,), e2 = p.execute(exe, [o1, bufs[1]], keep_event=True)     # consumes o1 on the same stream
+        seen, done = [], threading.Event()
+
+        def cb(err):
+            seen.append(err)
+            done.set()
+        keep = p.on_ready(e2, cb)
+        p.await_event(e1)
+        assert p.is_ready(e1)
+        r2 = p.ready_event(o2)
+        p.await_event(r2)
+        assert p.is_ready(r2) and p.is_ready(e2)
+        assert done.wait(30) and seen == [None]
+        got1, _ = p.to_host(o1)
+        got2, _ = p.to_host(o2)
+        w1 = a.astype(np.float64) @ b
+        w2 = got1.astype(np.float64) @ b
+        assert np.abs(got1 - w1).max() <= 1e-3 * np.abs(w1).max()
+        assert np.abs(got2 - w2).max() <= 1e-3 * np.abs(w2).max()
+        for ev in (e1, e2, r2):
+            p.destroy_event(ev)
+        del keep
+        for bb in bufs + [o1, o2]:
+            p.destroy_buffer(bb)
+        p.destroy_executable(exe)
+    finally:
+        p.destroy_client(client)

@@ -45,7 +45,18 @@ struct PJRT_Buffer;
 struct PJRT_Event;
 struct PJRT_Device_Attributes;
 struct PJRT_DeviceAssignmentSerialized;
-struct PJRT_ExecuteOptions;
+// PJRT_ExecuteOptions up to the fields this plugin reads (the donation list)
+struct PJRT_ExecuteOptions {
+  size_t struct_size;
+  PJRT_Extension_Base* extension_start;
+  void** send_callbacks;
+  void** recv_callbacks;
+  size_t num_send_ops;
+  size_t num_recv_ops;
+  int launch_id;
+  const int64_t* non_donatable_input_indices;
+  size_t num_non_donatable_input_indices;
+};
 struct PJRT_Buffer_MemoryLayout;
 
 enum PJRT_Error_Code {

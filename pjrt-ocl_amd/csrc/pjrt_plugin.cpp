@@ -19,7 +19,9 @@
 //     runs as one child process per client, started at Client_Create, with
 //     one framed request per compile (pjrt_amd/lower_service.py, --serve);
 //   * Execute binds the argument buffers as the program's zero-copy inputs,
-//     allocates fresh output buffers and runs the VM (plugin.cc:941-988).
+//     allocates fresh output buffers (or hands an output a donated argument's
+//     memory, when the lowering found that safe) and runs the VM
+//     (plugin.cc:941-988).
 // Every slot jaxlib may call is populated; the ones this plugin does not
 // provide return UNIMPLEMENTED naming the call (plugin.cc:95-102).  The four
 // that jaxlib cannot tolerate as stubs are implemented: Error_ForEachPayload,
@@ -146,7 +148,7 @@ class LowerService {
   // status: the one-shot exit code (0 ok, 2 unsupported, 3 internal); payload:
   // v3 bytes or the JSON error.  false = the service itself failed.
   bool compile(const char* code, size_t n, const vmrt_device_info& dev, const std::string& costs, uint32_t* status,
-               std::string* payload, std::string* err) {
+               std::string* payload, std::vector<std::pair<uint32_t, uint32_t>>* aliases, std::string* err) {
     if (!start(err)) return false;
     uint32_t head[4] = {dev.n_lanes, dev.ew_ts, dev.mma_t, uint32_t(costs.size())};
     uint64_t len = n;
@@ -156,11 +158,22 @@ class LowerService {
     req.append(code, n);
     std::string resp_head;
     if (!transfer(req, &resp_head, 16, err)) return restart_fail(err);
-    uint32_t st;
+    uint32_t st, n_alias;
     uint64_t plen;
     std::memcpy(&st, resp_head.data(), 4);
+    std::memcpy(&n_alias, resp_head.data() + 4, 4);
     std::memcpy(&plen, resp_head.data() + 8, 8);
     if (!transfer(std::string(), payload, plen, err)) return restart_fail(err);
+    aliases->clear();
+    if (n_alias) {
+      std::string raw;
+      if (n_alias > 65536 || !transfer(std::string(), &raw, uint64_t(n_alias) * 8, err)) return restart_fail(err);
+      for (uint32_t k = 0; k < n_alias; ++k) {
+        uint32_t io[2];
+        std::memcpy(io, raw.data() + 8 * k, 8);
+        aliases->emplace_back(io[0], io[1]);
+      }
+    }
     *status = st;
     return true;
   }
@@ -317,6 +330,9 @@ struct Program {
   std::vector<size_t> out_rank;
   std::vector<const char*> out_kinds;
   std::vector<size_t> out_kind_sizes;
+  // donations the program can take: (input, output) pairs whose memory an
+  // Execute may share when the input is donated (lowering.donation_aliases)
+  std::vector<std::pair<uint32_t, uint32_t>> aliases;
   ~Program() {
     if (prog) vmrt_unload(prog);
   }
@@ -682,9 +698,10 @@ PJRT_Error* Client_Compile(PJRT_Client_Compile_Args* a) {
     return make_error(PJRT_Error_Code_INVALID_ARGUMENT, "program format '" + format + "' (expected 'mlir')");
   uint32_t status = 0;
   std::string payload, err;
+  std::vector<std::pair<uint32_t, uint32_t>> aliases;
   {
     std::lock_guard<std::mutex> g(c->compile_mu);
-    if (!c->lower.compile(prog->code, prog->code_size, c->info, c->costs, &status, &payload, &err))
+    if (!c->lower.compile(prog->code, prog->code_size, c->info, c->costs, &status, &payload, &aliases, &err))
       return make_error(PJRT_Error_Code_INTERNAL, "lowering service: " + err);
   }
   if (status == 2) return make_error(PJRT_Error_Code_UNIMPLEMENTED, "unsupported program: " + payload);
@@ -717,6 +734,10 @@ PJRT_Error* Client_Compile(PJRT_Client_Compile_Args* a) {
     p->out_kinds.push_back(kKind);
     p->out_kind_sizes.push_back(sizeof kKind - 1);
   }
+  for (const auto& io : aliases)
+    if (io.first < p->in_dt.size() && io.second < p->out_dt.size() && p->in_bytes[io.first] == p->out_bytes[io.second] &&
+        p->in_dt[io.first] == p->out_dt[io.second])
+      p->aliases.push_back(io);
   auto* ex = new PJRT_LoadedExecutable;
   ex->client = c;
   ex->p = std::move(p);
@@ -952,6 +973,27 @@ PJRT_Error* LE_Execute(PJRT_LoadedExecutable_Execute_Args* a) {
     ins[i] = b->ptr;
   }
   PJRT_Client* c = ex->client;
+  // donation (docs/memory.md:26-27): an output the program may alias with a
+  // donated input takes that input's memory, and the input buffer is deleted.
+  // Arguments are donated unless listed in non_donatable_input_indices (with no
+  // options nothing is donated); a buffer passed twice is never donated.
+  std::vector<int> donor(p.out_dt.size(), -1);
+  if (a->options && !p.aliases.empty()) {
+    const PJRT_ExecuteOptions* o = a->options;
+    auto donatable = [&](uint32_t i) {
+      for (size_t k = 0; k < o->num_non_donatable_input_indices; ++k)
+        if (o->non_donatable_input_indices[k] == int64_t(i)) return false;
+      for (size_t j = 0; j < a->num_args; ++j)
+        if (j != i && a->argument_lists[0][j] == a->argument_lists[0][i]) return false;
+      return true;
+    };
+    std::vector<bool> used(a->num_args, false);
+    for (const auto& io : p.aliases)
+      if (!used[io.first] && donor[io.second] < 0 && donatable(io.first)) {
+        donor[io.second] = int(io.first);
+        used[io.first] = true;
+      }
+  }
   std::vector<std::unique_ptr<PJRT_Buffer>> outs;
   std::vector<void*> optr;
   char e[1024];
@@ -961,24 +1003,37 @@ PJRT_Error* LE_Execute(PJRT_LoadedExecutable_Execute_Args* a) {
     b->bytes = p.out_bytes[i];
     b->type = p.out_types[i];
     b->dims = p.out_dims[i];
-    if (int rc = vmrt_alloc(c->rt, b->bytes, &b->ptr, e, sizeof e)) {
-      for (auto& o : outs) o->release();
+    if (donor[i] >= 0) {
+      b->ptr = const_cast<void*>(ins[size_t(donor[i])]);   // taken over below, once the launch is queued
+    } else if (int rc = vmrt_alloc(c->rt, b->bytes, &b->ptr, e, sizeof e)) {
+      for (size_t k = 0; k < outs.size(); ++k)
+        if (donor[k] < 0) outs[k]->release();
       return from_vmrt(rc, e, "output buffer");
     }
     optr.push_back(b->ptr);
     outs.push_back(std::move(b));
   }
+  auto drop_outputs = [&] {
+    for (size_t k = 0; k < outs.size(); ++k)
+      if (donor[k] < 0) outs[k]->release();
+  };
   auto st = std::make_shared<ExecState>();
   st->prog = ex->p;
   st->waiter = c->waiter.get();
   if (vmrt_event_create(c->rt, &st->ev) != VMRT_OK) {
-    for (auto& o : outs) o->release();
+    drop_outputs();
     return make_error(PJRT_Error_Code_INTERNAL, "execute: event create failed");
   }
   if (int rc = vmrt_enqueue(p.prog, ins.data(), ins.size(), optr.data(), optr.size(), nullptr, e, sizeof e)) {
-    for (auto& o : outs) o->release();
+    drop_outputs();
     return from_vmrt(rc, e, "execute");
   }
+  for (size_t k = 0; k < outs.size(); ++k)
+    if (donor[k] >= 0) {                       // the donated input's memory now belongs to output k
+      PJRT_Buffer* in = a->argument_lists[0][size_t(donor[k])];
+      in->ptr = nullptr;
+      in->deleted = true;
+    }
   if (vmrt_event_record(c->rt, st->ev, nullptr) != VMRT_OK) st->wait();   // no event: complete it now
   for (size_t i = 0; i < outs.size(); ++i) {
     outs[i]->ready = st;

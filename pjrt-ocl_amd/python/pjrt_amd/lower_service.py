@@ -23,8 +23,10 @@ little-endian:
 
     request   u32 n_lanes, u32 ew_ts, u32 mma_t, u32 cost_length, u64 length,
               the cost table (cost_length bytes of JSON, vmrt_calibrate's), program bytes
-    response  u32 status (the one-shot exit code), u32 pad, u64 length, payload
-              (v3 bytes when status is 0, else the JSON error)
+    response  u32 status (the one-shot exit code), u32 n_aliases, u64 length, payload
+              (v3 bytes when status is 0, else the JSON error), then n_aliases x
+              {u32 input, u32 output}: the donations the program can take
+              (lowering.donation_aliases)
 
 A request with length 0xFFFFFFFFFFFFFFFF ends the server.
 """
@@ -40,6 +42,7 @@ EXIT_UNSUPPORTED = 2
 EXIT_INTERNAL = 3
 _REQ = struct.Struct("<IIIIQ")
 _RESP = struct.Struct("<IIQ")
+_ALIAS = struct.Struct("<II")
 _END = 0xFFFFFFFFFFFFFFFF
 
 
@@ -53,18 +56,21 @@ def _package():
     return lowering, scheduler
 
 
-def compile_bytes(program: bytes, cfg=None) -> tuple:
-    """(status, payload) for one program."""
+def compile_bytes(program: bytes, cfg=None, with_aliases: bool = False) -> tuple:
+    """(status, payload) for one program; with ``with_aliases`` also the
+    [(input, output)] donation aliases."""
     try:
         if not program:
             raise ValueError("empty program (expected a VHLO artifact or StableHLO text)")
         lowering, scheduler = _package()
         if cfg is None:
             cfg = scheduler.DeviceConfig.from_env()
-        return EXIT_OK, lowering.lower_and_schedule(program, cfg)
+        blob, aliases = lowering.lower_and_schedule(program, cfg, with_aliases=True)
+        return (EXIT_OK, blob, aliases) if with_aliases else (EXIT_OK, blob)
     except Exception as e:  # noqa: BLE001 -- the service boundary
         msg = json.dumps({"error": type(e).__name__, "message": str(e)}).encode()
-        return (EXIT_UNSUPPORTED if isinstance(e, NotImplementedError) else EXIT_INTERNAL), msg
+        status = EXIT_UNSUPPORTED if isinstance(e, NotImplementedError) else EXIT_INTERNAL
+        return (status, msg, []) if with_aliases else (status, msg)
 
 
 def _read_exact(f, n: int) -> bytes:
@@ -99,9 +105,10 @@ def serve(inp=None, out=None) -> int:
             cfg.ew_ts = ew_ts
         if mma_t:
             cfg.mma_t = mma_t
-        status, payload = compile_bytes(program, cfg)
-        out.write(_RESP.pack(status, 0, len(payload)))
+        status, payload, aliases = compile_bytes(program, cfg, with_aliases=True)
+        out.write(_RESP.pack(status, len(aliases), len(payload)))
         out.write(payload)
+        out.write(b"".join(_ALIAS.pack(i, o) for i, o in aliases))
         out.flush()
 
 

@@ -801,7 +801,8 @@ def detect_fixed_trip(op: M.Op, cval: dict):
 
 def lower_module(module: M.Module, fuse: bool = True) -> V.VMProgram:
     """A parsed module's public @main -> a VMProgram (tensor sections), fused and
-    with its arena packed by liveness."""
+    with its arena packed by liveness; ``io_aliases`` holds the donations the
+    program can take (``donation_aliases``)."""
     from . import passes
     prog = Lowerer(module).lower()
     if fuse:
@@ -813,7 +814,64 @@ def lower_module(module: M.Module, fuse: bool = True) -> V.VMProgram:
     if prog.arena_bytes >= 1 << 31:
         raise LoweringError(f"arena of {prog.arena_bytes} bytes exceeds the 31-bit offset space "
                             f"(bit 31 of a handle marks an I/O port)")
+    prog.io_aliases = donation_aliases(prog, module.main)
     return prog
+
+
+def donation_aliases(prog: V.VMProgram, main: M.Func, cfg=None) -> list:
+    """[(input, output)] pairs a donated argument may share memory with: the
+    argument carries ``tf.aliasing_output`` (what jax.jit(donate_argnums=...)
+    emits), the two have the same byte size, neither is also an output / input,
+    and every instruction reading the input runs in an earlier phase (a grid
+    barrier earlier) than every instruction writing the output, so on shared
+    memory no write can overtake a read.  Loops and branches count as one phase
+    each, as in passes.reuse_arena."""
+    from . import passes
+    from . import scheduler as S
+    pairs = []
+    for i in range(len(prog.inputs)):
+        a = main.arg_attr(i, "tf.aliasing_output")
+        if a is None:
+            continue
+        try:
+            o = M.attr_int(a)
+        except M.MlirSyntaxError:
+            continue
+        if 0 <= o < len(prog.outputs):
+            pairs.append((i, o))
+    if not pairs:
+        return []
+    cfg = cfg or S.DeviceConfig.from_env()
+    sched = S._Scheduler(prog, cfg)
+    phase = {}
+    for ph, (kind, payload) in enumerate(sched.levels(list(range(prog.main_len)))):
+        roots = payload if kind == "compute" else [payload]
+        for r in roots:
+            stack = [r]
+            while stack:
+                k = stack.pop()
+                phase[k] = ph
+                ins = prog.instrs[k]
+                if ins.op in (V.OP_WHILE, V.OP_IF):
+                    stack += list(range(ins.a, ins.a + ins.b)) + list(range(ins.n, ins.n + ins.imm))
+                elif ins.op == V.OP_FOR:
+                    stack += list(range(ins.n, ins.n + ins.imm))
+    for dot_i, ln_i in sched.ln_pro.items():         # a layernorm staged in its GEMV runs there
+        if dot_i in phase:
+            phase[ln_i] = phase[dot_i]
+    grp = S.overlap_groups(prog)
+    out = []
+    for i, o in pairs:
+        bi, bo = prog.inputs[i], prog.outputs[o]
+        if prog.buffers[bi].size_bytes != prog.buffers[bo].size_bytes or bi in prog.outputs or bo in prog.inputs:
+            continue
+        reads = [phase[k] for k, ins in enumerate(prog.instrs)
+                 if ins.op != V.OP_NOP and k in phase and grp[bi] in {grp[b] for b in passes.reads_of(ins, prog)}]
+        writes = [phase[k] for k, ins in enumerate(prog.instrs)
+                  if ins.op != V.OP_NOP and k in phase and grp[bo] in {grp[b] for b in passes.writes_of(ins)}]
+        if writes and (not reads or max(reads) < min(writes)):
+            out.append((i, o))
+    return out
 
 
 def lower_text(text: str, fuse: bool = True) -> V.VMProgram:
@@ -855,10 +913,12 @@ def lower_artifact(artifact: bytes) -> V.VMProgram:
     return lower_text(artifact_to_text(artifact))
 
 
-def lower_and_schedule(artifact: bytes, cfg=None) -> bytes:
+def lower_and_schedule(artifact: bytes, cfg=None, with_aliases: bool = False):
     """Program bytes -> VMProgram v3 bytes with the schedule for the device the
-    environment describes (PJRT_OCL_NLANES / _EW_TS / _MMA_T, scheduler.py:135-153)."""
+    environment describes (PJRT_OCL_NLANES / _EW_TS / _MMA_T, scheduler.py:135-153);
+    with ``with_aliases`` the pair (bytes, [(input, output)] donation aliases)."""
     from . import scheduler as S
     prog = lower_artifact(artifact)
     cfg = cfg or S.DeviceConfig.from_env()
-    return V.serialize(prog, S.schedule_program(prog, cfg))
+    blob = V.serialize(prog, S.schedule_program(prog, cfg))
+    return (blob, list(getattr(prog, "io_aliases", []))) if with_aliases else blob

@@ -255,6 +255,10 @@ class Func:
     result_types: list
     body: Block
     visibility: str = "public"
+    arg_attrs: list = dataclasses.field(default_factory=list)   # one dict per argument
+
+    def arg_attr(self, i: int, key: str, default=None):
+        return self.arg_attrs[i].get(key, default) if i < len(self.arg_attrs) else default
 
 
 @dataclasses.dataclass(eq=False)
@@ -881,15 +885,14 @@ class _Parser:
         self.expect("@")
         name = self.ident()
         self.expect("(")
-        args = []
+        args, arg_attrs = [], []
         while not self.eat(")"):
             self.ws()
             m = _VAL.match(self.s, self.i)
             self.i = m.end()
             self.expect(":")
             v = Value(m.group(1), self.type_())
-            if self.peek("{"):
-                self.attr_dict()
+            arg_attrs.append(self.attr_dict() if self.peek("{") else {})
             self.scopes[-1][m.group(1)] = v
             args.append(v)
             self.eat(",")
@@ -907,7 +910,7 @@ class _Parser:
         ops = []
         while not self.eat("}"):
             ops.append(self.op())
-        return Func(name, args, rtypes, Block(args, ops), vis)
+        return Func(name, args, rtypes, Block(args, ops), vis, arg_attrs)
 
     def generic_op_func(self) -> Func:
         self.string()                                   # "func.func"
@@ -928,8 +931,10 @@ class _Parser:
         ft = props.get("function_type")
         name = props.get("sym_name", "main")
         body = blocks[0]
+        aa = props.get("arg_attrs")
+        arg_attrs = [d if isinstance(d, dict) else {} for d in (aa.values if isinstance(aa, ArrayAttr) else aa or [])]
         return Func(name, body.args, list(ft.results) if isinstance(ft, FunctionType) else [], body,
-                    props.get("sym_visibility", "public"))
+                    props.get("sym_visibility", "public"), arg_attrs)
 
 
 def _struct_fields(body: str) -> dict:

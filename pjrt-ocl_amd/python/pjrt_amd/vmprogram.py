@@ -334,6 +334,9 @@ class VMProgram:
     # those like one buffer would serialise unrelated work.  Not serialized;
     # None: groups follow arena overlap.
     alias_groups: list | None = dataclasses.field(default=None, compare=False, repr=False)
+    # [(input index, output index)]: a donated input whose memory the output may
+    # take (the lowering's donation_aliases).  Not serialized.
+    io_aliases: list = dataclasses.field(default_factory=list, compare=False, repr=False)
 
 
 def _pad8(out: bytearray) -> None:

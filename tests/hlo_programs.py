@@ -149,3 +149,22 @@ def generic_chain(n=64):
   }}) : () -> ()
 }}) {{mhlo.num_partitions = 1 : i32}} : () -> ()
 """
+
+
+def donated_chain(n=64, alias_to=0, twice=True):
+    """def f(x, w): return (x @ w) @ w  with jax.jit(f, donate_argnums=0): the
+    donated x carries tf.aliasing_output.  twice=False: return x + w (read and
+    written in the same phase)."""
+    X = _t((n, n))
+    body = f"""
+    %0 = stablehlo.dot_general %arg0, %arg1, contracting_dims = [1] x [0], precision = [DEFAULT, DEFAULT] : ({X}, {X}) -> {X}
+    %1 = stablehlo.dot_general %0, %arg1, contracting_dims = [1] x [0], precision = [DEFAULT, DEFAULT] : ({X}, {X}) -> {X}
+    return %1 : {X}""" if twice else f"""
+    %1 = stablehlo.add %arg0, %arg1 : {X}
+    return %1 : {X}"""
+    return f"""
+module @jit_f {{
+  func.func public @main(%arg0: {X} {{tf.aliasing_output = {alias_to} : i32}}, %arg1: {X}) -> ({X} {{jax.result_info = ""}}) {{{body}
+  }}
+}}
+"""

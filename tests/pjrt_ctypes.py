@@ -78,6 +78,12 @@ ToHost = _args("ToHost", [("src", VP), ("layout", VP), ("dst", VP), ("dst_size",
 BufOne = _args("BufOne", [("buffer", VP)])
 BufType = _args("BufType", [("buffer", VP), ("type", C.c_int)])
 BufDims = _args("BufDims", [("buffer", VP), ("dims", C.POINTER(C.c_int64)), ("num_dims", SZ)])
+ExecOptions = _args("ExecOptions", [("send_callbacks", VP), ("recv_callbacks", VP), ("num_send_ops", SZ),
+                                    ("num_recv_ops", SZ), ("launch_id", C.c_int),
+                                    ("non_donatable", C.POINTER(C.c_int64)), ("num_non_donatable", SZ),
+                                    ("context", VP)])
+BufPointer = _args("BufPointer", [("buffer", VP), ("pointer", C.c_size_t)])
+BufDeleted = _args("BufDeleted", [("buffer", VP), ("is_deleted", C.c_bool)])
 EventOne = _args("EventOne", [("event", VP)])
 EventReady = _args("EventReady", [("event", VP), ("is_ready", C.c_bool)])
 OnReadyCb = C.CFUNCTYPE(None, VP, VP)
@@ -202,23 +208,36 @@ class Plugin:
         self.call("PJRT_Executable_Destroy", ExeOne(executable=e))
         return n
 
-    def execute(self, loaded, buffers, keep_event=False):
+    def execute(self, loaded, buffers, keep_event=False, non_donatable=None):
         """Output buffers of one Execute; with keep_event also its device
-        completion event (the caller destroys it)."""
+        completion event (the caller destroys it).  non_donatable: None passes
+        no execute options (nothing donated), else the indices not to donate."""
         n_out = self.num_outputs(loaded)
+        opts = None
+        if non_donatable is not None:
+            nd = (C.c_int64 * max(1, len(non_donatable)))(*non_donatable)
+            opts = ExecOptions(non_donatable=C.cast(nd, C.POINTER(C.c_int64)), num_non_donatable=len(non_donatable))
+            opts.struct_size = C.sizeof(ExecOptions)
         args = (VP * max(1, len(buffers)))(*buffers)
         arg_lists = (VP * 1)(C.cast(args, VP))
         outs = (VP * max(1, n_out))()
         out_lists = (VP * 1)(C.cast(outs, VP))
         events = (VP * 1)()
         a = Execute(executable=loaded, argument_lists=C.cast(arg_lists, VP), num_devices=1, num_args=len(buffers),
-                    output_lists=C.cast(out_lists, VP), events=C.cast(events, VP))
+                    output_lists=C.cast(out_lists, VP), events=C.cast(events, VP),
+                    options=C.cast(C.pointer(opts), VP) if opts is not None else None)
         self.call("PJRT_LoadedExecutable_Execute", a)
         if keep_event:
             return [outs[k] for k in range(n_out)], events[0]
         if events[0]:
             self.call("PJRT_Event_Destroy", EventOne(event=events[0]))
         return [outs[k] for k in range(n_out)]
+
+    def pointer(self, buf) -> int:
+        return self.call("PJRT_Buffer_UnsafePointer", BufPointer(buffer=buf)).pointer
+
+    def is_deleted(self, buf) -> bool:
+        return bool(self.call("PJRT_Buffer_IsDeleted", BufDeleted(buffer=buf)).is_deleted)
 
     # events
     def is_ready(self, ev) -> bool:

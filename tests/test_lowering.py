@@ -299,6 +299,20 @@ def test_reuse_arena_keeps_the_schedule():
     assert low.arena_bytes <= io + 64 * len(low.buffers)
 
 
+def test_donation_aliases():
+    """A donated argument (tf.aliasing_output) may share its memory with the
+    output when every read of it is a phase earlier than every write of the
+    output; in the same phase, or with a size mismatch, it may not."""
+    assert L.lower_text(H.donated_chain(64)).io_aliases == [(0, 0)]
+    assert L.lower_text(H.donated_chain(64, twice=False)).io_aliases == []
+    assert L.lower_text(H.donated_chain(64, alias_to=3)).io_aliases == []
+    text = H.donated_chain(64).replace(" {tf.aliasing_output = 0 : i32}", "")
+    assert L.lower_text(text).io_aliases == []
+    # the parser keeps each argument's attribute dictionary
+    m = M.parse_module(H.donated_chain(8))
+    assert M.attr_int(m.main.arg_attr(0, "tf.aliasing_output")) == 0 and m.main.arg_attr(1, "x") is None
+
+
 def test_planted_pass_mistake_is_caught(monkeypatch):
     """A GELU fusion that matched the cubic coefficient loosely (0.04715) would
     fuse a different function; the exact-constant gate must refuse, leaving the

@@ -102,6 +102,16 @@ def test_lower_service_one_shot_contract():
     assert empty.returncode == 3 and json.loads(empty.stderr)["error"] == "ValueError"
 
 
+def test_lower_service_reports_donation_aliases():
+    code = H.donated_chain(64).encode()
+    req = struct.pack("<IIIIQ", 4, 256, 64, 0, len(code)) + code + struct.pack("<IIIIQ", 0, 0, 0, 0, 0xFFFFFFFFFFFFFFFF)
+    r = _service(["--serve"], req)
+    assert r.returncode == 0, r.stderr
+    st, n_alias, n = struct.unpack_from("<IIQ", r.stdout, 0)
+    assert st == 0 and n_alias == 1
+    assert struct.unpack_from("<II", r.stdout, 16 + n) == (0, 0)
+
+
 def test_lower_service_server_frames():
     req = b""
     for text in (H.matmul(64, 32, 48), "not mlir at all"):
@@ -255,6 +265,36 @@ def test_execute_is_asynchronous_with_real_events():
         del keep
         for bb in bufs + [o1, o2]:
             p.destroy_buffer(bb)
+        p.destroy_executable(exe)
+    finally:
+        p.destroy_client(client)
+
+
+@pytest.mark.gpu
+def test_execute_donates_an_aliased_argument():
+    """(x @ w) @ w with x donated: the output takes x's device memory and x is
+    deleted; with x listed as non-donatable, or with no execute options, the
+    output gets memory of its own and x stays alive.  Results equal numpy."""
+    p = plugin()
+    client = p.create_client(sys.executable, P.LOWER_SERVICE)
+    try:
+        rng = np.random.default_rng(2025)
+        x = rng.standard_normal((256, 256)).astype(np.float32)
+        w = (rng.standard_normal((256, 256)) * 0.1).astype(np.float32)
+        want = (x.astype(np.float64) @ w) @ w
+        exe = p.compile(client, H.donated_chain(256))
+        for nd in (None, [0], []):
+            print(f"[gpu] pjrt: donation, non-donatable {nd}", file=sys.stderr, flush=True)
+            xb, wb = p.to_device(client, x), p.to_device(client, w)
+            xptr = p.pointer(xb)
+            (out,) = p.execute(exe, [xb, wb], non_donatable=nd)
+            got, _ = p.to_host(out)
+            assert np.abs(got - want).max() <= 1e-3 * np.abs(want).max()
+            donated = nd == []
+            assert p.is_deleted(xb) == donated
+            assert (p.pointer(out) == xptr) == donated
+            for bb in (xb, wb, out):
+                p.destroy_buffer(bb)
         p.destroy_executable(exe)
     finally:
         p.destroy_client(client)

@@ -313,10 +313,10 @@ def bench_attention(rt, steps, warmup, B=4, H=16, S=2048, D=128):
 
 
 def bench_lowered(rt, steps):
-    """The drop-in path: configs 1-4 as the StableHLO text a JAX program lowers
+    """The drop-in path: configs 1-5 as the StableHLO text a JAX program lowers
     to (pjrt_amd.stablehlo_configs), through the lowering and its fusion passes
     (what the plugin's Compile runs), timed beside the hand-built program of the
-    same config on the same inputs.  Reports both kernel times, their ratio,
+    same config on the same inputs (config 5: bench_c5_lowered).  Reports both kernel times, their ratio,
     the lowered program's tile ops and the largest difference between the two
     outputs."""
     from pjrt_amd import configs as CF
@@ -350,7 +350,7 @@ def bench_lowered(rt, steps):
         "c4": (H.attention(4, 16, 2048, 128, "bf16", True), hand_c4(), [bf16((4, 16, 2048, 128)) for _ in range(3)]),
     }
     names = {v: k for k, v in vars(V).items() if k.startswith("TOP_") and k != "TOP_MAX"}
-    out = {}
+    out = {"c5": bench_c5_lowered(rt)}
     for name, (text, hand, args) in cases.items():
         t0 = time.perf_counter()
         low = L.lower_text(text)
@@ -377,6 +377,57 @@ def bench_lowered(rt, steps):
                      "lowered_tile_ops": ops, "max_abs_diff_vs_hand_built": diff}
         log(f"lowered {name}: {ml * 1e3:.1f} us vs hand-built {mh * 1e3:.1f} us ({', '.join(ops)})")
     return out
+
+
+def bench_c5_lowered(rt, reps=3):
+    """Config 5 as the JAX program (pjrt_amd.stablehlo_configs.gpt_decode:
+    prefill, then a fori_loop decode with dynamic_update_slice KV caches, masked
+    attention and argmax) through the lowering, timed as bench_c5 times the
+    hand-built decoder: the full program against the same program cut to 8 loop
+    trips.  Also reports how many of the 129 tokens equal the hand-built
+    program's on the same inputs."""
+    from pjrt_amd import configs as CF
+    from pjrt_amd import lowering as L
+    from pjrt_amd import stablehlo_configs as H
+    c = CF.C5
+    args = CF.gpt_inputs(c)
+    dev_in = [rt.to_device(a) for a in args]
+    times, toks, lower_s = {}, {}, 0.0
+    saved = os.environ.get("PJRT_OCL_WHILE")
+    os.environ["PJRT_OCL_WHILE"] = "for"           # 8 trips would otherwise be unrolled
+    try:
+        for trips in (c.steps, 8):
+            t0 = time.perf_counter()
+            prog = L.lower_text(H.gpt_decode(c, trips=trips))
+            lower_s = max(lower_s, time.perf_counter() - t0)
+            lp = rt.compile(prog, arena_reuse=False)
+            dev_out = lp.alloc_outputs()
+            _, times[trips] = time_program(rt, lp, dev_in, dev_out, reps, 1)
+            if trips == c.steps:
+                toks["lowered"] = np.concatenate([dev_out[0].to_host(np.int32, (1,)),
+                                                  dev_out[1].to_host(np.int32, (c.steps,))])
+            for b in dev_out:
+                b.free()
+            lp.close()
+    finally:
+        if saved is None:
+            os.environ.pop("PJRT_OCL_WHILE", None)
+        else:
+            os.environ["PJRT_OCL_WHILE"] = saved
+    lp = rt.compile(CF.gpt_c5(c))
+    dev_out = lp.alloc_outputs()
+    lp.execute(dev_in, dev_out)
+    toks["hand_built"] = np.concatenate([dev_out[0].to_host(np.int32, (1,)), dev_out[1].to_host(np.int32, (c.steps,))])
+    for b in dev_out + dev_in:
+        b.free()
+    lp.close()
+    per_tok = (times[c.steps] - times[8]) / (c.steps - 8)
+    same = toks["lowered"] == toks["hand_built"]
+    log(f"lowered c5: {1e3 / per_tok:.1f} tokens/s, {int(same.sum())} of {same.size} tokens as hand-built")
+    return {"decode_tokens_per_s": round(1e3 / per_tok, 1), "ms_per_token": round(per_tok, 4),
+            "program_ms": round(times[c.steps], 3), "prefill_plus_8_steps_ms": round(times[8], 3),
+            "lower_s": round(lower_s, 2), "tokens_equal_to_hand_built": int(same.sum()),
+            "first_token_difference": int(np.argmin(same)) if not same.all() else None}
 
 
 def bench_c1(rt, steps, with_cpu=False):

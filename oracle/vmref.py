@@ -494,19 +494,28 @@ def attention(Q, Kb, Vb, scale, causal):
     return np.einsum("htc,hcd->htd", p, Vb.astype(np.float64)).astype(np.float32)
 
 
-def decode_attention(q, Kt, Vc, k, v, pos, scale):
+def decode_attention(q, Kt, Vc, k, v, pos, scale, krow=False, masked=False):
     """Extension OP_DECODE_ATTN (no reference counterpart; it is the per-step
     attention of the reference's decode idiom, DOT(q K^T) -> mask -> softmax ->
     DOT(P V), with the step's key/value appended to the cache prefix).
-    q, k, v [H, hd]; Kt [H, hd, C]; Vc [H, C, hd]; pos clamped to [0, C]."""
-    C = Kt.shape[2]
-    p = min(max(int(pos), 0), C)
-    keys = np.concatenate([Kt[:, :, :p].transpose(0, 2, 1), k[:, None, :]], 1).astype(np.float64)
+    q, k, v [H, hd]; Kt [H, hd, C] ([H, C, hd] with ``krow``); Vc [H, C, hd];
+    pos clamped to [0, C].  ``masked``: the form a decoder writes with the step's
+    key and value already stored at column pos and the keys after pos masked
+    (tools/bench_decode.py:47-52 is the unmasked append form): pos is clamped
+    to [0, C - 1] like the cache update's start, and a negative pos masks every
+    key, so the row is NaN as the decomposed softmax makes it."""
+    C = Kt.shape[1] if krow else Kt.shape[2]
+    p = min(max(int(pos), 0), C - 1 if masked else C)
+    kp = Kt[:, :p] if krow else Kt[:, :, :p].transpose(0, 2, 1)
+    keys = np.concatenate([kp, k[:, None, :]], 1).astype(np.float64)
     vals = np.concatenate([Vc[:, :p], v[:, None, :]], 1).astype(np.float64)
     s = np.einsum("hd,hcd->hc", q.astype(np.float64), keys) * scale
     e = np.exp(s - s.max(-1, keepdims=True))
     e /= e.sum(-1, keepdims=True)
-    return np.einsum("hc,hcd->hd", e, vals)
+    out = np.einsum("hc,hcd->hd", e, vals)
+    if masked and int(pos) < 0:
+        out[:] = np.nan
+    return out
 
 
 def _round_to(y, dt):
@@ -953,20 +962,21 @@ class TaskRunner:
     # 21: decode-step attention (extension): tile = head * S + split, p4 = H | S << 16;
     # a head's result is complete once its last split has run
     def top21(self, t, lo, hi):
-        H, S, hd, C = t.p[4] & 0xFFFF, max(1, t.p[4] >> 16), t.p[5], t.p[6]
+        H, S, hd, C = t.p[4] & 0xFFFF, max(1, t.p[4] >> 16), t.p[5] & 0xFFFF, t.p[6]
+        krow, masked = bool(t.p[5] >> 16 & 1), bool(t.p[5] >> 17 & 1)
         heads = [tile // S for tile in range(lo, min(hi, H * S)) if tile % S == S - 1]
         if not heads:
             return
         h0, h1 = heads[0], heads[-1] + 1
         ld = lambda bid, n: self.m.load_f(bid, t.adt)[:n]
         q = ld(t.a, H * hd).reshape(H, hd)
-        Kt = ld(t.b, H * hd * C).reshape(H, hd, C)
+        Kt = ld(t.b, H * hd * C).reshape((H, C, hd) if krow else (H, hd, C))
         Vc = ld(t.p[0], H * C * hd).reshape(H, C, hd)
         k = ld(t.p[1], H * hd).reshape(H, hd)
         v = ld(t.p[2], H * hd).reshape(H, hd)
         pos = int(self.m.view(t.p[3], I32)[0])
         sl = slice(h0, h1)
-        o = decode_attention(q[sl], Kt[sl], Vc[sl], k[sl], v[sl], pos, float(_bits_f32(t.p[7])))
+        o = decode_attention(q[sl], Kt[sl], Vc[sl], k[sl], v[sl], pos, float(_bits_f32(t.p[7])), krow, masked)
         self.m.store_f(t.dst, slice(h0 * hd, h1 * hd), o.reshape(-1).astype(np.float32), t.dt)
 
     # 15: strided partial-axis reduce

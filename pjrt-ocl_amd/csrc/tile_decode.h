@@ -25,8 +25,18 @@
 //
 // Task: a q, b K^T cache [H, hd, C], p0 V cache [H, C, hd], p1 k, p2 v, p3 pos
 // (i32 scalar, clamped to [0, C]), p4 H | S << 16 (S <= 1: no split), p5 hd
-// (multiple of 8, <= 256), p6 C (multiple of 8), p7 scale bits.  One dtype
-// (bf16 / f16 / f32) for every operand and the output; f32 arithmetic.
+// (multiple of 8, <= 256) | krow << 16 | masked << 17, p6 C (multiple of 8),
+// p7 scale bits.  One dtype (bf16 / f16 / f32) for every operand and the
+// output; f32 arithmetic.
+//
+// krow: the key cache holds rows [H, C, hd] (the layout a JAX decoder keeps,
+// tools/bench_decode.py:44-52) instead of K^T; hd is a power of two.  The score
+// pass then reads keys the way the P.V pass reads values: hd / 8 threads per
+// key, each a 16-byte run of channels, summed by lane shuffles.
+// masked: the decoder stored k and v at column pos before attending over the
+// keys up to pos (dynamic_update_slice, then a key <= pos mask): pos is clamped
+// to [0, C - 1] as the store's start is, and a negative pos leaves every key
+// masked, so the output is NaN as the decomposed softmax makes it.
 // Scratch (S > 1): [H * S][hd + 2] partials {max, sum, hd channels}, then H
 // arrival counters.
 #pragma once
@@ -60,7 +70,8 @@ template <uint32_t DT>
 VM_TILE void decode_attn_split(Args A, uint32_t ti, uint32_t tile) {
   A = uargs(A);
   const VM_K Task& t = task_of(A, ti);
-  const uint32_t hd = t.p[5], C = t.p[6];
+  const uint32_t hd = t.p[5] & 0xFFFF, C = t.p[6];
+  const bool krow = (t.p[5] >> 16) & 1, masked = (t.p[5] >> 17) & 1;
   const uint32_t H = t.p[4] & 0xFFFF, S = max(1u, t.p[4] >> 16);
   const float scale = __uint_as_float(t.p[7]);
   tile = uni(tile);
@@ -86,20 +97,32 @@ VM_TILE void decode_attn_split(Args A, uint32_t ti, uint32_t tile) {
   const uint32_t oc = nk ? min(o, nk / 8 - 1) : 0;
   const uint32_t kcol = min(k0 + 8 * oc, C - 8);
   const uint32_t dpt = (hd + 31) / 32;                        // <= kDecKU
-  Raw kr[kDecKU];
-  float qd[kDecKU];
-#pragma unroll
-  for (uint32_t u = 0; u < kDecKU; ++u)
-    if (u < dpt) {                                            // uniform: dpt is
-      const uint32_t d = min(dg + 32 * u, hd - 1);
-      kr[u] = gemv_ld<DT>(kt, uint64_t(d) * C + kcol);
-      qd[u] = load_f(q, DT, d);
-    }
-  // P.V: thread (cg = tid % cgs, rg = tid / cgs) holds channels [8 cg, +8) of
-  // rows rg, rg + rpp, ...; rows past nk re-read the last row (not accumulated)
+  // P.V (and the key rows of krow): thread (cg = tid % cgs, rg = tid / cgs)
+  // holds channels [8 cg, +8) of rows rg, rg + rpp, ...; rows past nk re-read
+  // the last row (not accumulated)
   const uint32_t cgs = hd / 8, rpp = kBlock / cgs;
   const uint32_t cg = tid % cgs, rg = min(tid / cgs, rpp - 1);
   const uint32_t vpt = (per + rpp - 1) / rpp;                 // <= kDecKU
+  Raw kr[kDecKU];
+  float qd[kDecKU];
+  Raw qrow;
+  if (krow) {
+    qrow = gemv_ld<DT>(q, cg * 8);
+#pragma unroll
+    for (uint32_t u = 0; u < kDecKU; ++u)
+      if (u < vpt) {
+        const uint32_t r = nk ? min(rg + rpp * u, nk - 1) : 0;
+        kr[u] = gemv_ld<DT>(kt, uint64_t(min(k0 + r, C - 1)) * hd + cg * 8);
+      }
+  } else {
+#pragma unroll
+    for (uint32_t u = 0; u < kDecKU; ++u)
+      if (u < dpt) {                                          // uniform: dpt is
+        const uint32_t d = min(dg + 32 * u, hd - 1);
+        kr[u] = gemv_ld<DT>(kt, uint64_t(d) * C + kcol);
+        qd[u] = load_f(q, DT, d);
+      }
+  }
   Raw vr[kDecKU];
 #pragma unroll
   for (uint32_t u = 0; u < kDecKU; ++u)
@@ -118,26 +141,47 @@ VM_TILE void decode_attn_split(Args A, uint32_t ti, uint32_t tile) {
   float* tmp = lds + kDecTmp;
   __syncthreads();                                   // the previous user of the LDS is done
   const float s_new = dec_block_sum(qn, red) * scale;   // the step's own key
-  const uint32_t pos = uni(uint32_t(praw < 0 ? 0 : praw > int32_t(C) ? int32_t(C) : praw));
+  const int32_t pmax = masked ? int32_t(C) - 1 : int32_t(C);
+  const uint32_t pos = uni(uint32_t(praw < 0 ? 0 : praw > pmax ? pmax : praw));
+  const bool no_key = masked && praw < 0;            // every key masked: NaN
 
   // ---- scores of the split's cache keys ---------------------------------------
-  float acc[8];
+  if (krow) {
+    float qv[8];
+    gemv_cvt<DT>(qrow, qv);
 #pragma unroll
-  for (int j = 0; j < 8; ++j) acc[j] = 0.0f;
+    for (uint32_t u = 0; u < kDecKU; ++u)
+      if (u < vpt) {                                          // uniform: vpt is
+        float w[8];
+        gemv_cvt<DT>(kr[u], w);
+        float sdot = 0.0f;
 #pragma unroll
-  for (uint32_t u = 0; u < kDecKU; ++u)
-    if (u < dpt && dg + 32 * u < hd) {
-      float w[8];
-      gemv_cvt<DT>(kr[u], w);
+        for (int j = 0; j < 8; ++j) sdot = fmaf(qv[j], w[j], sdot);
+        // the cgs threads of a key are adjacent lanes of one wave (cgs is a
+        // power of two dividing 64)
+        for (uint32_t msk = cgs >> 1; msk >= 1; msk >>= 1) sdot += __shfl_xor(sdot, msk, 64);
+        const uint32_t r = rg + rpp * u;
+        if (cg == 0 && r < nk) sc[r] = sdot * scale;
+      }
+  } else {
+    float acc[8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) acc[j] = fmaf(qd[u], w[j], acc[j]);
-    }
+    for (int j = 0; j < 8; ++j) acc[j] = 0.0f;
 #pragma unroll
-  for (int j = 0; j < 8; ++j)
-    for (int msk = 16; msk >= 1; msk >>= 1) acc[j] += __shfl_xor(acc[j], msk, 64);
-  if (dg == 0 && 8 * o < nk)
+    for (uint32_t u = 0; u < kDecKU; ++u)
+      if (u < dpt && dg + 32 * u < hd) {
+        float w[8];
+        gemv_cvt<DT>(kr[u], w);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) sc[8 * o + j] = acc[j] * scale;
+        for (int j = 0; j < 8; ++j) acc[j] = fmaf(qd[u], w[j], acc[j]);
+      }
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      for (int msk = 16; msk >= 1; msk >>= 1) acc[j] += __shfl_xor(acc[j], msk, 64);
+    if (dg == 0 && 8 * o < nk)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) sc[8 * o + j] = acc[j] * scale;
+  }
   __syncthreads();
 
   // ---- softmax over the split's keys up to pos (wave 0) -----------------------
@@ -217,7 +261,7 @@ VM_TILE void decode_attn_split(Args A, uint32_t ti, uint32_t tile) {
 
   gbyte* out = resolve(A, t.dst) + uint64_t(h) * hd * esz;
   if (S == 1) {
-    if (tid < hd) store_f(out, DT, tid, oacc / l);
+    if (tid < hd) store_f(out, DT, tid, no_key ? __builtin_nanf("") : oacc / l);
     return;
   }
   // split: publish the partial, count the arrival; the last split combines.
@@ -277,7 +321,7 @@ VM_TILE void decode_attn_split(Args A, uint32_t ti, uint32_t tile) {
           O = fmaf(o8[u], ms[k0b + u], O);
         }
     }
-    store_f(out, DT, tid, O / L);
+    store_f(out, DT, tid, no_key ? __builtin_nanf("") : O / L);
   }
 }
 

@@ -474,23 +474,30 @@ class Graph:
         return dst
 
     def decode_attention(self, q: Tensor, k: Tensor, v: Tensor, cache_kt: Tensor,
-                         cache_v: Tensor, pos: Tensor, scale: float) -> Tensor:
+                         cache_v: Tensor, pos: Tensor, scale: float, krow: bool = False,
+                         masked: bool = False) -> Tensor:
         """One decode step of attention per head (extension opcode
         OP_DECODE_ATTN): the keys are the cache prefix K^T[h, :, :pos] and the
         step's own key k[h], the values V[h, :pos] and v[h], so the step reads
         its new key/value straight from where they were computed and the cache
         update can run beside the next matmul.  q, k, v: [H, hd] (any shape of
-        H * hd elements); cache_kt: [H, hd, C]; cache_v: [H, C, hd]; pos: i32
-        scalar, clamped to [0, C].  All float operands share one dtype; the
-        output [H, hd] has it too.  Equals the decomposed
-        dot -> (mask beyond pos) -> softmax -> dot chain with pos's column of the
-        cache holding k and v."""
+        H * hd elements); cache_kt: [H, hd, C], or the key rows [H, C, hd] with
+        ``krow`` (hd a power of two); cache_v: [H, C, hd]; pos: i32 scalar,
+        clamped to [0, C].  All float operands share one dtype; the output
+        [H, hd] has it too.  Equals the decomposed dot -> (mask beyond pos) ->
+        softmax -> dot chain with pos's column of the cache holding k and v.
+        ``masked``: that chain as a decoder writes it after storing k and v at
+        pos: pos is clamped to [0, C - 1] like the store, and a negative pos
+        leaves no key, so the output is NaN."""
         if cache_kt.view or cache_v.view:
             raise GraphError("decode_attention: caches must be plain buffers")
         q, k, v = self.materialize(q), self.materialize(k), self.materialize(v)
         if len(cache_kt.shape) != 3 or len(cache_v.shape) != 3:
             raise GraphError("decode_attention: caches are [H, hd, C] and [H, C, hd]")
-        H, hd, C = cache_kt.shape
+        if krow:
+            H, C, hd = cache_kt.shape
+        else:
+            H, hd, C = cache_kt.shape
         if cache_v.shape != (H, C, hd):
             raise GraphError(f"decode_attention: V cache {cache_v.shape} != {(H, C, hd)}")
         for name, t in (("q", q), ("k", k), ("v", v)):
@@ -503,8 +510,11 @@ class Graph:
             raise GraphError("decode_attention: pos is an i32 scalar")
         if hd % 8 or hd > 256 or C % 8 or C > 0xFFFF:
             raise GraphError("decode_attention: hd and C must be multiples of 8 (hd <= 256)")
+        if krow and hd & (hd - 1):
+            raise GraphError("decode_attention: key rows need a power-of-two hd")
         dst = self._new((H, hd), q.dtype)
-        desc = self.add_aux([hd, k.buf, v.buf, pos.buf, V.f32_bits(scale)])
+        desc = self.add_aux([hd | int(krow) << 16 | int(masked) << 17, k.buf, v.buf, pos.buf,
+                             V.f32_bits(scale)])
         self.emit(V.Instr(V.OP_DECODE_ATTN, dst=dst.buf, a=q.buf, b=cache_kt.buf, n=H,
                           imm=C, aux=desc, imm2=cache_v.buf,
                           reads_hint=(cache_v.buf, k.buf, v.buf, pos.buf)))

@@ -98,6 +98,7 @@ class Lowerer:
         self.cval: dict = {}         # Value -> numpy value of a constant
         self.sbcast: dict = {}       # Value -> float: broadcast of an f32 scalar constant
         self.depth = 0
+        self.inplace: set = set()    # dynamic_update_slice ops that write their loop carry
 
     # ---- values ---------------------------------------------------------------------------
     def t(self, v: M.Value) -> G.Tensor:
@@ -340,6 +341,12 @@ class Lowerer:
         x = self.g.materialize(self.t(op.operands[0]))
         upd = self.t(op.operands[1])
         starts = [self.g.materialize(self.t(v)) for v in op.operands[2:]]
+        if op in self.inplace:
+            # the update of a loop carry whose old value nothing else reads
+            # (Lowerer.inplace_updates): written into the carry itself
+            self.g.dynamic_update_slice(x, upd, starts)
+            self.bind(op.results[0], x)
+            return
         # out-of-place: an identity gather copies the operand, then the update is
         # scattered into the copy (in place when a loop carry allows it)
         out = self.g.gather(x, x.shape, _rm_strides(x.shape), 0)
@@ -536,6 +543,7 @@ class Lowerer:
         g.begin()
         for a, c in zip(body.args, carries):
             self.env[a] = c
+        self.inplace |= inplace_updates(body)
         rets = [g.materialize(self.t(v)) for v in self.block(body.ops)]
         self.commit_carries(carries, rets)
         body_list = g.end()
@@ -549,50 +557,57 @@ class Lowerer:
     def commit_carries(self, carries, rets):
         """Write a body's results into its carries (lowering.py:1055-1180): in
         place when the result's only producer is an elementwise op or a
-        dynamic_update_slice of that very carry and nothing else in the body
-        reads the carry; otherwise through temporaries in two steps, so that a
-        swap or a passthrough never reads a carry already overwritten."""
+        dynamic_update_slice of that very carry, no other body instruction reads
+        the carry after that producer and no other result is the carry itself;
+        otherwise by a copy, through a temporary when another result reads the
+        carry (a swap or a passthrough must not see it overwritten)."""
         g = self.g
         body = g._stack[-1]
-        writers, reads = {}, {}
+        writers, readers = {}, {}
         for i, ins in enumerate(body):
             writers.setdefault(ins.dst, []).append(i)
             for b in _reads(ins, g):
                 if b == ins.dst and ins.op in (V.OP_DYNAMIC_UPDATE_SLICE, V.OP_SCATTER):
                     continue        # a partial write keeps the rest of its own dst
-                reads[b] = reads.get(b, 0) + 1
+                readers.setdefault(b, []).append(i)
         nested = any(ins.op in V.REGION_OPS for ins in body)
         carry_bufs = {c.buf for c in carries}
+        ret_bufs = [x.buf for x in rets]
         done = [False] * len(carries)
         for k, (c, r) in enumerate(zip(carries, rets)):
             if nested or r.buf == c.buf:
                 done[k] = r.buf == c.buf
                 continue
             w = writers.get(r.buf, [])
-            if r.buf in carry_bufs or reads.get(r.buf, 0) or [x.buf for x in rets].count(r.buf) != 1:
+            if r.buf in carry_bufs or readers.get(r.buf) or ret_bufs.count(r.buf) != 1 or c.buf in ret_bufs:
                 continue
             if len(w) == 1 and body[w[0]].op in INPLACE_SAFE:
-                prod = body[w[0]]
-                others = reads.get(c.buf, 0) - (1 if c.buf in _reads(prod, g) else 0)
-                if others == 0 and r.n == c.n:
-                    prod.dst = c.buf
+                # an elementwise producer may read the carry itself (same index)
+                if r.n == c.n and all(i < w[0] for i in readers.get(c.buf, []) if i != w[0]) \
+                        and c.buf not in writers:
+                    body[w[0]].dst = c.buf
                     done[k] = True
             elif len(w) == 2:
                 cp, dus = body[w[0]], body[w[1]]
                 if (cp.op == V.OP_GATHER_STRIDED and dus.op == V.OP_DYNAMIC_UPDATE_SLICE and cp.a == c.buf
-                        and _identity_gather(g.aux, cp.aux, c.n) and reads.get(c.buf, 0) == 1
+                        and _identity_gather(g.aux, cp.aux, c.n) and readers.get(c.buf) == [w[0]]
                         and c.buf not in writers):
                     cp.op = V.OP_NOP
                     cp.dst = cp.a = 0
                     dus.dst = c.buf
                     done[k] = True
-        temps = {}
+        # copies: first into the carries that no pending result reads, then into
+        # the others; a result that is itself such a carry goes through a
+        # temporary taken before any copy (a swap)
+        pending = {r.buf for k, r in enumerate(rets) if not done[k]}
+        late = {k for k, c in enumerate(carries) if not done[k] and c.buf in pending}
+        late_bufs = {carries[k].buf for k in late}
+        temps = {k: self._copy(rets[k]) for k in late if rets[k].buf in late_bufs}
         for k, (c, r) in enumerate(zip(carries, rets)):
-            if not done[k]:
-                temps[k] = self._copy(r)
-        for k, c in enumerate(carries):
-            if not done[k]:
-                g.copy_into(c, temps[k])
+            if not done[k] and k not in late:
+                g.copy_into(c, r)
+        for k in sorted(late):
+            g.copy_into(carries[k], temps.get(k, rets[k]))
 
     def unroll(self, op, trip, k, init, step):
         """Inline a counted loop's body ``trip`` times (lowering.py:893-934): the
@@ -653,6 +668,37 @@ class Lowerer:
             g.emit(ins)
         for r, o in zip(op.results, outs):
             self.bind(r, o)
+
+
+def inplace_updates(body: M.Block) -> set:
+    """The dynamic_update_slice ops of a loop body that can write their loop
+    carry in place (lowering.py:1055-1180 commits DUS carries in place the same
+    way): the op updates block argument k, its result is what the body returns
+    at position k, and nothing else in the body (nested regions included) uses
+    argument k, so the carry's old value is dead once the update has run.  Other
+    readers of the result then read the carry."""
+    uses: dict = {}
+
+    def walk(ops):
+        for o in ops:
+            for v in o.operands:
+                uses[v] = uses.get(v, 0) + 1
+            for region in o.regions:
+                for blk in region:
+                    walk(blk.ops)
+    walk(body.ops)
+    if not body.ops or body.ops[-1].name != "stablehlo.return":
+        return set()
+    producer = {r: o for o in body.ops for r in o.results}
+    rets = body.ops[-1].operands
+    out = set()
+    for k, (arg, v) in enumerate(zip(body.args, rets)):
+        o = producer.get(v)
+        if o is None or o.name != "stablehlo.dynamic_update_slice" or o.operands[0] is not arg:
+            continue
+        if uses.get(arg, 0) == 1 and sum(r is v for r in rets) == 1:
+            out.add(o)
+    return out
 
 
 INPLACE_SAFE = frozenset({

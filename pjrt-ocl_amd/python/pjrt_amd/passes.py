@@ -537,9 +537,9 @@ def fuse_norm_epilogue(prog: V.VMProgram) -> None:
             new = None
             if not flags & (V.LN_AFFINE | V.LN_GELU) and C.op == V.OP_MUL_F32 and C.n == total:
                 vec = None
-                if C.a == cur and not C.imm and C.imm2 and _is_row_broadcast(prog, C.imm2, seg):
+                if C.a == cur and not C.imm and _row_vector(prog, C.imm2, seg, total):
                     vec = C.b
-                elif C.b == cur and not C.imm2 and C.imm and _is_row_broadcast(prog, C.imm, seg):
+                elif C.b == cur and not C.imm2 and _row_vector(prog, C.imm, seg, total):
                     vec = C.a
                 if vec is not None and _dt(prog, vec) == V.DT_F32 and _elems(prog, vec) == seg:
                     # + beta must follow
@@ -549,9 +549,9 @@ def fuse_norm_epilogue(prog: V.VMProgram) -> None:
                         A = instrs[k]
                         bvec = None
                         if A.op == V.OP_ADD_F32 and A.n == total:
-                            if A.a == C.dst and not A.imm and A.imm2 and _is_row_broadcast(prog, A.imm2, seg):
+                            if A.a == C.dst and not A.imm and _row_vector(prog, A.imm2, seg, total):
                                 bvec = A.b
-                            elif A.b == C.dst and not A.imm2 and A.imm and _is_row_broadcast(prog, A.imm, seg):
+                            elif A.b == C.dst and not A.imm2 and _row_vector(prog, A.imm, seg, total):
                                 bvec = A.a
                         if bvec is not None and _dt(prog, bvec) == V.DT_F32 and _elems(prog, bvec) == seg \
                                 and _written_before(ix, bvec, li) and _written_before(ix, vec, li):
@@ -575,6 +575,14 @@ def fuse_norm_epilogue(prog: V.VMProgram) -> None:
                 instrs[x] = V.Instr(V.OP_NOP)
             changed = True
             break
+
+
+def _row_vector(prog, view1: int, seg: int, total: int) -> bool:
+    """An elementwise operand that reads a [seg] vector once per row: a
+    row-broadcast view, or the plain vector when there is one row."""
+    if view1:
+        return _is_row_broadcast(prog, view1, seg)
+    return total == seg
 
 
 def _written_before(ix, buf, idx) -> bool:
@@ -1002,15 +1010,334 @@ def fuse_attention(prog: V.VMProgram) -> None:
             if kv and _merged(*_view_desc(prog, kv)) == _merged(kt[1:4], kt[4:7], 0):
                 kv = len(prog.aux) + 1            # the plain transpose of a [G, C, hd] K
                 prog.aux.extend(kt)
+            last = tail[-1] if tail else d2i
+            free = sorted(consumed + [dot1, si] + mid + ([d2i] if tail else []))
+            qa, kb, vb = D1.a, D1.b, D2.b
+            placed = []
+            if adt in (V.DT_BF16, V.DT_F16) and hd in (64, 128) and scale > 0 and \
+                    (qv or vv or not (kv and prog.aux[kv - 1:kv + 7] == kt)):
+                # the matrix-core kernel reads Q and V as plain [G, rows, hd]
+                # and K as the transpose of a plain [G, C, hd]: strided operands
+                # (the heads of a fused QKV projection) are gathered into that
+                # layout first, in slots the fused chain frees
+                plan = _attn_gathers(prog, qa, kb, vb, qv, kv, vv, G1, M1, C, hd, adt, kt)
+                placed = _place_gathers(ix, sc, si, free, last, plan)
+                if placed is not None:
+                    for slot, ins in placed:
+                        free.remove(slot)
+                    qa, kb, vb, qv, kv, vv = plan[-1]
+                else:
+                    placed = []
             desc = len(prog.aux)
             prog.aux.extend([G1, M1, C, hd, _bits(scale), causal, qv, kv, vv])
-            last = tail[-1] if tail else d2i
-            for j in consumed + [dot1, si] + mid + ([d2i] if tail else []):
+            for j in free:
                 instrs[j] = V.Instr(V.OP_NOP)
-            instrs[last] = V.Instr(V.OP_FLASH_ATTN, dst=out, a=D1.a, b=D1.b, n=G1, imm=M1, imm2=D2.b,
-                                   aux=desc, reads_hint=(D2.b,))
+            for slot, ins in placed:
+                instrs[slot] = ins
+            instrs[last] = V.Instr(V.OP_FLASH_ATTN, dst=out, a=qa, b=kb, n=G1, imm=M1, imm2=vb,
+                                   aux=desc, reads_hint=(vb,))
             changed = True
             break
+
+
+def _attn_gathers(prog, qa, kb, vb, qv, kv, vv, G, M, C, hd, adt, kt):
+    """Gathers that put attention operands in the matrix-core layout: a list of
+    (source buffer, gather instruction) and, last, the new (q, k, v buffers,
+    q, k, v views); None when K's view is not one over [G, hd, C]."""
+    plan = []
+    if not (kv and prog.aux[kv - 1:kv + 7] == kt):
+        # B reads K^T [G, hd, C]: gather K [G, C, hd] with the last two axes swapped
+        if kv:
+            dims, st, off = _view_desc(prog, kv)
+            if list(dims) == [hd, C] and G == 1:
+                dims, st = [1, hd, C], [0] + list(st)
+            if list(dims) != [G, hd, C]:
+                return None
+        else:
+            st, off = [hd * C, C, 1], 0
+        k = _new_buffer(prog, G * C * hd, adt)
+        d = len(prog.aux)
+        prog.aux.extend([3, G, C, hd, st[0], st[2], st[1], off])
+        plan.append((kb, V.Instr(V.OP_GATHER_STRIDED, dst=k, a=kb, n=G * C * hd, aux=d)))
+        kb = k
+        kv = len(prog.aux) + 1
+        prog.aux.extend(kt)
+    if qv:
+        q = _new_buffer(prog, G * M * hd, adt)
+        plan.append((qa, V.Instr(V.OP_GATHER_STRIDED, dst=q, a=qa, n=G * M * hd, aux=qv - 1)))
+        qa, qv = q, 0
+    if vv:
+        v = _new_buffer(prog, G * C * hd, adt)
+        plan.append((vb, V.Instr(V.OP_GATHER_STRIDED, dst=v, a=vb, n=G * C * hd, aux=vv - 1)))
+        vb, vv = v, 0
+    plan.append((qa, kb, vb, qv, kv, vv))
+    return plan
+
+
+def _place_gathers(ix, sc, si, free, last, plan):
+    """(slot, instruction) for each gather of ``plan``: a freed slot after the
+    last write of its source in the chain's scope, before ``last``; None if
+    some gather finds none."""
+    if plan is None:
+        return None
+    taken, out = set(), []
+    for src, ins in plan[:-1]:
+        after = max([w for w in ix.writers.get(src, ()) if sc[w] == sc[si] and w < last], default=-1)
+        slot = next((j for j in free if j > after and j not in taken and j < last), None)
+        if slot is None:
+            return None
+        taken.add(slot)
+        out.append((slot, ins))
+    return out
+
+
+# ---- fuse_decode_attention (extension: no reference counterpart) ------------------------------
+
+def fuse_decode_attention(prog: V.VMProgram) -> None:
+    """The decode step a JAX decoder with a KV cache writes per layer
+
+        K' = dynamic_update_slice(K, k, pos)     V' = dynamic_update_slice(V, v, pos)
+        s = dot(q, K'^T) [* scale];  s = select(key <= pos, s, -inf)
+        o = dot(softmax(s) [-> convert], V') [-> convert]
+
+    => OP_DECODE_ATTN (masked; krow when the cache holds key rows [H, C, hd]):
+    one pass over the two caches instead of five barrier-separated ops.  The
+    reference lowers this chain op by op (python/pjrt_ocl/lowering.py:2664-2690
+    fuses only the constant-mask prefill form; tools/bench_decode.py:44-52 is
+    the unmasked append form).  The mask is proven by evaluating its predicate
+    for every position in [-2, C + 2]; the updates' position must be the same
+    buffer.  The updates stay: the op reads the caches after them."""
+    if _off("PJRT_OCL_DECODE_ATTN"):
+        return
+    outs = set(prog.outputs)
+    sc = scopes(prog)
+    consts = _const_values(prog)
+    changed = True
+    while changed:
+        changed = False
+        ix = _Index(prog)
+        instrs = prog.instrs
+        for si, SM in enumerate(instrs):
+            if SM.op != V.OP_SOFTMAX:
+                continue
+            m = _match_decode(prog, ix, sc, consts, outs, si)
+            if m is None:
+                continue
+            (q, kbuf, vbuf, kc, vc, posb, H, C, hd, krow, scale, out, chain, last, qgather, dk, dv) = m
+            desc = len(prog.aux)
+            prog.aux.extend([hd | int(krow) << 16 | 1 << 17, kbuf, vbuf, posb, _bits(scale)])
+            fused = V.Instr(V.OP_DECODE_ATTN, dst=out, a=q, b=kc, n=H, imm=C, imm2=vc, aux=desc,
+                            reads_hint=(vc, kbuf, vbuf, posb))
+            # the op reads cache columns before pos only, which the updates do
+            # not touch: it can run before them, so that they share a phase with
+            # what follows instead of delaying the attention by one.  Only when
+            # nothing else reads the caches in between.
+            seq = ([qgather] if qgather is not None else []) + [fused]
+            slots = sorted(set(chain) | {last})
+            others = [j for b in (kc, vc) for j in ix.live_readers(b)
+                      if min(dk, dv) < j <= last and j not in chain and j not in (dk, dv)]
+            if not others:
+                seq += [instrs[dk], instrs[dv]] if dk < dv else [instrs[dv], instrs[dk]]
+                slots = sorted(set(slots) | {dk, dv})
+            for j in slots:
+                instrs[j] = V.Instr(V.OP_NOP)
+            for j, ins in zip(slots, seq):
+                instrs[j] = ins
+            changed = True
+            break
+
+
+def _match_decode(prog, ix, sc, consts, outs, si):
+    """The pieces of one masked decode attention around softmax ``si``, or None."""
+    instrs = prog.instrs
+    SM = instrs[si]
+    C, rows = SM.imm, SM.n
+    consumed, scale, sel, dot1 = [], 1.0, None, None
+    cur = SM.a
+    for _ in range(6):
+        if cur in outs or len(ix.live_readers(cur)) != 1:
+            return None
+        w = ix.unique_writer(cur)
+        if w is None or sc[w] != sc[si]:
+            return None
+        P = instrs[w]
+        if P.op == V.OP_DOT:
+            dot1 = w
+            break
+        if P.op == V.OP_AFFINE_F32 and not P.imm2 and P.n == rows * C:
+            scale *= _f(P.imm)
+        elif P.op in (V.OP_MUL_F32, V.OP_DIV_F32) and not P.imm and P.imm2 and P.n == rows * C and \
+                _is_splat(prog, P.imm2) and P.b in consts and consts[P.b] not in (0.0,):
+            scale = scale * consts[P.b] if P.op == V.OP_MUL_F32 else scale / consts[P.b]
+        elif P.op == V.OP_SELECT_F32 and sel is None and P.n == rows * C:
+            neg = _eval_const(prog, ix, _peel_broadcast(prog, ix, P.b))
+            if neg is None or neg.size != 1 or not (float(neg[0]) == -math.inf or float(neg[0]) <= -1e30):
+                return None
+            sel = w
+        elif P.op == V.OP_GATHER_STRIDED and _is_identity_view(prog, P.aux + 1, P.n):
+            pass
+        else:
+            return None
+        consumed.append(w)
+        cur = P.a
+    if dot1 is None or sel is None:
+        return None
+    D1 = instrs[dot1]
+    M1, N1, hd, G1, av1, bv1, epi1, _ = _dot_fields_pass(D1)
+    if M1 != 1 or N1 != C or G1 != rows or len(ix.live_readers(D1.dst)) != 1 or D1.dst in outs:
+        return None
+    if epi1:
+        e = epi1 - 1
+        if prog.aux[e] != 1 or prog.aux[e + 1] != V.SUB_AFFINE or prog.aux[e + 2] != 0 or \
+                _f(prog.aux[e + 4]) != 0.0:
+            return None
+        scale *= _f(prog.aux[e + 3])
+    H = G1
+    # forward: softmax [-> convert] -> DOT2 [-> convert]
+    fwd = ix.live_readers(SM.dst)
+    if SM.dst in outs or len(fwd) != 1:
+        return None
+    p_buf, d2i, mid = SM.dst, fwd[0], []
+    if instrs[d2i].op == V.OP_CONVERT:
+        cv = instrs[d2i]
+        nxt = ix.live_readers(cv.dst)
+        if cv.dst in outs or len(nxt) != 1:
+            return None
+        mid.append(d2i)
+        p_buf, d2i = cv.dst, nxt[0]
+    D2 = instrs[d2i]
+    if D2.op != V.OP_DOT or D2.a != p_buf:
+        return None
+    M2, N2, K2, G2, av2, bv2, epi2, _ = _dot_fields_pass(D2)
+    if av2 or epi2 or G2 != H or M2 != 1 or K2 != C or N2 != hd:
+        return None
+    out, tail = D2.dst, []
+    rs = ix.live_readers(out)
+    if len(rs) == 1 and out not in outs and instrs[rs[0]].op == V.OP_CONVERT and \
+            instrs[rs[0]].a == out and sc[rs[0]] == sc[si]:
+        tail = [rs[0]]
+        out = instrs[rs[0]].dst
+    adt = _dt(prog, D1.a)
+    if adt not in (V.DT_F32, V.DT_F16, V.DT_BF16) or _dt(prog, D1.b) != adt or _dt(prog, D2.b) != adt \
+            or _dt(prog, out) != adt or _elems(prog, out) != H * hd:
+        return None
+    if hd % 8 or hd > 256 or C % 8 or C > 0xFFFF:
+        return None
+    if len({sc[x] for x in [dot1, si, d2i] + consumed + mid + tail}) != 1:
+        return None
+    last = tail[-1] if tail else d2i
+    # the caches: K as rows [H, C, hd] (dot1 reads its transpose) or as K^T
+    kc, vc = D1.b, D2.b
+    kview = _canonical_view(prog, bv1, H * hd * C)
+    if _elems(prog, kc) != H * C * hd or _elems(prog, vc) != H * C * hd or _canonical_view(prog, bv2, H * C * hd):
+        return None
+    if kview == 0:
+        krow, kshape = False, (H, hd, 1)
+    elif _merged(*_view_desc(prog, kview)) == _merged([H, hd, C], [C * hd, 1, hd], 0):
+        krow, kshape = True, (H, 1, hd)
+    else:
+        return None
+    if krow and hd & (hd - 1):
+        return None
+    # the updates that wrote pos's column just before: same position buffer
+    dk = _last_writer(ix, kc, dot1, sc)
+    dv = _last_writer(ix, vc, d2i, sc)
+    if dk is None or dv is None:
+        return None
+    uk = _dus_fields(prog, instrs[dk])
+    uv = _dus_fields(prog, instrs[dv])
+    if uk is None or uv is None:
+        return None
+    kdims, kids, kbuf = uk
+    vdims, vids, vbuf = uv
+    if tuple(kdims) != kshape or tuple(vdims) != (H, 1, hd):
+        return None
+    posb = kids[1] if krow else kids[2]
+    if vids[1] != posb or prog.buffers[posb].dtype != V.DT_I32 or _elems(prog, posb) != 1:
+        return None
+    if _elems(prog, kbuf) != H * hd or _elems(prog, vbuf) != H * hd or _dt(prog, kbuf) != adt or \
+            _dt(prog, vbuf) != adt:
+        return None
+    # nothing rewrites what the fused op reads between its sources and ``last``
+    # (no region op in between either: its sub-list could)
+    if any(instrs[j].op in _REGION_OPS for j in range(min(dk, dv, dot1), last) if sc[j] == sc[si]):
+        return None
+    for buf, since in ((kc, dk), (vc, dv), (kbuf, dk), (vbuf, dv), (posb, dk), (posb, dv), (D1.a, dot1)):
+        if any(since < w <= last for w in ix.writers.get(buf, ())):
+            return None
+    if not _mask_is_key_le_pos(prog, ix, instrs[sel].imm, posb, C):
+        return None
+    # q: the dot's A rows [H, 1, hd], contiguous
+    qv = _canonical_view(prog, av1, H * hd)
+    q, qgather = D1.a, None
+    if qv or _elems(prog, D1.a) != H * hd:
+        dims, st, off = _view_desc(prog, qv) if qv else ([H * hd], [1], 0)
+        if _merged(dims, st, off) != (((H * hd, 1),), off) and _merged(dims, st, off) != ((), off):
+            return None
+        q = _new_buffer(prog, H * hd, adt)
+        vdesc = len(prog.aux)
+        prog.aux.extend([1, H * hd, 1, off])
+        qgather = V.Instr(V.OP_GATHER_STRIDED, dst=q, a=D1.a, n=H * hd, aux=vdesc)
+    chain = consumed + [dot1, si, d2i] + mid + tail
+    return (q, kbuf, vbuf, kc, vc, posb, H, C, hd, krow, scale, out, chain, last, qgather, dk, dv)
+
+
+def _dot_fields_pass(ins):
+    """(M, N, K, G, aview, bview, epi, epi_res) of an in-memory OP_DOT."""
+    return (ins.n, ins.imm >> 16, ins.imm & 0xFFFF, max(1, ins.imm2), ins.aview, ins.bview, ins.epi,
+            ins.epi_res)
+
+
+def _last_writer(ix, buf, before, sc):
+    """The last instruction before ``before`` in the same scope that writes
+    ``buf``, if it is a dynamic_update_slice; None otherwise."""
+    ws = [w for w in ix.writers.get(buf, ()) if w < before and sc[w] == sc[before]]
+    if not ws:
+        return None
+    w = max(ws)
+    if ix.prog.instrs[w].op != V.OP_DYNAMIC_UPDATE_SLICE or ix.prog.instrs[w].dst != buf:
+        return None
+    return w
+
+
+def _dus_fields(prog, ins):
+    """(update dims, start buffers, update buffer) of a dynamic_update_slice
+    (aux: rank, update dims, strides, clamps, zeros, start buffers, is64)."""
+    a = ins.aux
+    rank = prog.aux[a]
+    if rank != 3 or prog.aux[a + 1 + 5 * rank]:
+        return None
+    dims = prog.aux[a + 1:a + 1 + rank]
+    ids = prog.aux[a + 1 + 4 * rank:a + 1 + 5 * rank]
+    return dims, ids, ins.a
+
+
+def _mask_is_key_le_pos(prog, ix, pred, posb, C) -> bool:
+    """The select predicate is key <= pos on every row, for every pos in
+    [-2, C + 2] and 3 C (all keys for pos >= C - 1, none for pos < 0)."""
+    pred = _peel_broadcast(prog, ix, pred)
+    keys = np.arange(C)
+    for v in list(range(-2, C + 3)) + [3 * C]:
+        m = _eval_const(prog, ix, pred, env={posb: np.array([v], np.int64)})
+        if m is None or m.size % C:
+            return False
+        if not np.array_equal(m.reshape(-1, C) != 0, np.broadcast_to(keys <= v, (m.size // C, C))):
+            return False
+    return True
+
+
+def _new_buffer(prog, n, dt) -> int:
+    """A fresh buffer of n elements at the arena's end (reuse_arena packs it)."""
+    size = n * V.DT_SIZE[dt]
+    off = -(-prog.arena_bytes // V.ARENA_ALIGN) * V.ARENA_ALIGN
+    prog.buffers.append(V.Buffer(off, size, dt))
+    prog.arena_bytes = off + max(-(-size // V.ARENA_ALIGN) * V.ARENA_ALIGN, V.ARENA_ALIGN)
+    if hasattr(prog, "_overlap_groups"):
+        try:
+            del prog._overlap_groups
+        except AttributeError:
+            pass
+    return len(prog.buffers) - 1
 
 
 def _merged(dims, st, off=None):
@@ -1062,11 +1389,14 @@ def _peel_broadcast(prog, ix, buf):
     return buf
 
 
-def _eval_const(prog, ix, buf, depth=0):
+def _eval_const(prog, ix, buf, depth=0, env=None):
     """Value of a buffer computed only from iotas, fills and constants (the
-    predicate of an attention mask), evaluated on the host; None otherwise."""
+    predicate of an attention mask), evaluated on the host; None otherwise.
+    ``env`` gives values for runtime buffers (a decode position)."""
     if depth > 12:
         return None
+    if env and buf in env:
+        return np.asarray(env[buf]).reshape(-1)
     for b, data in prog.consts:
         if b == buf:
             return np.frombuffer(bytes(data), V.DT_NUMPY[_dt(prog, b)]).copy()
@@ -1085,7 +1415,7 @@ def _eval_const(prog, ix, buf, depth=0):
         v = _f(ins.imm) if dt in (V.DT_F32, V.DT_F16, V.DT_BF16, V.DT_F64) else _i32(ins.imm)
         return np.full(n, v)
     if ins.op == V.OP_GATHER_STRIDED:
-        src = _eval_const(prog, ix, ins.a, depth + 1)
+        src = _eval_const(prog, ix, ins.a, depth + 1, env)
         if src is None:
             return None
         dims, st, off = _view_desc(prog, ins.aux + 1)
@@ -1100,8 +1430,8 @@ def _eval_const(prog, ix, buf, depth=0):
     if ins.op in (V.OP_CMP_F32, V.OP_ADD_F32, V.OP_SUB_F32, V.OP_AND, V.OP_OR):
         if ins.op in (V.OP_ADD_F32, V.OP_SUB_F32) and (ins.imm or ins.imm2):
             return None
-        a = _eval_const(prog, ix, ins.a, depth + 1)
-        b = _eval_const(prog, ix, ins.b, depth + 1)
+        a = _eval_const(prog, ix, ins.a, depth + 1, env)
+        b = _eval_const(prog, ix, ins.b, depth + 1, env)
         if a is None or b is None:
             return None
         if ins.op == V.OP_CMP_F32:
@@ -1110,7 +1440,7 @@ def _eval_const(prog, ix, buf, depth=0):
         return {V.OP_ADD_F32: np.add, V.OP_SUB_F32: np.subtract, V.OP_AND: np.logical_and,
                 V.OP_OR: np.logical_or}[ins.op](a, b)
     if ins.op in (V.OP_CONVERT, V.OP_COPY_F32):
-        return _eval_const(prog, ix, ins.a, depth + 1)
+        return _eval_const(prog, ix, ins.a, depth + 1, env)
     return None
 
 
@@ -1123,6 +1453,53 @@ def finalize_matmul_views(prog: V.VMProgram) -> None:
             prog.aux.extend([ins.aview, ins.bview, ins.epi, ins.epi_res])
 
 
+# ---- alias_slices (extension) -------------------------------------------------------------------
+
+def alias_slices(prog: V.VMProgram) -> None:
+    """A gather that copies one contiguous, 16-byte aligned run of its source
+    (a row slice such as q, k, v out of a decode step's fused projection)
+    becomes a buffer of its own on the source's bytes, and the copy goes: its
+    readers read the source in place.  The source must be written by exactly one
+    instruction (or be a constant) and not be a program input or output (those
+    are bound to caller memory, not the arena); the slice must be written only
+    by the gather and not be an output.  The scheduler orders accesses to
+    overlapping buffers as accesses to one (scheduler.overlap_groups), and
+    reuse_arena moves them together.  The reference keeps such slices as
+    strided views that each consumer re-reads (lowering.py:1481-1545)."""
+    if _off("PJRT_OCL_ALIAS_SLICES"):
+        return
+    ports = set(prog.inputs) | set(prog.outputs)
+    const_bufs = {b for b, _ in prog.consts}
+    ix = _Index(prog)
+    changed = False
+    for gi, g in enumerate(prog.instrs):
+        if g.op != V.OP_GATHER_STRIDED or g.dst in ports or g.a in ports or g.a == g.dst:
+            continue
+        if ix.writers.get(g.dst, []) != [gi]:
+            continue
+        if g.a not in const_bufs and len(ix.writers.get(g.a, ())) != 1:
+            continue
+        if g.a in const_bufs and ix.writers.get(g.a):
+            continue
+        dims, st, off = _view_desc(prog, g.aux + 1)
+        n = int(np.prod(dims)) if dims else 1
+        runs, _ = _merged(dims, st, off)
+        if n != g.n or not (runs == () or runs == ((n, 1),)):
+            continue
+        src, dst = prog.buffers[g.a], prog.buffers[g.dst]
+        esz = V.DT_SIZE[src.dtype]
+        if dst.dtype != src.dtype or off < 0 or (off + n) * esz > src.size_bytes or (off * esz) % 16:
+            continue
+        dst.arena_byte_offset = src.arena_byte_offset + off * esz
+        prog.instrs[gi] = V.Instr(V.OP_NOP)
+        changed = True
+    if changed and hasattr(prog, "_overlap_groups"):
+        try:
+            del prog._overlap_groups
+        except AttributeError:
+            pass
+
+
 # ---- reuse_arena (lowering.py:2813-2973) ------------------------------------------------------
 
 def reuse_arena(prog: V.VMProgram, cfg=None) -> None:
@@ -1131,7 +1508,10 @@ def reuse_arena(prog: V.VMProgram, cfg=None) -> None:
     first write of the other.  Inputs, outputs and constants live the whole
     program; everything a loop or branch touches lives for the region's whole
     phase; buffers that alias (a slice kept as a buffer of its own) move with
-    their parent."""
+    their parent.  The phases run instructions as soon as their dependencies
+    allow, not in program order, so the lifetimes must also be disjoint in
+    program order: the program stays correct when run one instruction after
+    another (the tensor-level semantics the oracle executes)."""
     from . import scheduler as S
     if _off("PJRT_OCL_ARENA_REUSE"):
         return
@@ -1151,6 +1531,7 @@ def reuse_arena(prog: V.VMProgram, cfg=None) -> None:
         else:
             phase[payload] = ph
             region_roots.append((payload, ph))
+    order = {i: i for i in range(prog.main_len)}       # program-order position
     for r, ph in region_roots:
         stack = [r]
         while stack:
@@ -1163,6 +1544,7 @@ def reuse_arena(prog: V.VMProgram, cfg=None) -> None:
             for lo_, hi_ in ranges:
                 for j in range(lo_, hi_):
                     phase[j] = ph
+                    order[j] = r
                     stack.append(j)
     # layernorms staged inside a GEMV run in the GEMV's phase
     for dot_i, ln_i in sched.ln_pro.items():
@@ -1171,26 +1553,32 @@ def reuse_arena(prog: V.VMProgram, cfg=None) -> None:
     n_ph = len(levels)
     lo = [n_ph + 1] * nb
     hi = [-1] * nb
+    lo2 = [prog.main_len + 1] * nb
+    hi2 = [-1] * nb
 
-    def touch(b, t):
+    def touch(b, t, t2):
         if 0 <= b < nb:
             lo[b] = min(lo[b], t)
             hi[b] = max(hi[b], t)
+            lo2[b] = min(lo2[b], t2)
+            hi2[b] = max(hi2[b], t2)
     for i, ins in enumerate(prog.instrs):
         if ins.op == V.OP_NOP or i not in phase:
             continue
-        t = phase[i]
         for b in reads_of(ins, prog) | writes_of(ins):
-            touch(b, t)
-    end = n_ph
+            touch(b, phase[i], order[i])
+    end, end2 = n_ph, prog.main_len
     for b in set(prog.inputs):
-        lo[b] = 0
+        lo[b] = lo2[b] = 0
         hi[b] = max(hi[b], 0)
+        hi2[b] = max(hi2[b], 0)
     for b in set(prog.outputs):
         lo[b] = min(lo[b], 0)
-        hi[b] = end
+        lo2[b] = min(lo2[b], 0)
+        hi[b], hi2[b] = end, end2
     for b, _ in prog.consts:
         lo[b], hi[b] = 0, end
+        lo2[b], hi2[b] = 0, end2
     # alias groups (arena-overlapping buffers of the bump layout) move as one;
     # the scheduler keeps ordering by them, not by the packed overlaps
     group = list(S.overlap_groups(prog))
@@ -1204,7 +1592,7 @@ def reuse_arena(prog: V.VMProgram, cfg=None) -> None:
         top = max(bufs[m].arena_byte_offset + bufs[m].size_bytes for m in mem)
         l = min(lo[m] for m in mem)
         h = max(hi[m] for m in mem)
-        units.append((root, mem, base, top - base, l, h))
+        units.append((root, mem, base, top - base, l, h, min(lo2[m] for m in mem), max(hi2[m] for m in mem)))
 
     def aligned(x):
         return -(-x // V.ARENA_ALIGN) * V.ARENA_ALIGN
@@ -1213,21 +1601,22 @@ def reuse_arena(prog: V.VMProgram, cfg=None) -> None:
     placed = []
     arena_end = 0
     new_off = {}
-    for root, mem, base, size, l, h in live_units:
+    for root, mem, base, size, l, h, l2, h2 in live_units:
         size_a = max(aligned(size), V.ARENA_ALIGN)
-        conflicts = sorted((o, e) for (pl, ph_, o, e) in placed if not (h < pl or ph_ < l))
+        conflicts = sorted((o, e) for (pl, ph_, pl2, ph2, o, e) in placed
+                           if not (h < pl or ph_ < l) or not (h2 < pl2 or ph2 < l2))
         off = 0
         for c0, c1 in conflicts:
             if off + size_a <= c0:
                 break
             off = max(off, c1)
-        placed.append((l, h, off, off + size_a))
+        placed.append((l, h, l2, h2, off, off + size_a))
         arena_end = max(arena_end, off + size_a)
         for m in mem:
             new_off[m] = off + bufs[m].arena_byte_offset - base
     # buffers no instruction touches (intermediates a fusion replaced) keep no
     # arena bytes at all
-    for root, mem, base, size, l, h in units:
+    for root, mem, base, size, l, h, _, _ in units:
         if h < 0:
             for m in mem:
                 new_off[m] = 0
@@ -1260,6 +1649,9 @@ def run_all(prog: V.VMProgram) -> None:
     dce(prog)
     fuse_attention(prog)
     dce(prog)
+    fuse_decode_attention(prog)
+    dce(prog)
     fuse_region(prog)
     dce(prog)
     finalize_matmul_views(prog)
+    alias_slices(prog)

@@ -614,7 +614,7 @@ def task_cost(task: V.Task, cfg: DeviceConfig, prog: V.VMProgram) -> float:
     if top == V.TOP_DECODE_ATTN:
         # each tile streams its share of a head's two cache slices (~15 GB/s per CU)
         H, S = task.p4 & 0xFFFF, max(1, task.p4 >> 16)
-        return H * S * (2.0 * task.p5 * task.p6 * asz / S / 15e3 + 3.0)
+        return H * S * (2.0 * (task.p5 & 0xFFFF) * task.p6 * asz / S / 15e3 + 3.0)
     if top in (V.TOP_RED_SEG, V.TOP_SOFTMAX_SEG, V.TOP_LAYERNORM_SEG,
                V.TOP_ARGMAX_SEG):
         n = task.p0 * task.p1
@@ -650,7 +650,7 @@ def task_work(task: V.Task, prog: V.VMProgram) -> tuple:
         C = prog.aux[task.p3 + 2] if task.p3 + 2 < len(prog.aux) else T
         return 2 * H * C * hd * asz, 4.0 * H * T * C * hd
     if top == V.TOP_DECODE_ATTN:
-        return 2 * (task.p4 & 0xFFFF) * task.p5 * task.p6 * asz, 0.0
+        return 2 * (task.p4 & 0xFFFF) * (task.p5 & 0xFFFF) * task.p6 * asz, 0.0
     if top in (V.TOP_RED_SEG, V.TOP_SOFTMAX_SEG, V.TOP_LAYERNORM_SEG, V.TOP_ARGMAX_SEG):
         return task.p0 * task.p1 * (asz + (dsz if top != V.TOP_RED_SEG else 0)), 0.0
     n = max(task.p0, task.p1) if top != V.TOP_EW else task.p1
@@ -702,9 +702,10 @@ def viewed_reads(ins: V.Instr) -> set:
 
 
 def _phases(prog, indices, tasks_of, fuse, extra_reads=None):
-    """Split ``indices`` (program order) into barrier-separated phases. A new
-    phase starts when an instruction has a cross-lane dependency on a member
-    of the current phase (RAW, WAW or WAR through a shared buffer).
+    """Split ``indices`` (program order) into barrier-separated phases: an
+    instruction with a cross-lane dependency (RAW, WAW or WAR through a shared
+    buffer) on an earlier one runs in a later phase; a lane-local one (an
+    elementwise chain) may share its phase.
     ``extra_reads``: {index: buffers} read beyond the instruction's own operands
     (a GEMV staging a fused layernorm reads the layernorm's inputs)."""
     instrs = prog.instrs
@@ -713,7 +714,7 @@ def _phases(prog, indices, tasks_of, fuse, extra_reads=None):
     def reads(k):
         r = instr_reads(instrs[k], prog)
         return r | extra_reads[k] if k in extra_reads else r
-    phases, cur = [], []
+    phases = []
     readers: dict = {}
     writers: dict = {}
 
@@ -738,6 +739,12 @@ def _phases(prog, indices, tasks_of, fuse, extra_reads=None):
         grp = overlap_groups(prog)
         return bool(({grp[x] for x in viewed_reads(b)} & wa) or ({grp[x] for x in viewed_reads(a)} & wb))
 
+    # each instruction goes to the earliest phase its dependencies allow (as
+    # soon as possible, not merely after the phase in progress): an
+    # independent op written late, such as a bias added to a residual for the
+    # next matmul's epilogue, runs beside earlier work instead of opening a
+    # phase of its own
+    level: dict = {}
     for j in indices:
         ins = instrs[j]
         cand = set()
@@ -746,18 +753,17 @@ def _phases(prog, indices, tasks_of, fuse, extra_reads=None):
         for b in instr_writes(ins, prog):
             cand.update(writers.get(b, ()))
             cand.update(readers.get(b, ()))
-        if cur and any(cross(j, i) for i in cand):
-            phases.append(cur)
-            cur = []
-            readers.clear()
-            writers.clear()
-        cur.append(j)
+        lv = 0
+        for i in cand:
+            lv = max(lv, level[i] + 1 if cross(j, i) else level[i])
+        level[j] = lv
+        while len(phases) <= lv:
+            phases.append([])
+        phases[lv].append(j)
         for b in reads(j):
             readers.setdefault(b, []).append(j)
         for b in instr_writes(ins, prog):
             writers.setdefault(b, []).append(j)
-    if cur:
-        phases.append(cur)
     return phases
 
 

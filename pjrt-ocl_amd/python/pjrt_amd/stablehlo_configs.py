@@ -161,3 +161,335 @@ module @jit_f {{
   }}
 }}
 """
+
+
+# ---- config 5: the GPT decoder as a JAX program ---------------------------------------------
+
+class _Emit:
+    """SSA text builder for one function body."""
+
+    def __init__(self, indent="    "):
+        self.lines, self.n, self.ind = [], 0, indent
+
+    def new(self, text):
+        name = f"%v{self.n}"
+        self.n += 1
+        self.lines.append(f"{self.ind}{name} = {text}")
+        return name
+
+    def const(self, value, dt="f32"):
+        lit = f"{value:.9e}" if dt.startswith("f") or dt == "bf16" else str(int(value))
+        return self.new(f"stablehlo.constant dense<{lit}> : tensor<{dt}>")
+
+    def splat(self, value, shape, dt="f32"):
+        c = self.const(value, dt)
+        return self.new(f"stablehlo.broadcast_in_dim {c}, dims = [] : (tensor<{dt}>) -> {_t(shape, dt)}")
+
+    def bcast(self, v, src_shape, shape, dims, dt="f32"):
+        return self.new(f"stablehlo.broadcast_in_dim {v}, dims = [{', '.join(map(str, dims))}] : "
+                        f"({_t(src_shape, dt)}) -> {_t(shape, dt)}")
+
+    def bin(self, op, a, b, shape, dt="f32"):
+        return self.new(f"stablehlo.{op} {a}, {b} : {_t(shape, dt)}")
+
+    def un(self, op, a, shape, dt="f32"):
+        return self.new(f"stablehlo.{op} {a} : {_t(shape, dt)}")
+
+    def convert(self, a, shape, src, dst):
+        return self.new(f"stablehlo.convert {a} : ({_t(shape, src)}) -> {_t(shape, dst)}")
+
+    def reshape(self, a, src, dst, dt):
+        return self.new(f"stablehlo.reshape {a} : ({_t(src, dt)}) -> {_t(dst, dt)}")
+
+    def transpose(self, a, src, perm, dt):
+        dst = tuple(src[p] for p in perm)
+        return self.new(f"stablehlo.transpose {a}, dims = [{', '.join(map(str, perm))}] : "
+                        f"({_t(src, dt)}) -> {_t(dst, dt)}")
+
+    def slice(self, a, src, starts, limits, dt):
+        dst = tuple(l - s for s, l in zip(starts, limits))
+        return self.new(f"stablehlo.slice {a} [{', '.join(f'{s}:{l}' for s, l in zip(starts, limits))}] : "
+                        f"({_t(src, dt)}) -> {_t(dst, dt)}")
+
+    def reduce(self, a, shape, dim, kind, init):
+        dst = tuple(s for k, s in enumerate(shape) if k != dim)
+        z = self.const(init)
+        return self.new(f"stablehlo.reduce({a} init: {z}) applies stablehlo.{kind} across dimensions = [{dim}] : "
+                        f"({_t(shape)}, tensor<f32>) -> {_t(dst)}")
+
+    def dot(self, a, b, ashape, bshape, oshape, adt, odt, lb=(), rb=(), lc=(1,), rc=(0,)):
+        bd = f"batching_dims = [{', '.join(map(str, lb))}] x [{', '.join(map(str, rb))}], " if lb else ""
+        return self.new(f"stablehlo.dot_general {a}, {b}, {bd}contracting_dims = [{', '.join(map(str, lc))}] x "
+                        f"[{', '.join(map(str, rc))}], precision = [DEFAULT, DEFAULT] : "
+                        f"({_t(ashape, adt)}, {_t(bshape, adt)}) -> {_t(oshape, odt)}")
+
+
+def _layernorm(e, x, rows, d, g, b, eps):
+    """jax layer norm of x [rows, d] f32 with gamma / beta [d] (jnp.mean /
+    jnp.var as reduce-sum over size, two passes), as the lowering's
+    layernorm-fusion pattern expects it."""
+    X, R, R1 = (rows, d), (rows,), (rows, 1)
+    s = e.reduce(x, X, 1, "add", 0.0)
+    s1 = e.bcast(s, R, R1, [0])
+    n = e.splat(float(d), R1)
+    mu = e.bin("divide", s1, n, R1)
+    mub = e.bcast(mu, R1, X, [0, 1])
+    xc = e.bin("subtract", x, mub, X)
+    sq = e.bin("multiply", xc, xc, X)
+    v = e.reduce(sq, X, 1, "add", 0.0)
+    v1 = e.bcast(v, R, R1, [0])
+    var = e.bin("divide", v1, n, R1)
+    ve = e.bin("add", var, e.splat(float(eps), R1), R1)
+    r = e.un("rsqrt", ve, R1)
+    rb = e.bcast(r, R1, X, [0, 1])
+    y = e.bin("multiply", xc, rb, X)
+    y = e.bin("multiply", y, e.bcast(g, (d,), X, [1]), X)
+    return e.bin("add", y, e.bcast(b, (d,), X, [1]), X)
+
+
+def _gelu(e, x, shape):
+    """jax.nn.gelu(x, approximate=True): 0.5 x (1 + tanh(c0 (x + c1 x^3)))."""
+    x2 = e.bin("multiply", x, x, shape)
+    x3 = e.bin("multiply", x, x2, shape)
+    t = e.bin("multiply", e.splat(0.044715, shape), x3, shape)
+    t = e.bin("add", x, t, shape)
+    t = e.bin("multiply", e.splat(0.7978845608, shape), t, shape)
+    t = e.un("tanh", t, shape)
+    t = e.bin("add", e.splat(1.0, shape), t, shape)
+    t = e.bin("multiply", e.splat(0.5, shape), t, shape)
+    return e.bin("multiply", x, t, shape)
+
+
+def _dense(e, h, w, bias, rows, k, n, gelu=False, out="bf16"):
+    """jnp.dot(h, w, preferred_element_type=f32) + bias [n], GELU'd, converted."""
+    y = e.dot(h, w, (rows, k), (k, n), (rows, n), "bf16", "f32")
+    y = e.bin("add", y, e.bcast(bias, (n,), (rows, n), [1]), (rows, n))
+    if gelu:
+        y = _gelu(e, y, (rows, n))
+    return e.convert(y, (rows, n), "f32", out) if out != "f32" else y
+
+
+def _argmax_row(e, logits, n):
+    """jnp.argmax over [1, n] f32 -> [1] i32 (variadic reduce over value and
+    iota, first index on ties)."""
+    I = _t((1, n), "i32")
+    io = e.new(f"stablehlo.iota dim = 1 : {I}")
+    ninf = e.new("stablehlo.constant dense<0xFF800000> : tensor<f32>")
+    z = e.const(0, "i32")
+    name = f"%v{e.n}"
+    e.n += 1
+    e.lines.append(f"""{e.ind}{name}:2 = "stablehlo.reduce"({logits}, {io}, {ninf}, {z}) <{{dimensions = array<i64: 1>}}> ({{
+{e.ind}^bb0(%a: tensor<f32>, %ai: tensor<i32>, %b: tensor<f32>, %bi: tensor<i32>):
+{e.ind}  %c0 = stablehlo.compare  GT, %a, %b,  FLOAT : (tensor<f32>, tensor<f32>) -> tensor<i1>
+{e.ind}  %c1 = stablehlo.compare  NE, %a, %a,  FLOAT : (tensor<f32>, tensor<f32>) -> tensor<i1>
+{e.ind}  %c2 = stablehlo.or %c0, %c1 : tensor<i1>
+{e.ind}  %c3 = stablehlo.compare  EQ, %a, %b,  FLOAT : (tensor<f32>, tensor<f32>) -> tensor<i1>
+{e.ind}  %c4 = stablehlo.compare  LT, %ai, %bi,  SIGNED : (tensor<i32>, tensor<i32>) -> tensor<i1>
+{e.ind}  %c5 = stablehlo.and %c3, %c4 : tensor<i1>
+{e.ind}  %c6 = stablehlo.or %c2, %c5 : tensor<i1>
+{e.ind}  %c7 = stablehlo.select %c6, %a, %b : tensor<i1>, tensor<f32>
+{e.ind}  %c8 = stablehlo.select %c6, %ai, %bi : tensor<i1>, tensor<i32>
+{e.ind}  stablehlo.return %c7, %c8 : tensor<f32>, tensor<i32>
+{e.ind}}}) : ({_t((1, n))}, {I}, tensor<f32>, tensor<i32>) -> ({_t((1,))}, {_t((1,), "i32")})""")
+    return f"{name}#1"
+
+
+def gpt_decode(c, emit_logits=False, mask_cmp="LE", trips=None):
+    """Config 5 as the JAX program a user would jit (``c``: configs.GptConfig):
+
+        def generate(ids, params):            # ids [T] i32, params as configs.gpt_param_shapes
+            x = wte[ids] + wpe[:T]             # bf16 tables, f32 residual stream
+            for each layer: causal self-attention (jax.nn.softmax over
+                einsum scores with a tril mask), output projection, GELU MLP,
+                pre-LN, writing every layer's k / v into a [H, C, hd] bf16 cache
+            tok = argmax(lnf(x[T-1]) @ lm_head)
+            def step(i, carry):                # lax.fori_loop over the decode steps
+                x = wte[tok] + wpe[T + i]
+                for each layer: q, k, v of the one row; the cache takes k, v at
+                    position T + i (dynamic_update_slice); attention over the
+                    cache with keys past the position masked to -inf
+                tok = argmax(lnf(x) @ lm_head); out = out.at[i].set(tok)
+            return tok0, out
+
+    Inputs and outputs are those of configs.gpt_c5 (same order and types), so
+    the two programs can be run on the same arrays; ``emit_logits`` adds the f32
+    logits of every step [steps + 1, vocab] as a third output, as gpt_c5's does.
+    ``mask_cmp`` is the comparison of the decode mask (key ``mask_cmp`` position;
+    tests plant another one).  ``trips`` runs only that many decode steps (same
+    inputs and outputs; for separating prefill from decode time)."""
+    H, hd, D, F, T, V = c.heads, c.hd, c.d, c.mlp, c.prompt, c.vocab
+    Cc = -(-c.ctx // 8) * 8
+    L = c.layers
+    from .configs import gpt_param_shapes
+    params = gpt_param_shapes(c)
+    args = [f"%ids: {_t((T,), 'i32')}"]
+    pname = {}
+    for k, (name, shape, dt) in enumerate(params):
+        pname[name] = f"%p{k}"
+        args.append(f"%p{k}: {_t(shape, dt)}")
+    scale = hd ** -0.5
+    e = _Emit()
+    # ---- prefill
+    ids2 = e.reshape("%ids", (T,), (T, 1), "i32")
+    te = e.new(f'"stablehlo.gather"({pname["wte"]}, {ids2}) <{{dimension_numbers = #stablehlo.gather<offset_dims = [1], '
+               f'collapsed_slice_dims = [0], start_index_map = [0], index_vector_dim = 1>, indices_are_sorted = false, '
+               f'slice_sizes = array<i64: 1, {D}>}}> : ({_t((V, D), "bf16")}, {_t((T, 1), "i32")}) -> {_t((T, D), "bf16")}')
+    pe = e.slice(pname["wpe"], (c.ctx, D), (0, 0), (T, D), "bf16")
+    x = e.bin("add", e.convert(te, (T, D), "bf16", "f32"), e.convert(pe, (T, D), "bf16", "f32"), (T, D))
+    zero = e.const(0, "i32")
+    caches = []
+    M_, MB = _t((T, T), "i32"), _t((T, T), "i1")
+    S4, S4B = (1, H, T, T), _t((1, H, T, T), "i1")
+    for l in range(L):
+        p = lambda n: pname[f"h{l}.{n}"]
+        h = e.convert(_layernorm(e, x, T, D, p("ln1_g"), p("ln1_b"), c.eps), (T, D), "f32", "bf16")
+        qkv = _dense(e, h, p("w_qkv"), p("b_qkv"), T, D, 3 * D)
+        heads = []
+        for s in range(3):
+            part = e.slice(qkv, (T, 3 * D), (0, s * D), (T, (s + 1) * D), "bf16")
+            r = e.reshape(part, (T, D), (T, H, hd), "bf16")
+            heads.append(e.transpose(r, (T, H, hd), (1, 0, 2), "bf16"))          # [H, T, hd]
+        kc = e.splat(0.0, (H, Cc, hd), "bf16")
+        vc = e.splat(0.0, (H, Cc, hd), "bf16")
+        kc = e.new(f"stablehlo.dynamic_update_slice {kc}, {heads[1]}, {zero}, {zero}, {zero} : "
+                   f"({_t((H, Cc, hd), 'bf16')}, {_t((H, T, hd), 'bf16')}, tensor<i32>, tensor<i32>, tensor<i32>) -> "
+                   f"{_t((H, Cc, hd), 'bf16')}")
+        vc = e.new(f"stablehlo.dynamic_update_slice {vc}, {heads[2]}, {zero}, {zero}, {zero} : "
+                   f"({_t((H, Cc, hd), 'bf16')}, {_t((H, T, hd), 'bf16')}, tensor<i32>, tensor<i32>, tensor<i32>) -> "
+                   f"{_t((H, Cc, hd), 'bf16')}")
+        caches += [kc, vc]
+        q4, k4, v4 = (e.reshape(hh, (H, T, hd), (1, H, T, hd), "bf16") for hh in heads)
+        s0 = e.dot(q4, k4, (1, H, T, hd), (1, H, T, hd), S4, "bf16", "f32", lb=(0, 1), rb=(0, 1), lc=(3,), rc=(3,))
+        s1 = e.bin("multiply", s0, e.splat(scale, S4), S4)
+        m0 = e.new(f"stablehlo.iota dim = 0 : {M_}")
+        m1 = e.new(f"stablehlo.iota dim = 1 : {M_}")
+        m2 = e.new(f"stablehlo.compare  GE, {m0}, {m1},  SIGNED : ({M_}, {M_}) -> {MB}")
+        m3 = e.new(f"stablehlo.broadcast_in_dim {m2}, dims = [2, 3] : ({MB}) -> {S4B}")
+        ninf = e.new("stablehlo.constant dense<0xFF800000> : tensor<f32>")
+        m4 = e.new(f"stablehlo.broadcast_in_dim {ninf}, dims = [] : (tensor<f32>) -> {_t(S4)}")
+        s2 = e.new(f"stablehlo.select {m3}, {s1}, {m4} : {S4B}, {_t(S4)}")
+        mi = e.new("stablehlo.constant dense<0xFF800000> : tensor<f32>")
+        r0 = e.new(f"stablehlo.reduce({s2} init: {mi}) applies stablehlo.maximum across dimensions = [3] : "
+                   f"({_t(S4)}, tensor<f32>) -> {_t((1, H, T))}")
+        r1 = e.bcast(r0, (1, H, T), (1, H, T, 1), [0, 1, 2])
+        r2 = e.bcast(r1, (1, H, T, 1), S4, [0, 1, 2, 3])
+        ex = e.un("exponential", e.bin("subtract", s2, r2, S4), S4)
+        u0 = e.reduce(ex, S4, 3, "add", 0.0)
+        u1 = e.bcast(u0, (1, H, T), (1, H, T, 1), [0, 1, 2])
+        u2 = e.bcast(u1, (1, H, T, 1), S4, [0, 1, 2, 3])
+        pr = e.convert(e.bin("divide", ex, u2, S4), S4, "f32", "bf16")
+        o0 = e.dot(pr, v4, S4, (1, H, T, hd), (1, H, T, hd), "bf16", "f32", lb=(0, 1), rb=(0, 1), lc=(3,), rc=(2,))
+        o1 = e.convert(o0, (1, H, T, hd), "f32", "bf16")
+        o2 = e.transpose(e.reshape(o1, (1, H, T, hd), (H, T, hd), "bf16"), (H, T, hd), (1, 0, 2), "bf16")
+        att = e.reshape(o2, (T, H, hd), (T, D), "bf16")
+        x = e.bin("add", x, e.bcast(p("b_o"), (D,), (T, D), [1]), (T, D))
+        x = e.bin("add", x, e.dot(att, p("w_o"), (T, D), (D, D), (T, D), "bf16", "f32"), (T, D))
+        h2 = e.convert(_layernorm(e, x, T, D, p("ln2_g"), p("ln2_b"), c.eps), (T, D), "f32", "bf16")
+        f = _dense(e, h2, p("w_fc"), p("b_fc"), T, D, F, gelu=True)
+        x = e.bin("add", x, e.bcast(p("b_proj"), (D,), (T, D), [1]), (T, D))
+        x = e.bin("add", x, e.dot(f, p("w_proj"), (T, F), (F, D), (T, D), "bf16", "f32"), (T, D))
+    last = e.slice(x, (T, D), (T - 1, 0), (T, D), "f32")
+
+    hf0 = e.convert(_layernorm(e, last, 1, D, pname["lnf_g"], pname["lnf_b"], c.eps), (1, D), "f32", "bf16")
+    lg0 = e.dot(hf0, pname["lm_head"], (1, D), (D, V), (1, V), "bf16", "f32")
+    tok0 = _argmax_row(e, lg0, V)
+    # ---- decode loop
+    out0 = e.splat(0, (c.steps,), "i32")
+    i0 = e.const(0, "i32")
+    KV = _t((H, Cc, hd), "bf16")
+    LG = _t((c.steps + 1, V))
+    ctypes_ = ["tensor<i32>", _t((1,), "i32"), _t((c.steps,), "i32")] + [KV] * (2 * L)
+    cvals = [i0, tok0, out0] + caches
+    bargs = ["%i", "%tok", "%out"] + [f"%c{k}" for k in range(2 * L)]
+    if emit_logits:
+        lz = e.splat(0.0, (c.steps + 1, V))
+        lg_all = e.new(f"stablehlo.dynamic_update_slice {lz}, {lg0}, {i0}, {i0} : ({LG}, {_t((1, V))}, "
+                       f"tensor<i32>, tensor<i32>) -> {LG}")
+        ctypes_.append(LG)
+        cvals.append(lg_all)
+        bargs.append("%lg")
+    b = _Emit(indent="      ")
+    one = b.const(1, "i32")
+    pos = b.new(f"stablehlo.add %i, {b.const(T, 'i32')} : tensor<i32>")
+    bz = b.const(0, "i32")
+    t2 = b.reshape("%tok", (1,), (1, 1), "i32")
+    te1 = b.new(f'"stablehlo.gather"({pname["wte"]}, {t2}) <{{dimension_numbers = #stablehlo.gather<offset_dims = [1], '
+                f'collapsed_slice_dims = [0], start_index_map = [0], index_vector_dim = 1>, indices_are_sorted = false, '
+                f'slice_sizes = array<i64: 1, {D}>}}> : ({_t((V, D), "bf16")}, {_t((1, 1), "i32")}) -> {_t((1, D), "bf16")}')
+    pe1 = b.new(f"stablehlo.dynamic_slice {pname['wpe']}, {pos}, {bz}, sizes = [1, {D}] : "
+                f"({_t((c.ctx, D), 'bf16')}, tensor<i32>, tensor<i32>) -> {_t((1, D), 'bf16')}")
+    xs = b.bin("add", b.convert(te1, (1, D), "bf16", "f32"), b.convert(pe1, (1, D), "bf16", "f32"), (1, D))
+    new_caches = []
+    S3 = (H, 1, Cc)
+    for l in range(L):
+        p = lambda n: pname[f"h{l}.{n}"]
+        h = b.convert(_layernorm(b, xs, 1, D, p("ln1_g"), p("ln1_b"), c.eps), (1, D), "f32", "bf16")
+        qkv = _dense(b, h, p("w_qkv"), p("b_qkv"), 1, D, 3 * D)
+        q, k, v = (b.reshape(b.slice(qkv, (1, 3 * D), (0, s * D), (1, (s + 1) * D), "bf16"), (1, D), (H, 1, hd), "bf16")
+                   for s in range(3))
+        kc = b.new(f"stablehlo.dynamic_update_slice %c{2 * l}, {k}, {bz}, {pos}, {bz} : ({KV}, {_t((H, 1, hd), 'bf16')}, "
+                   f"tensor<i32>, tensor<i32>, tensor<i32>) -> {KV}")
+        vc = b.new(f"stablehlo.dynamic_update_slice %c{2 * l + 1}, {v}, {bz}, {pos}, {bz} : ({KV}, {_t((H, 1, hd), 'bf16')}, "
+                   f"tensor<i32>, tensor<i32>, tensor<i32>) -> {KV}")
+        new_caches += [kc, vc]
+        sc = b.dot(q, kc, (H, 1, hd), (H, Cc, hd), S3, "bf16", "f32", lb=(0,), rb=(0,), lc=(2,), rc=(2,))
+        sc = b.bin("multiply", sc, b.splat(scale, S3), S3)
+        io = b.new(f"stablehlo.iota dim = 2 : {_t(S3, 'i32')}")
+        pb = b.new(f"stablehlo.broadcast_in_dim {pos}, dims = [] : (tensor<i32>) -> {_t(S3, 'i32')}")
+        vis = b.new(f"stablehlo.compare  {mask_cmp}, {io}, {pb},  SIGNED : ({_t(S3, 'i32')}, {_t(S3, 'i32')}) -> "
+                    f"{_t(S3, 'i1')}")
+        ni = b.new("stablehlo.constant dense<0xFF800000> : tensor<f32>")
+        nib = b.new(f"stablehlo.broadcast_in_dim {ni}, dims = [] : (tensor<f32>) -> {_t(S3)}")
+        sm = b.new(f"stablehlo.select {vis}, {sc}, {nib} : {_t(S3, 'i1')}, {_t(S3)}")
+        mi = b.new("stablehlo.constant dense<0xFF800000> : tensor<f32>")
+        mx = b.new(f"stablehlo.reduce({sm} init: {mi}) applies stablehlo.maximum across dimensions = [2] : "
+                   f"({_t(S3)}, tensor<f32>) -> {_t((H, 1))}")
+        mxb = b.bcast(mx, (H, 1), S3, [0, 1])
+        ex = b.un("exponential", b.bin("subtract", sm, mxb, S3), S3)
+        sm1 = b.reduce(ex, S3, 2, "add", 0.0)
+        pr = b.convert(b.bin("divide", ex, b.bcast(sm1, (H, 1), S3, [0, 1]), S3), S3, "f32", "bf16")
+        o = b.dot(pr, vc, S3, (H, Cc, hd), (H, 1, hd), "bf16", "f32", lb=(0,), rb=(0,), lc=(2,), rc=(1,))
+        att = b.reshape(b.convert(o, (H, 1, hd), "f32", "bf16"), (H, 1, hd), (1, D), "bf16")
+        xs = b.bin("add", xs, b.bcast(p("b_o"), (D,), (1, D), [1]), (1, D))
+        xs = b.bin("add", xs, b.dot(att, p("w_o"), (1, D), (D, D), (1, D), "bf16", "f32"), (1, D))
+        h2 = b.convert(_layernorm(b, xs, 1, D, p("ln2_g"), p("ln2_b"), c.eps), (1, D), "f32", "bf16")
+        f = _dense(b, h2, p("w_fc"), p("b_fc"), 1, D, F, gelu=True)
+        xs = b.bin("add", xs, b.bcast(p("b_proj"), (D,), (1, D), [1]), (1, D))
+        xs = b.bin("add", xs, b.dot(f, p("w_proj"), (1, F), (F, D), (1, D), "bf16", "f32"), (1, D))
+    hf = b.convert(_layernorm(b, xs, 1, D, pname["lnf_g"], pname["lnf_b"], c.eps), (1, D), "f32", "bf16")
+    lg = b.dot(hf, pname["lm_head"], (1, D), (D, V), (1, V), "bf16", "f32")
+    tok = _argmax_row(b, lg, V)
+    out = b.new(f"stablehlo.dynamic_update_slice %out, {tok}, %i : ({_t((c.steps,), 'i32')}, {_t((1,), 'i32')}, "
+                f"tensor<i32>) -> {_t((c.steps,), 'i32')}")
+    i1 = b.new(f"stablehlo.add %i, {one} : tensor<i32>")
+    rets = [i1, tok, out] + new_caches
+    if emit_logits:
+        rets.append(b.new(f"stablehlo.dynamic_update_slice %lg, {lg}, {i1}, {bz} : ({LG}, {_t((1, V))}, "
+                          f"tensor<i32>, tensor<i32>) -> {LG}"))
+    nres = len(cvals)
+    blockargs = ", ".join(f"{n}: {ty}" for n, ty in zip(bargs, ctypes_))
+    types = ", ".join(ctypes_)
+    loop = f"""    %w:{nres} = "stablehlo.while"({', '.join(cvals)}) ({{
+    ^bb0({blockargs}):
+      %lim = stablehlo.constant dense<{c.steps if trips is None else trips}> : tensor<i32>
+      %lt = stablehlo.compare  LT, %i, %lim,  SIGNED : (tensor<i32>, tensor<i32>) -> tensor<i1>
+      stablehlo.return %lt : tensor<i1>
+    }}, {{
+    ^bb0({blockargs}):
+{chr(10).join(b.lines)}
+      stablehlo.return {', '.join(rets)} : {types}
+    }}) : ({types}) -> ({types})"""
+    body = "\n".join(e.lines) + "\n" + loop
+    R1, RS = _t((1,), "i32"), _t((c.steps,), "i32")
+    res, rty = [tok0, "%w#2"], [R1, RS]
+    if emit_logits:
+        res.append(f"%w#{nres - 1}")
+        rty.append(LG)
+    return f"""
+module @jit_generate {{
+  func.func public @main({', '.join(args)}) -> ({', '.join(rty)}) {{
+{body}
+    return {', '.join(res)} : {', '.join(rty)}
+  }}
+}}
+"""

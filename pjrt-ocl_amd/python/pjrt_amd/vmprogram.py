@@ -49,10 +49,13 @@ which does not use them is byte-for-byte a reference program):
   the step's own key/value: ``out[h] = softmax(scale q[h] . [K^T[h, :, :pos],
   k[h]]) [V[h, :pos]; v[h]]``.  Instr: dst out, a q, b K^T cache [H, hd, C],
   n H, imm C, imm2 V cache [H, C, hd], aux -> [hd, k, v, pos buffer, scale
-  bits].  Task: p0 V, p1 k, p2 v, p3 pos, p4 H | S << 16, p5 hd, p6 C, p7
-  scale bits; tile = head * S + split, each split at most 64 cache keys,
-  combined by the last split through the task's scratch.  ``pos`` (i32
-  scalar) is clamped to [0, C].
+  bits].  Task: p0 V, p1 k, p2 v, p3 pos, p4 H | S << 16, p5 hd | krow << 16
+  | masked << 17, p6 C, p7 scale bits; tile = head * S + split, each split at
+  most 64 cache keys, combined by the last split through the task's scratch.
+  ``pos`` (i32 scalar) is clamped to [0, C].  ``krow``: the key cache holds
+  rows [H, C, hd] instead of K^T (hd a power of two).  ``masked``: the
+  decoder's form that stores k, v at pos before attending over keys <= pos:
+  pos is clamped to [0, C - 1] and a negative pos gives a NaN output.
 
 Task scratch: the loader gives each task that needs it (a split decode
 attention or argmax) its own zeroed region of device memory; the last split of

@@ -168,3 +168,34 @@ module @jit_f {{
   }}
 }}
 """
+
+
+def fori_shift(trips=5, swap=False):
+    """def f(x):   # a carry passed on while another is updated
+         return lax.fori_loop(0, trips, lambda i, c: (c[0] + 1.0, c[0]), (x, -x))
+    -> (x + trips, x + trips - 1): the second carry must see the first one's
+    value from before the update.  With ``swap`` the body is
+    ``lambda i, c: (c[1], c[0])``."""
+    ret = "%b, %a" if swap else "%3, %a"
+    return f"""
+module @jit_f {{
+  func.func public @main(%arg0: tensor<f32>) -> (tensor<f32>, tensor<f32>) {{
+    %c = stablehlo.constant dense<0> : tensor<i32>
+    %n = stablehlo.negate %arg0 : tensor<f32>
+    %0:3 = "stablehlo.while"(%c, %arg0, %n) ({{
+    ^bb0(%i: tensor<i32>, %a: tensor<f32>, %b: tensor<f32>):
+      %lim = stablehlo.constant dense<{trips}> : tensor<i32>
+      %1 = stablehlo.compare  LT, %i, %lim,  SIGNED : (tensor<i32>, tensor<i32>) -> tensor<i1>
+      stablehlo.return %1 : tensor<i1>
+    }}, {{
+    ^bb0(%i: tensor<i32>, %a: tensor<f32>, %b: tensor<f32>):
+      %one = stablehlo.constant dense<1> : tensor<i32>
+      %2 = stablehlo.add %i, %one : tensor<i32>
+      %f1 = stablehlo.constant dense<1.000000e+00> : tensor<f32>
+      %3 = stablehlo.add %a, %f1 : tensor<f32>
+      stablehlo.return %2, {ret} : tensor<i32>, tensor<f32>, tensor<f32>
+    }}) : (tensor<i32>, tensor<f32>, tensor<f32>) -> (tensor<i32>, tensor<f32>, tensor<f32>)
+    return %0#1, %0#2 : tensor<f32>, tensor<f32>
+  }}
+}}
+"""

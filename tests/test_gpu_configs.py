@@ -97,3 +97,31 @@ def test_gpt_c5_lane_fit_matches_every_lane():
     # the strip width, and with it the summation order of the bf16 GEMVs,
     # differs between the two schedules: the bf16 decoder tolerance applies
     assert check_decoder(got, want, 5e-3) >= 4
+
+
+def _lowered_decoder(c):
+    from pjrt_amd import lowering as L
+    from pjrt_amd import stablehlo_configs as SC
+    return L.lower_text(SC.gpt_decode(c, emit_logits=True))
+
+
+def test_lowered_gpt_decode_small():
+    """Config 5 as the JAX program, through the lowering (decode attention
+    fused, caches updated in place): the GPU against the oracle."""
+    c = CF.GptConfig(layers=2, d=128, heads=2, mlp=512, vocab=1000, prompt=128, steps=16)
+    args = CF.gpt_inputs(c, seed=11)
+    got, want = run_both(_lowered_decoder(c), args, oracle="tensor")
+    assert check_decoder(got, want, 5e-3) >= 1
+
+
+def test_lowered_gpt_decode_full_size_first_steps():
+    """The lowered full config-5 program (12 layers, d 768, vocab 32000,
+    512-token prompt) for the prefill and three decode steps, and beside it the
+    hand-built program on the same inputs."""
+    c = dataclasses.replace(CF.C5, steps=3)
+    args = CF.gpt_inputs(c)
+    prog = _lowered_decoder(c)
+    got, want = run_both(prog, args, oracle="tensor")
+    assert check_decoder(got, want, 5e-3) >= 1
+    hand, _ = blob_for(CF.gpt_c5(c, emit_logits=True))
+    assert check_decoder(got, run_gpu(hand, args), 5e-3) >= 1

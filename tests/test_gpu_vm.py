@@ -599,20 +599,28 @@ def test_flash_attention_score_jump(dt, causal, T, C, target):
     np.testing.assert_allclose(got[0][:, qi], want[:, qi], rtol=0, atol=2e-2 * np.abs(want).max())
 
 
-@pytest.mark.parametrize("dt,H,hd,C,pos,jump", [
-    ("bf16", 12, 64, 640, 600, None),       # the decoder's shape
-    ("bf16", 12, 64, 640, 0, None),         # the step's own key only
-    ("f16", 3, 8, 16, 16, None),            # full cache
-    ("f32", 2, 24, 24, -1, None),           # clamped position; 3 threads per V row
-    ("f32", 1, 256, 1032, 1030, None),      # widest head, 17 splits
-    ("bf16", 2, 128, 2056, 2050, 1500),     # 33 splits; a dominant key in an early one
-    ("bf16", 2, 64, 640, 300, "new"),       # a dominant new key
-    ("bf16", 4, 64, 640, 640, "new"),       # position past the cache: the step's key joins the last split
+@pytest.mark.parametrize("dt,H,hd,C,pos,jump,mode", [
+    ("bf16", 12, 64, 640, 600, None, ""),       # the decoder's shape
+    ("bf16", 12, 64, 640, 0, None, ""),         # the step's own key only
+    ("f16", 3, 8, 16, 16, None, ""),            # full cache
+    ("f32", 2, 24, 24, -1, None, ""),           # clamped position; 3 threads per V row
+    ("f32", 1, 256, 1032, 1030, None, ""),      # widest head, 17 splits
+    ("bf16", 2, 128, 2056, 2050, 1500, ""),     # 33 splits; a dominant key in an early one
+    ("bf16", 2, 64, 640, 300, "new", ""),       # a dominant new key
+    ("bf16", 4, 64, 640, 640, "new", ""),       # position past the cache: the step's key joins the last split
+    ("bf16", 12, 64, 640, 600, None, "krow masked"),   # the lowered JAX decoder's form
+    ("bf16", 12, 64, 640, 700, None, "krow masked"),   # past the cache: clamped to its last column
+    ("f16", 3, 256, 1032, 1030, None, "krow"),         # 32 threads per key row
+    ("bf16", 2, 128, 2056, 2050, 1500, "krow"),        # 33 splits, a dominant early key
+    ("f32", 1, 8, 64, 33, "new", "krow masked"),       # one thread per key row
+    ("f32", 2, 16, 32, -1, None, "masked"),            # no key left: NaN, as the softmax makes it
 ])
-def test_decode_attention(dt, H, hd, C, pos, jump):
+def test_decode_attention(dt, H, hd, C, pos, jump, mode):
     """TOP_DECODE_ATTN against float64 math on the same (rounded) inputs: keys
     are the cache prefix [0, pos) then the step's own key; splits of 64 cache
-    keys combine their partial softmax results."""
+    keys combine their partial softmax results.  ``krow``: the key cache is
+    [H, C, hd] rows; ``masked``: pos clamps to [0, C - 1], negative is NaN."""
+    krow, masked = "krow" in mode, "masked" in mode
     rng = np.random.default_rng(2024 + hd + C)
     q = rng.standard_normal((H, hd)).astype(np.float32)
     k = rng.standard_normal((H, hd)).astype(np.float32)
@@ -630,13 +638,14 @@ def test_decode_attention(dt, H, hd, C, pos, jump):
         q, k, v, ckt, cv = (vmref.bf16_to_f32(vmref.f32_to_bf16(t)) for t in (q, k, v, ckt, cv))
     elif dt == "f16":
         q, k, v, ckt, cv = (t.astype(np.float16).astype(np.float32) for t in (q, k, v, ckt, cv))
+    kc = np.ascontiguousarray(ckt.transpose(0, 2, 1)) if krow else ckt
     g = G.Graph()
     Q, K, Vv = (g.input((H, hd), dt) for _ in range(3))
-    CK, CV = g.input((H, hd, C), dt), g.input((H, C, hd), dt)
+    CK, CV = g.input(kc.shape, dt), g.input((H, C, hd), dt)
     POS = g.input((), "i32")
-    g.output(g.decode_attention(Q, K, Vv, CK, CV, POS, scale))
+    g.output(g.decode_attention(Q, K, Vv, CK, CV, POS, scale, krow=krow, masked=masked))
     prog = g.build()
-    want = vmref.decode_attention(q, ckt, cv, k, v, pos, scale)
+    want = vmref.decode_attention(q, kc, cv, k, v, pos, scale, krow, masked)
     tol = 1e-3 if dt == "f32" else 1e-2
     # keys split over CUs, 64 per split; a few lanes run several tiles each
     for nlanes in (None, 7):
@@ -644,8 +653,11 @@ def test_decode_attention(dt, H, hd, C, pos, jump):
         tk = next(tk for tk in vmref.parse(blob).tasks if tk.top == V.TOP_DECODE_ATTN)
         assert tk.p[4] >> 16 == -(-C // 64), tk.p[4]
         for _ in range(2):              # the arrival counters reset themselves
-            got, _ = run_both(blob, [q, k, v, ckt, cv, np.array(pos, np.int32)], oracle=None)
+            got, _ = run_both(blob, [q, k, v, kc, cv, np.array(pos, np.int32)], oracle=None)
             got = as_f32(got[0], V.DT_BY_NAME[dt]).astype(np.float64).reshape(H, hd)
+            if masked and pos < 0:
+                assert np.isnan(got).all() and np.isnan(want).all()
+                continue
             err = np.abs(got - want).max() / max(1e-6, np.abs(want).max())
             assert np.isfinite(got).all() and err <= tol, (nlanes, err)
 

@@ -207,6 +207,21 @@ def test_while_data_dependent():
 
 
 @pytest.mark.parametrize("mode", ["unroll", "for"])
+@pytest.mark.parametrize("swap", [False, True])
+def test_fori_carry_passthrough_and_swap(mode, swap, monkeypatch):
+    """(a, b) -> (a + 1, a) from (x, -x): the passed-on carry reads a's value
+    from before the update (x + 5, x + 4 after 5 trips), though the update of a
+    may run in place; (a, b) -> (b, a) five times gives (-x, x)."""
+    monkeypatch.setenv("PJRT_OCL_WHILE", mode)
+    prog, got, plain = both(H.fori_shift(5, swap), [np.float32(2.0)])
+    want = (-2.0, 2.0) if swap else (7.0, 6.0)
+    for out in (got, plain):
+        assert tuple(float(x) for x in out) == want
+    if mode == "for":
+        assert V.OP_FOR in live_ops(prog)
+
+
+@pytest.mark.parametrize("mode", ["unroll", "for"])
 def test_scan_stacking_dynamic_update_slice(mode, monkeypatch):
     """scan-style stacking ys[i] = x * (i + 1) through dynamic_update_slice: as
     OP_FOR the update writes the carry in place (no per-trip copy of ys)."""
@@ -311,6 +326,85 @@ def test_donation_aliases():
     # the parser keeps each argument's attribute dictionary
     m = M.parse_module(H.donated_chain(8))
     assert M.attr_int(m.main.arg_attr(0, "tf.aliasing_output")) == 0 and m.main.arg_attr(1, "x") is None
+
+
+GPT_TINY = dict(layers=2, d=64, heads=2, mlp=128, vocab=97, prompt=8, steps=4)
+
+
+def _decode_body(prog):
+    """Instructions of the decode loop body (the program's OP_FOR)."""
+    fors = [i for i in prog.instrs if i.op == V.OP_FOR]
+    assert len(fors) == 1
+    return [prog.instrs[j] for j in range(fors[0].n, fors[0].n + fors[0].imm) if prog.instrs[j].op != V.OP_NOP]
+
+
+@pytest.mark.parametrize("mode", ["unroll", "for"])
+def test_gpt_decode_program_lowers_to_the_decoder(mode, monkeypatch):
+    """Config 5 as the JAX program (prefill, then a fori_loop decode with KV
+    caches updated by dynamic_update_slice, a key <= pos mask, argmax): the
+    lowered program gives the tokens of the independent numpy decoder and its
+    logits within f32 rounding.  As a loop, each layer's decode step is one
+    OP_DECODE_ATTN, each layernorm one row op, and the caches are updated in
+    place (nothing copies a cache per step)."""
+    from pjrt_amd import configs as CF
+    from pjrt_amd import stablehlo_configs as SC
+    monkeypatch.setenv("PJRT_OCL_WHILE", mode)
+    c = CF.GptConfig(**GPT_TINY)
+    prog = L.lower_text(SC.gpt_decode(c, emit_logits=True))
+    args = CF.gpt_inputs(c, seed=5)
+    first, toks, logits = run(prog, args)
+    ref_toks, ref_logits = CF.gpt_reference(c, args)
+    np.testing.assert_array_equal(np.concatenate([first, toks]), ref_toks)
+    assert np.abs(logits - ref_logits).max() <= 1e-5 * np.abs(ref_logits).max()
+    if mode == "for":
+        body = _decode_body(prog)
+        ops = [i.op for i in body]
+        cache = c.heads * (-(-c.ctx // 8) * 8) * c.hd
+        assert ops.count(V.OP_DECODE_ATTN) == c.layers and V.OP_SOFTMAX not in ops
+        assert ops.count(V.OP_LAYERNORM_AFFINE) == 2 * c.layers + 1 and V.OP_MAP_REGION not in ops
+        assert not [i for i in body if i.op in (V.OP_GATHER_STRIDED, V.OP_CONVERT, V.OP_COPY_F32) and i.n == cache]
+
+
+def test_gpt_prefill_attention_gets_the_matrix_core_layout():
+    """The prefill's attention reads q, k, v as head views of the fused QKV
+    projection; the flash fusion gathers them into the matrix-core kernel's
+    layout (Q, V plain [H, T, hd], K the transpose of a plain [H, T, hd]), and
+    the decoder's tokens and logits are unchanged."""
+    from pjrt_amd import configs as CF
+    from pjrt_amd import stablehlo_configs as SC
+    c = CF.GptConfig(layers=1, d=128, heads=2, mlp=128, vocab=97, prompt=64, steps=4)
+    prog = L.lower_text(SC.gpt_decode(c, emit_logits=True))
+    (fa,) = [i for i in prog.instrs if i.op == V.OP_FLASH_ATTN]
+    G, M, C, hd, _, causal, qv, kv, vv = prog.aux[fa.aux:fa.aux + 9]
+    assert (G, M, C, hd, causal, qv, vv) == (2, 64, 64, 64, 1, 0, 0)
+    assert prog.aux[kv - 1:kv + 7] == [3, G, hd, C, C * hd, 1, hd, 0]
+    args = CF.gpt_inputs(c, seed=3)
+    first, toks, logits = run(prog, args)
+    ref_toks, ref_logits = CF.gpt_reference(c, args)
+    np.testing.assert_array_equal(np.concatenate([first, toks]), ref_toks)
+    assert np.abs(logits - ref_logits).max() <= 1e-5 * np.abs(ref_logits).max()
+
+
+def test_gpt_decode_unfused_and_planted_mask(monkeypatch):
+    """Without the decode fusion the decomposed chain (bf16 probabilities) still
+    decodes the same tokens; a planted mask (key < pos: the step's own key
+    left out) is not fused, and its logits differ from the decoder's."""
+    from pjrt_amd import configs as CF
+    from pjrt_amd import stablehlo_configs as SC
+    c = CF.GptConfig(**GPT_TINY)
+    args = CF.gpt_inputs(c, seed=5)
+    ref_toks, ref_logits = CF.gpt_reference(c, args)
+    monkeypatch.setenv("PJRT_OCL_DECODE_ATTN", "0")
+    plain = L.lower_text(SC.gpt_decode(c, emit_logits=True))
+    monkeypatch.delenv("PJRT_OCL_DECODE_ATTN")
+    assert V.OP_DECODE_ATTN not in live_ops(plain)
+    first, toks, logits = run(plain, args)
+    np.testing.assert_array_equal(np.concatenate([first, toks]), ref_toks)
+    assert np.abs(logits - ref_logits).max() <= 1e-2 * np.abs(ref_logits).max()
+    bad = L.lower_text(SC.gpt_decode(c, emit_logits=True, mask_cmp="LT"))
+    assert V.OP_DECODE_ATTN not in live_ops(bad)
+    _, _, bad_logits = run(bad, args)
+    assert np.abs(bad_logits[1:] - ref_logits[1:]).max() > 1e-2 * np.abs(ref_logits).max()
 
 
 def test_planted_pass_mistake_is_caught(monkeypatch):

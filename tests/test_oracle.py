@@ -548,6 +548,29 @@ def test_decode_attention_brute_force(pos):
     np.testing.assert_allclose(got, decode_attention_loops(q, ckt, cv, k, v, pos, 0.35), rtol=1e-5, atol=1e-6)
 
 
+@pytest.mark.parametrize("krow", [False, True])
+@pytest.mark.parametrize("masked", [False, True])
+@pytest.mark.parametrize("pos", [0, 9, 15, 16, 40, -3])
+def test_decode_attention_row_keys_and_masked_form(krow, masked, pos):
+    """``krow`` reads the key cache as rows [H, C, hd] (the same keys as the
+    K^T layout); ``masked`` (the decoder that stored k, v at pos first) clamps
+    pos to [0, C - 1] like that store, and a negative pos leaves no key: NaN."""
+    H, hd, C, scale = 3, 8, 16, 0.35
+    q, k, v, ckt, cv = _decode_inputs()
+    kc = np.ascontiguousarray(ckt.transpose(0, 2, 1)) if krow else ckt
+    g = G.Graph()
+    Q, K, Vv = (g.input((H, hd)) for _ in range(3))
+    CK, CV = g.input(kc.shape), g.input((H, C, hd))
+    POS = g.input((), "i32")
+    g.output(g.decode_attention(Q, K, Vv, CK, CV, POS, scale, krow=krow, masked=masked))
+    (got,) = both(g.build(), [q, k, v, kc, cv, np.array(pos, np.int32)])
+    if masked and pos < 0:
+        assert np.isnan(got).all()
+        return
+    p = min(max(pos, 0), C - 1 if masked else C)
+    np.testing.assert_allclose(got, decode_attention_loops(q, ckt, cv, k, v, p, scale), rtol=1e-5, atol=1e-6)
+
+
 @pytest.mark.parametrize("pos", [0, 5, 15])
 def test_decode_attention_equals_decomposed_chain(pos):
     """The fused step equals the decomposed chain of pinned ops: cache update at
@@ -577,7 +600,7 @@ def test_decode_attention_equals_decomposed_chain(pos):
 def test_planted_decode_new_key_is_caught(monkeypatch):
     """An oracle that reads the cache's column pos instead of the step's own key
     and value fails the brute-force check."""
-    def wrong(q, Kt, Vc, k, v, pos, scale):
+    def wrong(q, Kt, Vc, k, v, pos, scale, krow=False, masked=False):
         C = Kt.shape[2]
         p = min(max(int(pos), 0), C - 1)
         s = np.einsum("hd,hdc->hc", q.astype(np.float64), Kt[:, :, :p + 1].astype(np.float64)) * scale

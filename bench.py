@@ -350,7 +350,7 @@ def bench_lowered(rt, steps):
         "c4": (H.attention(4, 16, 2048, 128, "bf16", True), hand_c4(), [bf16((4, 16, 2048, 128)) for _ in range(3)]),
     }
     names = {v: k for k, v in vars(V).items() if k.startswith("TOP_") and k != "TOP_MAX"}
-    out = {"c5": bench_c5_lowered(rt)}
+    out = {"c5": bench_c5_lowered(rt), "reference_decode_step": bench_reference_decode(rt, steps)}
     for name, (text, hand, args) in cases.items():
         t0 = time.perf_counter()
         low = L.lower_text(text)
@@ -428,6 +428,40 @@ def bench_c5_lowered(rt, reps=3):
             "program_ms": round(times[c.steps], 3), "prefill_plus_8_steps_ms": round(times[8], 3),
             "lower_s": round(lower_s, 2), "tokens_equal_to_hand_built": int(same.sum()),
             "first_token_difference": int(np.argmin(same)) if not same.all() else None}
+
+
+REF_DECODE_US = {"base": (5702.0, 3835.0)}     # RTX PRO 6000, docs/decisions.md:2249-2253, 2369-2372
+
+
+def bench_reference_decode(rt, steps):
+    """The reference's own decode benchmark program (tools/bench_decode.py: one
+    f32 token through the layers, keys and values appended by concatenate), as
+    the StableHLO its jit lowers to, through our lowering: microseconds per
+    token (one program execution each) and the bytes a token must read (f32
+    weights plus the two caches, tools/bench_decode.py:83-89) per second.  The
+    reference published 5702 us/token for "base" on an RTX PRO 6000, 3835 with
+    its epilogue fusion."""
+    from pjrt_amd import lowering as L
+    from pjrt_amd import stablehlo_configs as H
+    out = {}
+    for name, cfg in H.DECODE_STEP_CONFIGS.items():
+        prog = L.lower_text(H.decode_step(cfg))
+        lp = rt.compile(prog, arena_reuse=False)
+        dev_in = [rt.to_device(a) for a in H.decode_step_inputs(cfg)]
+        dev_out = lp.alloc_outputs()
+        wall_ms, ms = time_program(rt, lp, dev_in, dev_out, max(20, steps), 5)
+        for b in dev_in + dev_out:
+            b.free()
+        lp.close()
+        nbytes = H.decode_step_bytes(cfg)
+        res = {"config": dict(zip(("d_model", "heads", "d_ff", "layers", "context"), cfg)),
+               "us_per_token": round(ms * 1e3, 2), "wall_us_per_token": round(wall_ms * 1e3, 2),
+               "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1), "bytes_per_token": nbytes}
+        if name in REF_DECODE_US:
+            res["reference_us_per_token_rtx_pro_6000"] = REF_DECODE_US[name][1]
+        out[name] = res
+        log(f"reference decode step {name}: {ms * 1e3:.1f} us/token")
+    return out
 
 
 def bench_c1(rt, steps, with_cpu=False):

@@ -49,6 +49,81 @@ struct AffineWalk {
   }
 };
 
+// A view whose innermost axis is contiguous, with the innermost extent, every
+// other stride and the offset whole multiples of 16 bytes, moves 16-byte runs:
+// the same map over 16-byte units (innermost extent and strides divided by the
+// elements per unit).  Four runs are loaded per thread before any is stored, so
+// a thread keeps four loads in flight instead of one; a view that is one
+// contiguous run (a slice of whole rows) skips the index walk altogether.
+// Returns false when the view does not qualify (the element path runs).
+VM_DEV bool gather_wide(const VM_K int32_t* aux, uint32_t x, gbyte* d, const gbyte* a, uint64_t e0,
+                        uint64_t e1, uint32_t es, bool scatter) {
+  const int rank = aux[x];
+  if (rank < 1 || rank > 8 || es > 16 || 16 % es || ((uintptr_t(a) | uintptr_t(d)) & 15)) return false;
+  const int64_t per = 16 / es;
+  const int64_t off = aux[x + 1 + 2 * rank];
+  if (aux[x + 2 * rank] != 1 || aux[x + rank] % per || off % per || off < 0) return false;
+  bool linear = true;
+  int64_t want = 1;
+  for (int e = rank - 1; e >= 0; --e) {
+    const int32_t dim = aux[x + 1 + e], st = aux[x + 1 + rank + e];
+    if (e < rank - 1 && st % per) return false;
+    if (dim != 1 && st != want) linear = false;
+    want *= dim;
+  }
+  const uint64_t c0 = e0 / uint64_t(per), c1 = e1 / uint64_t(per);    // e0, e1: whole units (see caller)
+  constexpr int U = 4;
+  const uint32_t tid = threadIdx.x;
+  if (linear) {
+    const VM_G v4u* src = (const VM_G v4u*)(scatter ? a : a + off * es);
+    VM_G v4u* dst = (VM_G v4u*)(scatter ? d + off * es : d);
+    for (uint64_t c = c0 + tid; c < c1; c += U * kBlock) {
+      v4u v[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        if (c + u * kBlock < c1) v[u] = src[c + u * kBlock];
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        if (c + u * kBlock < c1) dst[c + u * kBlock] = v[u];
+    }
+    return true;
+  }
+  if (c0 + tid >= c1) return true;
+  AffineWalk w;
+  w.rank = rank;
+  w.off = off / per;
+  int64_t rem = int64_t(c0 + tid);
+  for (int e = rank - 1; e >= 0; --e) {
+    w.dims[e] = e == rank - 1 ? int32_t(aux[x + 1 + e] / per) : aux[x + 1 + e];
+    w.strides[e] = e == rank - 1 ? 1 : int32_t(aux[x + 1 + rank + e] / per);
+    const int32_t cc = int32_t(rem % w.dims[e]);
+    rem /= w.dims[e];
+    w.coord[e] = cc;
+    w.off += int64_t(cc) * w.strides[e];
+  }
+  const VM_G v4u* src = (const VM_G v4u*)a;
+  VM_G v4u* dst = (VM_G v4u*)d;
+  for (uint64_t c = c0 + tid; c < c1; c += U * kBlock) {
+    v4u v[U];
+    int64_t o[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      o[u] = w.off;
+      if (c + (u + 1) * kBlock < c1) w.advance(kBlock);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (c + u * kBlock < c1) v[u] = scatter ? src[c + u * kBlock] : src[o[u]];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (c + u * kBlock < c1) {
+        if (scatter) dst[o[u]] = v[u];
+        else dst[c + u * kBlock] = v[u];
+      }
+  }
+  return true;
+}
+
 VM_TILE void gather_tiles(Args A, uint32_t ti, uint32_t lo, uint32_t hi, bool scatter) {
   A = uargs(A);
   const VM_K Task& t = task_of(A, ti);
@@ -61,6 +136,9 @@ VM_TILE void gather_tiles(Args A, uint32_t ti, uint32_t lo, uint32_t hi, bool sc
   gbyte* d = resolve(A, t.dst);
   const gbyte* a = resolve(A, t.a);
   const int rank = aux[t.p[0]];
+  // e0 is a multiple of ew_ts (a multiple of 16), e1 too or the element count,
+  // which a qualifying view makes a multiple of the elements per 16 bytes
+  if (gather_wide(aux, t.p[0], d, a, e0, e1, es, scatter)) return;
   if (rank > 8) {        // wide maps: direct evaluation per element
     for (uint64_t i = e0 + threadIdx.x; i < e1; i += kBlock) {
       const int64_t j = view_index(aux, t.p[0], i);

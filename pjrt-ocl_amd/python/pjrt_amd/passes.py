@@ -1094,19 +1094,23 @@ def _place_gathers(ix, sc, si, free, last, plan):
 # ---- fuse_decode_attention (extension: no reference counterpart) ------------------------------
 
 def fuse_decode_attention(prog: V.VMProgram) -> None:
-    """The decode step a JAX decoder with a KV cache writes per layer
+    """The decode step of a decoder with a KV cache, in either of the two forms
+    a JAX program writes per layer:
 
-        K' = dynamic_update_slice(K, k, pos)     V' = dynamic_update_slice(V, v, pos)
-        s = dot(q, K'^T) [* scale];  s = select(key <= pos, s, -inf)
-        o = dot(softmax(s) [-> convert], V') [-> convert]
+        masked:  K' = dynamic_update_slice(K, k, pos)   V' likewise with v
+                 s = dot(q, K'^T) [* scale];  s = select(key <= pos, s, -inf)
+                 o = dot(softmax(s) [-> convert], V') [-> convert]
+        append:  KK = concatenate([K, k], 1)   VV likewise     (no mask;
+                 o = dot(softmax(dot(q, KK^T) [* scale]), VV)  tools/bench_decode.py:47-52)
 
-    => OP_DECODE_ATTN (masked; krow when the cache holds key rows [H, C, hd]):
-    one pass over the two caches instead of five barrier-separated ops.  The
-    reference lowers this chain op by op (python/pjrt_ocl/lowering.py:2664-2690
-    fuses only the constant-mask prefill form; tools/bench_decode.py:44-52 is
-    the unmasked append form).  The mask is proven by evaluating its predicate
-    for every position in [-2, C + 2]; the updates' position must be the same
-    buffer.  The updates stay: the op reads the caches after them."""
+    => OP_DECODE_ATTN (krow when the keys are rows [H, C, hd]): one pass over the
+    two caches instead of five barrier-separated ops, the append form without
+    copying the caches into the concatenation.  The reference runs both chains
+    op by op (python/pjrt_ocl/lowering.py:2664-2690 fuses only the constant-mask
+    prefill form).  The mask is proven by evaluating its predicate for every
+    position in [-2, C + 2]; the updates' position must be the same buffer, and
+    the fused op runs before the updates (it reads cache columns before pos,
+    which they do not write).  The append form reads the caches with pos = C."""
     if _off("PJRT_OCL_DECODE_ATTN"):
         return
     outs = set(prog.outputs)
@@ -1123,9 +1127,9 @@ def fuse_decode_attention(prog: V.VMProgram) -> None:
             m = _match_decode(prog, ix, sc, consts, outs, si)
             if m is None:
                 continue
-            (q, kbuf, vbuf, kc, vc, posb, H, C, hd, krow, scale, out, chain, last, qgather, dk, dv) = m
+            (q, kbuf, vbuf, kc, vc, posb, H, C, hd, krow, scale, out, chain, last, qgather, dk, dv, masked) = m
             desc = len(prog.aux)
-            prog.aux.extend([hd | int(krow) << 16 | 1 << 17, kbuf, vbuf, posb, _bits(scale)])
+            prog.aux.extend([hd | int(krow) << 16 | int(masked) << 17, kbuf, vbuf, posb, _bits(scale)])
             fused = V.Instr(V.OP_DECODE_ATTN, dst=out, a=q, b=kc, n=H, imm=C, imm2=vc, aux=desc,
                             reads_hint=(vc, kbuf, vbuf, posb))
             # the op reads cache columns before pos only, which the updates do
@@ -1135,8 +1139,8 @@ def fuse_decode_attention(prog: V.VMProgram) -> None:
             seq = ([qgather] if qgather is not None else []) + [fused]
             slots = sorted(set(chain) | {last})
             others = [j for b in (kc, vc) for j in ix.live_readers(b)
-                      if min(dk, dv) < j <= last and j not in chain and j not in (dk, dv)]
-            if not others:
+                      if masked and min(dk, dv) < j <= last and j not in chain and j not in (dk, dv)]
+            if masked and not others:
                 seq += [instrs[dk], instrs[dv]] if dk < dv else [instrs[dv], instrs[dk]]
                 slots = sorted(set(slots) | {dk, dv})
             for j in slots:
@@ -1148,10 +1152,12 @@ def fuse_decode_attention(prog: V.VMProgram) -> None:
 
 
 def _match_decode(prog, ix, sc, consts, outs, si):
-    """The pieces of one masked decode attention around softmax ``si``, or None."""
+    """The pieces of one decode attention around softmax ``si``, or None: the
+    masked form (caches updated at pos, keys <= pos) or the append form (keys
+    and values concatenated with the step's own, no mask)."""
     instrs = prog.instrs
     SM = instrs[si]
-    C, rows = SM.imm, SM.n
+    nkeys, rows = SM.imm, SM.n
     consumed, scale, sel, dot1 = [], 1.0, None, None
     cur = SM.a
     for _ in range(6):
@@ -1164,12 +1170,12 @@ def _match_decode(prog, ix, sc, consts, outs, si):
         if P.op == V.OP_DOT:
             dot1 = w
             break
-        if P.op == V.OP_AFFINE_F32 and not P.imm2 and P.n == rows * C:
+        if P.op == V.OP_AFFINE_F32 and not P.imm2 and P.n == rows * nkeys:
             scale *= _f(P.imm)
-        elif P.op in (V.OP_MUL_F32, V.OP_DIV_F32) and not P.imm and P.imm2 and P.n == rows * C and \
+        elif P.op in (V.OP_MUL_F32, V.OP_DIV_F32) and not P.imm and P.imm2 and P.n == rows * nkeys and \
                 _is_splat(prog, P.imm2) and P.b in consts and consts[P.b] not in (0.0,):
             scale = scale * consts[P.b] if P.op == V.OP_MUL_F32 else scale / consts[P.b]
-        elif P.op == V.OP_SELECT_F32 and sel is None and P.n == rows * C:
+        elif P.op == V.OP_SELECT_F32 and sel is None and P.n == rows * nkeys:
             neg = _eval_const(prog, ix, _peel_broadcast(prog, ix, P.b))
             if neg is None or neg.size != 1 or not (float(neg[0]) == -math.inf or float(neg[0]) <= -1e30):
                 return None
@@ -1180,11 +1186,11 @@ def _match_decode(prog, ix, sc, consts, outs, si):
             return None
         consumed.append(w)
         cur = P.a
-    if dot1 is None or sel is None:
+    if dot1 is None:
         return None
     D1 = instrs[dot1]
     M1, N1, hd, G1, av1, bv1, epi1, _ = _dot_fields_pass(D1)
-    if M1 != 1 or N1 != C or G1 != rows or len(ix.live_readers(D1.dst)) != 1 or D1.dst in outs:
+    if M1 != 1 or N1 != nkeys or G1 != rows or len(ix.live_readers(D1.dst)) != 1 or D1.dst in outs:
         return None
     if epi1:
         e = epi1 - 1
@@ -1209,7 +1215,7 @@ def _match_decode(prog, ix, sc, consts, outs, si):
     if D2.op != V.OP_DOT or D2.a != p_buf:
         return None
     M2, N2, K2, G2, av2, bv2, epi2, _ = _dot_fields_pass(D2)
-    if av2 or epi2 or G2 != H or M2 != 1 or K2 != C or N2 != hd:
+    if av2 or epi2 or G2 != H or M2 != 1 or K2 != nkeys or N2 != hd:
         return None
     out, tail = D2.dst, []
     rs = ix.live_readers(out)
@@ -1221,52 +1227,42 @@ def _match_decode(prog, ix, sc, consts, outs, si):
     if adt not in (V.DT_F32, V.DT_F16, V.DT_BF16) or _dt(prog, D1.b) != adt or _dt(prog, D2.b) != adt \
             or _dt(prog, out) != adt or _elems(prog, out) != H * hd:
         return None
-    if hd % 8 or hd > 256 or C % 8 or C > 0xFFFF:
-        return None
     if len({sc[x] for x in [dot1, si, d2i] + consumed + mid + tail}) != 1:
         return None
     last = tail[-1] if tail else d2i
-    # the caches: K as rows [H, C, hd] (dot1 reads its transpose) or as K^T
-    kc, vc = D1.b, D2.b
-    kview = _canonical_view(prog, bv1, H * hd * C)
-    if _elems(prog, kc) != H * C * hd or _elems(prog, vc) != H * C * hd or _canonical_view(prog, bv2, H * C * hd):
+    # the keys as dot1 reads them: rows [H, nkeys, hd] (read through the
+    # transpose) or K^T [H, hd, nkeys]
+    kview = _canonical_view(prog, bv1, H * hd * nkeys)
+    if _elems(prog, D1.b) != H * nkeys * hd or _elems(prog, D2.b) != H * nkeys * hd or \
+            _canonical_view(prog, bv2, H * nkeys * hd):
         return None
     if kview == 0:
-        krow, kshape = False, (H, hd, 1)
-    elif _merged(*_view_desc(prog, kview)) == _merged([H, hd, C], [C * hd, 1, hd], 0):
-        krow, kshape = True, (H, 1, hd)
+        krow = False
+    elif _merged(*_view_desc(prog, kview)) == _merged([H, hd, nkeys], [nkeys * hd, 1, hd], 0):
+        krow = True
     else:
         return None
-    if krow and hd & (hd - 1):
+    if sel is not None:
+        m = _masked_decode_parts(prog, ix, sc, instrs[sel].imm, D1, D2, dot1, d2i, last, H, nkeys, hd,
+                                 krow, adt)
+    else:
+        m = _append_decode_parts(prog, ix, sc, D1, D2, dot1, last, H, nkeys, hd, krow, adt)
+    if m is None:
         return None
-    # the updates that wrote pos's column just before: same position buffer
-    dk = _last_writer(ix, kc, dot1, sc)
-    dv = _last_writer(ix, vc, d2i, sc)
-    if dk is None or dv is None:
-        return None
-    uk = _dus_fields(prog, instrs[dk])
-    uv = _dus_fields(prog, instrs[dv])
-    if uk is None or uv is None:
-        return None
-    kdims, kids, kbuf = uk
-    vdims, vids, vbuf = uv
-    if tuple(kdims) != kshape or tuple(vdims) != (H, 1, hd):
-        return None
-    posb = kids[1] if krow else kids[2]
-    if vids[1] != posb or prog.buffers[posb].dtype != V.DT_I32 or _elems(prog, posb) != 1:
-        return None
-    if _elems(prog, kbuf) != H * hd or _elems(prog, vbuf) != H * hd or _dt(prog, kbuf) != adt or \
-            _dt(prog, vbuf) != adt:
+    kc, vc, kbuf, vbuf, posb, C, masked, dk, dv = m
+    if hd % 8 or hd > 256 or C % 8 or C < 8 or C > 0xFFFF or (krow and hd & (hd - 1)):
         return None
     # nothing rewrites what the fused op reads between its sources and ``last``
     # (no region op in between either: its sub-list could)
-    if any(instrs[j].op in _REGION_OPS for j in range(min(dk, dv, dot1), last) if sc[j] == sc[si]):
+    lo = min(x for x in (dk, dv, dot1) if x is not None)
+    if any(instrs[j].op in _REGION_OPS for j in range(lo, last) if sc[j] == sc[si]):
         return None
-    for buf, since in ((kc, dk), (vc, dv), (kbuf, dk), (vbuf, dv), (posb, dk), (posb, dv), (D1.a, dot1)):
-        if any(since < w <= last for w in ix.writers.get(buf, ())):
+    srcs = [(kc, dk), (vc, dv), (kbuf, dk), (vbuf, dv), (D1.a, dot1)]
+    if masked:
+        srcs += [(posb, dk), (posb, dv)]
+    for buf, since in srcs:
+        if any((since if since is not None else dot1) < w <= last for w in ix.writers.get(buf, ())):
             return None
-    if not _mask_is_key_le_pos(prog, ix, instrs[sel].imm, posb, C):
-        return None
     # q: the dot's A rows [H, 1, hd], contiguous
     qv = _canonical_view(prog, av1, H * hd)
     q, qgather = D1.a, None
@@ -1278,8 +1274,78 @@ def _match_decode(prog, ix, sc, consts, outs, si):
         vdesc = len(prog.aux)
         prog.aux.extend([1, H * hd, 1, off])
         qgather = V.Instr(V.OP_GATHER_STRIDED, dst=q, a=D1.a, n=H * hd, aux=vdesc)
+    if posb is None:
+        posb = _new_buffer(prog, 1, V.DT_I32)
+        prog.consts.append((posb, np.array([C], "<i4").tobytes()))
     chain = consumed + [dot1, si, d2i] + mid + tail
-    return (q, kbuf, vbuf, kc, vc, posb, H, C, hd, krow, scale, out, chain, last, qgather, dk, dv)
+    return (q, kbuf, vbuf, kc, vc, posb, H, C, hd, krow, scale, out, chain, last, qgather, dk, dv, masked)
+
+
+def _masked_decode_parts(prog, ix, sc, pred, D1, D2, dot1, d2i, last, H, C, hd, krow, adt):
+    """The masked form: the caches dot1 / dot2 read were just updated at pos
+    (dynamic_update_slice, the same position buffer for both) and the mask is
+    key <= pos.  (kc, vc, k, v, pos, C, masked, update_k, update_v) or None."""
+    kc, vc = D1.b, D2.b
+    dk = _last_writer(ix, kc, dot1, sc)
+    dv = _last_writer(ix, vc, d2i, sc)
+    if dk is None or dv is None:
+        return None
+    uk = _dus_fields(prog, prog.instrs[dk])
+    uv = _dus_fields(prog, prog.instrs[dv])
+    if uk is None or uv is None:
+        return None
+    kdims, kids, kbuf = uk
+    vdims, vids, vbuf = uv
+    if tuple(kdims) != ((H, 1, hd) if krow else (H, hd, 1)) or tuple(vdims) != (H, 1, hd):
+        return None
+    posb = kids[1] if krow else kids[2]
+    if vids[1] != posb or prog.buffers[posb].dtype != V.DT_I32 or _elems(prog, posb) != 1:
+        return None
+    if _elems(prog, kbuf) != H * hd or _elems(prog, vbuf) != H * hd or _dt(prog, kbuf) != adt or \
+            _dt(prog, vbuf) != adt:
+        return None
+    if not _mask_is_key_le_pos(prog, ix, pred, posb, C):
+        return None
+    return kc, vc, kbuf, vbuf, posb, C, True, dk, dv
+
+
+def _append_decode_parts(prog, ix, sc, D1, D2, dot1, last, H, nkeys, hd, krow, adt):
+    """The append form (tools/bench_decode.py:47-52): the keys are
+    concatenate([K cache, k], axis 1) and the values likewise, both as rows
+    [H, C + 1, hd], every key visible.  The op then reads the caches in place
+    with pos = C.  (kc, vc, k, v, None, C, masked, None, None) or None."""
+    if not krow:
+        return None
+    C = nkeys - 1
+    got = []
+    for buf in (D1.b, D2.b):
+        ws = ix.writers.get(buf, ())
+        if len(ws) != 2 or len([j for j in ix.live_readers(buf) if j not in ws]) != 1:
+            return None
+        parts = {}
+        for w in ws:
+            S_ = prog.instrs[w]
+            if S_.op != V.OP_SCATTER or not S_.disjoint or sc[w] != sc[dot1] or w > dot1:
+                return None
+            a = S_.aux
+            rank = prog.aux[a]
+            if rank != 3:
+                return None
+            dims = tuple(prog.aux[a + 1:a + 4])
+            st = tuple(prog.aux[a + 4:a + 7])
+            off = prog.aux[a + 7]
+            if st != (nkeys * hd, hd, 1):
+                return None
+            parts[(dims, off)] = S_.a
+        cache, new = parts.get(((H, C, hd), 0)), parts.get(((H, 1, hd), C * hd))
+        if cache is None or new is None or prog.instrs[ws[0]].disjoint != prog.instrs[ws[1]].disjoint:
+            return None
+        if _elems(prog, cache) != H * C * hd or _elems(prog, new) != H * hd or _dt(prog, cache) != adt or \
+                _dt(prog, new) != adt:
+            return None
+        got.append((cache, new))
+    (kc, kbuf), (vc, vbuf) = got
+    return kc, vc, kbuf, vbuf, None, C, False, None, None
 
 
 def _dot_fields_pass(ins):
@@ -1647,9 +1713,9 @@ def run_all(prog: V.VMProgram) -> None:
     dce(prog)
     fuse_mma_epilogue(prog)
     dce(prog)
-    fuse_attention(prog)
-    dce(prog)
     fuse_decode_attention(prog)
+    dce(prog)
+    fuse_attention(prog)
     dce(prog)
     fuse_region(prog)
     dce(prog)

@@ -561,11 +561,12 @@ def _instr_reads(ins: V.Instr, prog: V.VMProgram) -> set:
         r = {ins.a}
     elif op == V.OP_DOT:
         r = {ins.a, ins.b}
-        epi_res = ins.epi_res
+        epi, epi_res = ins.epi, ins.epi_res
         if ins.aux and not (ins.aview or ins.bview or ins.epi):
-            if prog.aux[ins.aux + 2]:
-                epi_res = prog.aux[ins.aux + 3]
-        if epi_res:
+            epi, epi_res = prog.aux[ins.aux + 2], prog.aux[ins.aux + 3]
+        # the residual / bias is read when a micro-op takes it as its source
+        # (buffer 0 is a valid residual: the test is the epilogue's, not the id)
+        if epi and any(prog.aux[epi + 1 + 4 * k] in (1, 2) for k in range(prog.aux[epi - 1])):
             r.add(epi_res)
     else:
         r = {ins.a, ins.b}

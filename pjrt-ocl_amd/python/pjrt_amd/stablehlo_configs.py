@@ -493,3 +493,140 @@ module @jit_generate {{
   }}
 }}
 """
+
+
+# ---- the reference's decode benchmark step ---------------------------------------------------
+
+DECODE_STEP_CONFIGS = {              # (d_model, heads, d_ff, layers, context): tools/bench_decode.py:21-31
+    "small": (256, 4, 1024, 4, 128),
+    "base": (512, 8, 2048, 6, 256),
+    "large": (1024, 16, 4096, 6, 512),
+}
+DECODE_STEP_KEYS = ("ln1_b", "ln1_g", "ln2_b", "ln2_g", "w1", "w2", "wk", "wo", "wq", "wv")
+
+
+def decode_step_params(cfg):
+    """[(name, shape)] of the step's f32 inputs in jit argument order: x, kc,
+    vc, then each layer's parameter dict flattened by sorted key (JAX's pytree
+    order for a dict)."""
+    D, H, F, L, C = cfg
+    hd = D // H
+    shapes = {"ln1_b": (D,), "ln1_g": (D,), "ln2_b": (D,), "ln2_g": (D,), "w1": (D, F), "w2": (F, D),
+              "wk": (D, D), "wo": (D, D), "wq": (D, D), "wv": (D, D)}
+    out = [("x", (1, D)), ("kc", (L, H, C, hd)), ("vc", (L, H, C, hd))]
+    for l in range(L):
+        out += [(f"{l}.{k}", shapes[k]) for k in DECODE_STEP_KEYS]
+    return out
+
+
+def decode_step(cfg):
+    """One token of tools/bench_decode.py:35-65 (the reference's decode
+    benchmark), f32 throughout, ``cfg`` = (d_model, heads, d_ff, layers, C):
+
+        def step(x, kc, vc, params):          # x (1, D); kc, vc (L, H, C, hd)
+            for li, p in enumerate(params):
+                h = ln(x, p["ln1_g"], p["ln1_b"])       # mean / var by .mean(), (v + eps) ** -0.5
+                q, k, v = ((h @ p[w]).reshape(H, 1, hd) for w in ("wq", "wk", "wv"))
+                kk = jnp.concatenate([kc[li], k], axis=1)  # (H, C + 1, hd)
+                vv = jnp.concatenate([vc[li], v], axis=1)
+                a = softmax((q @ jnp.swapaxes(kk, -1, -2)) * hd ** -0.5)
+                x = x + (a @ vv).reshape(1, D) @ p["wo"]
+                h = ln(x, p["ln2_g"], p["ln2_b"])
+                x = x + gelu(h @ p["w1"]) @ p["w2"]   # 0.5 x (1 + tanh(c (x + 0.044715 x ** 3)))
+            return x"""
+    D, H, F, L, C = cfg
+    hd = D // H
+    params = decode_step_params(cfg)
+    pname = {n: f"%a{k}" for k, (n, _) in enumerate(params)}
+    args = [f"%a{k}: {_t(s)}" for k, (_, s) in enumerate(params)]
+    e = _Emit()
+    X, R1 = (1, D), (1, 1)
+
+    def mean_keep(v, shape):
+        s = e.reduce(v, shape, 1, "add", 0.0)
+        s = e.bin("divide", s, e.splat(float(shape[1]), (1,)), (1,))
+        return e.reshape(s, (1,), R1, "f32")
+
+    def ln(x, g, b):
+        m = mean_keep(x, X)
+        xc = e.bin("subtract", x, e.bcast(m, R1, X, [0, 1]), X)
+        v = mean_keep(e.bin("multiply", xc, xc, X), X)
+        ve = e.bin("add", v, e.splat(1e-5, R1), R1)
+        r = e.bin("power", ve, e.splat(-0.5, R1), R1)
+        y = e.bin("multiply", xc, e.bcast(r, R1, X, [0, 1]), X)
+        y = e.bin("multiply", y, e.bcast(g, (D,), X, [1]), X)
+        return e.bin("add", y, e.bcast(b, (D,), X, [1]), X)
+
+    def mm(a, w, k, n):
+        return e.dot(a, w, (1, k), (k, n), (1, n), "f32", "f32")
+
+    x = pname["x"]
+    S3, KK = (H, 1, C + 1), (H, C + 1, hd)
+    for l in range(L):
+        p = lambda n: pname[f"{l}.{n}"]
+        h = ln(x, p("ln1_g"), p("ln1_b"))
+        q, k, v = (e.reshape(mm(h, p(w), D, D), X, (H, 1, hd), "f32") for w in ("wq", "wk", "wv"))
+        parts = []
+        for cache, new in (("kc", k), ("vc", v)):
+            sl = e.slice(pname[cache], (L, H, C, hd), (l, 0, 0, 0), (l + 1, H, C, hd), "f32")
+            sl = e.reshape(sl, (1, H, C, hd), (H, C, hd), "f32")
+            parts.append(e.new(f"stablehlo.concatenate {sl}, {new}, dim = 1 : ({_t((H, C, hd))}, "
+                               f"{_t((H, 1, hd))}) -> {_t(KK)}"))
+        kk, vv = parts
+        kt = e.transpose(kk, KK, (0, 2, 1), "f32")
+        s = e.dot(q, kt, (H, 1, hd), (H, hd, C + 1), S3, "f32", "f32", lb=(0,), rb=(0,), lc=(2,), rc=(1,))
+        s = e.bin("multiply", s, e.splat(hd ** -0.5, S3), S3)
+        mi = e.new("stablehlo.constant dense<0xFF800000> : tensor<f32>")
+        mx = e.new(f"stablehlo.reduce({s} init: {mi}) applies stablehlo.maximum across dimensions = [2] : "
+                   f"({_t(S3)}, tensor<f32>) -> {_t((H, 1))}")
+        mx = e.reshape(mx, (H, 1), (H, 1, 1), "f32")
+        ex = e.un("exponential", e.bin("subtract", s, e.bcast(mx, (H, 1, 1), S3, [0, 1, 2]), S3), S3)
+        sm = e.reshape(e.reduce(ex, S3, 2, "add", 0.0), (H, 1), (H, 1, 1), "f32")
+        a = e.bin("divide", ex, e.bcast(sm, (H, 1, 1), S3, [0, 1, 2]), S3)
+        o = e.dot(a, vv, S3, KK, (H, 1, hd), "f32", "f32", lb=(0,), rb=(0,), lc=(2,), rc=(1,))
+        o = e.reshape(o, (H, 1, hd), X, "f32")
+        x = e.bin("add", x, mm(o, p("wo"), D, D), X)
+        h = ln(x, p("ln2_g"), p("ln2_b"))
+        f = mm(h, p("w1"), D, F)
+        F2 = (1, F)
+        f3 = e.bin("multiply", e.bin("multiply", f, f, F2), f, F2)
+        t = e.bin("add", f, e.bin("multiply", e.splat(0.044715, F2), f3, F2), F2)
+        t = e.un("tanh", e.bin("multiply", e.splat(0.7978845608, F2), t, F2), F2)
+        t = e.bin("add", e.splat(1.0, F2), t, F2)
+        g = e.bin("multiply", e.bin("multiply", e.splat(0.5, F2), f, F2), t, F2)
+        x = e.bin("add", x, mm(g, p("w2"), F, D), X)
+    body = "\n".join(e.lines)
+    return f"""
+module @jit__lambda_ {{
+  func.func public @main({', '.join(args)}) -> ({_t(X)}) {{
+{body}
+    return {x} : {_t(X)}
+  }}
+}}
+"""
+
+
+def decode_step_inputs(cfg, seed=0):
+    """Inputs of decode_step in its argument order, drawn as
+    tools/bench_decode.py:68-80 draws them (weights, caches ~ N(0, 0.02), x ~
+    N(0, 1), layernorm gains 1 and shifts 0; numpy's generator, not the same
+    stream)."""
+    import numpy as np
+    rng = np.random.default_rng(seed)
+    out = []
+    for name, shape in decode_step_params(cfg):
+        key = name.split(".")[-1]
+        if key in ("ln1_g", "ln2_g"):
+            out.append(np.ones(shape, np.float32))
+        elif key in ("ln1_b", "ln2_b"):
+            out.append(np.zeros(shape, np.float32))
+        else:
+            out.append((rng.standard_normal(shape) * (1.0 if name == "x" else 0.02)).astype(np.float32))
+    return out
+
+
+def decode_step_bytes(cfg) -> int:
+    """Bytes one step must read (tools/bench_decode.py:83-89): the f32 weights
+    once and the two caches."""
+    D, H, F, L, C = cfg
+    return L * (4 * D * D + 2 * D * F) * 4 + L * 2 * H * C * (D // H) * 4

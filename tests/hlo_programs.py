@@ -9,6 +9,8 @@ variadic reduce over (value, iota)); which exact StableHLO a given JAX version
 emits is not pinned here."""
 
 
+import numpy as np
+
 from pjrt_amd.stablehlo_configs import _t, attention, ln_gelu, matmul, mlp  # noqa: F401
 
 
@@ -199,3 +201,34 @@ module @jit_f {{
   }}
 }}
 """
+
+
+def decode_step_reference(cfg, arrays):
+    """tools/bench_decode.py:35-65 restated in float64 numpy: one decode token
+    through the layers, keys and values appended to the caches."""
+    from pjrt_amd import stablehlo_configs as SC
+    D, H, F, L, C = cfg
+    hd = D // H
+    P = {n: a.astype(np.float64) for (n, _), a in zip(SC.decode_step_params(cfg), arrays)}
+    x, kc, vc = P["x"], P["kc"], P["vc"]
+
+    def ln(x, g, b):
+        m = x.mean(-1, keepdims=True)
+        v = ((x - m) ** 2).mean(-1, keepdims=True)
+        return (x - m) / np.sqrt(v + 1e-5) * g + b
+
+    def gelu(x):
+        return 0.5 * x * (1.0 + np.tanh(0.7978845608 * (x + 0.044715 * x ** 3)))
+
+    for l in range(L):
+        p = lambda n: P[f"{l}.{n}"]
+        h = ln(x, p("ln1_g"), p("ln1_b"))
+        q, k, v = ((h @ p(w)).reshape(H, 1, hd) for w in ("wq", "wk", "wv"))
+        kk = np.concatenate([kc[l], k], 1)
+        vv = np.concatenate([vc[l], v], 1)
+        s = q @ kk.transpose(0, 2, 1) * hd ** -0.5
+        a = np.exp(s - s.max(-1, keepdims=True))
+        a /= a.sum(-1, keepdims=True)
+        x = x + (a @ vv).reshape(1, D) @ p("wo")
+        x = x + gelu(ln(x, p("ln2_g"), p("ln2_b")) @ p("w1")) @ p("w2")
+    return x

@@ -125,3 +125,20 @@ def test_lowered_gpt_decode_full_size_first_steps():
     assert check_decoder(got, want, 5e-3) >= 1
     hand, _ = blob_for(CF.gpt_c5(c, emit_logits=True))
     assert check_decoder(got, run_gpu(hand, args), 5e-3) >= 1
+
+
+@pytest.mark.parametrize("name", ["small", "base"])
+def test_reference_decode_step(name):
+    """One token of the reference's decode benchmark (tools/bench_decode.py,
+    f32, keys and values appended by concatenate), lowered: the GPU against
+    the oracle and against the float64 numpy statement of the step."""
+    import hlo_programs as HP
+    from pjrt_amd import lowering as L
+    from pjrt_amd import stablehlo_configs as SC
+    cfg = SC.DECODE_STEP_CONFIGS[name]
+    args = SC.decode_step_inputs(cfg, seed=1)
+    got, want = run_both(L.lower_text(SC.decode_step(cfg)), args, oracle="tensor")
+    ref = HP.decode_step_reference(cfg, args)
+    atol = 1e-4 * float(np.abs(ref).max())          # f32 GEMVs: summation order differs
+    assert_rel(got[0], want[0], 1e-4, atol, f"decode step {name} vs oracle")
+    assert_rel(got[0], ref, 1e-4, atol, f"decode step {name} vs numpy")

@@ -347,6 +347,36 @@ def test_gather_scatter_iota_dyn_embedding():
         np.testing.assert_array_equal(gv, wv, err_msg=f"output {k}")
 
 
+@pytest.mark.parametrize("ew_ts", [64, 4096])
+def test_gather_scatter_16_byte_runs(ew_ts):
+    """Views whose innermost axis is contiguous move 16-byte runs (four loads in
+    flight per thread): a transpose keeping the inner axis, row slices (one
+    contiguous run), an inner slice at a 16-byte offset, a broadcast, concat
+    pieces (scatters), in f32, bf16, bool and i64; an inner slice at an odd
+    offset takes the element path.  Bit-exact against the oracle, tiles cut
+    inside rows (ew_ts 64)."""
+    rng = np.random.default_rng(61)
+    a = rng.standard_normal((6, 10, 8)).astype(np.float32)
+    b = rng.standard_normal((4, 6, 16)).astype(np.float32)
+    c = rng.integers(0, 2, (3, 5, 32)).astype(V.DT_NUMPY[V.DT_BOOL])
+    e = rng.integers(-2 ** 40, 2 ** 40, (4, 3, 6)).astype(np.int64)
+    g = G.Graph()
+    x, y, z, w = g.input(a.shape), g.input(b.shape, "bf16"), g.input(c.shape, "bool"), g.input(e.shape, "i64")
+    outs = [g.transpose(x, (1, 0, 2)), g.slice(x, (2, 0, 0), (5, 10, 8)), g.slice(x, (0, 0, 4), (6, 10, 8)),
+            g.slice(x, (0, 0, 1), (6, 10, 5)), g.broadcast(g.slice(x, (0, 0, 0), (1, 10, 8)), (3, 10, 8), (0, 1, 2)),
+            g.concatenate([x, g.slice(x, (0, 0, 0), (6, 3, 8))], 1), g.transpose(y, (1, 0, 2)),
+            g.concatenate([y, y], 2), g.transpose(z, (1, 0, 2)), g.slice(z, (1, 0, 16), (3, 5, 32)),
+            g.transpose(w, (1, 0, 2))]
+    g.output(*outs)
+    got, want = run_both(g.build(), [a, V.f32_to_bf16(b), c, e], ew_ts=ew_ts)
+    for k, (gv, wv) in enumerate(zip(got, want)):
+        np.testing.assert_array_equal(gv, wv, err_msg=f"output {k}")
+    np.testing.assert_array_equal(got[0], a.transpose(1, 0, 2))
+    np.testing.assert_array_equal(got[5], np.concatenate([a, a[:, :3]], 1))
+    np.testing.assert_array_equal(got[8], c.transpose(1, 0, 2))
+    np.testing.assert_array_equal(got[10], e.transpose(1, 0, 2))
+
+
 # --- matmul --------------------------------------------------------------------------------------
 
 @pytest.mark.parametrize("dt", ["f32", "bf16"])

@@ -385,6 +385,28 @@ def test_gpt_prefill_attention_gets_the_matrix_core_layout():
     assert np.abs(logits - ref_logits).max() <= 1e-5 * np.abs(ref_logits).max()
 
 
+@pytest.mark.parametrize("fused", [True, False])
+def test_reference_decode_step(fused, monkeypatch):
+    """The reference's decode benchmark step (tools/bench_decode.py: f32, keys
+    and values appended with concatenate, no mask) against its float64 numpy
+    statement.  Fused, each layer's attention is one OP_DECODE_ATTN reading the
+    caches in place (no concatenation is built)."""
+    from pjrt_amd import stablehlo_configs as SC
+    if not fused:
+        monkeypatch.setenv("PJRT_OCL_DECODE_ATTN", "0")
+    cfg = (64, 2, 128, 2, 16)
+    prog = L.lower_text(SC.decode_step(cfg))
+    args = SC.decode_step_inputs(cfg, seed=4)
+    (got,) = run(prog, args)
+    want = H.decode_step_reference(cfg, args)
+    np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-5 * np.abs(want).max())
+    ops = live_ops(prog)
+    if fused:
+        assert ops.count(V.OP_DECODE_ATTN) == 2 and V.OP_SCATTER not in ops and V.OP_SOFTMAX not in ops
+    else:
+        assert V.OP_DECODE_ATTN not in ops
+
+
 def test_gpt_decode_unfused_and_planted_mask(monkeypatch):
     """Without the decode fusion the decomposed chain (bf16 probabilities) still
     decodes the same tokens; a planted mask (key < pos: the step's own key

@@ -488,3 +488,21 @@ def test_lane_fit_follows_the_measured_barrier_cost():
     dear = S.DeviceConfig(nlanes=256, costs={"barrier_us": 1.0, "barrier_us_per_lane": 0.5})
     assert S.lane_fit(prog, cheap) == 256
     assert S.lane_fit(prog, dear) == 128
+
+
+def test_residual_buffer_zero_is_a_read():
+    """A matmul epilogue's residual that is buffer 0 (the first input) is read:
+    the id is no 'no residual' marker, the epilogue's sources say so."""
+    g = G.Graph()
+    x = g.input((1, 16))
+    w = g.input((16, 16))
+    y = g.dot(x, w, residual=x, epilogue=[(V.SUB_ADD, 1, 0.0, 0.0)])
+    g.output(y)
+    prog = g.build()
+    (dot,) = [i for i in prog.instrs if i.op == V.OP_DOT]
+    assert x.buf == 0 and 0 in S.instr_reads(dot, prog)
+    g2 = G.Graph()
+    x2, w2 = g2.input((1, 16)), g2.input((16, 16))
+    g2.output(g2.dot(x2, w2))
+    (dot2,) = [i for i in g2.build().instrs if i.op == V.OP_DOT]
+    assert S.instr_reads(dot2, g2.build()) == {0, 1}

@@ -477,7 +477,7 @@ VM_DEV bool is_kt_view(const VM_K int32_t* aux, uint32_t kv, uint32_t H, uint32_
 // whole, since it maps virtual onto real blocks).  One call per lane, so the
 // register save / restore of the call is paid once.
 template <int HD, bool BF16>
-VM_TILE void attn_fast(Args A, uint32_t ti, uint32_t lo, uint32_t hi) {
+VM_LEAF void attn_fast(Args A, uint32_t ti, uint32_t lo, uint32_t hi) {
   A = uargs(A);
   const VM_K Task& t = task_of(A, ti);
   const AttnDesc P = attn_desc(A, t);
@@ -495,7 +495,7 @@ VM_TILE void attn_fast(Args A, uint32_t ti, uint32_t lo, uint32_t hi) {
   }
 }
 
-VM_TILE void flash_attn_tiles(Args A, uint32_t ti, uint32_t lo, uint32_t hi) {
+VM_DEV void flash_attn_tiles(Args A, uint32_t ti, uint32_t lo, uint32_t hi) {
   A = uargs(A);
   const VM_K Task& t = task_of(A, ti);
   const AttnDesc P = attn_desc(A, t);

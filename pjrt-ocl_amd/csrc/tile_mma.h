@@ -446,7 +446,7 @@ VM_DEV void store_fast(Args A, const MmaDesc& D, const f32x16 (&acc)[4][4], uint
 }
 
 template <bool BF16>
-VM_TILE void mma_tile16_fast(Args A, const MmaDesc* Dp, uint32_t tile) {
+VM_LEAF void mma_tile16_fast(Args A, const MmaDesc* Dp, uint32_t tile) {
   A = uargs(A);
   const MmaDesc D = load_desc(Dp);
   uint16_t* lds = lds_ptr<uint16_t>();
@@ -693,7 +693,7 @@ struct F32Stage {
   }
 };
 
-VM_TILE void mma_tile32_fast(Args A, const MmaDesc* Dp, uint32_t tile) {
+VM_LEAF void mma_tile32_fast(Args A, const MmaDesc* Dp, uint32_t tile) {
   A = uargs(A);
   const MmaDesc D = load_desc(Dp);
   float* lds = lds_ptr<float>();
@@ -753,7 +753,7 @@ constexpr int kMmaLdsBytes0 = Lds16<256>::kBytes > Lds32<256>::kBytes ? Lds16<25
 constexpr int kMmaLdsBytes1 = kFastLdsBytes > kMmaLdsBytes0 ? kFastLdsBytes : kMmaLdsBytes0;
 constexpr int kMmaLdsBytes = kF32FastLdsBytes > kMmaLdsBytes1 ? kF32FastLdsBytes : kMmaLdsBytes1;
 
-VM_TILE void mma_tiles(Args A, uint32_t ti, uint32_t lo, uint32_t hi) {
+VM_DEV void mma_tiles(Args A, uint32_t ti, uint32_t lo, uint32_t hi) {
   A = uargs(A);
   const VM_K Task& t = task_of(A, ti);
   MmaDesc D;

@@ -274,7 +274,45 @@ def bench_gemm(rt, dt, steps, warmup, M=4096, N=4096, K=4096):
             "ms_per_step": ms_step, "kernel_ms": ms_kernel,
             "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": MFMA_PEAK_TFLOPS[dt], "unit": "TFLOP/s",
                          "frac": round(tf / MFMA_PEAK_TFLOPS[dt], 4)},
-            "max_rel_err_64_rows": err}
+            "max_rel_err_64_rows": err, "vendor_library_tflops": library_gemm_tflops(dt, M, N, K)}
+
+
+def library_gemm_tflops(dt, M, N, K, steps=20):
+    """torch.matmul on the same shape and operand dtype (the vendor BLAS:
+    hipBLASLt / rocBLAS), timed with events on torch's stream in a child
+    process of its own: what AMD's own library reaches on this box, for
+    comparison only.  Its output is in the operand dtype (bf16 writes half the
+    bytes of this build's f32 output).  Skipped with --no-vendor (profiling
+    runs: torch's own kernels under a tracer are not ours to measure)."""
+    if os.environ.get("PJRT_AMD_BENCH_NO_VENDOR") == "1":
+        return None
+    code = f"""
+import torch
+tdt = torch.bfloat16 if {dt!r} == "bf16" else torch.float32
+torch.backends.cuda.matmul.allow_tf32 = False
+a = torch.randn({M}, {K}, device="cuda", dtype=tdt)
+b = torch.randn({K}, {N}, device="cuda", dtype=tdt)
+for _ in range(5):
+    c = a @ b
+torch.cuda.synchronize()
+e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+e0.record()
+for _ in range({steps}):
+    c = a @ b
+e1.record()
+torch.cuda.synchronize()
+print(2.0 * {M} * {N} * {K} / (e0.elapsed_time(e1) / {steps} * 1e-3) / 1e12)
+"""
+    import subprocess
+    try:
+        r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=120)
+        if r.returncode != 0:
+            log(f"vendor GEMM not measured: exit {r.returncode}")
+            return None
+        return round(float(r.stdout.strip().splitlines()[-1]), 1)
+    except (subprocess.SubprocessError, ValueError, IndexError) as e:
+        log(f"vendor GEMM not measured: {e}")
+        return None
 
 
 def bench_attention(rt, steps, warmup, B=4, H=16, S=2048, D=128):
@@ -620,6 +658,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workloads", default="c1,c2,c3,c4,c5,lowered")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-vendor", action="store_true",
+                    help="skip the vendor-library comparison figures (torch.matmul in a child process)")
     ap.add_argument("--device-profile", action="store_true",
                     help="profiling aid: print the per-task device profile of the C5 decode step and exit")
     ap.add_argument("--skip-c2", action="store_true",
@@ -629,6 +669,8 @@ def main():
     if args.gpus != 1:
         raise SystemExit("bench.py measures one GPU: this build has no multi-GPU path "
                          "(each GPU would run its own shard of the same megakernel; see DESIGN.md)")
+    if args.no_vendor:
+        os.environ["PJRT_AMD_BENCH_NO_VENDOR"] = "1"
     if args.device_profile:
         os.environ["PJRT_AMD_PROFILE"] = "1"       # read when the runtime is created
     from pjrt_amd.runtime import Runtime

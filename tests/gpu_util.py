@@ -81,3 +81,30 @@ def close_runtime():
     if _RT is not None:
         _RT.close()
         _RT = None
+
+
+def assert_product_elementwise(got, want, scale, rtol, what=""):
+    """Elementwise check of a matmul or attention output: |got - want| <= rtol *
+    scale, with ``scale`` the same product taken over absolute values (|A| |B|
+    for a GEMM, P |V| for attention).  A dot product's rounding error is bounded
+    by a multiple of that sum, so this is the north star's per-element relative
+    bar without a tolerance that blows up where the result cancels to ~0."""
+    got = np.asarray(got, np.float64).reshape(np.shape(want))
+    bad = ~(np.abs(got - want) <= rtol * scale)
+    if bad.any():
+        idx = np.argwhere(bad)[:5]
+        raise AssertionError(f"{what}: {int(bad.sum())} elements outside rtol {rtol} of their |.| product scale; "
+                             f"first {[tuple(i) for i in idx]}: got {[got[tuple(i)] for i in idx]} "
+                             f"want {[want[tuple(i)] for i in idx]} scale {[scale[tuple(i)] for i in idx]}")
+
+
+def attention_abs_scale(q, kt, v, scale, causal):
+    """P |V| in float64 for attention(q [H,T,hd], kt [H,hd,C], v [H,C,hd])."""
+    H, T, hd = q.shape
+    C = kt.shape[2]
+    s = np.einsum("htd,hdc->htc", q.astype(np.float64), kt.astype(np.float64)) * scale
+    if causal:
+        s = np.where(np.arange(C)[None, :] > np.arange(T)[:, None] + (C - T), -np.inf, s)
+    p = np.exp(s - s.max(-1, keepdims=True))
+    p /= p.sum(-1, keepdims=True)
+    return np.einsum("htc,hcd->htd", p, np.abs(v.astype(np.float64)))

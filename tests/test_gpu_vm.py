@@ -14,7 +14,7 @@ import numpy as np
 import pytest
 
 import vmprogs as P
-from gpu_util import as_f32, assert_rel, blob_for, run_both, runtime
+from gpu_util import as_f32, assert_product_elementwise, assert_rel, attention_abs_scale, blob_for, run_both, runtime
 from oracle import vmref
 from pjrt_amd import graph as G
 from pjrt_amd import vmprogram as V
@@ -411,6 +411,8 @@ def test_dot_random_tolerance_and_tiles(dt, rtol):
         got, _ = run_both(g.build(), [a, b], oracle=None)
         err = np.abs(got[0] - want).max() / np.abs(want).max()
         assert err <= rtol, (tile, err)
+        assert_product_elementwise(got[0], want, np.abs(a).astype(np.float64) @ np.abs(b).astype(np.float64), rtol,
+                                   f"{dt} tile {tile}")
 
 
 @pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
@@ -597,6 +599,9 @@ def test_flash_attention(dt, hd, causal, T, C):
     tol = 1e-3 if dt == "f32" else 1e-2
     err = np.abs(got[0] - want).max() / max(1e-6, np.abs(want).max())
     assert err <= tol, err
+    assert_product_elementwise(got[0], want.astype(np.float64),
+                               attention_abs_scale(q, np.transpose(k, (0, 2, 1)), v, 1.0 / np.sqrt(hd), causal), tol,
+                               f"flash {dt} hd {hd}")
 
 
 @pytest.mark.parametrize("dt,causal,T,C,target", [("bf16", True, 512, 512, 150.0), ("f16", False, 256, 384, 22.0)])

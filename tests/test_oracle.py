@@ -770,3 +770,22 @@ def test_planted_shift_mask_is_caught(monkeypatch):
     monkeypatch.setattr(vmref, "_int_op", wrong)
     with pytest.raises(AssertionError):
         test_ew_integer_bit_exact("i32", "shl")
+
+
+def test_elementwise_product_bound_catches_a_planted_error():
+    """The GPU tests' elementwise GEMM / attention check (|got - want| <= rtol
+    |A||B| per element) passes a bf16-rounded product and fails one element
+    perturbed by 2 % of its scale, including where the product cancels to ~0."""
+    from gpu_util import assert_product_elementwise
+    rng = np.random.default_rng(3)
+    a = rng.standard_normal((32, 48))
+    b = rng.standard_normal((48, 40))
+    want = a @ b
+    scale = np.abs(a) @ np.abs(b)
+    got = V.bf16_to_f32(V.f32_to_bf16(want.astype(np.float32)))
+    assert_product_elementwise(got, want, scale, 1e-2)
+    i = np.unravel_index(np.argmin(np.abs(want)), want.shape)
+    bad = got.astype(np.float64).copy()
+    bad[i] += 0.02 * scale[i]
+    with pytest.raises(AssertionError):
+        assert_product_elementwise(bad, want, scale, 1e-2)

@@ -101,6 +101,14 @@ __global__ __launch_bounds__(kBlock, 1) void vm_main(VmArgs args) {
   grid_barrier_init(A);
   const LaneSpan span = load_span((const VM_K LaneSpan*)A->lanes + lane);
   const VM_K Entry* ents = (const VM_K Entry*)A->entries + span.off;
+  // the loader put the task of the lane's first entry in span.pad: request the
+  // entry and that task record together (one scalar round trip, not two)
+  if (span.pad != 0xFFFFFFFFu) {
+    const Entry e0 = load_entry(ents);
+    const VM_K Task& t0 = task_of(A, span.pad);
+    asm volatile("" ::"s"(e0.tile_hi), "s"(t0.tile_op), "s"(t0.dst), "s"(t0.a), "s"(t0.b), "s"(t0.p[0]), "s"(t0.p[4]),
+                 "s"(t0.p[7]));
+  }
 
   uint32_t f_pc[kMaxDepth], f_end[kMaxDepth], f_own[kMaxDepth], f_phase[kMaxDepth];
   int sp = 0;

@@ -805,6 +805,19 @@ static uint64_t task_scratch_bytes(const Task& t) {
   return 0;
 }
 
+// The device copy of the lane table carries, in each span's pad word, the
+// task of the lane's first entry (0xFFFFFFFF when it is a control entry or the
+// lane has none): the kernel then requests that entry and its task record
+// together at launch instead of one after the other.
+static std::vector<LaneSpan> device_lanes(const std::vector<LaneSpan>& lanes, const std::vector<Entry>& entries) {
+  std::vector<LaneSpan> out = lanes;
+  for (LaneSpan& s : out) {
+    s.pad = 0xFFFFFFFFu;
+    if (s.root_len && s.off < entries.size() && entries[s.off].task < ENT_FOR) s.pad = entries[s.off].task;
+  }
+  return out;
+}
+
 // Host half of a load: parse, validate, choose ports, patch buffer ids to handles
 // and lay out the task scratch.  Fills lp (program, tile sizes, ports, I/O sizes,
 // scratch size) and the patched tables in `pr`; touches no device memory.
@@ -986,7 +999,8 @@ int vmrt_load(vmrt_runtime* rt, const void* bytes, size_t len, uint32_t ew_ts, u
   if (e == hipSuccess) e = up(reinterpret_cast<void**>(&lp->aux), aux.data(), aux.size() * 4);
   if (e == hipSuccess) e = up(reinterpret_cast<void**>(&lp->tasks), tasks.data(), tasks.size() * sizeof(Task));
   if (e == hipSuccess) e = up(reinterpret_cast<void**>(&lp->entries), entries.data(), entries.size() * sizeof(Entry));
-  if (e == hipSuccess) e = up(reinterpret_cast<void**>(&lp->lanes), P.lanes.data(), P.lanes.size() * sizeof(LaneSpan));
+  const std::vector<LaneSpan> dlanes = device_lanes(P.lanes, entries);
+  if (e == hipSuccess) e = up(reinterpret_cast<void**>(&lp->lanes), dlanes.data(), dlanes.size() * sizeof(LaneSpan));
   if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&lp->ctl), BAR_WORDS * 4);
   if (e == hipSuccess) e = hipMemset(lp->ctl, 0, BAR_WORDS * 4);
   if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&lp->scratch), std::max<uint64_t>(lp->scratch_bytes, 256));
@@ -1168,7 +1182,8 @@ int vmrt_run_noalloc(vmrt_runtime* rt, const void* bytes, size_t len, uint32_t e
   up(o_aux, pr.aux.data(), pr.aux.size() * 4);
   up(o_tasks, pr.tasks.data(), pr.tasks.size() * sizeof(Task));
   up(o_ent, pr.entries.data(), pr.entries.size() * sizeof(Entry));
-  up(o_lanes, P.lanes.data(), P.lanes.size() * sizeof(LaneSpan));
+  const std::vector<LaneSpan> dlanes = device_lanes(P.lanes, pr.entries);
+  up(o_lanes, dlanes.data(), dlanes.size() * sizeof(LaneSpan));
   for (auto& c : P.consts) up(o_arena + P.buffers[c.first].off, c.second.data(), c.second.size());
   if (e != hipSuccess) return set_err(err, errlen, VMRT_INTERNAL, "vmrt_run_noalloc upload: " + hip_msg(e));
   lp.arena = base + o_arena;

@@ -266,74 +266,64 @@ VM_TILE void mma_tile16(Args A, const MmaDesc* Dp, uint32_t tile) {
 // ---------------------------------------------------------------------------------
 // For unviewed row-major operands with M and N multiples of 256 and K a multiple of
 // 64 (the big square GEMMs).  Each wave owns a 128 x 128 quadrant as 4 x 4 blocks
-// of 32 x 32 accumulators (all 256 AGPRs).  The A slab (256 x 64) is staged
-// row-major; the B slab (64 x 256) is transposed in registers on its way to LDS
-// (8 x 8 blocks of 16-bit values, v_perm_b32), so that every MFMA operand fragment
-// is one ds_read_b128.  Rows are padded to 72 elements (144 B): the eight lanes of
-// a ds_read_b128 / ds_write_b128 phase then hit disjoint banks.  Global loads for
-// slab s+1 are in flight while the matrix cores consume slab s.
-constexpr int kFBK = 64;                          // K slab (elements)
-constexpr int kFLd = kFBK + 8;                    // LDS row stride (elements)
-constexpr int kFBuf = 2 * 256 * kFLd;             // elements per stage: A + B^T
-constexpr int kFastLdsBytes = 2 * kFBuf * 2;      // two stages of 16-bit elements
+// of 32 x 32 accumulators (all 256 AGPRs).  Both operand slabs go from global
+// memory straight into LDS (global_load_lds_dwordx4, no register staging), two
+// stages of 64 KiB:
+//   A slab, 256 rows x 64 k: rows of 128 B, dense.  The eight 16-byte k chunks of
+//     row r sit at slots chunk ^ ((r >> 1) & 7), so the 16 rows one ds_read_b128
+//     of a fragment touches in a cycle hit 16 distinct bank groups.
+//   B slab, 64 k rows x 256 n, as B is laid out (rows of 512 B).  The 32 chunks of
+//     row k sit at slots chunk ^ 4 (k & 3).  A fragment (8 k values of one column
+//     per lane) is read with two ds_read_b64_tr_b16: in each group of 16 lanes,
+//     lane 4e + q points at row k0 + e, columns n0 + 4q .. +3, and the transposed
+//     read gives lane i column n0 + i at rows k0 .. k0 + 3.  The 32 lanes of a half
+//     wave read four rows, 64 B each, whose swizzled slots cover the 64 banks once.
+constexpr int kFBK = 64;                                // K slab (elements)
+constexpr uint32_t kFStage = 65536;                     // bytes per stage: A 32 KiB + B 32 KiB
+constexpr uint32_t kFStageB = 32768;                    // B's offset in a stage
+constexpr int kFStoreBytes = 128 * (256 + 4) * 4;       // store_fast's staging tile
+constexpr int kFastLdsBytes = 2 * int(kFStage) > kFStoreBytes ? 2 * int(kFStage) : kFStoreBytes;
 
-struct FastStage {
-  v4u ra[8], rb[8];
+typedef __attribute__((address_space(3))) uint8_t lds_u8;
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+typedef __attribute__((address_space(3))) u16x8 lds_u16x8;
 
-  // A: chunk c = t + 256 j is row c / 8, k chunk c % 8.  B: thread t takes the
-  // 8 x 8 block of k group t % 8 and n chunk t / 8 (one 16-byte row piece per k).
-  // a, b: uniform slab origins (A at row m0 / column k0, B at row k0 / column n0);
-  // per-thread offsets are 32-bit so the loads take an SGPR base.
-  VM_DEV void load_a(const gbyte* a, uint32_t K) {
-    const uint32_t t = threadIdx.x;
-    const uint32_t oa = ((t >> 3) * K + (t & 7) * 8) * 2;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) ra[j] = *(const VM_G v4u*)(a + (oa + uint32_t(j) * 64u * K));
-  }
-  VM_DEV void load_b(const gbyte* b, uint32_t N) {
-    const uint32_t t = threadIdx.x;
-    const uint32_t ob = ((t & 7) * 8 * N + (t >> 3) * 8) * 2;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) rb[i] = *(const VM_G v4u*)(b + (ob + uint32_t(i) * 2u * N));
-  }
-  VM_DEV void load(const gbyte* a, const gbyte* b, uint32_t K, uint32_t N) {
-    load_a(a, K);
-    load_b(b, N);
-  }
+// One 16-byte global -> LDS transfer per lane: lane l of the wave writes LDS bytes
+// [lds + 16 l, +16) with base[voff].  Issued from asm: the compiler, which cannot
+// tell which LDS bytes the transfer writes, would otherwise wait for it before
+// every LDS read.  The tile waits for its transfers itself (vmcnt) before the
+// block barrier that publishes a stage.  One wait state between the M0 write and
+// the transfer that reads it.
+VM_DEV void dma16(const gbyte* base, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
+               :
+               : "s"(lds), "v"(voff), "s"(base)
+               : "memory", "m0");
+}
+VM_DEV void wait_vm0() { __builtin_amdgcn_s_waitcnt(0x0F70); }    // s_waitcnt vmcnt(0)
+VM_DEV void wait_vm16() { __builtin_amdgcn_s_waitcnt(0x4F70); }   // s_waitcnt vmcnt(16)
 
-  VM_DEV void store_a(uint16_t* s) const {
-    const uint32_t t = threadIdx.x;
-    uint16_t* la = s + (t >> 3) * kFLd + (t & 7) * 8;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) *reinterpret_cast<v4u*>(la + 32 * j * kFLd) = ra[j];
+// The transfers of one slab: 8 rounds for A, 8 for B, one dwordx4 per thread each.
+// A round j fills stage bytes [4096 j, +4096): wave w rows 32 j + 8 w + l / 8; B
+// round j fills [32768 + 4096 j, +4096): wave w k rows 8 j + 2 w + l / 32.  Each
+// lane fetches the chunk whose swizzled slot is its own 16 bytes.
+struct FastDma {
+  uint32_t oa, ob;        // per-lane byte offsets of round 0 in the A and B slabs
+  uint32_t wo;            // the wave's 1 KiB within a round (wave-uniform)
+  VM_DEV void init(uint32_t K, uint32_t N) {
+    const uint32_t l = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const uint32_t ra = 8 * w + (l >> 3);
+    oa = ra * K * 2 + (((l & 7) ^ ((ra >> 1) & 7)) * 16);
+    const uint32_t rb = 2 * w + (l >> 5);
+    ob = rb * N * 2 + (((l & 31) ^ (4 * (rb & 3))) * 16);
+    wo = uni(1024 * w);
   }
-  // Pins the staged B registers at this point: the transpose below cannot be
-  // hoisted above it (up to the global loads, which would wait for them at the top
-  // of the slab).
-  VM_DEV void pin_b() {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) asm volatile("" : "+v"(rb[i]));
-  }
-  VM_DEV void store_b(uint16_t* s) const {
-    const uint32_t t = threadIdx.x;
-    uint16_t* lb = s + 256 * kFLd + (t >> 3) * 8 * kFLd + (t & 7) * 8;
-#pragma unroll
-    for (int jn = 0; jn < 8; ++jn) {
-      // column n = 8 * (t / 8) + jn: its 16-bit value from each of the 8 k rows
-      const uint32_t sel = (jn & 1) ? 0x07060302u : 0x05040100u;
-      const int w = jn >> 1;
-      v4u o;
-      o.x = __builtin_amdgcn_perm(rb[1][w], rb[0][w], sel);
-      o.y = __builtin_amdgcn_perm(rb[3][w], rb[2][w], sel);
-      o.z = __builtin_amdgcn_perm(rb[5][w], rb[4][w], sel);
-      o.w = __builtin_amdgcn_perm(rb[7][w], rb[6][w], sel);
-      *reinterpret_cast<v4u*>(lb + jn * kFLd) = o;
-    }
-  }
-  VM_DEV void store(uint16_t* s) {
-    store_a(s);
-    pin_b();
-    store_b(s);
+  // round r of 16 (A rounds 0-7, B rounds 8-15) of the slab at a (A[m0, k0]) and
+  // b (B[k0, n0]) into the stage at LDS address st
+  VM_DEV void round(const gbyte* a, const gbyte* b, uint32_t K, uint32_t N, uint32_t st, int r) const {
+    if (r < 8) dma16(a + uint64_t(r) * 64 * K, oa, st + wo + 4096 * r);
+    else dma16(b + uint64_t(r - 8) * 16 * N, ob, st + kFStageB + wo + 4096 * (r - 8));
   }
 };
 
@@ -449,7 +439,8 @@ template <bool BF16>
 VM_LEAF void mma_tile16_fast(Args A, const MmaDesc* Dp, uint32_t tile) {
   A = uargs(A);
   const MmaDesc D = load_desc(Dp);
-  uint16_t* lds = lds_ptr<uint16_t>();
+  const uint32_t lds0 = uni(uint32_t(reinterpret_cast<uintptr_t>(lds_ptr<lds_u8>())));
+  const lds_u8* L = (const lds_u8*)lds0;
   uint32_t g, m0, n0;
   fast_origin(D, uni(tile), &g, &m0, &n0);
   const uint32_t K = D.K, N = D.N;
@@ -463,27 +454,36 @@ VM_LEAF void mma_tile16_fast(Args A, const MmaDesc* Dp, uint32_t tile) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
   const uint32_t nk = K / kFBK;
-  FastStage st;
-  st.load(a, b, K, N);
-  __syncthreads();                      // the previous user of the LDS is done
-  st.store(lds);
-  __syncthreads();
-  const uint32_t fa = (wm * 128 + (lane & 31)) * kFLd + (lane >> 5) * 8;
-  const uint32_t fb = 256 * kFLd + (wn * 128 + (lane & 31)) * kFLd + (lane >> 5) * 8;
-  // Operand fragments of one 16-deep k step, double-buffered: the fragments of
-  // step kk+1 are read while the MFMAs of step kk run.  Per slab:
-  //   kk 0: MFMAs
-  //   kk 1: MFMAs interleaved with the next slab's A going into the idle stage,
-  //         then the A loads of the slab after it
-  //   kk 2: the same for B, transposed on the way
-  //   block barrier (the idle stage is complete; the current one fully read)
-  //   kk 3: MFMAs, while the first fragments of the next slab are read
+  FastDma dm;
+  dm.init(K, N);
+  auto slab_a = [&](uint32_t s) { return a + uint64_t(s) * kFBK * 2; };
+  auto slab_b = [&](uint32_t s) { return b + uint64_t(s) * kFBK * N * 2; };
+  // Fragment addresses within a stage.  A, block i, k step kk: row wm 128 + 32 i +
+  // (l & 31), chunk 2 kk + (l >> 5).  B, block j, k step kk: this lane points at
+  // row 16 kk + 8 (g >> 1) + e (+ 4 for the second read), column wn 128 + 32 j +
+  // 16 (g & 1) + 4 q, where g = l >> 4, e = (l >> 2) & 3, q = l & 3.
+  uint32_t fa[4], fb[4];
+  {
+    const uint32_t r = wm * 128 + (lane & 31), sw = (r >> 1) & 7;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) fa[kk] = r * 128 + (((2 * kk + (lane >> 5)) ^ sw) * 16);
+    const uint32_t gq = lane >> 4, e = (lane >> 2) & 3, q = lane & 3;
+    const uint32_t row = 8 * (gq >> 1) + e;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      fb[j] = kFStageB + row * 512 + ((wn * 16 + 4 * (uint32_t(j) ^ e) + 2 * (gq & 1) + (q >> 1)) * 16) + (q & 1) * 8;
+  }
   u16x8 af[2][4], bfr[2][4];
-  auto frags = [&](int p, const uint16_t* stage, int kk) {
+  auto frags = [&](int p, uint32_t st, int kk) {
+    const lds_u8* S = L + (st - lds0);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) af[p][i] = *reinterpret_cast<const u16x8*>(stage + fa + i * 32 * kFLd + kk * 16);
+    for (int i = 0; i < 4; ++i) af[p][i] = *(const lds_u16x8*)(S + fa[kk] + 4096 * i);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) bfr[p][j] = *reinterpret_cast<const u16x8*>(stage + fb + j * 32 * kFLd + kk * 16);
+    for (int j = 0; j < 4; ++j) {
+      const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(S + fb[j] + 8192 * kk));
+      const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(S + fb[j] + 8192 * kk + 2048));
+      bfr[p][j] = __builtin_bit_cast(u16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+    }
   };
   auto mfmas = [&](int p) {
 #pragma unroll
@@ -491,16 +491,29 @@ VM_LEAF void mma_tile16_fast(Args A, const MmaDesc* Dp, uint32_t tile) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) acc[i][j] = mfma16<BF16>(af[p][i], bfr[p][j], acc[i][j]);
   };
-  // The staged registers hold slab ks+1 during slab ks; each half is refilled with
-  // slab ks+2 right after it is written to LDS, so a load has about a whole slab
-  // of MFMAs to land.  (Past the last slab the last slab is reloaded: harmless.)
-  auto slab_a = [&](uint32_t s) { return a + uint64_t(min(s, nk - 1) * kFBK) * 2; };
-  auto slab_b = [&](uint32_t s) { return b + uint64_t(min(s, nk - 1) * kFBK) * N * 2; };
-  st.load(slab_a(1), slab_b(1), K, N);
-  frags(0, lds, 0);
-  for (uint32_t ks = 0; ks < nk; ++ks) {
-    const uint16_t* cur = lds + (ks & 1) * kFBuf;
-    uint16_t* nxt = lds + ((ks + 1) & 1) * kFBuf;
+  const uint32_t st0 = lds0, st1 = lds0 + kFStage;
+  __syncthreads();                      // the previous user of the LDS is done
+#pragma unroll
+  for (int r = 0; r < 16; ++r) dm.round(slab_a(0), slab_b(0), K, N, st0, r);
+  if (nk > 1) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) dm.round(slab_a(1), slab_b(1), K, N, st1, r);
+    wait_vm16();                        // slab 0 landed; slab 1 may still be in flight
+  } else {
+    wait_vm0();
+  }
+  __syncthreads();
+  frags(0, st0, 0);
+  // Per slab: k steps 0-2 read the next step's fragments while their MFMAs run;
+  // then this lane's transfers of slab ks+1 are waited for and the block barrier
+  // publishes that stage (and retires every read of the current one); k step 3's
+  // MFMAs then run interleaved with the transfers of slab ks+2 into the stage just
+  // retired, after the first fragments of slab ks+1 are requested (past the last
+  // slab they read a stale stage and go unused).  Each slab is one basic block, so
+  // the accumulators stay in their AGPRs: the last two slabs, which transfer
+  // nothing, run in a loop of their own.
+  auto slab = [&](uint32_t ks, auto dma) {
+    const uint32_t cur = (ks & 1) ? st1 : st0, nxt = (ks & 1) ? st0 : st1;
     __builtin_amdgcn_sched_barrier(0);
     frags(1, cur, 1);
     __builtin_amdgcn_sched_barrier(0);
@@ -509,35 +522,33 @@ VM_LEAF void mma_tile16_fast(Args A, const MmaDesc* Dp, uint32_t tile) {
     frags(0, cur, 2);
     __builtin_amdgcn_sched_barrier(0);
     mfmas(1);
-    st.store_a(nxt);
-#pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);   // 1 MFMA
-      __builtin_amdgcn_sched_group_barrier(0x200, 1, 1);   // 1 DS write
-    }
-    __builtin_amdgcn_sched_group_barrier(0x008, 8, 1);
     __builtin_amdgcn_sched_barrier(0);
-    st.load_a(slab_a(ks + 2), K);
     frags(1, cur, 3);
-    st.pin_b();
     __builtin_amdgcn_sched_barrier(0);
     mfmas(0);
-    st.store_b(nxt);
-#pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 2);   // 1 MFMA
-      __builtin_amdgcn_sched_group_barrier(0x002, 4, 2);   // 4 VALU (v_perm_b32)
-      __builtin_amdgcn_sched_group_barrier(0x200, 1, 2);   // 1 DS write
-    }
-    __builtin_amdgcn_sched_group_barrier(0x008, 8, 2);
     __builtin_amdgcn_sched_barrier(0);
-    st.load_b(slab_b(ks + 2), N);
+    wait_vm0();
     __syncthreads();
     frags(0, nxt, 0);
     __builtin_amdgcn_sched_barrier(0);
-    mfmas(1);
+    if constexpr (decltype(dma)::value) {
+      const gbyte* an = slab_a(ks + 2);
+      const gbyte* bn = slab_b(ks + 2);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        acc[r >> 2][r & 3] = mfma16<BF16>(af[1][r >> 2], bfr[1][r & 3], acc[r >> 2][r & 3]);
+        __builtin_amdgcn_sched_barrier(0);
+        dm.round(an, bn, K, N, cur, r);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    } else {
+      mfmas(1);
+    }
     __builtin_amdgcn_sched_barrier(0);
-  }
+  };
+  uint32_t ks = 0;
+  for (; ks + 2 < nk; ++ks) slab(ks, std::true_type());
+  for (; ks < nk; ++ks) slab(ks, std::false_type());
   if (D.dt == DT_F32) store_fast<true>(A, D, acc, g, m0, n0);
   else store_fast<false>(A, D, acc, g, m0, n0);
 }

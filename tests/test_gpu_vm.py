@@ -416,11 +416,13 @@ def test_dot_random_tolerance_and_tiles(dt, rtol):
 
 
 @pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
-@pytest.mark.parametrize("Gb,M,K,N", [(1, 512, 320, 768), (1, 1024, 128, 2048), (2, 256, 192, 1024)])
+@pytest.mark.parametrize("Gb,M,K,N", [(1, 512, 320, 768), (1, 1024, 128, 2048), (2, 256, 192, 1024),
+                                      (1, 256, 64, 512)])
 def test_dot_fast_path_exact(dt, Gb, M, K, N):
     """256 x 256 output tiles (the MFMA fast paths: 16-bit operands in K slabs of
     64, f32 in slabs of 16; 1024 x 2048 also takes the XCD tile swizzle, Gb=2 the
-    batch offsets): integer-valued operands give the exact f32 result."""
+    batch offsets, K=64 a single 16-bit slab): integer-valued operands give the
+    exact f32 result."""
     rng = np.random.default_rng(72)
     a = rng.integers(-3, 4, (Gb, M, K)).astype(np.float32)
     b = rng.integers(-3, 4, (Gb, K, N)).astype(np.float32)

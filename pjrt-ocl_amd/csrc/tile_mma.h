@@ -270,8 +270,9 @@ VM_TILE void mma_tile16(Args A, const MmaDesc* Dp, uint32_t tile) {
 // memory straight into LDS (global_load_lds_dwordx4, no register staging), two
 // stages of 64 KiB:
 //   A slab, 256 rows x 64 k: rows of 128 B, dense.  The eight 16-byte k chunks of
-//     row r sit at slots chunk ^ ((r >> 1) & 7), so the 16 rows one ds_read_b128
-//     of a fragment touches in a cycle hit 16 distinct bank groups.
+//     row r sit at slots chunk ^ aswz(r), so that a fragment's ds_read_b128 hits
+//     distinct bank groups both in any 16 consecutive lanes (16 rows, one chunk)
+//     and in lanes 0-7 with 32-39 (8 rows, chunks c and c + 1).
 //   B slab, 64 k rows x 256 n, as B is laid out (rows of 512 B).  The 32 chunks of
 //     row k sit at slots chunk ^ 4 (k & 3).  A fragment (8 k values of one column
 //     per lane) is read with two ds_read_b64_tr_b16: in each group of 16 lanes,
@@ -283,6 +284,13 @@ constexpr uint32_t kFStage = 65536;                     // bytes per stage: A 32
 constexpr uint32_t kFStageB = 32768;                    // B's offset in a stage
 constexpr int kFStoreBytes = 128 * (256 + 4) * 4;       // store_fast's staging tile
 constexpr int kFastLdsBytes = 2 * int(kFStage) > kFStoreBytes ? 2 * int(kFStage) : kFStoreBytes;
+
+// A-slab slot swizzle of row r: ((r >> 1) & 3) << 1 | ((r >> 3) & 1).  Rows of one
+// parity among 16 consecutive rows get 8 distinct values; among 8 consecutive
+// rows (aligned), 4 values whose halves (bits 1-2) differ, so chunks c and c ^ 1
+// of those rows land on 8 distinct slots.  A 128-byte row spans half the banks,
+// so rows of opposite parity never meet.
+VM_DEV uint32_t aswz(uint32_t r) { return (((r >> 1) & 3) << 1) | ((r >> 3) & 1); }
 
 typedef __attribute__((address_space(3))) uint8_t lds_u8;
 typedef short s16x4 __attribute__((ext_vector_type(4)));
@@ -302,7 +310,7 @@ VM_DEV void dma16(const gbyte* base, uint32_t voff, uint32_t lds) {
                : "memory", "m0");
 }
 VM_DEV void wait_vm0() { __builtin_amdgcn_s_waitcnt(0x0F70); }    // s_waitcnt vmcnt(0)
-VM_DEV void wait_vm16() { __builtin_amdgcn_s_waitcnt(0x4F70); }   // s_waitcnt vmcnt(16)
+VM_DEV void wait_vm8() { __builtin_amdgcn_s_waitcnt(0x0F78); }    // s_waitcnt vmcnt(8)
 
 // The transfers of one slab: 8 rounds for A, 8 for B, one dwordx4 per thread each.
 // A round j fills stage bytes [4096 j, +4096): wave w rows 32 j + 8 w + l / 8; B
@@ -314,7 +322,7 @@ struct FastDma {
   VM_DEV void init(uint32_t K, uint32_t N) {
     const uint32_t l = threadIdx.x & 63, w = threadIdx.x >> 6;
     const uint32_t ra = 8 * w + (l >> 3);
-    oa = ra * K * 2 + (((l & 7) ^ ((ra >> 1) & 7)) * 16);
+    oa = ra * K * 2 + (((l & 7) ^ aswz(ra)) * 16);
     const uint32_t rb = 2 * w + (l >> 5);
     ob = rb * N * 2 + (((l & 31) ^ (4 * (rb & 3))) * 16);
     wo = uni(1024 * w);
@@ -464,7 +472,7 @@ VM_LEAF void mma_tile16_fast(Args A, const MmaDesc* Dp, uint32_t tile) {
   // 16 (g & 1) + 4 q, where g = l >> 4, e = (l >> 2) & 3, q = l & 3.
   uint32_t fa[4], fb[4];
   {
-    const uint32_t r = wm * 128 + (lane & 31), sw = (r >> 1) & 7;
+    const uint32_t r = wm * 128 + (lane & 31), sw = aswz(r);
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) fa[kk] = r * 128 + (((2 * kk + (lane >> 5)) ^ sw) * 16);
     const uint32_t gq = lane >> 4, e = (lane >> 2) & 3, q = lane & 3;
@@ -497,27 +505,42 @@ VM_LEAF void mma_tile16_fast(Args A, const MmaDesc* Dp, uint32_t tile) {
   for (int r = 0; r < 16; ++r) dm.round(slab_a(0), slab_b(0), K, N, st0, r);
   if (nk > 1) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) dm.round(slab_a(1), slab_b(1), K, N, st1, r);
-    wait_vm16();                        // slab 0 landed; slab 1 may still be in flight
+    for (int r = 0; r < 8; ++r) dm.round(slab_a(1), slab_b(1), K, N, st1, r);
+    wait_vm8();                         // slab 0 landed; slab 1's A rounds may be in flight
   } else {
     wait_vm0();
   }
   __syncthreads();
   frags(0, st0, 0);
-  // Per slab: k steps 0-2 read the next step's fragments while their MFMAs run;
-  // then this lane's transfers of slab ks+1 are waited for and the block barrier
-  // publishes that stage (and retires every read of the current one); k step 3's
-  // MFMAs then run interleaved with the transfers of slab ks+2 into the stage just
-  // retired, after the first fragments of slab ks+1 are requested (past the last
-  // slab they read a stale stage and go unused).  Each slab is one basic block, so
-  // the accumulators stay in their AGPRs: the last two slabs, which transfer
-  // nothing, run in a loop of their own.
-  auto slab = [&](uint32_t ks, auto dma) {
+  // Per slab: k steps 0-2 read the next step's fragments while their MFMAs run,
+  // and k step 0 issues the B rounds of slab ks+1 (one per two MFMAs) into the
+  // other stage; then this lane's transfers of slab ks+1 are waited for and the
+  // block barrier publishes that stage (and retires every read of the current
+  // one); k step 3's MFMAs then run beside the A rounds of slab ks+2 into the
+  // stage just retired, after the first fragments of slab ks+1 are requested (past
+  // the last slab they read a stale stage and go unused).  Each slab is one basic
+  // block, so the accumulators stay in their AGPRs: the last two slabs, which
+  // transfer less, run outside the main loop.
+  auto mfma_r = [&](int p, int r) {
+    acc[r >> 2][r & 3] = mfma16<BF16>(af[p][r >> 2], bfr[p][r & 3], acc[r >> 2][r & 3]);
+  };
+  auto slab = [&](uint32_t ks, auto da, auto db) {
     const uint32_t cur = (ks & 1) ? st1 : st0, nxt = (ks & 1) ? st0 : st1;
     __builtin_amdgcn_sched_barrier(0);
     frags(1, cur, 1);
     __builtin_amdgcn_sched_barrier(0);
-    mfmas(0);
+    if constexpr (decltype(db)::value) {
+      const gbyte* bn = slab_b(ks + 1);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        mfma_r(0, r);
+        __builtin_amdgcn_sched_barrier(0);
+        if (r & 1) dm.round(a, bn, K, N, nxt, 8 + (r >> 1));
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    } else {
+      mfmas(0);
+    }
     __builtin_amdgcn_sched_barrier(0);
     frags(0, cur, 2);
     __builtin_amdgcn_sched_barrier(0);
@@ -531,14 +554,13 @@ VM_LEAF void mma_tile16_fast(Args A, const MmaDesc* Dp, uint32_t tile) {
     __syncthreads();
     frags(0, nxt, 0);
     __builtin_amdgcn_sched_barrier(0);
-    if constexpr (decltype(dma)::value) {
+    if constexpr (decltype(da)::value) {
       const gbyte* an = slab_a(ks + 2);
-      const gbyte* bn = slab_b(ks + 2);
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        acc[r >> 2][r & 3] = mfma16<BF16>(af[1][r >> 2], bfr[1][r & 3], acc[r >> 2][r & 3]);
+        mfma_r(1, r);
         __builtin_amdgcn_sched_barrier(0);
-        dm.round(an, bn, K, N, cur, r);
+        if (r & 1) dm.round(an, b, K, N, cur, r >> 1);
         __builtin_amdgcn_sched_barrier(0);
       }
     } else {
@@ -547,8 +569,9 @@ VM_LEAF void mma_tile16_fast(Args A, const MmaDesc* Dp, uint32_t tile) {
     __builtin_amdgcn_sched_barrier(0);
   };
   uint32_t ks = 0;
-  for (; ks + 2 < nk; ++ks) slab(ks, std::true_type());
-  for (; ks < nk; ++ks) slab(ks, std::false_type());
+  for (; ks + 2 < nk; ++ks) slab(ks, std::true_type(), std::true_type());
+  if (ks + 1 < nk) slab(ks++, std::false_type(), std::true_type());
+  if (ks < nk) slab(ks, std::false_type(), std::false_type());
   if (D.dt == DT_F32) store_fast<true>(A, D, acc, g, m0, n0);
   else store_fast<false>(A, D, acc, g, m0, n0);
 }

@@ -6,16 +6,19 @@
 //
 // Matrix-core path (bf16/f16, hd = 64 or 128, scale > 0, K read through the usual
 // [H,hd,C] transpose view of a [H,C,hd] buffer): a lane takes 256 query rows, 64
-// per wave as two 32-row sub-tiles, and streams K/V in 64-key blocks staged
-// through LDS (double-buffered, one barrier per block).  Per sub-tile each wave
-// computes
+// per wave as two 32-row sub-tiles, and streams K/V in 64-key blocks that go
+// from global memory straight into LDS (global_load_lds_dwordx4; double-buffered,
+// one barrier per block).  Per sub-tile each wave computes
 //   S^T (keys x 32 queries) = K_blk (keys x hd) . Q^T (hd x 32)
 // so both MFMA operands are contiguous along hd, and the S^T accumulators are
 // already the B operand of
 //   O^T (hd x 32 queries) += V_blk^T (hd x keys) . P^T (keys x 32 queries).
-// V is stored transposed in LDS (rows = hd, columns = keys; transposed in
-// registers with byte permutes on the way in) so an A fragment of V^T is one
-// 16-byte LDS read.  Key rows of a 32-key half are read permuted (kperm) so that
+// K and V blocks keep their [key][hd] layout in LDS, rows dense, 16-byte hd
+// chunks at swizzled slots (kswz, vswz).  A K fragment is one ds_read_b128; an A
+// fragment of V^T (8 consecutive keys of one hd column per lane) is two
+// ds_read_b64_tr_b16 (in each group of 16 lanes, lane 4e + q points at key row
+// k0 + e, hd columns d0 + 4q .. +3, and receives column d0 + lane % 16 at rows
+// k0 .. k0 + 3).  Key rows of a 32-key half are read permuted (kperm) so that
 // the 8 keys a lane holds per 16-key MFMA step are consecutive.  K and V
 // fragments are read once per wave and used by both sub-tiles.
 //
@@ -38,15 +41,31 @@ namespace vm {
 
 constexpr int kAttnKeys = 64;            // keys per streamed block
 constexpr int kAttnRows = 256;           // query rows per lane step (4 waves x 64)
-constexpr int kAttnLdV = kAttnKeys + 8;  // V^T row stride (elements): 16-byte aligned rows
 template <int HD>
 struct AttnLds {
-  static constexpr int kLdK = HD + 8;                         // K row stride (elements)
-  static constexpr int kKBuf = kAttnKeys * kLdK;
-  static constexpr int kBuf = kKBuf + HD * kAttnLdV;          // elements per stage
-  static constexpr int kBytes = 2 * kBuf * 2;
+  static constexpr uint32_t kRow = HD * 2;                    // bytes per key row
+  static constexpr uint32_t kKBytes = kAttnKeys * kRow;       // K block; V block follows
+  static constexpr uint32_t kStage = 2 * kKBytes;
+  static constexpr uint32_t kRounds = kKBytes / 4096;         // block-wide 16-byte transfers per operand
+  static constexpr int kBytes = 2 * int(kStage);
 };
 constexpr int kAttnLdsBytes = AttnLds<128>::kBytes;
+
+// Slot swizzles of the 16-byte hd chunks of key row r (chunk c at slot c ^ swz).
+// K (ds_read_b128 fragments, rows kperm-ordered): distinct bank groups for any 16
+// consecutive lanes and for lanes 0-7 with 32-39.  V (transposed reads of four
+// consecutive rows, 64 bytes each, per half wave): the four rows' pieces cover
+// the 64 banks once.
+template <int HD>
+VM_DEV uint32_t kswz(uint32_t r) {
+  if constexpr (HD == 128) return (((r & 3) | (((r >> 3) & 1) << 2)) << 1) | ((r >> 2) & 1);
+  else return ((((r >> 1) & 1) | (((r >> 3) & 1) << 1)) << 1) | ((r >> 2) & 1);
+}
+template <int HD>
+VM_DEV uint32_t vswz(uint32_t r) {
+  if constexpr (HD == 128) return 4 * (r & 3);
+  else return 4 * ((r >> 1) & 1);
+}
 
 // Row r of an S^T accumulator block holds key kperm(r) of the 32-key half:
 // r = 8j + 4g + i (j = v/4 register group, g = lane/32, i = v%4) -> key
@@ -112,7 +131,6 @@ VM_DEV void attn_block_mfma(Args A, uint32_t ti, uint32_t h, uint32_t row0, uint
   vhi = uni(vhi);
   typedef AttnLds<HD> L;
   const uint32_t T = P.T, C = P.C, dt = (t.tile_op >> 8) & 0xFF;
-  uint16_t* lds = lds_ptr<uint16_t>();
   constexpr int KS = HD / 16;            // MFMA steps over hd for S
   constexpr int DB = HD / 32;            // 32-row d blocks of O^T
   const uint32_t lane = threadIdx.x & 63, wave = uni(threadIdx.x >> 6), g = lane >> 5;
@@ -151,66 +169,56 @@ VM_DEV void attn_block_mfma(Args A, uint32_t ti, uint32_t h, uint32_t row0, uint
   const int32_t wq_lo = int32_t(qw0) + shift;
   const int32_t wq_hi = int32_t(min(qw0 + 63, T - 1)) + shift;
 
-  // Staging.  K: 64 keys x HD/8 chunks of 8 elements, HD/32 per thread, stored as
-  // rows.  V: groups of KG consecutive keys x one 8-element chunk, one group per
-  // thread, transposed into V^T rows.
-  constexpr int NK = kAttnKeys * HD / 8 / kBlock;
-  constexpr int KG = HD == 128 ? 4 : 2;
-  constexpr int NG = kAttnKeys / KG;                         // key groups per block
-  v4u rk[NK], rv[KG];
-  const uint32_t vg = threadIdx.x % NG, vdc = threadIdx.x / NG;
-  auto gload = [&](uint32_t kb) {
+  // Staging: per block, kRounds transfers per operand and thread.  Round j of
+  // wave w, lane l fills stage bytes 4096 j + 1024 w + 16 l of the operand: key
+  // row r = (4096 j + 1024 w + 16 l) / kRow, slot (16 l % kRow) / 16, so the lane
+  // fetches chunk slot ^ swz(r) of key min(kb 64 + r, C - 1).  Keys past C are
+  // masked out of S; their V rows are zeroed by the lane that fetched them, once
+  // its own transfers have landed, so 0-weight keys add 0.
+  const uint32_t lds0 = uni(uint32_t(reinterpret_cast<uintptr_t>(lds_ptr<lds_u8>())));
+  const lds_u8* LB = (const lds_u8*)lds0;
+  const uint32_t st0 = lds0, st1 = lds0 + L::kStage;
+  const uint32_t wo = uni(1024 * wave);
+  const uint32_t dr = (1024 * wave + 16 * lane) / L::kRow;            // row within a round
+  const uint32_t dslot = (16 * lane) % L::kRow / 16;
+  const uint32_t dk = (dslot ^ kswz<HD>(dr)) * 16, dv = (dslot ^ vswz<HD>(dr)) * 16;
+  constexpr uint32_t kRowsPerRound = 4096 / L::kRow;
+  const gbyte* Kg = (const gbyte*)K;
+  const gbyte* Vg = (const gbyte*)V;
+  auto dma_block = [&](uint32_t st, uint32_t kb) {
 #pragma unroll
-    for (int j = 0; j < NK; ++j) {
-      const uint32_t c = threadIdx.x + j * kBlock;
-      const uint32_t key = min(kb * kAttnKeys + c / (HD / 8), C - 1);
-      rk[j] = *(const VM_G v4u*)(K + uint64_t(key) * HD + (c % (HD / 8)) * 8);
+    for (uint32_t j = 0; j < L::kRounds; ++j) {
+      const uint32_t key = min(kb * kAttnKeys + j * kRowsPerRound + dr, C - 1);
+      dma16(Kg, key * L::kRow + dk, st + 4096 * j + wo);
     }
 #pragma unroll
-    for (int i = 0; i < KG; ++i) {
-      const uint32_t key = min(kb * kAttnKeys + vg * KG + i, C - 1);
-      rv[i] = *(const VM_G v4u*)(V + uint64_t(key) * HD + vdc * 8);
+    for (uint32_t j = 0; j < L::kRounds; ++j) {
+      const uint32_t key = min(kb * kAttnKeys + j * kRowsPerRound + dr, C - 1);
+      dma16(Vg, key * L::kRow + dv, st + L::kKBytes + 4096 * j + wo);
     }
   };
-  auto lstore = [&](uint16_t* buf, uint32_t kb) {
-    uint16_t* lk = buf;
-    uint16_t* lv = buf + L::kKBuf;
-#pragma unroll
-    for (int j = 0; j < NK; ++j) {
-      const uint32_t c = threadIdx.x + j * kBlock;
-      *reinterpret_cast<v4u*>(lk + (c / (HD / 8)) * L::kLdK + (c % (HD / 8)) * 8) = rk[j];
-    }
-    // keys past C hold a copy of key C - 1: zero them so 0-weight rows add 0
+  auto zero_tail = [&](uint32_t st, uint32_t kb) {
     if (kb * kAttnKeys + kAttnKeys > C) {
 #pragma unroll
-      for (int i = 0; i < KG; ++i)
-        if (kb * kAttnKeys + vg * KG + i >= C) rv[i] = v4u_make(0, 0, 0, 0);
-    }
-    uint32_t x[KG][4];
-#pragma unroll
-    for (int i = 0; i < KG; ++i) {
-      x[i][0] = rv[i].x;
-      x[i][1] = rv[i].y;
-      x[i][2] = rv[i].z;
-      x[i][3] = rv[i].w;
-    }
-#pragma unroll
-    for (int p = 0; p < 4; ++p) {
-      uint16_t* r0 = lv + (vdc * 8 + 2 * p) * kAttnLdV + vg * KG;
-      uint16_t* r1 = r0 + kAttnLdV;
-      if constexpr (KG == 4) {
-        *reinterpret_cast<v2u*>(r0) = v2u_make(__builtin_amdgcn_perm(x[1][p], x[0][p], 0x05040100u),
-                                               __builtin_amdgcn_perm(x[3][p], x[2][p], 0x05040100u));
-        *reinterpret_cast<v2u*>(r1) = v2u_make(__builtin_amdgcn_perm(x[1][p], x[0][p], 0x07060302u),
-                                               __builtin_amdgcn_perm(x[3][p], x[2][p], 0x07060302u));
-      } else {
-        *reinterpret_cast<uint32_t*>(r0) = __builtin_amdgcn_perm(x[1][p], x[0][p], 0x05040100u);
-        *reinterpret_cast<uint32_t*>(r1) = __builtin_amdgcn_perm(x[1][p], x[0][p], 0x07060302u);
-      }
+      for (uint32_t j = 0; j < L::kRounds; ++j)
+        if (kb * kAttnKeys + j * kRowsPerRound + dr >= C)
+          *(__attribute__((address_space(3))) v4u*)(LB + (st - lds0) + L::kKBytes + 4096 * j + wo + 16 * lane) =
+              v4u_make(0, 0, 0, 0);
     }
   };
+  // V^T fragment addresses (block db, second read at +4 rows): key row 16 ks +
+  // 8 (gq >> 1) + e, hd chunk 4 db + 2 (gq & 1) + (q >> 1), half q & 1, where
+  // gq = lane >> 4, e = (lane >> 2) & 3, q = lane & 3.
+  uint32_t vfa[DB];
+  {
+    const uint32_t gq = lane >> 4, e = (lane >> 2) & 3, q = lane & 3;
+    const uint32_t row = 8 * (gq >> 1) + e, sw = vswz<HD>(row);
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+      vfa[db] = L::kKBytes + row * L::kRow + (((4 * uint32_t(db) + 2 * (gq & 1) + (q >> 1)) ^ sw) * 16) + (q & 1) * 8;
+  }
 
-  const uint32_t krow = kperm(lane & 31);
+  const uint32_t krow = kperm(lane & 31), ksw = kswz<HD>(krow);
   const int32_t qlim0 = int32_t(qw0 + (lane & 31)) + shift;   // last visible key, sub-tile 0
   // probabilities of a pass are exp2(scale' s - m_ref) with m_ref fixed per row; a
   // row sum partial above this bound flags the block for the exact pass (P must
@@ -268,7 +276,7 @@ VM_DEV void attn_block_mfma(Args A, uint32_t ti, uint32_t h, uint32_t row0, uint
     redo = redo || !(rs <= bound);      // also catches inf (NaN rows propagate as in the reference)
     l_part[u] += rs;
   };
-  auto s_tiles = [&](const uint16_t* lk, f32x16 (&s0)[2], f32x16 (&s1)[2]) {
+  auto s_tiles = [&](const lds_u8* S, f32x16 (&s0)[2], f32x16 (&s1)[2]) {
     // the two 32-key halves are independent accumulation chains: alternate them
     // so consecutive MFMAs never wait on each other's result
     u16x8 kf[2][KS];
@@ -276,7 +284,7 @@ VM_DEV void attn_block_mfma(Args A, uint32_t ti, uint32_t h, uint32_t row0, uint
     for (int kh = 0; kh < 2; ++kh)
 #pragma unroll
       for (int st = 0; st < KS; ++st)
-        kf[kh][st] = *reinterpret_cast<const u16x8*>(lk + (kh * 32 + krow) * L::kLdK + st * 16 + 8 * g);
+        kf[kh][st] = *(const lds_u16x8*)(S + (kh * 32 + krow) * L::kRow + (((2 * uint32_t(st) + g) ^ ksw) * 16));
     s0[0] = s0[1] = s1[0] = s1[1] = f32x16{};
 #pragma unroll
     for (int st = 0; st < KS; ++st)
@@ -291,9 +299,9 @@ VM_DEV void attn_block_mfma(Args A, uint32_t ti, uint32_t h, uint32_t row0, uint
   // sub-tile 0's softmax while sub-tile 1's S^T is on the matrix cores, then
   // P^T . V of sub-tile 0 while sub-tile 1's softmax runs (V^T fragments read
   // once, used twice).
-  auto body = [&](auto maskc, auto maxc, const uint16_t* lk, const uint16_t* lv, uint32_t key0) {
+  auto body = [&](auto maskc, auto maxc, const lds_u8* S, uint32_t key0) {
     f32x16 s0[2], s1[2];
-    s_tiles(lk, s0, s1);
+    s_tiles(S, s0, s1);
     u16x8 p0[4], p1[4];
     if constexpr (decltype(maskc)::value) mask_s(s0, 0, key0);
     probs(maxc, s0, 0, p0);
@@ -302,8 +310,11 @@ VM_DEV void attn_block_mfma(Args A, uint32_t ti, uint32_t h, uint32_t row0, uint
 #pragma unroll
     for (int db = 0; db < DB; ++db)
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks)
-        vf[db][ks] = *reinterpret_cast<const u16x8*>(lv + (db * 32 + (lane & 31)) * kAttnLdV + ks * 16 + 8 * g);
+      for (int ks = 0; ks < 4; ++ks) {
+        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(S + vfa[db] + ks * 16 * L::kRow));
+        const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(S + vfa[db] + (ks * 16 + 4) * L::kRow));
+        vf[db][ks] = __builtin_bit_cast(u16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+      }
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
@@ -315,9 +326,9 @@ VM_DEV void attn_block_mfma(Args A, uint32_t ti, uint32_t h, uint32_t row0, uint
       for (int db = 0; db < DB; ++db) o[1][db] = mfma16<BF16>(vf[db][ks], p1[ks], o[1][db]);
   };
   // Exact pass 1: the true scaled row maxima over all visible keys.
-  auto max_body = [&](auto maskc, auto, const uint16_t* lk, const uint16_t* lv, uint32_t key0) {
+  auto max_body = [&](auto maskc, auto, const lds_u8* S, uint32_t key0) {
     f32x16 s0[2], s1[2];
-    s_tiles(lk, s0, s1);
+    s_tiles(S, s0, s1);
     if constexpr (decltype(maskc)::value) {
       mask_s(s0, 0, key0);
       mask_s(s1, 1, key0);
@@ -326,8 +337,10 @@ VM_DEV void attn_block_mfma(Args A, uint32_t ti, uint32_t h, uint32_t row0, uint
     m_run[1] = fmaxf(m_run[1], row_max(s1));
   };
 
-  // One sweep over the key blocks: per block, prefetch the next into registers,
-  // compute on this one, store the next into the other LDS stage.  Blocks wholly
+  // One sweep over the key blocks: per block, start the next block's transfers
+  // into the other LDS stage (its last reader passed the previous barrier),
+  // compute on this one, wait for this lane's transfers, then the block barrier
+  // publishes the next stage.  Blocks wholly
   // below this wave's diagonal (and inside the keys) run unmasked; the rest are
   // masked, and those past the wave's last row's causal limit are skipped.  The
   // two kinds run in two loops (not one loop with a branch) so the body is laid
@@ -336,25 +349,24 @@ VM_DEV void attn_block_mfma(Args A, uint32_t ti, uint32_t h, uint32_t row0, uint
   if (P.causal) nfull = min(nfull, wq_lo >= kAttnKeys - 1 ? uint32_t(wq_lo - (kAttnKeys - 1)) / kAttnKeys + 1 : 0u);
   auto sweep = [&](auto fn) {
     __syncthreads();                    // LDS free from the previous user
-    if (nblk) {
-      gload(0);
-      lstore(lds, 0);
-    }
+    if (nblk) dma_block(st0, 0);
     // every global load so far (the Q fragments too) has landed: said explicitly
     // so the compiler's wait counting does not carry the Q loads into the loop
-    // (where their waits would stall on the next block's K/V prefetch)
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    wait_vm0();
+    if (nblk) zero_tail(st0, 0);
     __syncthreads();
     auto step = [&](auto maskc, auto maxc, uint32_t kb) {
-      const uint16_t* buf = lds + (kb & 1) * L::kBuf;
-      if (kb + 1 < nblk) gload(kb + 1);
+      const uint32_t cur = (kb & 1) ? st1 : st0, nxt = (kb & 1) ? st0 : st1;
+      if (kb + 1 < nblk) dma_block(nxt, kb + 1);
       const uint32_t key0 = kb * kAttnKeys;
+      const lds_u8* S = LB + (cur - lds0);
       if constexpr (decltype(maskc)::value) {
-        if (wave_rows && (!P.causal || int32_t(key0) <= wq_hi)) fn(maskc, maxc, buf, buf + L::kKBuf, key0);
+        if (wave_rows && (!P.causal || int32_t(key0) <= wq_hi)) fn(maskc, maxc, S, key0);
       } else {
-        fn(maskc, maxc, buf, buf + L::kKBuf, key0);
+        fn(maskc, maxc, S, key0);
       }
-      if (kb + 1 < nblk) lstore(lds + ((kb + 1) & 1) * L::kBuf, kb + 1);
+      wait_vm0();
+      if (kb + 1 < nblk) zero_tail(nxt, kb + 1);
       __syncthreads();
     };
     uint32_t kb = 0;

@@ -582,6 +582,7 @@ def test_dot_views_batch_epilogue():
 
 @pytest.mark.parametrize("dt,hd,causal,T,C", [("bf16", 128, True, 256, 256), ("bf16", 128, False, 128, 384),
                                               ("bf16", 64, True, 384, 512), ("f16", 128, True, 128, 128),
+                                              ("bf16", 128, True, 96, 200), ("f16", 64, False, 64, 130),
                                               ("f32", 32, True, 40, 56), ("bf16", 80, False, 64, 100)])
 def test_flash_attention(dt, hd, causal, T, C):
     rng = np.random.default_rng(1004)
@@ -604,6 +605,26 @@ def test_flash_attention(dt, hd, causal, T, C):
     assert_product_elementwise(got[0], want.astype(np.float64),
                                attention_abs_scale(q, np.transpose(k, (0, 2, 1)), v, 1.0 / np.sqrt(hd), causal), tol,
                                f"flash {dt} hd {hd}")
+
+
+@pytest.mark.parametrize("hd", [64, 128])
+def test_flash_attention_partial_block_inf_value(hd):
+    """Matrix-core path with a partial last key block (C = 200): every query sees
+    key C - 1, whose value row is +inf, so every output is +inf.  The block's
+    slots past C hold copies of key C - 1 and get probability 0; they must add 0
+    (zeroed), not 0 * inf = NaN."""
+    rng = np.random.default_rng(1005)
+    H, T, C = 2, 64, 200
+    q = vmref.bf16_to_f32(vmref.f32_to_bf16(rng.standard_normal((H, T, hd)).astype(np.float32)))
+    k = vmref.bf16_to_f32(vmref.f32_to_bf16(rng.standard_normal((H, C, hd)).astype(np.float32)))
+    v = vmref.bf16_to_f32(vmref.f32_to_bf16(rng.standard_normal((H, C, hd)).astype(np.float32)))
+    v[:, C - 1, :] = np.inf
+    g = G.Graph()
+    Q, K, Vv = g.input(q.shape, "bf16"), g.input(k.shape, "bf16"), g.input(v.shape, "bf16")
+    g.output(g.flash_attention(Q, K, Vv, 1.0 / np.sqrt(hd), False, out_dtype="f32"))
+    got, _ = run_both(g.build(), [q, k, v], oracle=None)
+    assert np.isposinf(vmref.attention(q, np.transpose(k, (0, 2, 1)), v, 1.0 / np.sqrt(hd), False)).all()
+    assert np.isposinf(got[0]).all(), int(np.isnan(got[0]).sum())
 
 
 @pytest.mark.parametrize("dt,causal,T,C,target", [("bf16", True, 512, 512, 150.0), ("f16", False, 256, 384, 22.0)])

@@ -577,6 +577,7 @@ class TaskRunner:
         self.m = m
         self.ts = ew_ts
         self.mma_t = mma_t
+        self.splits = {}            # (task, output tile) -> K-split tiles run so far
 
     def run(self, t: Task, lo: int, hi: int):
         fn = getattr(self, f"top{t.top}", None)
@@ -700,12 +701,28 @@ class TaskRunner:
         return A, B, M, N, K, G
 
     def top1(self, t, lo, hi):
+        """Matmul tiles.  A K-split task (p3 bits 28-31, this build's extension)
+        has S tiles per output tile; the output tile is written, from the whole
+        product, once all S of its tiles have run (in any order), which is when
+        the device's last-arriving split writes it."""
         m = self.m
         A, B, M, N, K, G = self._mma_operands(t)
         code = (t.p[3] >> 24) & 0xF
         T = {1: 64, 2: 128, 3: 256}.get(code, self.mma_t)
+        S = 1 << (t.p[3] >> 28)
         tn, tm = -(-N // T), -(-M // T)
         per = tn * tm
+        if S > 1:
+            done = []
+            for tile in range(lo, hi):
+                key = (id(t), tile // S)
+                self.splits[key] = self.splits.get(key, 0) + 1
+                if self.splits[key] == S:
+                    del self.splits[key]
+                    done.append(tile // S)
+            lo, hi, tiles = 0, 0, done
+        else:
+            tiles = range(lo, hi)
         out = np.zeros((G, M, N), np.float32)
         have = self.m.load_f(t.dst, t.dt)[:G * M * N].reshape(G, M, N).copy()
         res = None
@@ -714,7 +731,7 @@ class TaskRunner:
                 res = self.m.load_f(t.p[7])
             except Exception:
                 res = None
-        for tile in range(lo, hi):
+        for tile in tiles:
             g, loc = tile // per, tile % per
             tr, tc = loc // tn, loc % tn
             r0, r1 = tr * T, min(tr * T + T, M)
@@ -1144,7 +1161,7 @@ def _whole_tiles(t: Task, ew_ts: int, mma_t: int) -> int:
         return max(1, -(-p[0] // ew_ts))
     if t.top == 1:
         T = {1: 64, 2: 128, 3: 256}.get((p[3] >> 24) & 0xF, mma_t)
-        return -(-p[0] // T) * -(-p[1] // T) * max(1, p[3] & 0xFFFFFF)
+        return -(-p[0] // T) * -(-p[1] // T) * max(1, p[3] & 0xFFFFFF) << (p[3] >> 28)
     if t.top == 3:
         return max(1, -(-p[0] // p[1]))
     if t.top == 4:

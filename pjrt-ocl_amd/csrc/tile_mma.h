@@ -1,7 +1,15 @@
 // TOP_MMA: C[g] = A[g] (MxK) . B[g] (KxN) (+ store epilogue), f32 accumulate on
 // CDNA4 matrix cores (reference semantics: ops/mma.cl:362-434, epilogue 74-96).
-// Task: p0 M, p1 N, p2 K, p3 G (bits 0-23) | tile-edge code (bits 24-27),
-// p4 A view+1, p5 B view+1, p6 epilogue descriptor+1, p7 residual handle.
+// Task: p0 M, p1 N, p2 K, p3 G (bits 0-23) | tile-edge code (bits 24-27) |
+// log2 of the K split (bits 28-31, extension), p4 A view+1, p5 B view+1, p6
+// epilogue descriptor+1, p7 residual handle.
+//
+// K split (extension, for matmuls whose output tiles leave most lanes idle):
+// with S = 2^(p3 >> 28) > 1, tile t is split t % S of output tile t / S and
+// covers K slabs [k0, k1) of width ceil(K / S) rounded up to whole slabs.  It
+// publishes its f32 partial tile in the task's scratch and counts its arrival;
+// the split that arrives last sums the S partials in split order (deterministic,
+// whichever arrives last), applies the epilogue and stores the tile.
 //
 // One output tile of T x T (T = 64/128/256) per tile index.  The block's four
 // wave64s split it 2 x 2; each wave owns (T/2)^2 outputs as (T/64)^2 blocks of
@@ -34,6 +42,8 @@ struct MmaDesc {
   const gbyte* res;         // epilogue second input
   uint32_t av, bv, epi;     // view / epilogue aux offsets + 1 (0 = none)
   uint32_t dt, adt;
+  uint32_t k0, k1;          // K range of this tile (a K split's share; else 0, K)
+  uint32_t S, split, ti;    // K split count, this tile's split, task index
 };
 
 // Store epilogue micro-program (mma.cl:67-96): {n, n x {kind, src, s, t}}, src 0
@@ -61,18 +71,85 @@ struct MmaCfg {
   static constexpr int kBN = T / 64;
 };
 
+// Epilogue kinds the lowering fuses into a matmul store (affine, GELU, a binary op
+// with the residual or a per-column operand), evaluated inline by the fast path:
+// a call would force the 256 live accumulator AGPRs through scratch.
+VM_DEV bool epi_inline_ok(Args A, uint32_t epi) {
+  if (!epi) return true;
+  const VM_K int32_t* e = aux_of(A) + (epi - 1);
+  const int nm = e[0];
+  for (int k = 0; k < nm; ++k) {
+    const uint32_t kind = uint32_t(e[1 + 4 * k]);
+    if (!(kind == SUB_AFFINE || kind == SUB_GELU || kind == SUB_COPY || kind <= SUB_DIV || kind == SUB_MAX ||
+          kind == SUB_MIN))
+      return false;
+  }
+  return true;
+}
+
+VM_DEV float epi_inline(uint32_t kind, float x, float y, float s, float t) {
+  switch (kind) {
+    case SUB_AFFINE: return fmaf(x, s, t);
+    case SUB_GELU: return gelu(x);
+    case SUB_ADD: return x + y;
+    case SUB_MUL: return x * y;
+    case SUB_SUB: return x - y;
+    case SUB_DIV: return x / y;
+    case SUB_MAX: return fmaxf(x, y);
+    case SUB_MIN: return fminf(x, y);
+    default: return x;
+  }
+}
+
 template <int T>
 VM_DEV void store_acc(Args A, const MmaDesc& D, const f32x16 (&acc)[MmaCfg<T>::kBM][MmaCfg<T>::kBN], uint32_t g,
                       uint32_t m0, uint32_t n0) {
   const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const uint32_t wm = wave >> 1, wn = wave & 1;
+  // 64-wide tiles (the small matmuls' tile, one 32 x 32 block per wave): an
+  // epilogue of the inline kinds (affine, GELU, binary ops; the fast paths' set)
+  // gets its operands loaded before the first is used -- the column value once,
+  // the block's 16 residual values together (indices clamped into the output,
+  // results past it not stored) -- so the store costs one memory round trip, not
+  // one per element (config 1's bias + relu matmuls).  Larger tiles and other
+  // kinds evaluate per element: unrolled over four or more blocks, the inline
+  // evaluation pushes the accumulators of a 128-wide tile into scratch.
+  const bool inl = T == 64 && D.epi && epi_inline_ok(A, D.epi);
+  const VM_K int32_t* e = aux_of(A) + (D.epi ? D.epi - 1 : 0);
+  const int nm = inl ? e[0] : 0;
+  bool need_res = false, need_col = false;
+  for (int k = 0; k < nm; ++k) {
+    need_res |= e[2 + 4 * k] == 1;
+    need_col |= e[2 + 4 * k] == 2;
+  }
+  const VM_G float* res = (const VM_G float*)D.res;
 #pragma unroll
   for (int bm = 0; bm < MmaCfg<T>::kBM; ++bm) {
 #pragma unroll
     for (int bn = 0; bn < MmaCfg<T>::kBN; ++bn) {
       const uint32_t col = n0 + wn * (T / 2) + bn * 32 + (lane & 31);
       const uint32_t rbase = m0 + wm * (T / 2) + bm * 32 + 4 * (lane >> 5);
-      if (D.epi) {
+      if (inl) {
+        const uint32_t cc = min(col, D.N - 1);
+        const float yc = need_col ? res[cc] : 0.0f;
+        float yr[16];
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const uint32_t row = min(rbase + 8 * (v >> 2) + (v & 3), D.M - 1);
+          yr[v] = need_res ? res[(uint64_t(g) * D.M + row) * D.N + cc] : 0.0f;
+        }
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const uint32_t row = rbase + 8 * (v >> 2) + (v & 3);
+          float x = acc[bm][bn][v];
+          for (int k = 0; k < nm; ++k) {
+            const uint32_t kind = uint32_t(e[1 + 4 * k]), src = uint32_t(e[2 + 4 * k]);
+            const float sv = __int_as_float(e[3 + 4 * k]), tv = __int_as_float(e[4 + 4 * k]);
+            x = epi_inline(kind, x, src == 1 ? yr[v] : src == 2 ? yc : src == 3 ? sv : x, sv, tv);
+          }
+          if (row < D.M && col < D.N) store_f(D.d, D.dt, (uint64_t(g) * D.M + row) * D.N + col, x);
+        }
+      } else if (D.epi) {
 #pragma unroll 1
         for (int v = 0; v < 16; ++v) {
           const uint32_t row = rbase + 8 * (v >> 2) + (v & 3);
@@ -90,6 +167,80 @@ VM_DEV void store_acc(Args A, const MmaDesc& D, const f32x16 (&acc)[MmaCfg<T>::k
       }
     }
   }
+}
+
+__shared__ uint32_t vm_mma_last;       // this lane's split arrived last (K-split combine)
+
+// Store of a general tile: the tile itself, or (K split) its f32 partial.  A
+// partial is written in register order, 16 bytes per thread and step (values
+// 4q .. 4q + 3 of thread x at [(tile S + split) NQ + q] kBlock + x, NQ = T^2 /
+// (4 kBlock)), coalesced.  Each thread waits for its own stores to complete, the
+// block barrier orders them before thread 0's arrival, an agent-scope
+// acquire-release add on the tile's counter: its release writes this XCD's L2
+// back (the partial included), its acquire (in the last arriver) invalidates the
+// reader's caches, and the block barrier after it orders the other threads'
+// reads after the invalidation -- the grid barrier's publish / acquire pattern.
+// The last arriver resets the counter (the next run of the task is ordered after
+// this one by a grid barrier) and sums partials 0 .. S-1 in that order, loading
+// several splits' partials before the first add (one memory round trip per
+// batch, not per value).
+template <int T>
+VM_DEV void mma_store(Args A, const MmaDesc& D, f32x16 (&acc)[MmaCfg<T>::kBM][MmaCfg<T>::kBN], uint32_t tile,
+                      uint32_t g, uint32_t m0, uint32_t n0) {
+  if (D.S <= 1) return store_acc<T>(A, D, acc, g, m0, n0);
+  using C = MmaCfg<T>;
+  constexpr uint32_t NQ = C::kBM * C::kBN * 4;             // float4 steps per thread
+  constexpr uint32_t B = NQ <= 4 ? 8 : NQ <= 16 ? 2 : 1;   // splits per load batch (<= 32 float4)
+  v4f* sp = reinterpret_cast<v4f*>(A->scratch + A->task_scratch[D.ti]);
+  const uint64_t nbase = uint64_t(D.tm) * D.tn * D.G;
+  uint32_t* arrivals = reinterpret_cast<uint32_t*>(sp + nbase * D.S * NQ * kBlock);
+  v4f* mine = sp + (uint64_t(tile) * D.S + D.split) * NQ * kBlock + threadIdx.x;
+#pragma unroll
+  for (int bm = 0; bm < C::kBM; ++bm)
+#pragma unroll
+    for (int bn = 0; bn < C::kBN; ++bn)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const f32x16& x = acc[bm][bn];
+        mine[((bm * C::kBN + bn) * 4 + q) * kBlock] = v4f_make(x[4 * q], x[4 * q + 1], x[4 * q + 2], x[4 * q + 3]);
+      }
+  __builtin_amdgcn_s_waitcnt(0x0F70);                 // vmcnt(0): this thread's stores are done
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const uint32_t before = __hip_atomic_fetch_add(arrivals + tile, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    const bool last = before == D.S - 1;
+    if (last) __hip_atomic_store(arrivals + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    vm_mma_last = last;
+  }
+  __syncthreads();
+  if (!vm_mma_last) return;
+  const v4f* hp = sp + uint64_t(tile) * D.S * NQ * kBlock + threadIdx.x;
+  for (uint32_t s0 = 0; s0 < D.S; s0 += B) {
+    v4f part[B][NQ];
+#pragma unroll
+    for (uint32_t u = 0; u < B; ++u)             // past S: re-read the last split (not added)
+#pragma unroll
+      for (uint32_t q = 0; q < NQ; ++q) part[u][q] = hp[(uint64_t(min(s0 + u, D.S - 1)) * NQ + q) * kBlock];
+#pragma unroll
+    for (uint32_t u = 0; u < B; ++u)
+      if (s0 + u < D.S) {
+#pragma unroll
+        for (int bm = 0; bm < C::kBM; ++bm)
+#pragma unroll
+          for (int bn = 0; bn < C::kBN; ++bn)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const v4f y = part[u][(bm * C::kBN + bn) * 4 + q];
+              f32x16& x = acc[bm][bn];
+              if (s0 + u == 0) {
+                x[4 * q] = y.x; x[4 * q + 1] = y.y; x[4 * q + 2] = y.z; x[4 * q + 3] = y.w;
+              } else {
+                x[4 * q] += y.x; x[4 * q + 1] += y.y; x[4 * q + 2] += y.z; x[4 * q + 3] += y.w;
+              }
+            }
+      }
+  }
+  store_acc<T>(A, D, acc, g, m0, n0);
 }
 
 // Operand element (g, m, k) with a view or an unaligned row: 8 (16-bit) or 4
@@ -135,16 +286,16 @@ struct Stage16 {
       const uint32_t c = threadIdx.x + j * kBlock;
       const uint32_t m = m0 + (c >> 2), k = k0 + (c & 3) * 8;
       const uint64_t lin = (uint64_t(g) * D.M + m) * D.K + k;
-      const bool in = m < D.M && k < D.K;
+      const bool in = m < D.M && k < D.k1;
       if (vec) ra[j] = in ? gld((const VM_G v4u*)(gcast<uint16_t>(D.a) + lin)) : v4u_make(0, 0, 0, 0);
-      else ra[j] = in ? gather_chunk(A, D.a, D.av, lin, D.K - k, 2) : v4u_make(0, 0, 0, 0);
+      else ra[j] = in ? gather_chunk(A, D.a, D.av, lin, D.k1 - k, 2) : v4u_make(0, 0, 0, 0);
     }
 #pragma unroll
     for (int j = 0; j < kChunks; ++j) {
       const uint32_t c = threadIdx.x + j * kBlock;
       const uint32_t k = k0 + c / (T / 8), n = n0 + (c % (T / 8)) * 8;
       const uint64_t lin = (uint64_t(g) * D.K + k) * D.N + n;
-      const bool in = k < D.K && n < D.N;
+      const bool in = k < D.k1 && n < D.N;
       if (vec) rb[j] = in ? gld((const VM_G v4u*)(gcast<uint16_t>(D.b) + lin)) : v4u_make(0, 0, 0, 0);
       else rb[j] = in ? gather_chunk(A, D.b, D.bv, lin, D.N - n, 2) : v4u_make(0, 0, 0, 0);
     }
@@ -195,6 +346,11 @@ VM_DEV MmaDesc load_desc(const MmaDesc* p) {
   D.epi = uni(p->epi);
   D.dt = uni(p->dt);
   D.adt = uni(p->adt);
+  D.k0 = uni(p->k0);
+  D.k1 = uni(p->k1);
+  D.S = uni(p->S);
+  D.split = uni(p->split);
+  D.ti = uni(p->ti);
   return D;
 }
 
@@ -224,15 +380,15 @@ VM_TILE void mma_tile16(Args A, const MmaDesc* Dp, uint32_t tile) {
 #pragma unroll
     for (int j = 0; j < C::kBN; ++j) acc[i][j] = f32x16{};
 
-  const uint32_t nk = (D.K + kBK16 - 1) / kBK16;
+  const uint32_t nk = (D.k1 - D.k0 + kBK16 - 1) / kBK16;
   Stage16<T> st;
-  st.load(A, D, g, m0, n0, 0, vec);
+  st.load(A, D, g, m0, n0, D.k0, vec);
   __syncthreads();                      // previous user of the LDS is done
   st.store(lds);
   __syncthreads();
   for (uint32_t ks = 0; ks < nk; ++ks) {
     const uint16_t* cur = lds + (ks & 1) * Lds16<T>::kBuf;
-    if (ks + 1 < nk) st.load(A, D, g, m0, n0, (ks + 1) * kBK16, vec);
+    if (ks + 1 < nk) st.load(A, D, g, m0, n0, D.k0 + (ks + 1) * kBK16, vec);
     const uint16_t* la = cur;
     const uint16_t* lb = cur + Lds16<T>::kA;
 #pragma unroll
@@ -258,7 +414,7 @@ VM_TILE void mma_tile16(Args A, const MmaDesc* Dp, uint32_t tile) {
     if (ks + 1 < nk) st.store(lds + ((ks + 1) & 1) * Lds16<T>::kBuf);
     __syncthreads();
   }
-  store_acc<T>(A, D, acc, g, m0, n0);
+  mma_store<T>(A, D, acc, uni(tile), g, m0, n0);
 }
 
 // ---------------------------------------------------------------------------------
@@ -351,36 +507,6 @@ VM_DEV void fast_origin(const MmaDesc& D, uint32_t tile, uint32_t* g, uint32_t* 
   } else {
     *m0 = (loc / D.tn) * 256;
     *n0 = (loc % D.tn) * 256;
-  }
-}
-
-// Epilogue kinds the lowering fuses into a matmul store (affine, GELU, a binary op
-// with the residual or a per-column operand), evaluated inline by the fast path:
-// a call would force the 256 live accumulator AGPRs through scratch.
-VM_DEV bool epi_inline_ok(Args A, uint32_t epi) {
-  if (!epi) return true;
-  const VM_K int32_t* e = aux_of(A) + (epi - 1);
-  const int nm = e[0];
-  for (int k = 0; k < nm; ++k) {
-    const uint32_t kind = uint32_t(e[1 + 4 * k]);
-    if (!(kind == SUB_AFFINE || kind == SUB_GELU || kind == SUB_COPY || kind <= SUB_DIV || kind == SUB_MAX ||
-          kind == SUB_MIN))
-      return false;
-  }
-  return true;
-}
-
-VM_DEV float epi_inline(uint32_t kind, float x, float y, float s, float t) {
-  switch (kind) {
-    case SUB_AFFINE: return fmaf(x, s, t);
-    case SUB_GELU: return gelu(x);
-    case SUB_ADD: return x + y;
-    case SUB_MUL: return x * y;
-    case SUB_SUB: return x - y;
-    case SUB_DIV: return x / y;
-    case SUB_MAX: return fmaxf(x, y);
-    case SUB_MIN: return fminf(x, y);
-    default: return x;
   }
 }
 
@@ -601,16 +727,16 @@ struct Stage32 {
       const uint32_t c = threadIdx.x + j * kBlock;
       const uint32_t m = m0 + (c >> 2), k = k0 + (c & 3) * 4;
       const uint64_t lin = (uint64_t(g) * D.M + m) * D.K + k;
-      const bool in = m < D.M && k < D.K;
+      const bool in = m < D.M && k < D.k1;
       if (vec) ra[j] = in ? gld((const VM_G v4u*)(gcast<float>(D.a) + lin)) : v4u_make(0, 0, 0, 0);
-      else ra[j] = in ? gather_chunk(A, D.a, D.av, lin, D.K - k, 4) : v4u_make(0, 0, 0, 0);
+      else ra[j] = in ? gather_chunk(A, D.a, D.av, lin, D.k1 - k, 4) : v4u_make(0, 0, 0, 0);
     }
 #pragma unroll
     for (int j = 0; j < kChunks; ++j) {
       const uint32_t c = threadIdx.x + j * kBlock;
       const uint32_t k = k0 + c / (T / 4), n = n0 + (c % (T / 4)) * 4;
       const uint64_t lin = (uint64_t(g) * D.K + k) * D.N + n;
-      const bool in = k < D.K && n < D.N;
+      const bool in = k < D.k1 && n < D.N;
       if (vec) rb[j] = in ? gld((const VM_G v4u*)(gcast<float>(D.b) + lin)) : v4u_make(0, 0, 0, 0);
       else rb[j] = in ? gather_chunk(A, D.b, D.bv, lin, D.N - n, 4) : v4u_make(0, 0, 0, 0);
     }
@@ -655,15 +781,15 @@ VM_TILE void mma_tile32(Args A, const MmaDesc* Dp, uint32_t tile) {
   for (int i = 0; i < C::kBM; ++i)
 #pragma unroll
     for (int j = 0; j < C::kBN; ++j) acc[i][j] = f32x16{};
-  const uint32_t nk = (D.K + kBK32 - 1) / kBK32;
+  const uint32_t nk = (D.k1 - D.k0 + kBK32 - 1) / kBK32;
   Stage32<T> st;
-  st.load(A, D, g, m0, n0, 0, vec);
+  st.load(A, D, g, m0, n0, D.k0, vec);
   __syncthreads();
   st.store(lds);
   __syncthreads();
   for (uint32_t ks = 0; ks < nk; ++ks) {
     const float* cur = lds + (ks & 1) * Lds32<T>::kBuf;
-    if (ks + 1 < nk) st.load(A, D, g, m0, n0, (ks + 1) * kBK32, vec);
+    if (ks + 1 < nk) st.load(A, D, g, m0, n0, D.k0 + (ks + 1) * kBK32, vec);
     const float* la = cur;
     const float* lb = cur + Lds32<T>::kA;
 #pragma unroll
@@ -684,7 +810,7 @@ VM_TILE void mma_tile32(Args A, const MmaDesc* Dp, uint32_t tile) {
     if (ks + 1 < nk) st.store(lds + ((ks + 1) & 1) * Lds32<T>::kBuf);
     __syncthreads();
   }
-  store_acc<T>(A, D, acc, g, m0, n0);
+  mma_store<T>(A, D, acc, uni(tile), g, m0, n0);
 }
 
 // ---- f32 fast path ---------------------------------------------------------------
@@ -808,15 +934,30 @@ VM_DEV void mma_tiles(Args A, uint32_t ti, uint32_t lo, uint32_t hi) {
   D.res = t.p[6] ? resolve(A, t.p[7]) : D.a;
   D.dt = (t.tile_op >> 8) & 0xFF;
   D.adt = (t.tile_op >> 16) & 0xFF;
-  hi = min(hi, D.tm * D.tn * D.G);
+  D.S = 1u << ((t.p[3] >> 28) & 0xF);
+  D.ti = ti;
+  D.k0 = 0;
+  D.k1 = D.K;
+  D.split = 0;
+  hi = min(hi, D.tm * D.tn * D.G * D.S);
   const bool h16 = D.adt == DT_BF16 || D.adt == DT_F16, bf = D.adt == DT_BF16;
-  const bool fast = h16 && T == 256 && !D.av && !D.bv && D.M % 256 == 0 && D.N % 256 == 0 && D.K % kFBK == 0 &&
+  // a K split's share: whole slabs of the general tiles (32 16-bit or 16 f32 k)
+  const uint32_t bk = h16 ? uint32_t(kBK16) : uint32_t(kBK32);
+  const uint32_t ksh = ((D.K + D.S - 1) / D.S + bk - 1) / bk * bk;
+  const bool fast = D.S == 1 && h16 && T == 256 && !D.av && !D.bv && D.M % 256 == 0 && D.N % 256 == 0 && D.K % kFBK == 0 &&
                     D.N < (1u << 22) && ((uintptr_t(D.a) | uintptr_t(D.b)) & 15) == 0 &&
                     (D.dt == DT_F32 || D.dt == DT_BF16 || D.dt == DT_F16) && epi_inline_ok(A, D.epi);
-  const bool fast32 = D.adt == DT_F32 && T == 256 && !D.av && !D.bv && D.M % 256 == 0 && D.N % 256 == 0 &&
+  const bool fast32 = D.S == 1 && D.adt == DT_F32 && T == 256 && !D.av && !D.bv && D.M % 256 == 0 && D.N % 256 == 0 &&
                       D.K % kF32BK == 0 && D.N < (1u << 22) && ((uintptr_t(D.a) | uintptr_t(D.b)) & 15) == 0 &&
                       (D.dt == DT_F32 || D.dt == DT_BF16 || D.dt == DT_F16) && epi_inline_ok(A, D.epi);
-  for (uint32_t tile = lo; tile < hi; ++tile) {
+  for (uint32_t ts = lo; ts < hi; ++ts) {
+    uint32_t tile = ts;
+    if (D.S > 1) {                      // split ts % S of output tile ts / S
+      tile = ts / D.S;
+      D.split = ts % D.S;
+      D.k0 = min(D.split * ksh, D.K);
+      D.k1 = min(D.k0 + ksh, D.K);
+    }
     if (fast32) {
       mma_tile32_fast(A, &D, tile);
     } else if (fast) {

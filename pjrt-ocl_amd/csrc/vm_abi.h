@@ -66,6 +66,8 @@ constexpr uint32_t kDecSplitKeys = 64;
 constexpr uint32_t kArgmaxMaxSplits = 256;
 // TOP_GEMV: rows (M) per task at most.
 constexpr uint32_t kGemvMaxM = 8;
+// TOP_MMA: log2 of the K split (task p3 bits 28-31) at most.
+constexpr uint32_t kMmaMaxSplitLog2 = 5;
 constexpr int kMaxPorts = 256;          // power of two: handles mask the port index
 
 // Per-program control buffer: status words, then one arrival word per lane.

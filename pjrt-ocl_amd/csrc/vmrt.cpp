@@ -316,7 +316,7 @@ struct Checker {
       case TOP_MMA: {
         const uint32_t code = (t.p[3] >> 24) & 0xF;
         const uint64_t T = code == 1 ? 64 : code == 2 ? 128 : code == 3 ? 256 : mma_t;
-        return cdiv(t.p[0], T) * cdiv(t.p[1], T) * std::max<uint64_t>(1, t.p[3] & 0xFFFFFF);
+        return cdiv(t.p[0], T) * cdiv(t.p[1], T) * std::max<uint64_t>(1, t.p[3] & 0xFFFFFF) << (t.p[3] >> 28);
       }
       case TOP_RED_PART: return t.p[1] ? std::max<uint64_t>(1, cdiv(t.p[0], t.p[1])) : 1;
       case TOP_RED_COMB: return 1;
@@ -497,6 +497,7 @@ struct Checker {
       case TOP_MMA: {
         const uint64_t M = t.p[0], N = t.p[1], K = t.p[2], G = std::max<uint32_t>(1, t.p[3] & 0xFFFFFF);
         if (adt != DT_F32 && adt != DT_BF16 && adt != DT_F16) return fail(ti, "matmul operand dtype");
+        if ((t.p[3] >> 28) > kMmaMaxSplitLog2) return fail(ti, "matmul K split");
         if (dt != DT_F32 && dt != DT_BF16 && dt != DT_F16) return fail(ti, "matmul result dtype");
         if (t.p[4] ? !view_ok(t.p[4], G * M * K, elems(t.a, adt)) : !has(t.a, G * M * K, adt))
           return fail(ti, "matmul A");
@@ -795,8 +796,15 @@ void vmrt_unload(vmrt_program* p) {
 
 // Scratch bytes a task needs (0: none): a split decode attention keeps one
 // partial (running max, sum, hd channels) per split and head, and one arrival
-// counter per head.
-static uint64_t task_scratch_bytes(const Task& t) {
+// counter per head; a K-split matmul one f32 partial tile per split and output
+// tile, and one arrival counter per output tile.
+static uint64_t task_scratch_bytes(const Task& t, uint32_t mma_t) {
+  if ((t.tile_op & 0xFF) == TOP_MMA && (t.p[3] >> 28)) {
+    const uint32_t code = (t.p[3] >> 24) & 0xF;
+    const uint64_t T = code == 1 ? 64 : code == 2 ? 128 : code == 3 ? 256 : mma_t;
+    const uint64_t tiles = ((t.p[0] + T - 1) / T) * ((t.p[1] + T - 1) / T) * std::max<uint64_t>(1, t.p[3] & 0xFFFFFF);
+    return (tiles * (uint64_t(1) << (t.p[3] >> 28)) * T * T + tiles) * 4;
+  }
   if ((t.tile_op & 0xFF) == TOP_ARGMAX_SEG && t.p[3] > 1) return (2ull * t.p[0] * t.p[3] + t.p[0]) * 4;
   if ((t.tile_op & 0xFF) == TOP_DECODE_ATTN && (t.p[4] >> 16) > 1) {
     const uint64_t H = t.p[4] & 0xFFFF, S = t.p[4] >> 16, hd = t.p[5] & 0xFFFF;
@@ -955,7 +963,7 @@ static int prepare_program(vmrt_runtime* rt, vmrt_program* lp, const void* bytes
   std::vector<uint32_t>& task_scratch = pr->task_scratch;
   task_scratch.assign(tasks.size(), 0);
   for (size_t i = 0; i < tasks.size(); ++i) {
-    const uint64_t nb = task_scratch_bytes(tasks[i]);
+    const uint64_t nb = task_scratch_bytes(tasks[i], lp->mma_t);
     if (!nb) continue;
     task_scratch[i] = uint32_t(lp->scratch_bytes);
     lp->scratch_bytes += (nb + 255) & ~uint64_t(255);

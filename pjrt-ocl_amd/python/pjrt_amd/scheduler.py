@@ -76,6 +76,9 @@ class DeviceConfig:
     # Per-task MMA tile selection (extension): pick the largest tile edge that
     # still gives every lane work; False keeps every MMA at the default edge.
     mma_autotile: bool = True
+    # Matmuls whose tiles leave most lanes idle split K over more lanes
+    # (extension; ``mma_split_log2``).
+    mma_splitk: bool = True
     # Matmuls of at most 8 rows as column-strip TOP_GEMV tasks (extension), and
     # the narrowest strip width they may use.
     gemv: bool = True
@@ -109,6 +112,7 @@ class DeviceConfig:
                    costs=costs,
                    fuse=env.get("PJRT_OCL_FUSE", "1") != "0",
                    mma_autotile=env.get("PJRT_AMD_MMA_AUTOTILE", "1") != "0",
+                   mma_splitk=env.get("PJRT_AMD_MMA_SPLITK", "1") != "0",
                    gemv=env.get("PJRT_AMD_GEMV", "1") != "0",
                    gemv_min_strip=max(0, min(256, geti("PJRT_AMD_GEMV_STRIP", 0))),
                    ln_gemv=env.get("PJRT_AMD_LN_GEMV", "1") != "0",
@@ -166,7 +170,7 @@ def n_tiles(task: V.Task, cfg: DeviceConfig) -> int:
     if top == V.TOP_MMA:
         t = mma_tile_edge(task, cfg)
         g = max(1, task.p3 & 0xFFFFFF)
-        return math.ceil(task.p0 / t) * math.ceil(task.p1 / t) * g
+        return math.ceil(task.p0 / t) * math.ceil(task.p1 / t) * g << (task.p3 >> V.MMA_SPLIT_SHIFT)
     if top == V.TOP_RED_PART:
         return max(1, math.ceil(task.p0 / task.p1)) if task.p1 else 1
     if top == V.TOP_RED_COMB:
@@ -458,8 +462,10 @@ def instr_to_task(ins: V.Instr, prog: V.VMProgram, cfg: DeviceConfig) -> V.Task:
             code = V.MMA_TILE_CODES.get(ins.mma_tile, 0)
             if not code and cfg.mma_autotile:
                 code = V.MMA_TILE_CODES[_auto_mma_tile(M, N, G, cfg)]
+            edge = V.MMA_CODE_TILE.get(code, cfg.mma_t)
+            split = mma_split_log2(M, N, K, G, edge, adt, cfg)
             t = V.Task(V.TOP_MMA, ins.dst, ins.a, ins.b, M, N, K,
-                       G | (code << 24), aview, bview, epi,
+                       G | (code << 24) | (split << V.MMA_SPLIT_SHIFT), aview, bview, epi,
                        epi_res if epi else 0)
     else:
         raise ScheduleError(f"scheduler: no task mapping for opcode {op}")
@@ -475,6 +481,31 @@ def _auto_mma_tile(M: int, N: int, G: int, cfg: DeviceConfig) -> int:
         if math.ceil(M / t) * math.ceil(N / t) * G >= cfg.nlanes:
             return t
     return 64
+
+
+def mma_split_log2(M: int, N: int, K: int, G: int, edge: int, adt: int, cfg: DeviceConfig) -> int:
+    """log2 of the K split of a matmul (extension; 0 = none).  A matmul whose
+    output tiles leave at least half the lanes idle and whose K spans at least
+    four slabs of the general tile (16 f32 or 32 16-bit k) is cut along K into S
+    splits: the largest power of two, at most 32, that keeps every split at two
+    slabs or more and the split tiles within the lanes.  Each split's tile waits
+    on its own loads only once per slab, so the loads of a deep, narrow product
+    (config 1's [256, 512] x [512, 64]: four 64 x 64 tiles) no longer run one
+    slab after another on a few lanes.  256-wide tiles are never split (they
+    cover large outputs, and their combine would hold 64 float4 per thread)."""
+    if not cfg.mma_splitk:
+        return 0
+    tiles = math.ceil(M / edge) * math.ceil(N / edge) * max(1, G)
+    slab = 16 if adt == V.DT_F32 else 32
+    if tiles * 2 > cfg.nlanes or K < 4 * slab:
+        return 0
+    if edge == 256:
+        return 0
+    lg = 0
+    while (lg < V.MMA_MAX_SPLIT_LOG2 and tiles << (lg + 1) <= cfg.nlanes
+           and math.ceil(K / (1 << (lg + 1))) >= 2 * slab):
+        lg += 1
+    return lg
 
 
 def _region_inputs_from_aux(ins: V.Instr, prog: V.VMProgram) -> list:

@@ -207,6 +207,9 @@ LN_TWO_PASS = 4   # variance as mean((x - mu)^2) instead of E[x^2] - mu^2
 # MMA task p3: batch count in bits 0..23, tile-edge code in bits 24..27
 MMA_TILE_CODES = {0: 0, 64: 1, 128: 2, 256: 3}
 MMA_CODE_TILE = {1: 64, 2: 128, 3: 256}
+# TOP_MMA p3 bits 28-31: log2 of the K split (extension), at most 5
+MMA_SPLIT_SHIFT = 28
+MMA_MAX_SPLIT_LOG2 = 5
 
 # ---- entry sentinels (scheduler.py:80-85) ---------------------------------------
 ENT_NOP = 0xFFFFFFFF

@@ -451,6 +451,33 @@ def test_dot_fast_path_epilogue(in_dt, out_dt):
     assert_rel(as_f32(got[0], odt), as_f32(want[0], odt), BF16_ULP if out_dt == "bf16" else 1e-5, 1e-6, "fast epilogue")
 
 
+@pytest.mark.parametrize("dt", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("Gb,M,K,N", [(1, 256, 512, 64), (2, 100, 300, 70), (1, 64, 1000, 128), (1, 256, 128, 512)])
+def test_dot_split_k_exact(dt, Gb, M, K, N):
+    """K-split matmul tiles (few output tiles, deep K; K = 300 leaves the last
+    split short, or empty): each split publishes its partial tile, the last to
+    arrive sums them in split order and applies the bias + relu epilogue.
+    Integer-valued operands give the exact product; the program runs twice, so the
+    second run finds the arrival counters reset."""
+    rng = np.random.default_rng(74)
+    a = rng.integers(-3, 4, (Gb, M, K)).astype(np.float32)
+    b = rng.integers(-3, 4, (Gb, K, N)).astype(np.float32)
+    bias = rng.integers(-9, 10, N).astype(np.float32)
+    g = G.Graph()
+    x, y, bb = g.input(a.shape, dt), g.input(b.shape, dt), g.input(bias.shape)
+    g.output(g.dot(x, y, residual=bb, epilogue=[(V.SUB_ADD, 2, 0.0, 0.0), (V.SUB_MAX, 3, 0.0, 0.0)]))
+    blob, cfg = blob_for(g.build())
+    task = vmref.parse(blob).tasks[0]
+    assert task.top == V.TOP_MMA and task.p[3] >> V.MMA_SPLIT_SHIFT >= 1, hex(task.p[3])
+    want = np.maximum(np.matmul(a.astype(np.float64), b.astype(np.float64)) + bias, 0.0).astype(np.float32)
+    lp = runtime().load(blob)
+    try:
+        for run in range(2):
+            np.testing.assert_array_equal(lp(a, b, bias)[0], want, err_msg=f"run {run}")
+    finally:
+        lp.close()
+
+
 def test_dot_fast_path_random_bf16():
     rng = np.random.default_rng(1003)
     M = K = N = 1024

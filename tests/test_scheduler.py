@@ -158,7 +158,54 @@ def test_mma_autotile_picks_parallel_tile():
     a, b = g.input((512, 768)), g.input((768, 768))
     g.output(g.dot(a, b))
     sched = S.schedule_program(g.build(), S.DeviceConfig(nlanes=256, mma_t=128))
-    assert (sched.tasks[0].p3 >> 24) == V.MMA_TILE_CODES[64]
+    assert (sched.tasks[0].p3 >> 24) & 0xF == V.MMA_TILE_CODES[64]
+
+
+# --- K-split matmuls (extension) -----------------------------------------------------
+
+def test_mma_split_k_choice():
+    """Config 1's matmuls on 128 lanes: [256,128]x[128,512] as 32 tiles of 64 x 64
+    split 4 ways (two 16-deep slabs each), [256,512]x[512,64] as 4 tiles split 16
+    ways; never a split for big outputs, shallow K, or with the switch off."""
+    cfg = S.DeviceConfig(nlanes=128)
+    assert S.mma_split_log2(256, 512, 128, 1, 64, V.DT_F32, cfg) == 2
+    assert S.mma_split_log2(256, 64, 512, 1, 64, V.DT_F32, cfg) == 4
+    assert S.mma_split_log2(256, 64, 512, 1, 64, V.DT_BF16, cfg) == 3      # 32-deep 16-bit slabs
+    assert S.mma_split_log2(4096, 4096, 4096, 1, 256, V.DT_BF16, cfg) == 0
+    assert S.mma_split_log2(256, 64, 48, 1, 64, V.DT_F32, cfg) == 0
+    assert S.mma_split_log2(64, 64, 1 << 20, 1, 64, V.DT_F32, cfg) == V.MMA_MAX_SPLIT_LOG2
+    off = S.DeviceConfig.from_env({"PJRT_AMD_MMA_SPLITK": "0", "PJRT_OCL_NLANES": "128"})
+    assert S.mma_split_log2(256, 64, 512, 1, 64, V.DT_F32, off) == 0
+    g = G.Graph()
+    x, w = g.input((256, 512)), g.input((512, 64))
+    g.output(g.dot(x, w))
+    t = S.schedule_program(g.build(), S.DeviceConfig(nlanes=128, fit_lanes=False)).tasks[0]
+    assert t.p3 >> V.MMA_SPLIT_SHIFT == 4
+    assert S.n_tiles(t, S.DeviceConfig(nlanes=128)) == 4 * 16
+
+
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+@pytest.mark.parametrize("Gb,M,K,N", [(1, 256, 512, 64), (2, 100, 300, 70), (1, 64, 1000, 128)])
+def test_mma_split_k_tiles_exact(dt, Gb, M, K, N):
+    """Integer-valued operands give an exact product however K is cut: the lane
+    simulator (tiles in forward and reverse lane order, each output tile written
+    once all its splits have run) gives the float64 product bit for bit, with a
+    bias + relu epilogue on the combined sum."""
+    from oracle import vmref
+    rng = np.random.default_rng(8)
+    a = rng.integers(-3, 4, (Gb, M, K)).astype(np.float32)
+    b = rng.integers(-3, 4, (Gb, K, N)).astype(np.float32)
+    bias = rng.integers(-9, 10, N).astype(np.float32)
+    g = G.Graph()
+    x, y, bb = g.input(a.shape, dt), g.input(b.shape, dt), g.input(bias.shape)
+    g.output(g.dot(x, y, residual=bb, epilogue=[(V.SUB_ADD, 2, 0.0, 0.0), (V.SUB_MAX, 3, 0.0, 0.0)]))
+    prog = g.build()
+    sched = S.schedule_program(prog, S.DeviceConfig(nlanes=128, fit_lanes=False))
+    assert sched.tasks[0].p3 >> V.MMA_SPLIT_SHIFT >= 1
+    blob = V.serialize(prog, sched)
+    got = vmref.execute_schedule(blob, [a, b, bias])[0]
+    want = np.maximum(np.matmul(a.astype(np.float64), b.astype(np.float64)) + bias, 0.0)
+    np.testing.assert_array_equal(got, want.astype(np.float32))
 
 
 # --- skinny matmuls as split-K TOP_GEMV tasks ----------------------------------------

@@ -458,7 +458,11 @@ typedef __attribute__((address_space(3))) u16x8 lds_u16x8;
 // tell which LDS bytes the transfer writes, would otherwise wait for it before
 // every LDS read.  The tile waits for its transfers itself (vmcnt) before the
 // block barrier that publishes a stage.  One wait state between the M0 write and
-// the transfer that reads it.
+// the transfer that reads it.  M0 is a reserved register, so the clobber is a
+// statement of intent the compiler may not honour: the functions that issue
+// these transfers (the 16-bit GEMM fast path, the attention tile) contain no
+// other M0 use in this build (no indirect register moves, no message sends),
+// checked in their gfx950 assembly.
 VM_DEV void dma16(const gbyte* base, uint32_t voff, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
                :

@@ -36,6 +36,7 @@ enum {
 
 typedef struct vmrt_runtime vmrt_runtime;
 typedef struct vmrt_program vmrt_program;
+typedef struct vmrt_launch vmrt_launch;
 
 typedef struct {
   int32_t device;              /* HIP device ordinal */
@@ -66,10 +67,13 @@ void vmrt_default_options(vmrt_options* opts);
  * Replaces OclRuntime::Create (runtime.h:120-135; runtime.cc:255-662). */
 int vmrt_create(const vmrt_options* opts, vmrt_runtime** out, char* err, size_t errlen);
 
-/* Replaces OclRuntime::~OclRuntime.  Waits for the device, then unloads every
+/* Replaces OclRuntime::~OclRuntime.  Waits for the runtime's stream and for each
+ * loaded program's latest launch on the stream it was enqueued on (which must
+ * still exist; other work on the device is not waited for), then unloads every
  * program still loaded on this runtime (a program borrows its runtime's device,
  * stream and mutex, runtime.h:365): their handles are invalid afterwards and must
- * not be passed to vmrt_unload or any other call. */
+ * not be passed to vmrt_unload or any other call.  Launch handles of
+ * vmrt_submit must be released before. */
 void vmrt_destroy(vmrt_runtime* rt);
 
 /* Device parameters the lowering must schedule for: these are the values the
@@ -86,7 +90,8 @@ int vmrt_load(vmrt_runtime* rt, const void* bytes, size_t len, uint32_t ew_ts, u
               vmrt_program** out, char* err, size_t errlen);
 
 /* Replaces LoadedProgram::~LoadedProgram (runtime.cc:1076-1086).  Waits for the
- * program's last launch first. */
+ * program's latest launch first, on the stream it was enqueued on (which must
+ * still exist). */
 void vmrt_unload(vmrt_program* prog);
 
 /* Program signature (executable metadata the PJRT layer reports,
@@ -112,8 +117,10 @@ int vmrt_enqueue(vmrt_program* prog, const void* const* inputs, size_t n_inputs,
 /* Parse, validate and run a VMProgram v3 blob once, synchronously, without
  * allocating: no hipMalloc / hipFree and no allocating library routine.  No
  * counterpart in the reference: it is for callers that cannot allocate device
- * memory (code under HIP graph capture, tight serving loops, harnesses that
- * forbid hipMalloc).  The program's arena, side tables, barrier words and task
+ * memory (tight serving loops, harnesses that forbid hipMalloc).  It is not for
+ * use under HIP graph capture: it uploads the program's tables with copies on
+ * the runtime's stream and synchronizes that stream before it returns.  The
+ * program's arena, side tables, barrier words and task
  * scratch live in a static device array of 64 MiB per GPU, reserved when the
  * library loads and held until the process ends; a program needing more is
  * rejected with VMRT_RESOURCE_EXHAUSTED.  Inputs and outputs are the caller's
@@ -124,6 +131,26 @@ int vmrt_enqueue(vmrt_program* prog, const void* const* inputs, size_t n_inputs,
 int vmrt_run_noalloc(vmrt_runtime* rt, const void* bytes, size_t len, uint32_t ew_ts, uint32_t mma_t,
                      const void* const* inputs, size_t n_inputs, void* const* outputs, size_t n_outputs, char* err,
                      size_t errlen);
+
+/* One launch with a status of its own, for callers with several launches of
+ * one program in flight (the PJRT plugin's asynchronous Execute).  Enqueues the
+ * program on the runtime's stream as vmrt_enqueue does, followed by a status
+ * epilogue that copies the VM status word into a slot of pinned host memory
+ * owned by this launch and, when the launch aborted, clears the program's
+ * control words and task scratch, so a launch queued behind it starts clean.
+ * vmrt_launch_query returns VMRT_OK once the launch and its epilogue have
+ * completed and VMRT_UNAVAILABLE while they have not, without waiting and
+ * without taking the runtime's lock; vmrt_launch_wait waits for them and returns
+ * this launch's own outcome (VMRT_INTERNAL with the VM's message when it
+ * aborted).  vmrt_launch_release waits for the launch and frees the handle.  No
+ * counterpart in the reference, whose execution is synchronous
+ * (plugin.cc:175-184, runtime.cc:2185-2189).  The program's shared status word
+ * is left clear, so vmrt_program_status does not report a submitted launch. */
+int vmrt_submit(vmrt_program* prog, const void* const* inputs, size_t n_inputs, void* const* outputs,
+                size_t n_outputs, vmrt_launch** out, char* err, size_t errlen);
+int vmrt_launch_query(vmrt_launch* launch);
+int vmrt_launch_wait(vmrt_launch* launch, char* err, size_t errlen);
+void vmrt_launch_release(vmrt_launch* launch);
 
 /* Wait for the stream of the program's latest launch (the runtime's, or the
  * stream given to vmrt_enqueue, which must still exist), then read and clear

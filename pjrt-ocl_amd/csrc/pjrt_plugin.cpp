@@ -7,13 +7,16 @@
 //   * buffers are pool-owned HIP device memory (vmrt_alloc), filled and read
 //     back synchronously;
 //   * Execute is asynchronous: the program is launched on the runtime's stream
-//     (vmrt_enqueue) and a HIP event recorded after it is the Execute's
-//     completion event and its outputs' ready event, whose error is the VM
-//     status word read once the event completes (a barrier time-out, say).
+//     with a status of its own (vmrt_submit), which is the Execute's
+//     completion event and its outputs' ready event; its error is that
+//     launch's VM status (a barrier time-out, say), never another launch's.
 //     Everything runs on the one stream, so later launches and copies are
 //     ordered after it and pool memory may be reused at once.  OnReady
 //     callbacks of pending events run on one waiter thread per client.  (The
 //     reference's events are born complete, plugin.cc:175-184.);
+//   * the runtime is shared by the client, its executables and its buffers,
+//     and closed when the last of them goes, so an executable or buffer that
+//     outlives its client is still destroyed safely;
 //   * Compile hands the StableHLO program to the Python lowering service and
 //     loads the VMProgram v3 bytes it returns (plugin.cc:748-819); the service
 //     runs as one child process per client, started at Client_Create, with
@@ -62,6 +65,16 @@ struct PJRT_Error {
 namespace {
 struct ExecState;
 class Waiter;
+
+// The runtime, shared by the client, its executables and its buffers, and
+// destroyed with the last of them (a program or buffer freed after its client
+// still needs the runtime that owns its memory).
+struct RtOwner {
+  vmrt_runtime* rt = nullptr;
+  ~RtOwner() {
+    if (rt) vmrt_destroy(rt);
+  }
+};
 }  // namespace
 
 struct PJRT_DeviceDescription {
@@ -287,6 +300,7 @@ size_t type_size(PJRT_Buffer_Type t) {
 }  // namespace
 
 struct PJRT_Client {
+  std::shared_ptr<RtOwner> owner;   // holds the runtime; rt is owner->rt
   vmrt_runtime* rt = nullptr;
   vmrt_device_info info{};
   PJRT_Device device;
@@ -297,12 +311,13 @@ struct PJRT_Client {
   std::string version;
   std::string costs;     // the cost table handed to the lowering (JSON), or empty
   std::mutex compile_mu;
-  std::unique_ptr<Waiter> waiter;      // runs OnReady callbacks of pending events
+  std::shared_ptr<Waiter> waiter;      // runs OnReady callbacks of pending events
   ~PJRT_Client();
 };
 
 struct PJRT_Buffer {
   PJRT_Client* client = nullptr;
+  std::shared_ptr<RtOwner> owner;      // the runtime whose pool holds ptr
   void* ptr = nullptr;
   size_t bytes = 0;
   PJRT_Buffer_Type type = PJRT_Buffer_Type_INVALID;
@@ -310,7 +325,7 @@ struct PJRT_Buffer {
   bool deleted = false;
   std::shared_ptr<ExecState> ready;    // the Execute that produced it (null: ready)
   void release() {
-    if (ptr && client && client->rt) vmrt_free(client->rt, ptr);
+    if (ptr && owner && owner->rt) vmrt_free(owner->rt, ptr);
     ptr = nullptr;
   }
 };
@@ -319,6 +334,7 @@ namespace {
 // The compiled program and its signature; shared by the loaded executable and
 // the PJRT_Executable views handed out for metadata.
 struct Program {
+  std::shared_ptr<RtOwner> owner;      // released after the program is unloaded
   vmrt_program* prog = nullptr;
   std::string name, fingerprint;
   int64_t code_bytes = 0;
@@ -340,41 +356,27 @@ struct Program {
 }  // namespace
 
 namespace {
-// Completion of one Execute: a HIP event recorded after the launch on the
-// runtime's stream, and the program whose VM status word is read (and cleared)
-// once the event has completed.  Shared by the Execute's completion event and
-// the ready events of its outputs.
+// Completion of one Execute: its launch (vmrt_submit), whose own status is read
+// once it has completed.  Shared by the Execute's completion event and the
+// ready events of its outputs.  Querying takes no runtime lock and never waits.
 struct ExecState {
-  void* ev = nullptr;
-  std::shared_ptr<Program> prog;
-  Waiter* waiter = nullptr;
+  vmrt_launch* launch = nullptr;
+  std::shared_ptr<Program> prog;       // keeps the program (and the runtime) alive
+  std::weak_ptr<Waiter> waiter;
   std::mutex mu;
   bool done = false;
   PJRT_Error_Code code = PJRT_Error_Code_OK;
   std::string message;
   ~ExecState() {
-    if (ev) vmrt_event_destroy(ev);
-  }
-  void finish_locked(int rc) {
-    if (done) return;
-    done = true;
-    if (rc != VMRT_OK) {
-      code = PJRT_Error_Code_INTERNAL;
-      message = "execute: waiting for the device failed";
-      return;
-    }
-    char e[1024];
-    if (int st = vmrt_program_status(prog->prog, e, sizeof e)) {
-      code = static_cast<PJRT_Error_Code>(st);
-      message = std::string("execute: ") + e;
-    }
+    if (launch) vmrt_launch_release(launch);
   }
   bool ready() {
-    std::lock_guard<std::mutex> g(mu);
-    if (done) return true;
-    const int rc = vmrt_event_query(ev);
-    if (rc == VMRT_UNAVAILABLE) return false;
-    finish_locked(rc);
+    {
+      std::lock_guard<std::mutex> g(mu);
+      if (done) return true;
+    }
+    if (launch && vmrt_launch_query(launch) == VMRT_UNAVAILABLE) return false;
+    wait();                         // complete: reads the launch's status without waiting
     return true;
   }
   void wait() {
@@ -382,9 +384,15 @@ struct ExecState {
       std::lock_guard<std::mutex> g(mu);
       if (done) return;
     }
-    const int rc = vmrt_event_synchronize(ev);
+    char e[1024] = "";
+    const int rc = launch ? vmrt_launch_wait(launch, e, sizeof e) : VMRT_OK;
     std::lock_guard<std::mutex> g(mu);
-    finish_locked(rc);
+    if (done) return;
+    done = true;
+    if (rc != VMRT_OK) {
+      code = static_cast<PJRT_Error_Code>(rc);
+      message = std::string("execute: ") + e;
+    }
   }
   // a new error object for the outcome (null: success); call once done
   PJRT_Error* error() {
@@ -446,7 +454,7 @@ class Waiter {
 PJRT_Client::~PJRT_Client() {
   waiter.reset();             // pending callbacks run first
   lower.stop();
-  if (rt) vmrt_destroy(rt);
+  owner.reset();              // the runtime goes with the last executable or buffer
 }
 
 struct PJRT_Event {
@@ -517,11 +525,12 @@ PJRT_Error* Event_Await(PJRT_Event_Await_Args* a) {
 }
 PJRT_Error* Event_OnReady(PJRT_Event_OnReady_Args* a) {
   const std::shared_ptr<ExecState>& s = a->event->s;
-  if (!s || s->ready() || !s->waiter) {
+  std::shared_ptr<Waiter> w = s ? s->waiter.lock() : nullptr;
+  if (!s || s->ready() || !w) {
     if (s) s->wait();
     a->callback(s ? s->error() : nullptr, a->user_arg);
   } else {
-    s->waiter->post(s, a->callback, a->user_arg);
+    w->post(s, a->callback, a->user_arg);
   }
   return nullptr;
 }
@@ -608,8 +617,10 @@ PJRT_Error* Client_Create(PJRT_Client_Create_Args* a) {
   vmrt_default_options(&o);
   char e[1024];
   if (int rc = vmrt_create(&o, &c->rt, e, sizeof e)) return from_vmrt(rc, e, "device");
+  c->owner = std::make_shared<RtOwner>();
+  c->owner->rt = c->rt;
   vmrt_device_info_get(c->rt, &c->info);
-  c->waiter = std::make_unique<Waiter>();
+  c->waiter = std::make_shared<Waiter>();
   c->version = vmrt_version();
   c->costs = cost_table(c->rt, c->info);
   PJRT_Device& d = c->device;
@@ -707,6 +718,7 @@ PJRT_Error* Client_Compile(PJRT_Client_Compile_Args* a) {
   if (status == 2) return make_error(PJRT_Error_Code_UNIMPLEMENTED, "unsupported program: " + payload);
   if (status != 0) return make_error(PJRT_Error_Code_INTERNAL, "lowering failed: " + payload);
   auto p = std::make_shared<Program>();
+  p->owner = c->owner;
   char e[1024];
   if (int rc = vmrt_load(c->rt, payload.data(), payload.size(), c->info.ew_ts, c->info.mma_t, &p->prog, e, sizeof e))
     return from_vmrt(rc, e, "load");
@@ -760,6 +772,7 @@ PJRT_Error* Client_BufferFromHostBuffer(PJRT_Client_BufferFromHostBuffer_Args* a
   }
   auto b = std::make_unique<PJRT_Buffer>();
   b->client = a->client;
+  b->owner = a->client->owner;
   b->bytes = n * es;
   b->type = a->type;
   b->dims.assign(a->dims, a->dims + a->num_dims);
@@ -1000,6 +1013,7 @@ PJRT_Error* LE_Execute(PJRT_LoadedExecutable_Execute_Args* a) {
   for (size_t i = 0; i < p.out_dt.size(); ++i) {
     auto b = std::make_unique<PJRT_Buffer>();
     b->client = c;
+    b->owner = c->owner;
     b->bytes = p.out_bytes[i];
     b->type = p.out_types[i];
     b->dims = p.out_dims[i];
@@ -1019,12 +1033,8 @@ PJRT_Error* LE_Execute(PJRT_LoadedExecutable_Execute_Args* a) {
   };
   auto st = std::make_shared<ExecState>();
   st->prog = ex->p;
-  st->waiter = c->waiter.get();
-  if (vmrt_event_create(c->rt, &st->ev) != VMRT_OK) {
-    drop_outputs();
-    return make_error(PJRT_Error_Code_INTERNAL, "execute: event create failed");
-  }
-  if (int rc = vmrt_enqueue(p.prog, ins.data(), ins.size(), optr.data(), optr.size(), nullptr, e, sizeof e)) {
+  st->waiter = c->waiter;
+  if (int rc = vmrt_submit(p.prog, ins.data(), ins.size(), optr.data(), optr.size(), &st->launch, e, sizeof e)) {
     drop_outputs();
     return from_vmrt(rc, e, "execute");
   }
@@ -1034,7 +1044,6 @@ PJRT_Error* LE_Execute(PJRT_LoadedExecutable_Execute_Args* a) {
       in->ptr = nullptr;
       in->deleted = true;
     }
-  if (vmrt_event_record(c->rt, st->ev, nullptr) != VMRT_OK) st->wait();   // no event: complete it now
   for (size_t i = 0; i < outs.size(); ++i) {
     outs[i]->ready = st;
     a->output_lists[0][i] = outs[i].release();
@@ -1100,7 +1109,7 @@ PJRT_Error* Buf_ToHostBuffer(PJRT_Buffer_ToHostBuffer_Args* a) {
   }
   char e[1024];
   if (b->bytes)
-    if (int rc = vmrt_d2h(b->client->rt, a->dst, b->ptr, b->bytes, e, sizeof e)) return from_vmrt(rc, e, "device to host");
+    if (int rc = vmrt_d2h(b->owner->rt, a->dst, b->ptr, b->bytes, e, sizeof e)) return from_vmrt(rc, e, "device to host");
   a->event = new PJRT_Event{};
   return nullptr;
 }

@@ -176,7 +176,7 @@ VM_DEV void attn_block_mfma(Args A, uint32_t ti, uint32_t h, uint32_t row0, uint
   // masked out of S; their V rows are zeroed by the lane that fetched them, once
   // its own transfers have landed, so 0-weight keys add 0.
   const uint32_t lds0 = uni(uint32_t(reinterpret_cast<uintptr_t>(lds_ptr<lds_u8>())));
-  const lds_u8* LB = (const lds_u8*)lds0;
+  const lds_u8* LB = (const lds_u8*)uintptr_t(lds0);
   const uint32_t st0 = lds0, st1 = lds0 + L::kStage;
   const uint32_t wo = uni(1024 * wave);
   const uint32_t dr = (1024 * wave + 16 * lane) / L::kRow;            // row within a round

@@ -101,6 +101,22 @@ VM_DEV float epi_inline(uint32_t kind, float x, float y, float s, float t) {
   }
 }
 
+// One 32 x 32 block through the epilogue program, element by element (the
+// general path for epilogue kinds the store cannot evaluate inline).  A function
+// of its own, taking the block by value: the caller's loop over blocks then
+// unrolls, so its accumulators stay in registers.
+VM_TILE void store_block_epi(Args A, uint32_t epi, const gbyte* res, gbyte* d, uint32_t dt, uint32_t M, uint32_t N,
+                             f32x16 blk, uint32_t g, uint32_t rbase, uint32_t col) {
+#pragma unroll 1
+  for (int v = 0; v < 16; ++v) {
+    const uint32_t row = rbase + 8 * (v >> 2) + (v & 3);
+    if (row < M && col < N) {
+      const uint64_t elem = (uint64_t(g) * M + row) * N + col;
+      store_f(d, dt, elem, apply_epilogue(A, epi, res, elem, col, blk[v]));
+    }
+  }
+}
+
 template <int T>
 VM_DEV void store_acc(Args A, const MmaDesc& D, const f32x16 (&acc)[MmaCfg<T>::kBM][MmaCfg<T>::kBN], uint32_t g,
                       uint32_t m0, uint32_t n0) {
@@ -129,7 +145,7 @@ VM_DEV void store_acc(Args A, const MmaDesc& D, const f32x16 (&acc)[MmaCfg<T>::k
     for (int bn = 0; bn < MmaCfg<T>::kBN; ++bn) {
       const uint32_t col = n0 + wn * (T / 2) + bn * 32 + (lane & 31);
       const uint32_t rbase = m0 + wm * (T / 2) + bm * 32 + 4 * (lane >> 5);
-      if (inl) {
+      if (T == 64 && inl) {
         const uint32_t cc = min(col, D.N - 1);
         const float yc = need_col ? res[cc] : 0.0f;
         float yr[16];
@@ -150,14 +166,7 @@ VM_DEV void store_acc(Args A, const MmaDesc& D, const f32x16 (&acc)[MmaCfg<T>::k
           if (row < D.M && col < D.N) store_f(D.d, D.dt, (uint64_t(g) * D.M + row) * D.N + col, x);
         }
       } else if (D.epi) {
-#pragma unroll 1
-        for (int v = 0; v < 16; ++v) {
-          const uint32_t row = rbase + 8 * (v >> 2) + (v & 3);
-          if (row < D.M && col < D.N) {
-            const uint64_t elem = (uint64_t(g) * D.M + row) * D.N + col;
-            store_f(D.d, D.dt, elem, apply_epilogue(A, D.epi, D.res, elem, col, acc[bm][bn][v]));
-          }
-        }
+        store_block_epi(A, D.epi, D.res, D.d, D.dt, D.M, D.N, acc[bm][bn], g, rbase, col);
       } else {
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
@@ -457,17 +466,23 @@ typedef __attribute__((address_space(3))) u16x8 lds_u16x8;
 // [lds + 16 l, +16) with base[voff].  Issued from asm: the compiler, which cannot
 // tell which LDS bytes the transfer writes, would otherwise wait for it before
 // every LDS read.  The tile waits for its transfers itself (vmcnt) before the
-// block barrier that publishes a stage.  One wait state between the M0 write and
-// the transfer that reads it.  M0 is a reserved register, so the clobber is a
-// statement of intent the compiler may not honour: the functions that issue
-// these transfers (the 16-bit GEMM fast path, the attention tile) contain no
-// other M0 use in this build (no indirect register moves, no message sends),
-// checked in their gfx950 assembly.
+// block barrier that publishes a stage.  The transfer takes its LDS address from
+// M0, which the compiler reserves and does not let an asm statement declare as
+// clobbered, so the statement leaves M0 as it found it: it saves M0 in an SGPR
+// of its own, loads the address, waits the one state the M0 write needs before
+// the transfer reads it, issues the transfer (which takes M0 at issue) and puts
+// the saved value back.
 VM_DEV void dma16(const gbyte* base, uint32_t voff, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
-               :
-               : "s"(lds), "v"(voff), "s"(base)
-               : "memory", "m0");
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %1\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %2, %3\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "s"(lds), "v"(voff), "s"(base)
+      : "memory");
 }
 VM_DEV void wait_vm0() { __builtin_amdgcn_s_waitcnt(0x0F70); }    // s_waitcnt vmcnt(0)
 VM_DEV void wait_vm8() { __builtin_amdgcn_s_waitcnt(0x0F78); }    // s_waitcnt vmcnt(8)
@@ -578,7 +593,7 @@ VM_LEAF void mma_tile16_fast(Args A, const MmaDesc* Dp, uint32_t tile) {
   A = uargs(A);
   const MmaDesc D = load_desc(Dp);
   const uint32_t lds0 = uni(uint32_t(reinterpret_cast<uintptr_t>(lds_ptr<lds_u8>())));
-  const lds_u8* L = (const lds_u8*)lds0;
+  const lds_u8* L = (const lds_u8*)uintptr_t(lds0);
   uint32_t g, m0, n0;
   fast_origin(D, uni(tile), &g, &m0, &n0);
   const uint32_t K = D.K, N = D.N;

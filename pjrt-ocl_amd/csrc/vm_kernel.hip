@@ -224,9 +224,39 @@ __global__ __launch_bounds__(kBlock, 1) void vm_main(VmArgs args) {
   }
 }
 
+// Status epilogue of a launch submitted with vmrt_submit, run after it on the
+// same stream: copies the program's status words into the launch's own slot (host
+// memory, slot layout in launch_slots.h) and, when the launch aborted, clears
+// the control words and the task scratch, so a later launch of the program
+// queued behind this one starts from the state the loader leaves (an aborted
+// launch can leave arrival flags and split counters part-way).  One block:
+// every thread reads the status before the block barrier, and only then may
+// any thread clear it.
+__global__ __launch_bounds__(1024) void vm_status_epilogue(uint32_t* ctl, uint32_t* slot, uint32_t* scratch,
+                                                          uint64_t scratch_words) {
+  const uint32_t err = __hip_atomic_load(&ctl[BAR_ERROR], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const uint32_t info = __hip_atomic_load(&ctl[BAR_ERRINFO], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    __hip_atomic_store(&slot[0], err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    __hip_atomic_store(&slot[1], info, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    __hip_atomic_store(&slot[2], 0x53544154u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+  }
+  if (err == VM_OK) return;
+  for (uint32_t i = threadIdx.x; i < uint32_t(BAR_WORDS); i += blockDim.x) ctl[i] = 0;
+  for (uint64_t i = threadIdx.x; i < scratch_words; i += blockDim.x) scratch[i] = 0;
+}
+
 }  // namespace vm
 
 // ---- host side of the launch (called by the runtime) ------------------------------------
+extern "C" hipError_t vm_status_epilogue_launch(uint32_t* ctl, uint32_t* slot, uint8_t* scratch,
+                                                uint64_t scratch_bytes, hipStream_t stream) {
+  uint32_t* words = reinterpret_cast<uint32_t*>(scratch);
+  uint64_t n_words = scratch_bytes / 4;
+  void* args[] = {&ctl, &slot, &words, &n_words};
+  return hipLaunchKernel(reinterpret_cast<const void*>(&vm::vm_status_epilogue), dim3(1), dim3(1024), args, 0, stream);
+}
 extern "C" int vm_kernel_smem_bytes() { return vm::kSmemBytes; }
 
 extern "C" hipError_t vm_kernel_prepare() {

@@ -24,12 +24,15 @@
 #include <vector>
 
 #include "../../include/vmrt.h"
+#include "launch_slots.h"
 #include "vm_abi.h"
 
 extern "C" int vm_kernel_smem_bytes();
 extern "C" hipError_t vm_kernel_prepare();
 extern "C" hipError_t vm_kernel_occupancy(int* blocks_per_cu);
 extern "C" hipError_t vm_kernel_launch(const vm::VmArgs* args, hipStream_t stream, int cooperative);
+extern "C" hipError_t vm_status_epilogue_launch(uint32_t* ctl, uint32_t* slot, uint8_t* scratch, uint64_t scratch_bytes,
+                                                hipStream_t stream);
 
 namespace {
 
@@ -632,6 +635,13 @@ constexpr int kMaxDevices = 64;
 static std::mutex g_scratch_mu;
 static uint8_t* g_scratch_dev[kMaxDevices];
 
+// Pinned host memory for the launches' status slots (the device writes them).
+static void* slot_alloc(size_t bytes) {
+  void* p = nullptr;
+  return hipHostMalloc(&p, bytes, hipHostMallocCoherent | hipHostMallocMapped) == hipSuccess ? p : nullptr;
+}
+static void slot_free(void* p) { (void)hipHostFree(p); }
+
 struct vmrt_runtime {
   int device = 0;
   hipStream_t stream = nullptr;
@@ -640,6 +650,15 @@ struct vmrt_runtime {
   std::mutex mu;     // serialises execute / transfers (runtime.h:233, 301)
   Pool pool;
   std::set<vmrt_program*> programs;   // loaded and not yet unloaded (guarded by mu)
+  vmrt_host::SlotPool slots{slot_alloc, slot_free};   // per-launch status (vmrt_submit)
+};
+
+// A launch submitted with vmrt_submit: the event recorded after its status
+// epilogue, and the slot that epilogue writes.
+struct vmrt_launch {
+  vmrt_runtime* rt = nullptr;
+  hipEvent_t ev = nullptr;
+  uint32_t* slot = nullptr;
 };
 
 struct vmrt_program {
@@ -744,11 +763,15 @@ static void free_program_memory(vmrt_program* p);
 void vmrt_destroy(vmrt_runtime* rt) {
   if (!rt) return;
   hipSetDevice(rt->device);
-  hipDeviceSynchronize();   // programs may have been enqueued on caller streams
+  // the runtime's stream, and each program's latest launch on a caller's stream
+  // (which must still exist); other work on the device is not waited for
+  hipStreamSynchronize(rt->stream);
   {
     // programs still loaded are unloaded with their runtime: they borrow its
     // device, stream and mutex (runtime.h:365), so none may outlive it
     std::lock_guard<std::mutex> g(rt->mu);
+    for (vmrt_program* p : rt->programs)
+      if (p->launched && p->last_stream != rt->stream) hipStreamSynchronize(p->last_stream);
     for (vmrt_program* p : rt->programs) {
       free_program_memory(p);
       delete p;
@@ -787,9 +810,9 @@ void vmrt_unload(vmrt_program* p) {
   std::lock_guard<std::mutex> g(rt->mu);
   if (!rt->programs.erase(p)) return;   // not a live program of this runtime
   hipSetDevice(rt->device);
-  // the program may have been enqueued on a caller's stream that no longer
-  // exists: wait for the whole device before its memory is released
-  if (p->launched) hipDeviceSynchronize();
+  // its latest launch, on the runtime's stream or the caller's stream it was
+  // enqueued on (which must still exist), finishes before its memory goes
+  if (p->launched) hipStreamSynchronize(p->last_stream);
   free_program_memory(p);
   delete p;
 }
@@ -1114,12 +1137,9 @@ static int check_status(vmrt_program* p, char* err, size_t errlen) {
   hipMemset(p->ctl, 0, BAR_WORDS * 4);
   // an aborted launch can leave arrival counters part-way
   if (p->scratch) hipMemset(p->scratch, 0, std::max<uint64_t>(p->scratch_bytes, 256));
-  const char* what = st[BAR_ERROR] == VM_ERR_BARRIER_TIMEOUT ? "grid barrier timed out (lanes not co-resident, "
-                                                                "or non-uniform control across lanes)"
-                     : st[BAR_ERROR] == VM_ERR_FRAME_DEPTH ? "control frame stack overflow"
-                     : st[BAR_ERROR] == VM_ERR_BAD_TASK    ? "unsupported tile op reached the device"
-                                                           : "VM error";
-  return set_err(err, errlen, VMRT_INTERNAL, fmt("VM aborted: %s (code %u, detail %u)", what, st[BAR_ERROR], st[BAR_ERRINFO]));
+  return set_err(err, errlen, VMRT_INTERNAL,
+                 fmt("VM aborted: %s (code %u, detail %u)", vmrt_host::vm_error_text(st[BAR_ERROR]), st[BAR_ERROR],
+                     st[BAR_ERRINFO]));
 }
 
 int vmrt_enqueue(vmrt_program* p, const void* const* inputs, size_t n_in, void* const* outputs, size_t n_out,
@@ -1141,6 +1161,64 @@ int vmrt_execute(vmrt_program* p, const void* const* inputs, size_t n_in, void* 
   hipError_t e = hipStreamSynchronize(p->rt->stream);
   if (e != hipSuccess) return set_err(err, errlen, VMRT_INTERNAL, "VM execution: " + hip_msg(e));
   return check_status(p, err, errlen);
+}
+
+int vmrt_submit(vmrt_program* p, const void* const* inputs, size_t n_in, void* const* outputs, size_t n_out,
+                vmrt_launch** out, char* err, size_t errlen) {
+  if (!p || !out) return set_err(err, errlen, VMRT_INVALID_ARGUMENT, "null argument");
+  vmrt_runtime* rt = p->rt;
+  std::lock_guard<std::mutex> g(rt->mu);
+  hipSetDevice(rt->device);
+  auto l = std::make_unique<vmrt_launch>();
+  l->rt = rt;
+  l->slot = rt->slots.take();
+  if (!l->slot) return set_err(err, errlen, VMRT_RESOURCE_EXHAUSTED, "launch status slot: pinned host allocation failed");
+  uint32_t* slot_dev = nullptr;
+  hipError_t e = hipHostGetDevicePointer(reinterpret_cast<void**>(&slot_dev), l->slot, 0);
+  if (e == hipSuccess) e = hipEventCreateWithFlags(&l->ev, hipEventDisableTiming);
+  if (e != hipSuccess) {
+    rt->slots.give(l->slot);
+    return set_err(err, errlen, VMRT_INTERNAL, "launch status: " + hip_msg(e));
+  }
+  int rc = enqueue_locked(p, inputs, n_in, outputs, n_out, rt->stream, err, errlen);
+  if (rc == VMRT_OK) {
+    e = vm_status_epilogue_launch(p->ctl, slot_dev, p->scratch, std::max<uint64_t>(p->scratch_bytes, 256), rt->stream);
+    if (e == hipSuccess) e = hipEventRecord(l->ev, rt->stream);
+    if (e != hipSuccess) rc = set_err(err, errlen, VMRT_INTERNAL, "launch status epilogue: " + hip_msg(e));
+  }
+  if (rc != VMRT_OK) {
+    // nothing of this launch may still write the slot when it is handed out again
+    hipStreamSynchronize(rt->stream);
+    hipEventDestroy(l->ev);
+    rt->slots.give(l->slot);
+    return rc;
+  }
+  *out = l.release();
+  return VMRT_OK;
+}
+
+int vmrt_launch_query(vmrt_launch* l) {
+  if (!l) return VMRT_INVALID_ARGUMENT;
+  const hipError_t e = hipEventQuery(l->ev);
+  return e == hipSuccess ? VMRT_OK : e == hipErrorNotReady ? VMRT_UNAVAILABLE : VMRT_INTERNAL;
+}
+
+int vmrt_launch_wait(vmrt_launch* l, char* err, size_t errlen) {
+  if (!l) return set_err(err, errlen, VMRT_INVALID_ARGUMENT, "null launch");
+  const hipError_t e = hipEventSynchronize(l->ev);
+  if (e != hipSuccess) return set_err(err, errlen, VMRT_INTERNAL, "VM execution: " + hip_msg(e));
+  std::string msg;
+  const int rc = vmrt_host::slot_status(l->slot, &msg);
+  return rc ? set_err(err, errlen, rc, msg) : VMRT_OK;
+}
+
+void vmrt_launch_release(vmrt_launch* l) {
+  if (!l) return;
+  hipSetDevice(l->rt->device);
+  hipEventSynchronize(l->ev);     // the epilogue has written the slot before it is reused
+  hipEventDestroy(l->ev);
+  l->rt->slots.give(l->slot);
+  delete l;
 }
 
 int vmrt_run_noalloc(vmrt_runtime* rt, const void* bytes, size_t len, uint32_t ew_ts, uint32_t mma_t,

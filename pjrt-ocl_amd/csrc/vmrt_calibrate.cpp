@@ -219,8 +219,8 @@ extern "C" int vmrt_calibrate(vmrt_runtime* rt, char* json, size_t cap, char* er
   vmrt_device_info_get(rt, &I);
   std::string msg;
   Timer T{rt, &msg};
-  // per-tile cost of each family on one lane: slope between t and 2t tiles
-  static const char* kKeys[4] = {"ew_tile_us", "mma_tile_us", "reduce_tile_us", "gather_tile_us"};
+  // per-tile cost of each family on one lane (ew, mma, reduce, gather: the
+  // reference's four keys, written below): slope between t and 2t tiles
   const uint32_t t_lo[4] = {32, 8, 32, 32};
   double us[4];
   for (int f = 0; f < 4; ++f) {

@@ -83,6 +83,11 @@ SIGNATURES = {
     "vmrt_execute": (ctypes.c_int, [_VP, ctypes.POINTER(_VP), _SZ, ctypes.POINTER(_VP), _SZ, _CP, _SZ]),
     "vmrt_enqueue": (ctypes.c_int, [_VP, ctypes.POINTER(_VP), _SZ, ctypes.POINTER(_VP), _SZ, _VP, _CP, _SZ]),
     "vmrt_program_status": (ctypes.c_int, [_VP, _CP, _SZ]),
+    "vmrt_submit": (ctypes.c_int, [_VP, ctypes.POINTER(_VP), _SZ, ctypes.POINTER(_VP), _SZ, ctypes.POINTER(_VP), _CP,
+                                   _SZ]),
+    "vmrt_launch_query": (ctypes.c_int, [_VP]),
+    "vmrt_launch_wait": (ctypes.c_int, [_VP, _CP, _SZ]),
+    "vmrt_launch_release": (None, [_VP]),
     "vmrt_run_noalloc": (ctypes.c_int, [_VP, _VP, _SZ, _U32, _U32, ctypes.POINTER(_VP), _SZ, ctypes.POINTER(_VP),
                                         _SZ, _CP, _SZ]),
     "vmrt_program_profile": (ctypes.c_int, [_VP, ctypes.POINTER(ctypes.c_uint64), _SZ, ctypes.c_int, _CP, _SZ]),
@@ -379,6 +384,39 @@ class Event:
             pass
 
 
+class Launch:
+    """One submitted launch and its own status (vmrt_submit)."""
+
+    def __init__(self, rt: Runtime, handle):
+        self.rt = rt
+        self._h = handle
+
+    def done(self) -> bool:
+        """Whether the launch has completed (no wait)."""
+        rc = self.rt._lib.vmrt_launch_query(self._h)
+        if rc not in (OK, UNAVAILABLE):
+            raise VmrtError(rc, "launch query")
+        return rc == OK
+
+    def wait(self) -> None:
+        """Wait for the launch; raise if it aborted."""
+        err = ctypes.create_string_buffer(_ERRLEN)
+        _check(self.rt._lib.vmrt_launch_wait(self._h, err, _ERRLEN), err)
+
+    def release(self) -> None:
+        h, self._h = self._h, None
+        if h and not self.rt.closed:
+            self.rt._lib.vmrt_launch_release(h)
+
+    def __del__(self):
+        if sys.is_finalizing():
+            return
+        try:
+            self.release()
+        except Exception:
+            pass
+
+
 class IOSpec:
     def __init__(self, dtype: int, nbytes: int, shape: tuple):
         self.dtype, self.nbytes, self.shape = dtype, nbytes, shape
@@ -457,6 +495,15 @@ class LoadedProgram:
         err = ctypes.create_string_buffer(_ERRLEN)
         _check(self.rt._lib.vmrt_enqueue(self._live(), ins, len(inputs), outs, len(outputs), _VP(stream or 0), err,
                                          _ERRLEN), err)
+
+    def submit(self, inputs, outputs) -> "Launch":
+        """Launch on the runtime's stream with a status of its own (vmrt_submit)."""
+        ins, outs = self._arrays(inputs, outputs)
+        err = ctypes.create_string_buffer(_ERRLEN)
+        h = _VP()
+        _check(self.rt._lib.vmrt_submit(self._live(), ins, len(inputs), outs, len(outputs), ctypes.byref(h), err,
+                                        _ERRLEN), err)
+        return Launch(self.rt, h)
 
     def status(self) -> None:
         """Synchronize and raise if the VM aborted (barrier time-out etc.)."""

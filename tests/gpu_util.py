@@ -108,3 +108,33 @@ def attention_abs_scale(q, kt, v, scale, causal):
     p = np.exp(s - s.max(-1, keepdims=True))
     p /= p.sum(-1, keepdims=True)
     return np.einsum("htc,hcd->htd", p, np.abs(v.astype(np.float64)))
+
+
+def check_decoder(got, want, rel, pinned, what="decoder"):
+    """Greedy decoding, step by step: the logits of every step agree within
+    ``rel`` of the oracle's largest logit, and the tokens are equal until a step
+    where the oracle's top two logits lie within twice that tolerance (a
+    near-tie: either token is a correct greedy choice, and the two runs diverge
+    from there).  Inputs and kernels are deterministic, so the count of
+    token-exact steps is a fixed property of the case: it must reach ``pinned``,
+    the count measured on the MI355X (all steps where nothing diverges).
+    Returns (verified steps, steps, step of the near-tie or None)."""
+    (g_first, g_toks, g_logits), (w_first, w_toks, w_logits) = got, want
+    tg, tw = np.concatenate([g_first, g_toks]), np.concatenate([w_first, w_toks])
+    tol = rel * float(np.abs(w_logits).max())
+    verified, tie = 0, None
+    for s in range(len(tw)):
+        err = float(np.abs(g_logits[s] - w_logits[s]).max())
+        assert err <= tol, f"{what}: step {s}: logits differ by {err} > {tol}"
+        top = np.sort(w_logits[s])[-2:]
+        if tg[s] != tw[s]:
+            gap = float(top[1] - top[0])
+            assert gap <= 2 * tol, f"{what}: step {s}: token {tg[s]} != {tw[s]} (top-two gap {gap} > {2 * tol})"
+            tie = s
+            print(f"[gpu] {what}: step {s} is a near-tie (top-two gap {gap:.3g} <= {2 * tol:.3g}); the runs "
+                  f"diverge there", file=sys.stderr, flush=True)
+            break
+        verified += 1
+    print(f"[gpu] {what}: {verified} of {len(tw)} steps verified token-exact", file=sys.stderr, flush=True)
+    assert verified >= min(pinned, len(tw)), f"{what}: {verified} token-exact steps, {pinned} measured"
+    return verified, len(tw), tie

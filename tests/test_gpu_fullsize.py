@@ -12,7 +12,7 @@ import sys
 import numpy as np
 import pytest
 
-from gpu_util import as_f32, assert_rel, blob_for, run_both, runtime
+from gpu_util import as_f32, assert_rel, blob_for, check_decoder, run_both, runtime
 from oracle import vmref
 from pjrt_amd import configs as CF
 from pjrt_amd import graph as G
@@ -146,32 +146,16 @@ def test_c4_full_size_attention():
         assert (err <= bound).all(), f"head {h}: {int((err > bound).sum())} elements outside the bound"
 
 
-def check_decoder(got, want, rel):
-    (g_first, g_toks, g_logits), (w_first, w_toks, w_logits) = got, want
-    tg, tw = np.concatenate([g_first, g_toks]), np.concatenate([w_first, w_toks])
-    tol = rel * float(np.abs(w_logits).max())
-    verified = 0
-    for s in range(len(tw)):
-        err = float(np.abs(g_logits[s] - w_logits[s]).max())
-        assert err <= tol, f"step {s}: logits differ by {err} > {tol}"
-        top = np.sort(w_logits[s])[-2:]
-        if tg[s] != tw[s]:
-            assert top[1] - top[0] <= 2 * tol, f"step {s}: token {tg[s]} != {tw[s]} (gap {top[1] - top[0]})"
-            break
-        verified += 1
-    say(f"decoder: {verified} of {len(tw)} steps verified token-exact")
-    return verified
-
-
 @pytest.mark.timeout(420)
 def test_c5_full_128_step_loop_against_oracle():
     """The benchmarked config-5 program (prompt 512, 128 greedy decode steps in one
     FOR loop), with per-step logits, against the CPU oracle's execution of the same
     bytes: logits within 5e-3 of the largest, tokens equal until the first
-    near-tie (the rule of test_gpu_configs.check_decoder)."""
+    near-tie (gpu_util.check_decoder).  Measured on the MI355X: steps 0-69 are
+    token-exact and step 70 is a near-tie, where the runs diverge."""
     c = CF.C5
     args = CF.gpt_inputs(c)
     blob, _ = blob_for(CF.gpt_c5(c, emit_logits=True))
     say("C5 full 128-step program")
     got, want = run_both(blob, args, oracle="tensor")
-    assert check_decoder(got, want, 5e-3) >= 16
+    check_decoder(got, want, 5e-3, pinned=70, what="config-5 decoder, 128 steps")

@@ -858,3 +858,38 @@ def test_calibrate_cost_table():
     a = np.linspace(-2, 2, 70000, dtype=np.float32)
     got, want = run_both(blob, [a])
     assert_rel(got[0], want[0], 4e-6, 1e-6, "calibrated schedule")
+
+
+def test_submitted_launches_report_their_own_status():
+    """vmrt_submit: four launches of one program in flight on the runtime's
+    stream, each followed by its status epilogue into a slot of its own.  Waited
+    for out of order, each completes with its own outputs (a K-split matmul, so
+    the task scratch's arrival counters are reused launch after launch), and the
+    program's shared status word stays clear for vmrt_program_status."""
+    rt = runtime()
+    M, K, N = 256, 512, 64
+    g = G.Graph()
+    a, b = g.input((M, K)), g.input((K, N))
+    g.output(g.dot(a, b))
+    lp = rt.compile(g.build())
+    rng = np.random.default_rng(7)
+    ins, outs, want = [], [], []
+    for _ in range(4):
+        A = rng.integers(-3, 4, (M, K)).astype(np.float32)
+        B = rng.integers(-3, 4, (K, N)).astype(np.float32)
+        ins.append([rt.to_device(A), rt.to_device(B)])
+        outs.append(lp.alloc_outputs())
+        want.append(A.astype(np.float64) @ B.astype(np.float64))
+    launches = [lp.submit(ins[i], outs[i]) for i in range(4)]
+    try:
+        for i in reversed(range(4)):
+            launches[i].wait()
+            assert launches[i].done()
+            np.testing.assert_array_equal(outs[i][0].to_host(np.float32, (M, N)), want[i])
+        lp.status()
+    finally:
+        for launch in launches:
+            launch.release()
+        for buf in [x for row in ins + outs for x in row]:
+            buf.free()
+        lp.close()

@@ -214,12 +214,16 @@ def gpt_c5(c: GptConfig = C5, emit_logits: bool = False, trips: int | None = Non
     return g.build()
 
 
-def gpt_reference(c: GptConfig, arrays, steps=None):
+def gpt_reference(c: GptConfig, arrays, steps=None, bf16_stores=True):
     """Independent numpy statement of the same decoder (float64 math with bf16
-    rounding where the program stores bf16), for pinning the oracle on tiny
+    rounding where the program stores bf16; with ``bf16_stores`` False, no
+    rounding: the f32-widened decoder), for pinning the oracle on tiny
     configurations: returns (tokens [1 + steps], logits [1 + steps, vocab])."""
     steps = c.steps if steps is None else steps
-    bf = lambda a: V.bf16_to_f32(V.f32_to_bf16(np.asarray(a, np.float32))).astype(np.float64)
+    if bf16_stores:
+        bf = lambda a: V.bf16_to_f32(V.f32_to_bf16(np.asarray(a, np.float32))).astype(np.float64)
+    else:
+        bf = lambda a: np.asarray(a, np.float64)
     names = ["ids"] + [n for n, _, _ in gpt_param_shapes(c)]
     P = {}
     for n, a in zip(names, arrays):

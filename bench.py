@@ -731,9 +731,22 @@ def profile_c5(rt, steps=16):
     per_step_us = (ms1 - ms0) * 1e3 / steps
     bar_n = (pr1["barriers"] - pr0["barriers"]) / lanes / steps
     bar_us = (pr1["barrier_us"] - pr0["barrier_us"]) / lanes / steps
+    span_us = (pr1["lane_us"] - pr0["lane_us"]) / lanes / steps
+    flag_us = (pr1["flag_us"] - pr0["flag_us"]) / lanes / steps
+    tile_us = (sum(t[1] for t in pr1["tasks"]) - sum(t[1] for t in pr0["tasks"])) / lanes / steps
     print(f"C5 decode step on {lanes} lanes: {per_step_us:.1f} us per step (events), "
           f"{bar_n:.1f} grid barriers per step, average lane wait in them {bar_us:.1f} us per step "
           f"({bar_us / max(bar_n, 1):.2f} us per barrier)")
+    # where one lane's step goes: the lane's span (launch start to its end) is
+    # its tiles, its barrier waits, its completion-flag waits and the rest
+    # (entry loads, the frame walk, block barriers between entries, and the
+    # profiling atomics themselves)
+    print("per lane and decode step (us):")
+    for name, v in (("tiles (entries, incl. their closing block barrier)", tile_us),
+                    ("grid barrier waits", bar_us), ("completion-flag waits", flag_us),
+                    ("rest: entry dispatch, frame walk, profiling", span_us - tile_us - bar_us - flag_us),
+                    ("lane span (sum of the above)", span_us), ("kernel time per step (events)", per_step_us)):
+        print(f"  {name:52s} {v:8.1f}")
     base = {i: (tot, cnt) for i, tot, _, cnt in pr0["tasks"]}
     by_op, rows = {}, []
     for i, tot, mx, cnt in pr1["tasks"]:

@@ -162,8 +162,9 @@ int vmrt_program_status(vmrt_program* prog, char* err, size_t errlen);
 /* Per-task profile of the executions since the last reset, when the program was
  * loaded with PJRT_AMD_PROFILE=1 (FAILED_PRECONDITION otherwise).  Fills
  * 4 + 4 * n_tasks words, in 100 MHz ticks: [0] lane-time spent in grid barriers,
- * [1] lane-barriers; task i at 4 + 4 i: lane-time summed over its entries, the
- * longest single entry, the entry count.  Replaces the reference's per-phase
+ * [1] lane-barriers, [2] lane-time from launch start to each lane's end, [3]
+ * lane-time waiting for completion flags; task i at 4 + 4 i: lane-time summed
+ * over its entries, the longest single entry, the entry count.  Replaces the reference's per-phase
  * profiling queue (PJRT_OCL_PROFILE, runtime.cc:2122-2195). */
 int vmrt_program_profile(vmrt_program* prog, uint64_t* out, size_t n_words, int reset, char* err, size_t errlen);
 

@@ -55,6 +55,7 @@ INTS = (I32, U32, I64)
 NOP, BARRIER, WHILE, IF, FOR = (0xFFFFFFFF, 0xFFFFFFFE, 0xFFFFFFFD,
                                 0xFFFFFFFC, 0xFFFFFFFB)
 SENTINELS = (NOP, BARRIER, WHILE, IF, FOR)
+FLAG_NONE = 0xFFFFFFFF     # an entry field that names no completion flag
 
 # parity pins: how each semantic function is checked (see tests/test_oracle.py)
 PINS = {
@@ -136,6 +137,7 @@ class Prog:
     streams: list | None = None
     root_lens: list | None = None
     n_lanes: int = 0
+    n_flags: int = 0
 
 
 def parse(data: bytes) -> Prog:
@@ -190,7 +192,7 @@ def parse(data: bytes) -> Prog:
     p = Prog(arena, bufs, inputs, outputs, shapes[:nin], shapes[nin:], consts,
              instrs, main_len, aux)
     if pos < len(data):
-        nt, ne, _nf, nl = struct.unpack_from("<4I", data, pos)
+        nt, ne, nf, nl = struct.unpack_from("<4I", data, pos)
         pos += 16
         if not 1 <= nl <= 4096:
             raise FormatError("bad n_lanes")
@@ -211,10 +213,25 @@ def parse(data: bytes) -> Prog:
         for _ in range(ne):
             ents.append(struct.unpack_from("<8I", data, pos))
             pos += 32
+        if nf:
+            # completion flags (this build's extension of the reserved WAIT /
+            # SIGNAL fields): each flag signaled by at most one tile entry,
+            # ranges inside [0, n_flags), no entry both waiting and signaling
+            signaled = set()
+            for e in ents:
+                if e[0] in SENTINELS:
+                    continue
+                if e[4] and (e[3] == FLAG_NONE or e[3] + e[4] > nf or e[5] != FLAG_NONE):
+                    raise FormatError("bad completion-flag wait")
+                if e[5] != FLAG_NONE:
+                    if e[5] >= nf or e[5] in signaled:
+                        raise FormatError("bad completion-flag signal")
+                    signaled.add(e[5])
         p.tasks = tasks
         p.streams = [ents[o:o + c] for o, c, _ in lt]
         p.root_lens = [r for _, _, r in lt]
         p.n_lanes = nl
+        p.n_flags = nf
     if pos != len(data):
         raise FormatError("trailing bytes")
     return p
@@ -1271,11 +1288,30 @@ def execute_schedule(data_or_prog, args, ew_ts: int = 4096, mma_t: int = 128,
         base = m.arena.copy()
 
         def go(lanes):
+            # each lane runs its entries in stream order; with completion flags
+            # an entry that waits runs only once every flag of its range was
+            # signaled in this phase, so lanes take turns, in `lanes` order,
+            # each going as far as it can
             m.arena[:] = base
-            for ln in lanes:
-                for e in by_lane[ln]:
-                    tr.run(prog.tasks[e[0]], e[1], e[2])
-            return m.arena.copy()
+            pos = dict.fromkeys(lanes, 0)
+            signaled = set()
+            while True:
+                moved = False
+                for ln in lanes:
+                    es = by_lane[ln]
+                    while pos[ln] < len(es):
+                        e = es[pos[ln]]
+                        if prog.n_flags and e[4] and not all(f in signaled for f in range(e[3], e[3] + e[4])):
+                            break
+                        tr.run(prog.tasks[e[0]], e[1], e[2])
+                        if prog.n_flags and e[5] != FLAG_NONE:
+                            signaled.add(e[5])
+                        pos[ln] += 1
+                        moved = True
+                if all(pos[ln] == len(by_lane[ln]) for ln in lanes):
+                    return m.arena.copy()
+                if not moved:
+                    raise AssertionError("completion flags: a wait that no entry of its phase signals")
 
         fwd = go(order)
         if check_order and len(order) > 1:

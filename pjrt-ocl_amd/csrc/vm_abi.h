@@ -83,8 +83,9 @@ enum : uint32_t {
 // XCDs per device: workgroup i of a launch is dispatched to XCD i % kXcds.
 constexpr uint32_t kXcds = 8;
 // Profiling counters (100 MHz ticks of s_memrealtime): [0] lane-time in grid
-// barriers, [1] lane-barriers; task i at kStatTask + 4 i: lane-time summed over
-// its entries, longest single entry, entry count.
+// barriers, [1] lane-barriers, [2] lane-time from launch start to the lane's
+// end, [3] lane-time waiting for completion flags; task i at kStatTask + 4 i:
+// lane-time summed over its entries, longest single entry, entry count.
 constexpr uint32_t kStatTask = 4;
 
 enum VmError : uint32_t {
@@ -127,6 +128,9 @@ struct VmArgs {
   uint64_t* stats;          // profiling counters (null: off), see kStat*
   uint8_t* scratch;         // loader-owned scratch, zeroed at load (split partials, arrival counters)
   const uint32_t* task_scratch;   // per task: byte offset of its scratch region
+  uint64_t* flags;          // completion flags (extension), n_flags words in the scratch; null: none
+  uint32_t seq;             // this launch's sequence number (the high half of a flag value)
+  uint32_t pad_;
   uint8_t* ports[kMaxPorts];
 };
 

@@ -305,6 +305,55 @@ VM_DEV bool grid_barrier(Args A, Pre&& pre) {
 
 VM_DEV bool grid_barrier(Args A) { return grid_barrier(A, NoPre()); }
 
+// ---- completion flags (extension of the entries' reserved WAIT / SIGNAL fields) ------
+// A tile entry may signal one flag when its tiles are done, and wait for a range of
+// flags before it starts: a point-to-point dependency inside one barrier phase in
+// place of a grid barrier (the scheduler uses it where a consumer's tiles read the
+// output of only a few producer tiles, such as one head's q, k and v).  A flag is a
+// 64-bit word holding the identity of the phase instance that last signaled it:
+// the launch's sequence number in the high half, the count of grid barriers the
+// lane has passed in this launch, plus one, in the low half.  Every lane passes
+// the same barriers, so producer and consumer compute the same identity; a value
+// left by an earlier launch, loop trip or phase never equals it, so flags need no
+// reset.  The loader checks that every waited flag has exactly one signaling
+// entry in the same barrier segment and that, in each lane's segment, no entry
+// signals after one that waits: signals never wait, so every wait ends.
+VM_DEV uint64_t phase_tag(Args A, uint32_t nbar) { return (uint64_t(A->seq) << 32) | (nbar + 1u); }
+
+// After the entry's tiles: the block's stores are complete (block barrier), and
+// thread 0's agent-scope release publishes them with the flag, as a lane's
+// arrival at the grid barrier does.
+VM_DEV void flag_signal(Args A, uint32_t f, uint64_t tag) {
+  __syncthreads();
+  if (threadIdx.x == 0) __hip_atomic_store(&A->flags[f], tag, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Before the entry's tiles: thread i polls flags f0 + i, f0 + i + 256, ... until
+// each holds `tag`, then an agent-scope acquire and a block barrier order the
+// tiles' reads after the producers' writes.  Polls give up after the barrier's
+// time-out (the VM error word then ends the launch).  Returns false to abort.
+VM_DEV bool flag_wait(Args A, uint32_t f0, uint32_t n, uint64_t tag) {
+  __shared__ uint32_t s_fok;
+  if (threadIdx.x == 0) s_fok = 1;
+  __syncthreads();
+  const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+  bool ok = true;
+  for (uint32_t i = threadIdx.x; ok && i < n; i += kBlock) {
+    uint64_t* p = &A->flags[f0 + i];
+    for (uint32_t poll = 0; __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != tag; ++poll) {
+      if (barrier_timed_out(A, t0, poll)) {
+        ok = false;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
+  }
+  if (!ok) s_fok = 0;
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  __syncthreads();
+  return s_fok != 0;
+}
+
 // Record an error from a lane (first error wins) so the host can report it.
 VM_DEV void raise_error(Args A, uint32_t code, uint32_t info) {
   if (threadIdx.x == 0) {

@@ -7,7 +7,8 @@
 //   FOR      -> body sub-list, barrier, x trip count (wait_flag)
 //   IF       -> then / else sub-list chosen by the cond value
 //   NOP      -> skip
-//   task     -> run tiles [tile_lo, tile_hi) of tasks[task]
+//   task     -> run tiles [tile_lo, tile_hi) of tasks[task]; an entry may first
+//               wait for completion flags and afterwards signal one (vm_device.h)
 // Consecutive task entries of one lane form a fused chain: a block barrier with a
 // workgroup fence separates them, because a tile op maps elements to threads
 // differently from its producer (vm_main.cl:82-100).
@@ -98,6 +99,7 @@ __global__ __launch_bounds__(kBlock, 1) void vm_main(VmArgs args) {
   (void)args;
   const Args A = (Args)__builtin_amdgcn_kernarg_segment_ptr();
   const uint32_t lane = blockIdx.x;
+  const uint64_t t_launch = A->stats ? __builtin_amdgcn_s_memrealtime() : 0;   // profiling: the lane's span
   grid_barrier_init(A);
   const LaneSpan span = load_span((const VM_K LaneSpan*)A->lanes + lane);
   const VM_K Entry* ents = (const VM_K Entry*)A->entries + span.off;
@@ -117,6 +119,7 @@ __global__ __launch_bounds__(kBlock, 1) void vm_main(VmArgs args) {
   f_own[0] = kRootOwner;
   f_phase[0] = 0;
   bool pub = false;     // a tile entry ran since the last barrier
+  uint32_t nbar = 0;    // grid barriers this lane has passed in this launch (completion flag values)
 
   for (;;) {
     if (f_pc[sp] >= f_end[sp]) {
@@ -131,6 +134,7 @@ __global__ __launch_bounds__(kBlock, 1) void vm_main(VmArgs args) {
       // (warming a FOR body's first entry when another trip follows)
       const bool again = w.task == ENT_FOR && f_phase[sp] > 1;
       if (!timed_barrier(A, ents, again ? w.tile_lo : 0u, again ? w.tile_lo + w.tile_hi : 0u)) return;
+      ++nbar;
       pub = false;
       if (w.task == ENT_FOR) {
         if (--f_phase[sp] != 0) {
@@ -163,6 +167,7 @@ __global__ __launch_bounds__(kBlock, 1) void vm_main(VmArgs args) {
     const Entry en = load_entry(ents + epc);
     if (en.task == ENT_BARRIER) {
       if (!timed_barrier(A, ents, epc + 1, f_end[sp])) return;
+      ++nbar;
       pub = false;
       ++f_pc[sp];
       continue;
@@ -205,6 +210,14 @@ __global__ __launch_bounds__(kBlock, 1) void vm_main(VmArgs args) {
     if (en.task != ENT_NOP) {
       if (pub) __syncthreads();
       pub = true;
+      // the loader sets wait_count 0 and signal_flag FLAG_NONE on entries without flags
+      if (en.wait_count) {
+        const uint64_t tw = A->stats ? __builtin_amdgcn_s_memrealtime() : 0;
+        if (!flag_wait(A, en.wait_flag, en.wait_count, phase_tag(A, nbar))) return;
+        if (A->stats && threadIdx.x == 0)
+          __hip_atomic_fetch_add(A->stats + 3, __builtin_amdgcn_s_memrealtime() - tw, __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT);
+      }
       if (A->stats) {
         const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
         exec_tiles(A, en.task, en.tile_lo, en.tile_hi);
@@ -219,9 +232,13 @@ __global__ __launch_bounds__(kBlock, 1) void vm_main(VmArgs args) {
       } else {
         exec_tiles(A, en.task, en.tile_lo, en.tile_hi);
       }
+      if (en.signal_flag != FLAG_NONE) flag_signal(A, en.signal_flag, phase_tag(A, nbar));
     }
     ++f_pc[sp];
   }
+  if (A->stats && threadIdx.x == 0)
+    __hip_atomic_fetch_add(A->stats + 2, __builtin_amdgcn_s_memrealtime() - t_launch, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Status epilogue of a launch submitted with vmrt_submit, run after it on the

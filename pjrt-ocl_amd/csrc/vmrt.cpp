@@ -215,6 +215,11 @@ bool parse_program(const uint8_t* data, size_t len, Program* P, std::string* err
 // stream, nesting must fit the kernel's 8-frame stack.
 struct CtlSig {
   std::vector<uint64_t> toks;
+  // tile entries in walk order: (entry index in the lane's stream, segment),
+  // the segment being the control-token count before the entry -- equal in
+  // two lanes exactly when the entries sit between the same pair of grid
+  // barriers (control is uniform)
+  std::vector<std::pair<uint32_t, uint64_t>> tiles;
 };
 
 bool control_sig(const Program& P, uint32_t lane, uint32_t start, uint32_t len, int depth, CtlSig* sig,
@@ -262,7 +267,69 @@ bool control_sig(const Program& P, uint32_t lane, uint32_t start, uint32_t len, 
           *err = fmt("lane %u entry %u: task index out of range", lane, i);
           return false;
         }
+        sig->tiles.emplace_back(i, sig->toks.size());
         break;
+    }
+  }
+  return true;
+}
+
+// ---- completion flags (extension of the reserved WAIT / SIGNAL entry fields) --------------
+// A program declaring n_flags > 0 may let tile entries signal one flag and wait
+// for a range of flags.  Checked so that every wait ends: each flag is signaled
+// by exactly one tile entry; every waited flag is signaled in the same barrier
+// segment; no entry both waits and signals; and in each lane's segment no entry
+// signals after one that waits (signals never block, so all happen).  With
+// n_flags == 0 the fields of tile entries carry no meaning (the reference leaves
+// them FLAG_NONE) and the loader clears them.
+constexpr uint32_t kMaxFlags = 1u << 20;
+
+bool check_flags(const Program& P, const std::vector<CtlSig>& sigs, std::string* err) {
+  if (!P.n_flags) return true;
+  if (P.n_flags > kMaxFlags) {
+    *err = fmt("%u completion flags (at most %u)", P.n_flags, kMaxFlags);
+    return false;
+  }
+  std::vector<int64_t> sig_seg(P.n_flags, -1);
+  for (uint32_t l = 0; l < sigs.size(); ++l)
+    for (const auto& t : sigs[l].tiles) {
+      const Entry& e = P.entries[P.lanes[l].off + t.first];
+      if (e.signal_flag == FLAG_NONE) continue;
+      if (e.signal_flag >= P.n_flags) {
+        *err = fmt("lane %u entry %u: signals flag %u of %u", l, t.first, e.signal_flag, P.n_flags);
+        return false;
+      }
+      if (sig_seg[e.signal_flag] >= 0) {
+        *err = fmt("completion flag %u is signaled by more than one entry", e.signal_flag);
+        return false;
+      }
+      sig_seg[e.signal_flag] = int64_t(t.second);
+    }
+  for (uint32_t l = 0; l < sigs.size(); ++l) {
+    int64_t wait_seg = -1;     // segment of the last waiting entry seen in walk order
+    for (const auto& t : sigs[l].tiles) {
+      const Entry& e = P.entries[P.lanes[l].off + t.first];
+      const bool waits = e.wait_count != 0;
+      if (waits) {
+        if (e.signal_flag != FLAG_NONE) {
+          *err = fmt("lane %u entry %u: both waits for and signals completion flags", l, t.first);
+          return false;
+        }
+        if (e.wait_flag == FLAG_NONE || uint64_t(e.wait_flag) + e.wait_count > P.n_flags) {
+          *err = fmt("lane %u entry %u: waits for flags outside [0, %u)", l, t.first, P.n_flags);
+          return false;
+        }
+        for (uint32_t f = e.wait_flag; f < e.wait_flag + e.wait_count; ++f)
+          if (sig_seg[f] != int64_t(t.second)) {
+            *err = fmt("lane %u entry %u: waits for flag %u, which no entry of the same phase signals", l, t.first,
+                       f);
+            return false;
+          }
+        wait_seg = int64_t(t.second);
+      } else if (e.signal_flag != FLAG_NONE && wait_seg == int64_t(t.second)) {
+        *err = fmt("lane %u entry %u: signals a completion flag after an entry of the same phase waits", l, t.first);
+        return false;
+      }
     }
   }
   return true;
@@ -675,6 +742,8 @@ struct vmrt_program {
   size_t stats_words = 0;
   uint8_t* scratch = nullptr;                 // split partials + arrival counters, zeroed at load
   uint64_t scratch_bytes = 0;
+  uint64_t flag_off = 0;                      // byte offset of the completion flags in the scratch
+  uint32_t launch_seq = 0;                    // launches so far (completion flag values)
   uint32_t* task_scratch = nullptr;           // per task: byte offset of its scratch region
   std::vector<int> input_port, output_port;   // -1 = arena copy
   std::vector<uint32_t> in_bytes, out_bytes;
@@ -876,18 +945,18 @@ static int prepare_program(vmrt_runtime* rt, vmrt_program* lp, const void* bytes
                    fmt("program scheduled for %u lanes; this device holds %u co-resident lanes", n_lanes,
                        rt->info.max_lanes));
 
-  // control uniformity across lanes
+  // control uniformity across lanes, then the completion flags
   {
-    CtlSig ref;
+    std::vector<CtlSig> sigs(n_lanes);
     for (uint32_t l = 0; l < n_lanes; ++l) {
-      CtlSig s;
+      CtlSig& s = sigs[l];
       if (!control_sig(P, l, 0, P.lanes[l].root_len, 0, &s, &msg))
         return set_err(err, errlen, VMRT_INVALID_ARGUMENT, "LoadedProgram: " + msg);
-      if (l == 0) ref = s;
-      else if (s.toks != ref.toks)
+      if (l > 0 && s.toks != sigs[0].toks)
         return set_err(err, errlen, VMRT_INVALID_ARGUMENT,
                        fmt("LoadedProgram: lane %u control flow differs from lane 0 (non-uniform barriers)", l));
     }
+    if (!check_flags(P, sigs, &msg)) return set_err(err, errlen, VMRT_INVALID_ARGUMENT, "LoadedProgram: " + msg);
   }
   // task footprints and entry tile ranges
   Checker chk{P, lp->ew_ts, lp->mma_t, &msg, uint32_t(vm_kernel_smem_bytes())};
@@ -973,6 +1042,14 @@ static int prepare_program(vmrt_runtime* rt, vmrt_program* lp, const void* bytes
   std::vector<Entry>& entries = pr->entries;
   entries = P.entries;
   for (Entry& e : entries) {
+    if (e.task < ENT_FOR) {        // a tile entry: no flags unless the program declares them
+      if (!P.n_flags || !e.wait_count) {
+        e.wait_flag = FLAG_NONE;
+        e.wait_count = 0;
+      }
+      if (!P.n_flags) e.signal_flag = FLAG_NONE;
+      continue;
+    }
     if (e.task == ENT_WHILE || e.task == ENT_IF) {
       const Buffer& b = P.buffers[e.signal_flag];
       const uint32_t w = dt_size(b.dtype);
@@ -993,6 +1070,11 @@ static int prepare_program(vmrt_runtime* rt, vmrt_program* lp, const void* bytes
     if (lp->scratch_bytes > 0xFFFFFFFFull)
       return set_err(err, errlen, VMRT_RESOURCE_EXHAUSTED, "LoadedProgram: task scratch exceeds 4 GiB");
   }
+  // completion flags: 64-bit words after the task scratch (zeroed with it)
+  lp->flag_off = lp->scratch_bytes;
+  lp->scratch_bytes += (uint64_t(P.n_flags) * 8 + 255) & ~uint64_t(255);
+  if (lp->scratch_bytes > 0xFFFFFFFFull)
+    return set_err(err, errlen, VMRT_RESOURCE_EXHAUSTED, "LoadedProgram: task scratch exceeds 4 GiB");
   for (size_t i = 0; i < P.inputs.size(); ++i) lp->in_bytes.push_back(uint32_t(P.buffers[P.inputs[i]].size));
   for (size_t i = 0; i < P.outputs.size(); ++i) lp->out_bytes.push_back(uint32_t(P.buffers[P.outputs[i]].size));
 
@@ -1065,6 +1147,7 @@ int vmrt_load(vmrt_runtime* rt, const void* bytes, size_t len, uint32_t ew_ts, u
   a.stats = lp->stats;
   a.scratch = lp->scratch;
   a.task_scratch = lp->task_scratch;
+  a.flags = P.n_flags ? reinterpret_cast<uint64_t*>(lp->scratch + lp->flag_off) : nullptr;
   for (int k = 0; k < kMaxPorts; ++k) a.ports[k] = lp->arena;   // unbound ports point at the arena
   rt->programs.insert(lp.get());
   *out = lp.release();
@@ -1102,6 +1185,7 @@ static int enqueue_locked(vmrt_program* p, const void* const* inputs, size_t n_i
                    fmt("expected %zu inputs and %zu outputs, got %zu and %zu", P.inputs.size(), P.outputs.size(), n_in,
                        n_out));
   VmArgs a = p->args;
+  a.seq = ++p->launch_seq;     // a new identity for this launch's completion flag values
   hipError_t e = hipSuccess;
   for (size_t i = 0; i < n_in; ++i) {
     if (!inputs[i] && p->in_bytes[i]) return set_err(err, errlen, VMRT_INVALID_ARGUMENT, fmt("input %zu is null", i));
@@ -1289,6 +1373,7 @@ int vmrt_run_noalloc(vmrt_runtime* rt, const void* bytes, size_t len, uint32_t e
   a.stats = nullptr;
   a.scratch = lp.scratch;
   a.task_scratch = reinterpret_cast<const uint32_t*>(base + o_tsc);
+  a.flags = P.n_flags ? reinterpret_cast<uint64_t*>(lp.scratch + lp.flag_off) : nullptr;
   for (int k = 0; k < kMaxPorts; ++k) a.ports[k] = lp.arena;
   int rc = enqueue_locked(&lp, inputs, n_in, outputs, n_out, s, err, errlen);
   // the host tables above stay alive until the copies and the launch are done

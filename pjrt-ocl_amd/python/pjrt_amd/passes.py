@@ -1588,9 +1588,15 @@ def reuse_arena(prog: V.VMProgram, cfg=None) -> None:
     cfg = cfg or S.DeviceConfig.from_env()
     sched = S._Scheduler(prog, cfg)
     levels = sched.levels(list(range(prog.main_len)))
+    # a level the scheduler may join to the one before it (completion flags in
+    # place of the barrier between them) shares that level's phase time
+    joined = sched.joined_levels(levels)
     phase = {}
     region_roots = []
-    for ph, (kind, payload) in enumerate(levels):
+    ph = -1
+    for k, (kind, payload) in enumerate(levels):
+        if k not in joined:
+            ph += 1
         if kind == "compute":
             for i in payload:
                 phase[i] = ph
@@ -1616,7 +1622,7 @@ def reuse_arena(prog: V.VMProgram, cfg=None) -> None:
     for dot_i, ln_i in sched.ln_pro.items():
         if dot_i in phase:
             phase[ln_i] = phase[dot_i]
-    n_ph = len(levels)
+    n_ph = ph + 1
     lo = [n_ph + 1] * nb
     hi = [-1] * nb
     lo2 = [prog.main_len + 1] * nb

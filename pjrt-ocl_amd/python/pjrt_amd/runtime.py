@@ -512,15 +512,17 @@ class LoadedProgram:
 
     def profile(self, reset: bool = True) -> dict:
         """Per-task device time since the last reset (the program must have been
-        loaded with PJRT_AMD_PROFILE=1): {"barrier_us", "barriers", "tasks":
-        [(task, lane_us_sum, max_entry_us, entries)]}, microseconds."""
+        loaded with PJRT_AMD_PROFILE=1): {"barrier_us", "barriers", "lane_us"
+        (launch start to each lane's end, summed over lanes), "flag_us"
+        (completion-flag waits), "tasks": [(task, lane_us_sum, max_entry_us,
+        entries)]}, microseconds."""
         n_tasks = len(V.parse(self._blob).schedule.tasks)
         words = 4 + 4 * n_tasks
         buf = (ctypes.c_uint64 * words)()
         err = ctypes.create_string_buffer(_ERRLEN)
         _check(self.rt._lib.vmrt_program_profile(self._live(), buf, words, int(reset), err, _ERRLEN), err)
         v = np.frombuffer(buf, np.uint64).astype(np.float64)
-        return {"barrier_us": v[0] / 100.0, "barriers": int(v[1]),
+        return {"barrier_us": v[0] / 100.0, "barriers": int(v[1]), "lane_us": v[2] / 100.0, "flag_us": v[3] / 100.0,
                 "tasks": [(i, v[4 + 4 * i] / 100.0, v[5 + 4 * i] / 100.0, int(v[6 + 4 * i])) for i in range(n_tasks)]}
 
     def __call__(self, *args):

@@ -92,6 +92,11 @@ class DeviceConfig:
     # A program may run on half the lanes when the work model below says the
     # saved per-phase overhead outweighs the halved bandwidth (extension).
     fit_lanes: bool = True
+    # A decode attention whose q, k and v come from TOP_GEMV strips of the
+    # phase before it joins that phase: its tiles wait for completion flags
+    # that the strips of their head signal, instead of a grid barrier
+    # (extension of the entries' WAIT / SIGNAL fields; ``_flag_edges``).
+    counters: bool = True
 
     @classmethod
     def from_env(cls, environ=None) -> "DeviceConfig":
@@ -117,7 +122,8 @@ class DeviceConfig:
                    gemv_min_strip=max(0, min(256, geti("PJRT_AMD_GEMV_STRIP", 0))),
                    ln_gemv=env.get("PJRT_AMD_LN_GEMV", "1") != "0",
                    idle_master=(env["PJRT_AMD_IDLE_MASTER"] != "0") if env.get("PJRT_AMD_IDLE_MASTER") else None,
-                   fit_lanes=env.get("PJRT_AMD_FIT_LANES", "1") != "0")
+                   fit_lanes=env.get("PJRT_AMD_FIT_LANES", "1") != "0",
+                   counters=env.get("PJRT_AMD_COUNTERS", "1") != "0")
 
 
 # --- instruction -> task ------------------------------------------------------
@@ -822,7 +828,7 @@ def xcd_lane_order(n_lanes: int, n_xcd: int = 8) -> list:
     return [x + n_xcd * j for x in range(n_xcd) for j in range(n_lanes // n_xcd)]
 
 
-def pack_units(units, n_lanes: int, idle_master: bool = False):
+def pack_units(units, n_lanes: int, idle_master: bool = False, loads=None):
     """units: [(task_ids, tiles, cost, quantum[, xcd_grouped])] -> [(lane, Entry)].
 
     Each unit is cut into k = min(tiles/quantum, ceil(n_lanes * cost share))
@@ -832,7 +838,8 @@ def pack_units(units, n_lanes: int, idle_master: bool = False):
     unit (neighbouring chunks read the same operands), to the first lane in
     XCD-grouped order, so neighbouring chunks land on one XCD.  ``idle_master``:
     a phase with fewer chunks than lanes keeps lane 0 free (C5: 1006 -> 1015
-    tokens/s in alternating runs)."""
+    tokens/s in alternating runs).  ``loads``: the lanes' work so far in the
+    phase (updated in place), when this call adds to a phase already packed."""
     out = []
     if not units:
         return out
@@ -849,7 +856,8 @@ def pack_units(units, n_lanes: int, idle_master: bool = False):
             if hi > lo:
                 chunks.append((cost * (hi - lo) / tiles, uid, tids, lo, hi, grouped))
     chunks.sort(key=lambda c: (-c[0], c[1], c[3]))
-    loads = [0.0] * n_lanes
+    if loads is None:
+        loads = [0.0] * n_lanes
     plain, grouped_order = range(n_lanes), xcd_lane_order(n_lanes)
     if idle_master and 1 < len(chunks) < n_lanes:
         # a phase that leaves lanes idle leaves lane 0 (the grid barrier's
@@ -894,6 +902,7 @@ class _Scheduler:
         # estimated microseconds per launch (work model of lane_fit)
         self.weight = 1.0
         self.est = 0.0
+        self.n_flags = 0          # completion flags handed out (``emit_flagged``)
 
     def task_id(self, i: int) -> int:
         tid = self.task_of.get(i)
@@ -958,7 +967,11 @@ class _Scheduler:
             comps.setdefault(find(i), []).append(i)
         return [sorted(v) for v in comps.values()]
 
-    def emit_phase(self, indices):
+    def reads(self, i):
+        r = instr_reads(self.prog.instrs[i], self.prog)
+        return r | self.extra_reads[i] if i in self.extra_reads else r
+
+    def phase_units(self, indices):
         shaped, maps = [], []
         for i in sorted(indices):
             (maps if self.task(i).tile_op == V.TOP_EW else shaped).append(i)
@@ -977,20 +990,173 @@ class _Scheduler:
             t0 = self.tasks[tids[0]]
             cost = sum(task_cost(self.tasks[t], self.cfg, self.prog) for t in tids)
             units.append((tids, n_tiles(t0, self.cfg), cost, 1))
-        for lane, e in pack_units(units, self.n, master_idle(self.cfg)):
+        return units
+
+    def emit_phase(self, indices):
+        for lane, e in pack_units(self.phase_units(indices), self.n, master_idle(self.cfg)):
             self.lanes[lane].append(e)
         self.est += self.weight * phase_us([self.task(i) for i in indices if i not in self.ln_fused],
                                            self.n, self.cfg, self.prog)
 
+    # -- completion flags: a consumer phase joined to its producer phase ---------------
+
+    def _flag_edges(self, prod, cons):
+        """Phase ``cons`` can join phase ``prod`` with completion flags when every
+        instruction in it is a decode attention whose only dependencies on
+        ``prod`` are reads of its q, k and v from the output of TOP_GEMV tasks
+        there (no write-after-read or write-after-write, caches and position
+        written earlier).  Returns {consumer: (GEMV indices, per head the byte
+        ranges of its q, k and v)}, or None."""
+        prog, bufs = self.prog, self.prog.buffers
+        if not self.cfg.counters:
+            return None
+        grp = overlap_groups(prog)
+        edges = {}
+        for j in cons:
+            ins = prog.instrs[j]
+            if ins.op != V.OP_DECODE_ATTN:
+                return None
+            hd = prog.aux[ins.aux] & 0xFFFF
+            kb, vb, posb = prog.aux[ins.aux + 1:ins.aux + 4]
+            qkv = {grp[ins.a], grp[kb], grp[vb]}
+            if qkv & {grp[ins.b], grp[ins.imm2], grp[posb]}:
+                return None
+            wj, rj = instr_writes(ins, prog), self.reads(j)
+            # the arena bytes the consumer writes must not be bytes any producer
+            # reads or writes, aliases and arena packing included
+            dst = bufs[ins.dst]
+            wbytes = (dst.arena_byte_offset, dst.arena_byte_offset + dst.size_bytes)
+            gemvs = []
+            for i in prod:
+                wi, ri = instr_writes(prog.instrs[i], prog), self.reads(i)
+                if wj & (wi | ri):
+                    return None
+                for b in self.raw_operands(i):
+                    B = bufs[b]
+                    if B.size_bytes and B.arena_byte_offset < wbytes[1] and wbytes[0] < B.arena_byte_offset + B.size_bytes:
+                        return None
+                raw = rj & wi
+                if not raw:
+                    continue
+                if raw - qkv or self.task(i).tile_op != V.TOP_GEMV:
+                    return None
+                gemvs.append(i)
+            if not gemvs:
+                return None
+            es = V.DT_SIZE[bufs[ins.a].dtype]
+            heads = [[(bufs[b].arena_byte_offset + h * hd * es, bufs[b].arena_byte_offset + (h + 1) * hd * es)
+                      for b in (ins.a, kb, vb)] for h in range(ins.n)]
+            edges[j] = (gemvs, heads)
+        return edges
+
+    def raw_operands(self, i):
+        """Buffer ids (not alias groups) instruction ``i`` reads or writes,
+        with the inputs of a layernorm staged in it."""
+        ins = self.prog.instrs[i]
+        ids = _instr_reads(ins, self.prog) | _instr_writes(ins, self.prog)
+        if i in self.ln_pro:
+            ids |= _instr_reads(self.prog.instrs[self.ln_pro[i]], self.prog)
+        return {b for b in ids if 0 <= b < len(self.prog.buffers)}
+
+    def joined_levels(self, lv) -> set:
+        """Levels k whose phase joins level k - 1's with completion flags
+        (``_flag_edges``); a joined level is not joined onward.  The arena
+        packing gives such a level the phase time of the one before it."""
+        out, k = set(), 1
+        while k < len(lv):
+            if lv[k - 1][0] == "compute" and lv[k][0] == "compute" and self._flag_edges(lv[k - 1][1], lv[k][1]):
+                out.add(k)
+                k += 2
+            else:
+                k += 1
+        return out
+
+    def _gemv_bytes(self, i, lo, hi):
+        """Arena byte ranges TOP_GEMV tiles [lo, hi) of instruction ``i`` write."""
+        t, dst = self.task(i), self.prog.buffers[self.prog.instrs[i].dst]
+        M, N, w = t.p0, t.p1, t.p4
+        es, ncb = V.DT_SIZE[dst.dtype], -(-N // w)
+        out = []
+        for tile in range(lo, hi):
+            g, nb = divmod(tile, ncb)
+            for m in range(M):
+                a = dst.arena_byte_offset + ((g * M + m) * N + nb * w) * es
+                out.append((a, a + min(w, N - nb * w) * es))
+        return out
+
+    def emit_flagged(self, prod, cons, edges) -> bool:
+        """One phase for ``prod`` and ``cons`` (see ``_flag_edges``).  The
+        producer phase is packed as usual; every chunk of a GEMV that some head
+        reads signals a flag of its own, numbered head by head, so the strips
+        of a head hold consecutive flags; the decode attention is packed after
+        them onto the least-loaded lanes, each chunk waiting for the flags of
+        the heads it covers.  Every lane runs its producer entries before its
+        consumer entries, so every wait ends.  False (nothing emitted) when a
+        producer chunk serves more than one head."""
+        loads = [0.0] * self.n
+        placed = pack_units(self.phase_units(prod), self.n, master_idle(self.cfg), loads)
+        by_tid = {}
+        for j, (gemvs, _) in edges.items():
+            for i in gemvs:
+                by_tid.setdefault(self.task_id(i), set()).add(i)
+        members = {}
+        for _lane, e in placed:
+            if e.task not in by_tid:
+                continue
+            served = set()
+            for i in by_tid[e.task]:
+                wr = self._gemv_bytes(i, e.tile_lo, e.tile_hi)
+                for j, (gemvs, heads) in edges.items():
+                    if i not in gemvs:
+                        continue
+                    for h, rngs in enumerate(heads):
+                        if any(a < d and c < b for a, b in wr for c, d in rngs):
+                            served.add((j, h))
+            if len(served) > 1:
+                return False
+            if served:
+                members.setdefault(served.pop(), []).append(e)
+        base, f = {}, self.n_flags
+        for j in sorted(edges):
+            for h in range(len(edges[j][1])):
+                base[(j, h)] = f
+                for e in sorted(members.get((j, h), []), key=lambda e: (e.task, e.tile_lo)):
+                    e.signal_flag = f
+                    f += 1
+        end = {g: base[g] + len(members.get(g, [])) for g in base}
+        waits = pack_units(self.phase_units(cons), self.n, master_idle(self.cfg), loads)
+        for _lane, e in waits:
+            j = next(j for j in edges if self.task_id(j) == e.task)
+            S = max(1, self.tasks[e.task].p4 >> 16)
+            lo, hi = base[(j, e.tile_lo // S)], end[(j, (e.tile_hi - 1) // S)]
+            if hi > lo:
+                e.wait_flag, e.wait_count = lo, hi - lo
+        for lane, e in placed + waits:
+            self.lanes[lane].append(e)
+        self.n_flags = f
+        self.est += self.weight * phase_us([self.task(i) for i in list(prod) + list(cons) if i not in self.ln_fused],
+                                           self.n, self.cfg, self.prog)
+        return True
+
     def schedule_range(self, indices, trailing_barrier: bool):
         lv = self.levels(indices)
-        for k, (kind, payload) in enumerate(lv):
+        k = 0
+        while k < len(lv):
+            kind, payload = lv[k]
             if kind == "compute":
-                self.emit_phase(payload)
+                joined = False
+                if k + 1 < len(lv) and lv[k + 1][0] == "compute":
+                    edges = self._flag_edges(payload, lv[k + 1][1])
+                    joined = bool(edges) and self.emit_flagged(payload, lv[k + 1][1], edges)
+                if joined:
+                    k += 1
+                else:
+                    self.emit_phase(payload)
             else:
                 self.emit_region(payload)
             if trailing_barrier or k != len(lv) - 1:
                 self.barrier()
+            k += 1
 
     def emit_region(self, i):
         ins = self.prog.instrs[i]
@@ -1075,7 +1241,7 @@ def schedule_program(prog: V.VMProgram, cfg: DeviceConfig | None = None) -> V.Sc
     lanes, sc = _fit(prog, cfg)
     if sc is None:
         sc = _schedule(prog, dataclasses.replace(cfg, nlanes=lanes, fit_lanes=False))
-    return V.Schedule(lanes, sc.tasks, sc.lanes, sc.root_lens)
+    return V.Schedule(lanes, sc.tasks, sc.lanes, sc.root_lens, sc.n_flags)
 
 
 def schedule_bytes(prog: V.VMProgram, cfg: DeviceConfig | None = None) -> bytes:

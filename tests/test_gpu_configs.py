@@ -68,8 +68,9 @@ def test_gpt_c5_lane_fit_matches_every_lane():
     c = dataclasses.replace(CF.C5, steps=16)
     prog = CF.gpt_c5(c, emit_logits=True)
     args = CF.gpt_inputs(c)
-    fit, _ = blob_for(prog)
-    full, _ = blob_for(prog, fit_lanes=False)
+    # barrier-only schedules: the work model's lane choice was fitted on them
+    fit, _ = blob_for(prog, counters=False)
+    full, _ = blob_for(prog, fit_lanes=False, counters=False)
     lanes = vmref.parse(fit).n_lanes, vmref.parse(full).n_lanes
     print(f"[gpu] lane fit: {lanes[0]} lanes against {lanes[1]}", file=sys.stderr, flush=True)
     if runtime().info["n_lanes"] >= 128:
@@ -124,3 +125,28 @@ def test_reference_decode_step(name):
     atol = 1e-4 * float(np.abs(ref).max())          # f32 GEMVs: summation order differs
     assert_rel(got[0], want[0], 1e-4, atol, f"decode step {name} vs oracle")
     assert_rel(got[0], ref, 1e-4, atol, f"decode step {name} vs numpy")
+
+
+@pytest.mark.parametrize("full", [False, True])
+def test_decoder_completion_flags_match_barriers(full):
+    """The decoder scheduled with completion flags (each layer's decode
+    attention in its QKV GEMV's phase, waiting for its head's strips) gives
+    bit-identical tokens and logits to the same program scheduled with grid
+    barriers only: the tiles and their summation orders are the same, only the
+    synchronisation differs."""
+    c = dataclasses.replace(CF.C5, steps=16) if full else CF.GptConfig(layers=2, d=128, heads=2, mlp=512,
+                                                                      vocab=1000, prompt=128, steps=16)
+    prog = CF.gpt_c5(c, emit_logits=True)
+    args = CF.gpt_inputs(c, seed=11)
+    # one lane count for both (the strip widths, and so the summation orders,
+    # follow it): half the device's, as the benchmarked decoder runs
+    lanes = max(1, runtime().info["n_lanes"] // 2)
+    on, _ = blob_for(prog, nlanes=lanes, fit_lanes=False, counters=True)
+    off, _ = blob_for(prog, nlanes=lanes, fit_lanes=False, counters=False)
+    assert vmref.parse(on).n_flags > 0 and vmref.parse(off).n_flags == 0
+    a, b = run_gpu(on, args), run_gpu(off, args)
+    for x, y in zip(a, b):
+        np.testing.assert_array_equal(x, y)
+    if not full:
+        _, want = run_both(on, args, oracle="tensor")
+        check_decoder(a, want, 5e-3, pinned=17, what="small decoder with completion flags")

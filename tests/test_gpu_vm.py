@@ -893,3 +893,64 @@ def test_submitted_launches_report_their_own_status():
         for buf in [x for row in ins + outs for x in row]:
             buf.free()
         lp.close()
+
+
+def test_loader_rejects_bad_completion_flags():
+    """The loader refuses flag uses whose waits might not end: a flag signaled
+    twice, a wait for a flag signaled in another phase, and an entry that
+    signals after an entry of its lane and phase waits."""
+    import dataclasses as dc
+    from pjrt_amd import configs as CF
+    from pjrt_amd import scheduler as S
+    from pjrt_amd.runtime import VmrtError
+    c = CF.GptConfig(layers=2, d=128, heads=2, mlp=256, vocab=300, prompt=32, steps=2)
+    prog = CF.gpt_c5(c)
+    cfg = S.DeviceConfig(nlanes=16, counters=True, fit_lanes=False)
+    sched = S.schedule_program(prog, cfg)
+    assert sched.n_flags > 0
+    rt = runtime()
+
+    def blob(fn):
+        st = [[dc.replace(e) for e in s] for s in sched.lane_streams]
+        fn(st)
+        return V.serialize(prog, V.Schedule(sched.n_lanes, sched.tasks, st, sched.root_lens, sched.n_flags))
+
+    lp = rt.load(blob(lambda st: None), ew_ts=cfg.ew_ts, mma_t=cfg.mma_t)      # as scheduled: loads
+    lp.close()
+    ent = [(l, k) for l, s in enumerate(sched.lane_streams) for k, e in enumerate(s)]
+    sig = [(l, k) for l, k in ent if sched.lane_streams[l][k].task not in V.CONTROL_SENTINELS
+           and sched.lane_streams[l][k].signal_flag != V.FLAG_NONE]
+    wt = [(l, k) for l, k in ent if sched.lane_streams[l][k].task not in V.CONTROL_SENTINELS
+          and sched.lane_streams[l][k].wait_count]
+
+    def twice(st):
+        st[sig[1][0]][sig[1][1]].signal_flag = st[sig[0][0]][sig[0][1]].signal_flag
+
+    def other_phase(st):           # the waiter of the last-numbered flags (layer 1) waits for flag 0 (layer 0)
+        l, k = max(wt, key=lambda lk: sched.lane_streams[lk[0]][lk[1]].wait_flag)
+        assert st[l][k].wait_flag > 0
+        st[l][k].wait_flag, st[l][k].wait_count = 0, 1
+
+    def after_wait(st):
+        # a signaling entry of another lane moved into a waiting entry's lane,
+        # right after the wait (same phase); both lanes' FOR body ranges follow
+        def phase_of(lane, k):
+            return sum(1 for x in range(k) if st[lane][x].task == V.ENT_BARRIER)
+
+        lw, kw = wt[0]
+        ls, ks = next((l, k) for l, k in sig if l != lw and phase_of(l, k) == phase_of(lw, kw))
+        e = st[ls].pop(ks)
+        st[lw].insert(kw + 1, e)
+        for lane, pos, d in ((ls, ks, -1), (lw, kw + 1, +1)):
+            for f in st[lane]:
+                if f.task == V.ENT_FOR:
+                    if f.tile_lo <= pos < f.tile_lo + f.tile_hi + (d > 0):
+                        f.tile_hi += d
+                    elif f.tile_lo > pos:
+                        f.tile_lo += d
+
+    for name, fn in (("twice", twice), ("other phase", other_phase), ("signal after wait", after_wait)):
+        print(f"[gpu] loader flag case: {name}", file=sys.stderr, flush=True)
+        with pytest.raises(VmrtError) as ei:
+            rt.load(blob(fn), ew_ts=cfg.ew_ts, mma_t=cfg.mma_t)
+        assert ei.value.code == 3 and "flag" in str(ei.value), str(ei.value)

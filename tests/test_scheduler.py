@@ -440,11 +440,12 @@ def test_layernorm_row_interleave():
 
 
 def test_lane_fit():
-    """A program of many small phases (the decode loop) runs on half the
-    lanes; bandwidth- and MFMA-bound programs keep every lane."""
+    """A program of many small phases (the decode loop, scheduled with grid
+    barriers only) runs on half the lanes; bandwidth- and MFMA-bound programs
+    keep every lane."""
     import dataclasses
     from pjrt_amd import configs as CF
-    cfg = S.DeviceConfig(nlanes=256)
+    cfg = S.DeviceConfig(nlanes=256, counters=False)
     dec = CF.gpt_c5(dataclasses.replace(CF.C5, layers=2, steps=8))
     assert S.lane_fit(dec, cfg) == 128
     assert S.schedule_program(dec, cfg).n_lanes == 128
@@ -553,3 +554,144 @@ def test_residual_buffer_zero_is_a_read():
     g2.output(g2.dot(x2, w2))
     (dot2,) = [i for i in g2.build().instrs if i.op == V.OP_DOT]
     assert S.instr_reads(dot2, g2.build()) == {0, 1}
+
+
+# --- completion flags (extension of the WAIT / SIGNAL entry fields) -------------------
+
+def _decoder(counters, nlanes=16):
+    import dataclasses
+    from pjrt_amd import configs as CF
+    c = CF.GptConfig(layers=2, d=128, heads=4, mlp=256, vocab=300, prompt=32, steps=3)
+    prog = CF.gpt_c5(c, emit_logits=True)
+    cfg = S.DeviceConfig(nlanes=nlanes, counters=counters, fit_lanes=False)
+    sched = S.schedule_program(prog, cfg)
+    return c, prog, sched, cfg
+
+
+def _segments(stream):
+    """The lane's entries split at its barriers (one list per phase)."""
+    out = [[]]
+    for e in stream:
+        if e.task == V.ENT_BARRIER:
+            out.append([])
+        elif e.task not in V.CONTROL_SENTINELS:
+            out[-1].append(e)
+    return out
+
+
+def test_counters_join_decode_attention_to_its_qkv_phase():
+    """With completion flags each layer's decode attention runs in its QKV
+    GEMV's phase (one grid barrier fewer per layer, per decode step); every
+    attention entry waits for exactly the flags of the strips that write its
+    heads' q, k and v (recomputed here from the arena byte ranges), every
+    signaling entry comes before any waiting entry of its lane and phase, and
+    the schedule computes what the barrier-only one computes, in both lane
+    orders of the oracle's simulator."""
+    from pjrt_amd import configs as CF
+    c, prog, on, cfg = _decoder(True)
+    _, _, off, _ = _decoder(False)
+    nbar = lambda sc: sum(1 for e in sc.lane_streams[0] if e.task == V.ENT_BARRIER)
+    assert nbar(off) - nbar(on) == c.layers            # the FOR body is scheduled once
+    assert on.n_flags > 0 and off.n_flags == 0
+    bufs = prog.buffers
+    # who signals what, and the bytes each signaling GEMV entry writes
+    signal = {}
+    for s in on.lane_streams:
+        for e in s:
+            if e.task not in V.CONTROL_SENTINELS and e.signal_flag != V.FLAG_NONE:
+                assert e.signal_flag not in signal
+                t = on.tasks[e.task]
+                assert t.tile_op == V.TOP_GEMV
+                dst = next(b for b in range(len(bufs)) if bufs[b].arena_byte_offset == bufs[t.dst].arena_byte_offset
+                           and bufs[b].size_bytes == bufs[t.dst].size_bytes)
+                es = V.DT_SIZE[bufs[dst].dtype]
+                lo = bufs[dst].arena_byte_offset + e.tile_lo * t.p4 * es
+                hi = bufs[dst].arena_byte_offset + min(e.tile_hi * t.p4, t.p1) * es
+                signal[e.signal_flag] = (e.task, lo, hi)
+    assert sorted(signal) == list(range(on.n_flags))
+    waits = 0
+    for s in on.lane_streams:
+        for seg in _segments(s):
+            seen_wait = False
+            for e in seg:
+                if e.wait_count:
+                    seen_wait = True
+                    waits += 1
+                    t = on.tasks[e.task]
+                    assert t.tile_op == V.TOP_DECODE_ATTN
+                    H, Sp = t.p4 & 0xFFFF, max(1, t.p4 >> 16)
+                    hd = t.p5 & 0xFFFF
+                    es = V.DT_SIZE[bufs[t.a].dtype]
+                    heads = range(e.tile_lo // Sp, (e.tile_hi - 1) // Sp + 1)
+                    need = set()
+                    for f, (_, lo, hi) in signal.items():
+                        for b in (t.a, t.p1, t.p2):           # q, k, v
+                            o = bufs[b].arena_byte_offset
+                            if any(lo < o + (h + 1) * hd * es and o + h * hd * es < hi for h in heads):
+                                need.add(f)
+                    assert set(range(e.wait_flag, e.wait_flag + e.wait_count)) == need
+                elif e.signal_flag != V.FLAG_NONE:
+                    assert not seen_wait
+    assert waits >= c.layers
+    args = CF.gpt_inputs(c, seed=11)
+    a = vmref.execute_schedule(V.serialize(prog, on), args)
+    b = vmref.execute_schedule(V.serialize(prog, off), args)
+    for x, y in zip(a, b):
+        np.testing.assert_array_equal(x, y)
+    want_tok, want_logits = CF.gpt_reference(c, args)
+    np.testing.assert_array_equal(np.concatenate(a[:2]), want_tok)
+
+
+def test_counters_off_by_switch_and_for_other_consumers():
+    """PJRT_AMD_COUNTERS=0 keeps every barrier; a phase whose consumer is not a
+    decode attention fed by GEMV strips is never joined."""
+    cfg = S.DeviceConfig.from_env({"PJRT_AMD_COUNTERS": "0"})
+    assert not cfg.counters
+    g = G.Graph()
+    x, w = g.input((1, 256)), g.input((256, 512))
+    y = g.dot(x, w)
+    g.output(g.reduce_last(y, V.RED_SUM))
+    sched = S.schedule_program(g.build(), S.DeviceConfig(nlanes=16, fit_lanes=False))
+    assert sched.n_flags == 0
+    assert all(e.wait_count == 0 and e.signal_flag == V.FLAG_NONE
+               for s in sched.lane_streams for e in s if e.task not in V.CONTROL_SENTINELS)
+
+
+def test_oracle_rejects_bad_completion_flags():
+    """The oracle's parser rejects a flag signaled twice or a wait outside
+    n_flags, and its simulator reports a wait no entry of the phase signals."""
+    import dataclasses
+    c, prog, on, cfg = _decoder(True)
+    args = None
+
+    def mutate(fn):
+        streams = [[dataclasses.replace(e) for e in s] for s in on.lane_streams]
+        fn(streams)
+        return V.serialize(prog, V.Schedule(on.n_lanes, on.tasks, streams, on.root_lens, on.n_flags))
+
+    sig = [(l, k) for l, s in enumerate(on.lane_streams) for k, e in enumerate(s)
+           if e.task not in V.CONTROL_SENTINELS and e.signal_flag != V.FLAG_NONE]
+    wt = [(l, k) for l, s in enumerate(on.lane_streams) for k, e in enumerate(s)
+          if e.task not in V.CONTROL_SENTINELS and e.wait_count]
+
+    def twice(st):
+        (l0, k0), (l1, k1) = sig[0], sig[1]
+        st[l1][k1].signal_flag = st[l0][k0].signal_flag
+
+    def outside(st):
+        l, k = wt[0]
+        st[l][k].wait_count = on.n_flags + 1 - st[l][k].wait_flag
+
+    for fn in (twice, outside):
+        with pytest.raises(vmref.FormatError):
+            vmref.parse(mutate(fn))
+
+    def unsignaled(st):          # the first producer of a waited range stops signaling
+        l, k = wt[0]
+        f = st[l][k].wait_flag
+        for ls, ks in sig:
+            if st[ls][ks].signal_flag == f:
+                st[ls][ks].signal_flag = V.FLAG_NONE
+    from pjrt_amd import configs as CF
+    with pytest.raises(AssertionError, match="completion flags"):
+        vmref.execute_schedule(mutate(unsignaled), CF.gpt_inputs(c, seed=11))

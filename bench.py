@@ -543,11 +543,12 @@ def bench_c5_lowered(rt, reps=3):
     program's on the same inputs."""
     from pjrt_amd import configs as CF
     from pjrt_amd import lowering as L
+    from pjrt_amd import scheduler as S
     from pjrt_amd import stablehlo_configs as H
     c = CF.C5
     args = CF.gpt_inputs(c)
     dev_in = [rt.to_device(a) for a in args]
-    times, toks, lower_s = {}, {}, 0.0
+    times, toks, lower_s, lanes = {}, {}, 0.0, None
     saved = os.environ.get("PJRT_OCL_WHILE")
     os.environ["PJRT_OCL_WHILE"] = "for"           # 8 trips would otherwise be unrolled
     try:
@@ -555,7 +556,9 @@ def bench_c5_lowered(rt, reps=3):
             t0 = time.perf_counter()
             prog = L.lower_text(H.gpt_decode(c, trips=trips))
             lower_s = max(lower_s, time.perf_counter() - t0)
-            lp = rt.compile(prog, arena_reuse=False)
+            if lanes is None:          # the full program's lane count, for both (see bench_c5)
+                lanes = S.lane_fit(prog, rt.scheduler_config())
+            lp = rt.compile(prog, arena_reuse=False, nlanes=lanes, fit_lanes=False)
             dev_out = lp.alloc_outputs()
             _, times[trips] = time_program(rt, lp, dev_in, dev_out, reps, 1)
             if trips == c.steps:
@@ -650,16 +653,20 @@ def bench_c5(rt, reps=3, with_cpu=False):
     """Config 5: GPT decoder (12 layers, d 768, vocab 32000, bf16), 512-token
     prompt then 128 greedy decode steps in one FOR loop.  Decode tokens/s comes
     from the difference between the full program and the same program cut to 8
-    loop trips (prefill and launch cancel)."""
+    loop trips (prefill and launch cancel).  Both run on the lane count the
+    scheduler picks for the full program (lane_fit), so that their prefills
+    are the same work on the same lanes."""
     import dataclasses
     from pjrt_amd import configs as CF
+    from pjrt_amd import scheduler as S
     c = CF.C5
     args = CF.gpt_inputs(c)
     dev_in = [rt.to_device(a) for a in args]
+    lanes = S.lane_fit(CF.gpt_c5(c), rt.scheduler_config())
     times = {}
     toks = None
     for trips in (c.steps, 8):
-        lp = rt.compile(CF.gpt_c5(c, trips=trips))
+        lp = rt.compile(CF.gpt_c5(c, trips=trips), nlanes=lanes, fit_lanes=False)
         dev_out = lp.alloc_outputs()
         _, ms = time_program(rt, lp, dev_in, dev_out, reps, 1)
         times[trips] = ms
@@ -676,7 +683,7 @@ def bench_c5(rt, reps=3, with_cpu=False):
     achieved = bytes_tok / (per_tok * 1e-3) / 1e9
     assert toks.min() >= 0 and toks.max() < c.vocab
     res = {"workload": "C5 GPT decoder 12L d768 H12 mlp3072 vocab32000 bf16, prompt 512, 128 greedy steps "
-                       "in one FOR loop",
+                       "in one FOR loop", "lanes": lanes,
            "decode_tokens_per_s": round(1e3 / per_tok, 1), "ms_per_token": round(per_tok, 4),
            "program_ms": round(times[c.steps], 3), "prefill_plus_8_steps_ms": round(times[8], 3),
            "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -706,10 +713,14 @@ def profile_c5(rt, steps=16):
     c = dataclasses.replace(CF.C5, steps=steps)
     args = CF.gpt_inputs(c)
     dev_in = [rt.to_device(a) for a in args]
+    # both programs on the lane count of the benchmarked decoder (128 steps),
+    # so that the difference holds the decode steps and nothing else
+    cfg = rt.scheduler_config()
+    cfg = dataclasses.replace(cfg, nlanes=S.lane_fit(CF.gpt_c5(CF.C5), cfg), fit_lanes=False)
     res = {}
     for trips in (0, steps):
         prog = CF.gpt_c5(c, trips=trips)
-        sched = S.schedule_program(prog, rt.scheduler_config())
+        sched = S.schedule_program(prog, cfg)
         lp = rt.load(V.serialize(prog, sched))
         outs = lp.alloc_outputs()
         lp.execute(dev_in, outs)

@@ -97,6 +97,8 @@ class DeviceConfig:
     # that the strips of their head signal, instead of a grid barrier
     # (extension of the entries' WAIT / SIGNAL fields; ``_flag_edges``).
     counters: bool = True
+    # A streaming layernorm's lanes take rows nlanes apart (``row_interleave``).
+    ln_interleave: bool = True
 
     @classmethod
     def from_env(cls, environ=None) -> "DeviceConfig":
@@ -123,7 +125,8 @@ class DeviceConfig:
                    ln_gemv=env.get("PJRT_AMD_LN_GEMV", "1") != "0",
                    idle_master=(env["PJRT_AMD_IDLE_MASTER"] != "0") if env.get("PJRT_AMD_IDLE_MASTER") else None,
                    fit_lanes=env.get("PJRT_AMD_FIT_LANES", "1") != "0",
-                   counters=env.get("PJRT_AMD_COUNTERS", "1") != "0")
+                   counters=env.get("PJRT_AMD_COUNTERS", "1") != "0",
+                   ln_interleave=env.get("PJRT_AMD_LN_INTERLEAVE", "1") != "0")
 
 
 # --- instruction -> task ------------------------------------------------------
@@ -255,7 +258,7 @@ def row_interleave(n_rows: int, cfg: DeviceConfig) -> int:
     so each lane's contiguous chunk of logical rows is a stride-nlanes set of
     real rows and the lanes stream neighbouring rows together (C2, alternating
     runs on one MI355X: 38.7 against 39.6 us).  0: rows as they are."""
-    if cfg.nlanes <= 1 or n_rows < 2 * cfg.nlanes or n_rows % cfg.nlanes:
+    if not cfg.ln_interleave or cfg.nlanes <= 1 or n_rows < 2 * cfg.nlanes or n_rows % cfg.nlanes:
         return 0
     return n_rows // cfg.nlanes
 

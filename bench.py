@@ -687,7 +687,10 @@ def bench_c5(rt, reps=3, with_cpu=False):
            "decode_tokens_per_s": round(1e3 / per_tok, 1), "ms_per_token": round(per_tok, 4),
            "program_ms": round(times[c.steps], 3), "prefill_plus_8_steps_ms": round(times[8], 3),
            "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                        "frac": round(achieved / HBM_PEAK_GBS, 4), "bytes_per_token": int(bytes_tok)}}
+                        "frac": round(achieved / HBM_PEAK_GBS, 4), "bytes_per_token": int(bytes_tok),
+                        # measured FETCH_SIZE + WRITE_SIZE per decode token, calibrated against a copy
+                        # (profiles/vm_main_c5_traffic.txt)
+                        "traffic": (load_traffic("c5") or {}).get("bytes_per_token")}}
     if with_cpu:
         log("C5 CPU baseline")
         cpu, ctoks = cpu_baseline_c5(c, args)

@@ -67,7 +67,7 @@ VM_DEV void dec_cvt8(const typename GemvRaw<DT>::T& r, float (&w)[8]) { gemv_cvt
 // pays one memory round trip, then the scores, the softmax and P.V come out of
 // registers, lane shuffles and LDS.
 template <uint32_t DT>
-VM_TILE void decode_attn_split(Args A, uint32_t ti, uint32_t tile) {
+VM_DEV void decode_attn_split(Args A, uint32_t ti, uint32_t tile) {
   A = uargs(A);
   const VM_K Task& t = task_of(A, ti);
   const uint32_t hd = t.p[5] & 0xFFFF, C = t.p[6];
@@ -325,16 +325,22 @@ VM_TILE void decode_attn_split(Args A, uint32_t ti, uint32_t tile) {
   }
 }
 
-VM_TILE void decode_attn_tiles(Args A, uint32_t ti, uint32_t lo, uint32_t hi) {
+// One leaf per dtype with the split inlined, for the reason gemv_run gives.
+template <uint32_t DT>
+VM_LEAF void decode_attn_run(Args A, uint32_t ti, uint32_t lo, uint32_t hi) {
   A = uargs(A);
+  lo = uni(lo);
+  hi = uni(hi);
+  for (uint32_t tile = lo; tile < hi; ++tile) decode_attn_split<DT>(A, ti, tile);
+}
+
+VM_DEV void decode_attn_tiles(Args A, uint32_t ti, uint32_t lo, uint32_t hi) {
   const VM_K Task& t = task_of(A, ti);
   const uint32_t dt = (t.tile_op >> 8) & 0xFF;
   hi = min(hi, max(1u, (t.p[4] & 0xFFFF) * max(1u, t.p[4] >> 16)));
-  for (uint32_t tile = lo; tile < hi; ++tile) {
-    if (dt == DT_BF16) decode_attn_split<DT_BF16>(A, ti, tile);
-    else if (dt == DT_F16) decode_attn_split<DT_F16>(A, ti, tile);
-    else decode_attn_split<DT_F32>(A, ti, tile);
-  }
+  if (dt == DT_BF16) decode_attn_run<DT_BF16>(A, ti, lo, hi);
+  else if (dt == DT_F16) decode_attn_run<DT_F16>(A, ti, lo, hi);
+  else decode_attn_run<DT_F32>(A, ti, lo, hi);
 }
 
 }  // namespace vm

@@ -27,7 +27,7 @@ struct EwOp {
 
 // f32 contiguous range [e0, e1): v4f body, scalar tail.
 template <uint32_t SUB>
-VM_TILE void ew_f32_range(gbyte* dp, const gbyte* ap, const gbyte* bp, uint64_t e0, uint64_t e1, float s,
+VM_DEV void ew_f32_range(gbyte* dp, const gbyte* ap, const gbyte* bp, uint64_t e0, uint64_t e1, float s,
                           float t) {
   dp = uni_ptr(dp);
   ap = uni_ptr(ap);
@@ -77,7 +77,7 @@ template <bool BF16>
 VM_DEV uint32_t f2h(float f) { return BF16 ? f32_to_bf16(f) : f32_to_f16(f); }
 
 template <uint32_t SUB, bool BF16>
-VM_TILE void ew_h16_range(gbyte* dp, const gbyte* ap, const gbyte* bp, uint64_t e0, uint64_t e1, float s,
+VM_DEV void ew_h16_range(gbyte* dp, const gbyte* ap, const gbyte* bp, uint64_t e0, uint64_t e1, float s,
                           float t) {
   dp = uni_ptr(dp);
   ap = uni_ptr(ap);
@@ -279,7 +279,7 @@ VM_DEV void copy_elem(gbyte* d, uint64_t di, const gbyte* s, uint64_t si, uint32
 }
 
 // Compare, select, convert, bitcast, is_finite, LTS: mixed-dtype subops.
-VM_TILE void ew_special(Args A, uint32_t ti, uint64_t e0, uint64_t e1) {
+VM_DEV void ew_special(Args A, uint32_t ti, uint64_t e0, uint64_t e1) {
   A = uargs(A);
   const VM_K Task& t = task_of(A, ti);
   const uint32_t sub = uni(t.p[0]);
@@ -343,7 +343,7 @@ VM_TILE void ew_special(Args A, uint32_t ti, uint64_t e0, uint64_t e1) {
 }
 
 // Integer, bool and f64 elementwise.
-VM_TILE void ew_intlike(Args A, uint32_t ti, uint64_t e0, uint64_t e1) {
+VM_DEV void ew_intlike(Args A, uint32_t ti, uint64_t e0, uint64_t e1) {
   A = uargs(A);
   const VM_K Task& t = task_of(A, ti);
   const uint32_t sub = uni(t.p[0]), dt = uni((t.tile_op >> 8) & 0xFF);
@@ -394,7 +394,7 @@ VM_TILE void ew_intlike(Args A, uint32_t ti, uint64_t e0, uint64_t e1) {
 }
 
 // f32 / f16 / bf16 scalar path: folded views, misalignment, libm-heavy subops.
-VM_TILE void ew_float_scalar(Args A, uint32_t ti, uint64_t e0, uint64_t e1) {
+VM_DEV void ew_float_scalar(Args A, uint32_t ti, uint64_t e0, uint64_t e1) {
   A = uargs(A);
   const VM_K Task& t = task_of(A, ti);
   const uint32_t sub = uni(t.p[0]), dt = uni((t.tile_op >> 8) & 0xFF);
@@ -421,7 +421,12 @@ VM_TILE void ew_float_scalar(Args A, uint32_t ti, uint64_t e0, uint64_t e1) {
   }
 }
 
-VM_TILE void ew_tile(Args A, uint32_t ti, uint32_t lo, uint32_t hi) {
+// A leaf with its loops inlined: as a function calling (or jumping to) separate
+// loop functions it followed the calling convention, saving its callee-saved
+// registers to scratch on entry and reloading them before each jump, a memory
+// round trip per entry.  Called only from the kernel, a leaf leaves the saving
+// to the kernel (interprocedural register allocation).
+VM_LEAF void ew_tile(Args A, uint32_t ti, uint32_t lo, uint32_t hi) {
   A = uargs(A);
   const VM_K Task& t = task_of(A, ti);
   const uint32_t sub = uni(t.p[0]), n = uni(t.p[1]);

@@ -197,7 +197,7 @@ VM_DEV void gemv_consume(const typename GemvRaw<ADT>::T (&raw)[U], uint32_t M, u
 // the epilogue's residual values, then two weight chunks; later chunks are
 // issued as earlier ones are consumed.
 template <uint32_t ADT, int MM>
-VM_TILE void gemv_tile(Args A, uint32_t ti, uint32_t tile) {
+VM_DEV void gemv_tile(Args A, uint32_t ti, uint32_t tile) {
   A = uargs(A);
   constexpr int U = gemv_u<ADT>();
   const VM_K Task& t = task_of(A, ti);
@@ -342,21 +342,34 @@ VM_TILE void gemv_tile(Args A, uint32_t ti, uint32_t tile) {
   }
 }
 
-VM_TILE void gemv_tiles(Args A, uint32_t ti, uint32_t lo, uint32_t hi) {
+// One leaf per operand type and M class runs an entry's tiles with the tile
+// inlined.  A wrapper that called the tile as a function would follow the
+// calling convention around every call (its callee-saved registers to scratch
+// on entry and back before it returns: a memory round trip at the end of each
+// GEMV entry, and 7 KB of scratch writes per entry that the grid barrier's
+// release writes back).  Called only from the kernel and never as a tail call,
+// a leaf leaves the saving to the kernel, which keeps what it needs in
+// registers the leaf does not touch.
+template <uint32_t ADT, int MM>
+VM_LEAF void gemv_run(Args A, uint32_t ti, uint32_t lo, uint32_t hi) {
   A = uargs(A);
+  lo = uni(lo);
+  hi = uni(hi);
+  for (uint32_t tile = lo; tile < hi; ++tile) gemv_tile<ADT, MM>(A, ti, tile);
+}
+
+VM_DEV void gemv_tiles(Args A, uint32_t ti, uint32_t lo, uint32_t hi) {
   const VM_K Task& t = task_of(A, ti);
   const uint32_t M = t.p[0], adt = (t.tile_op >> 16) & 0xFF;
   const uint32_t total = max(1u, t.p[3]) * ((t.p[1] + t.p[4] - 1) / t.p[4]);
   hi = min(hi, total);
-  for (uint32_t tile = lo; tile < hi; ++tile) {
-    if (adt == DT_BF16) {
-      if (M == 1) gemv_tile<DT_BF16, 1>(A, ti, tile);
-      else gemv_tile<DT_BF16, kGemvMaxM>(A, ti, tile);
-    } else if (adt == DT_F16) {
-      gemv_tile<DT_F16, kGemvMaxM>(A, ti, tile);
-    } else {
-      gemv_tile<DT_F32, kGemvMaxM>(A, ti, tile);
-    }
+  if (adt == DT_BF16) {
+    if (M == 1) gemv_run<DT_BF16, 1>(A, ti, lo, hi);
+    else gemv_run<DT_BF16, kGemvMaxM>(A, ti, lo, hi);
+  } else if (adt == DT_F16) {
+    gemv_run<DT_F16, kGemvMaxM>(A, ti, lo, hi);
+  } else {
+    gemv_run<DT_F32, kGemvMaxM>(A, ti, lo, hi);
   }
 }
 

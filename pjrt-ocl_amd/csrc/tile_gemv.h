@@ -17,8 +17,8 @@
 // Tile t = g * ceil(N / CW) + nb covers columns [CW nb, CW nb + CW) of batch g.
 // Threads: CW / 8 column groups (one 16-byte bf16 load per row each) x RP =
 // 2048 / CW row phases; thread (cg, rp) accumulates rows rp, rp + RP, ... with up
-// to 16 row loads in flight.  The RP row-phase sums are added in a fixed order
-// through LDS.
+// to 16 row loads in flight.  The RP row-phase sums are added in a fixed order:
+// by DPP row rotations inside each 16-lane row, then the row partials through LDS.
 #pragma once
 #include "tile_mma.h"
 #include "tile_reduce.h"
@@ -166,6 +166,71 @@ VM_DEV void gemv_ln_rows(Args A, const VM_K Task& L, uint32_t M, uint32_t K, flo
   }
 }
 
+// The same layernorm for one row (M = 1) whose K <= kGemvXU kBlock elements are
+// already in registers (element threadIdx.x + u kBlock in x[u], 0 past K),
+// normalised in place.  The sums are the ones gemv_ln_rows forms (per thread in
+// u order, DPP wave sums, the four waves added in order), so the results are the
+// same bits, with one LDS exchange and block barrier per sum instead of two
+// passes over the row in LDS and two barriers per sum.  st: 3 kWaves floats of
+// LDS that no other stage of the tile uses.
+template <uint32_t DT>
+VM_DEV void gemv_ln_regs(const VM_K Task& L, uint32_t K, float (&x)[kGemvXU], const float (&gv)[kGemvXU],
+                         const float (&bv)[kGemvXU], float* st) {
+  const uint32_t flags = L.p[3];
+  const float eps = __uint_as_float(L.p[2]);
+  const bool affine = flags & LN_AFFINE, do_gelu = flags & LN_GELU, two_pass = flags & LN_TWO_PASS;
+  const float inv_n = 1.0f / float(K);
+  const uint32_t wave = threadIdx.x >> 6;
+  const bool lead = (threadIdx.x & 63) == 0;
+  float s = 0.0f, s2 = 0.0f;
+#pragma unroll
+  for (int u = 0; u < kGemvXU; ++u) {
+    s += x[u];
+    s2 = fmaf(x[u], x[u], s2);
+  }
+  s = wave_sum(s);
+  if (!two_pass) s2 = wave_sum(s2);
+  if (lead) {
+    st[wave] = s;
+    st[kWaves + wave] = s2;
+  }
+  __syncthreads();
+  float ts = st[0], ts2 = st[kWaves];
+#pragma unroll
+  for (int k = 1; k < kWaves; ++k) {
+    ts += st[k];
+    ts2 += st[kWaves + k];
+  }
+  const float mean = ts * inv_n;
+  float var;
+  if (two_pass) {
+    float q = 0.0f;
+#pragma unroll
+    for (int u = 0; u < kGemvXU; ++u) {
+      const float dv = x[u] - mean;
+      if (threadIdx.x + u * kBlock < K) q = fmaf(dv, dv, q);
+    }
+    q = wave_sum(q);
+    if (lead) st[2 * kWaves + wave] = q;
+    __syncthreads();
+    float tq = st[2 * kWaves];
+#pragma unroll
+    for (int k = 1; k < kWaves; ++k) tq += st[2 * kWaves + k];
+    var = tq * inv_n;
+  } else {
+    var = ts2 * inv_n - mean * mean;
+  }
+  const float rstd = rsqrtf(var + eps);
+  const float shift = -mean * rstd;
+#pragma unroll
+  for (int u = 0; u < kGemvXU; ++u) {
+    float z = fmaf(x[u], rstd, shift);
+    if (affine) z = fmaf(z, gv[u], bv[u]);
+    if (do_gelu) z = gelu(z);
+    x[u] = gemv_round<DT>(z);
+  }
+}
+
 template <uint32_t ADT, int U>
 VM_DEV void gemv_issue(typename GemvRaw<ADT>::T (&raw)[U], const gbyte* b, uint32_t N, uint32_t K, uint32_t k,
                        uint32_t RP, uint32_t col) {
@@ -209,11 +274,11 @@ VM_DEV void gemv_tile(Args A, uint32_t ti, uint32_t tile) {
   const gbyte* a = resolve(A, t.a) + uint64_t(g) * M * K * esz;
   const gbyte* b = resolve(A, t.b) + uint64_t(g) * K * N * esz;
   const uint32_t cgs = CW / 8, RP = kBlock / cgs;
-  // LDS: x [M][K], then the row-phase sums [RP][M][CW] (= 2048 M floats), then the
-  // first-pass sums; the loader checks that M * K + 4096 M floats fit
+  // LDS: x [M][K], then the row partials [P][M][CW] (at most 2048 M floats), then
+  // the layernorm's sums; the loader checks that M * K + 4096 M floats fit
   float* xs = lds_ptr<float>();
   float* red = xs + ((M * K + 3) & ~3u);
-  float* tmp = red + 2048 * M;
+  float* st = red + 2048 * M;
   const uint32_t nx = M * K;
 
   // x, or the fused layernorm's input with its gamma / beta, as raw bits
@@ -262,7 +327,12 @@ VM_DEV void gemv_tile(Args A, uint32_t ti, uint32_t tile) {
     gemv_xcvt(gr, gv, DT_F32, K);
     gemv_xcvt(br, bv, DT_F32, K);
   }
-  __syncthreads();                       // the previous user of the LDS is done
+  // No block barrier before the first LDS write: the entry starts after one (a
+  // grid barrier, a completion-flag wait or the block sync between entries), and
+  // the previous tile of this entry reads only its row partials from here on,
+  // which this stage does not write.
+  const bool lnreg = lnp && xreg && M == 1 && K <= kGemvXU * kBlock;
+  if (lnreg) gemv_ln_regs<ADT>(L, K, xv, gv, bv, st);
   if (xreg) {
 #pragma unroll
     for (int u = 0; u < kGemvXU; ++u) {
@@ -285,8 +355,8 @@ VM_DEV void gemv_tile(Args A, uint32_t ti, uint32_t tile) {
     for (uint32_t i = threadIdx.x; i < nx; i += kBlock) xs[i] = load_f(xsrc, xdt, i);
   }
   __syncthreads();
-  if (lnp) {
-    gemv_ln_rows<ADT>(A, L, M, K, xs, red, gv, bv);
+  if (lnp && !lnreg) {
+    gemv_ln_rows<ADT>(A, L, M, K, xs, st, gv, bv);
     __syncthreads();
   }
 
@@ -303,21 +373,30 @@ VM_DEV void gemv_tile(Args A, uint32_t ti, uint32_t tile) {
     gemv_consume<ADT, U, MM>(r1, M, K, kb + step + rp, RP, xs, acc);
     if (kb + 3 * step < K) gemv_issue<ADT, U>(r1, b, N, K, kb + 3 * step + rp, RP, col);
   }
+  // Row-phase sums: the lanes of a 16-lane row that hold one column group (lanes
+  // cg, cg + cgs, ...) add theirs by DPP row rotations (by cgs, 2 cgs, .. 8); the
+  // P = kBlock / max(16, cgs) row partials then go through LDS, and one thread per
+  // output adds them in row order.  (Alternating C5 runs: 1263.5 / 1260.8 ->
+  // 1280.2 / 1280.9 tokens/s together with the register layernorm above.)
+  const uint32_t rw = max(16u, cgs), P = kBlock / rw;
 #pragma unroll
   for (int m = 0; m < MM; ++m)
-    if (m < int(M))
 #pragma unroll
-      for (int j = 0; j < 8; ++j) red[(rp * M + m) * CW + cg * 8 + j] = acc[m][j];
-  __syncthreads();
-
-  // Sum the RP row phases of each of the M * CW outputs in a fixed order: J
-  // threads per output each add every J-th phase, then one thread adds the J.
-  const uint32_t J = outs >= kBlock ? 1u : kBlock / outs;
-  for (uint32_t i = threadIdx.x; i < outs * J; i += kBlock) {
-    const uint32_t o = i % outs, j = i / outs;
-    float v = 0.0f;
-    for (uint32_t r = j; r < RP; r += J) v += red[r * outs + o];
-    tmp[j * outs + o] = v;
+    for (int j = 0; j < 8; ++j) {
+      float v = acc[m][j];
+      if (cgs < 2) v += dpp<0x121>(v);
+      if (cgs < 4) v += dpp<0x122>(v);
+      if (cgs < 8) v += dpp<0x124>(v);
+      if (cgs < 16) v += dpp<0x128>(v);
+      acc[m][j] = v;
+    }
+  if ((threadIdx.x & 15) < cgs) {
+    const uint32_t pr = threadIdx.x / rw;
+#pragma unroll
+    for (int m = 0; m < MM; ++m)
+      if (m < int(M))
+#pragma unroll
+        for (int j = 0; j < 8; ++j) red[(pr * M + m) * CW + cg * 8 + j] = acc[m][j];
   }
   __syncthreads();
 
@@ -327,7 +406,7 @@ VM_DEV void gemv_tile(Args A, uint32_t ti, uint32_t tile) {
     const uint32_t m = o / CW, n = nb * CW + o % CW;
     if (n >= N) continue;
     float x = 0.0f;
-    for (uint32_t j = 0; j < J; ++j) x += tmp[j * outs + o];
+    for (uint32_t q = 0; q < P; ++q) x += red[q * outs + o];
     const uint64_t elem = (uint64_t(g) * M + m) * N + n;
     const bool first = o == threadIdx.x;
     for (int k = 0; k < nm; ++k) {

@@ -79,7 +79,7 @@ def test_gpt_c5_lane_fit_matches_every_lane():
     want = run_gpu(full, args)
     # the strip width, and with it the summation order of the bf16 GEMVs,
     # differs between the two schedules: the bf16 decoder tolerance applies
-    check_decoder(got, want, 5e-3, pinned=13, what="half-lane vs all-lane decoder")
+    check_decoder(got, want, 5e-3, pinned=17, what="half-lane vs all-lane decoder")
 
 
 def _lowered_decoder(c):

@@ -151,11 +151,14 @@ def test_c5_full_128_step_loop_against_oracle():
     """The benchmarked config-5 program (prompt 512, 128 greedy decode steps in one
     FOR loop), with per-step logits, against the CPU oracle's execution of the same
     bytes: logits within 5e-3 of the largest, tokens equal until the first
-    near-tie (gpu_util.check_decoder).  Measured on the MI355X: steps 0-69 are
-    token-exact and step 70 is a near-tie, where the runs diverge."""
+    near-tie (gpu_util.check_decoder).  Measured on the MI355X: all 129 steps are
+    token-exact.  Step 70 is a near-tie of the oracle's logits (top-two gap 5.4e-3
+    against a tolerance of 2.8e-2), so a change of summation order in the GEMVs may
+    flip it: that ends the comparison there, below the pin, and the pin is then
+    re-measured, not lowered silently."""
     c = CF.C5
     args = CF.gpt_inputs(c)
     blob, _ = blob_for(CF.gpt_c5(c, emit_logits=True))
     say("C5 full 128-step program")
     got, want = run_both(blob, args, oracle="tensor")
-    check_decoder(got, want, 5e-3, pinned=70, what="config-5 decoder, 128 steps")
+    check_decoder(got, want, 5e-3, pinned=129, what="config-5 decoder, 128 steps")

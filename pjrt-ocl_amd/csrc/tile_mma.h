@@ -510,6 +510,65 @@ struct FastDma {
   }
 };
 
+// The same transfers for a ragged tile (M or N not a multiple of 256, or K not a
+// multiple of 64; K and N multiples of 8): every address is clamped into the
+// operand -- A rows past M re-read row M - 1, B columns past N the last 8, k past
+// K the last 8 columns of A / the last row of B -- so no transfer leaves the
+// buffers, and each lane's LDS slot is where the aligned tile puts it.  Rows and
+// columns past M / N are computed but not stored; the k past K are zeroed in LDS
+// (RaggedDma::zero) before the stage is published, in both operands, so that
+// they add 0 whatever the clamped data holds.
+struct RaggedDma {
+  uint32_t ra, ca, rb, cb;  // per lane: A row within a round and its k chunk; B k row within a round and n chunk
+  uint32_t wo;
+  const gbyte* a;           // A[g, m0, 0]
+  const gbyte* b;           // B[g, 0, n0]
+  uint32_t M, N, K, m0, n0;
+  VM_DEV void init(const gbyte* a_, const gbyte* b_, uint32_t M_, uint32_t N_, uint32_t K_, uint32_t m0_, uint32_t n0_) {
+    const uint32_t l = threadIdx.x & 63, w = threadIdx.x >> 6;
+    ra = 8 * w + (l >> 3);
+    ca = (l & 7) ^ aswz(ra);
+    rb = 2 * w + (l >> 5);
+    cb = (l & 31) ^ (4 * (rb & 3));
+    wo = uni(1024 * w);
+    a = a_;
+    b = b_;
+    M = M_;
+    N = N_;
+    K = K_;
+    m0 = m0_;
+    n0 = n0_;
+  }
+  // round r of slab s into the stage at st
+  VM_DEV void round(uint32_t s, uint32_t st, int r) const {
+    if (r < 8) {
+      const uint32_t row = min(m0 + 32 * uint32_t(r) + ra, M - 1) - m0;
+      const uint32_t k = min(s * kFBK + 8 * ca, K - 8);
+      dma16(a, row * K * 2 + k * 2, st + wo + 4096 * r);
+    } else {
+      // the slab's rows from a scalar base, so the lane offset stays below 64 rows
+      const uint32_t k = min(s * kFBK + 8 * uint32_t(r - 8) + rb, K - 1) - s * kFBK;
+      const uint32_t n = min(n0 + 8 * cb, N - 8) - n0;
+      dma16(b + uint64_t(s) * kFBK * N * 2, k * N * 2 + n * 2, st + kFStageB + wo + 4096 * (r - 8));
+    }
+  }
+  // zero this lane's slots that hold k >= K of the last slab s (after the lane's
+  // transfers into st have landed, before the block barrier that publishes st)
+  VM_DEV void zero(uint32_t s, uint32_t st) const {
+    const uint32_t kv = K - s * kFBK;                    // valid k of the slab, a multiple of 8
+    typedef __attribute__((address_space(3))) v4u lds_v4u;
+    const uint32_t l = threadIdx.x & 63;
+    if (8 * ca >= kv) {
+#pragma unroll
+      for (int r = 0; r < 8; ++r) *(lds_v4u*)uintptr_t(st + wo + 4096 * r + 16 * l) = v4u_make(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int r = 0; r < 8; ++r)
+      if (8 * uint32_t(r) + rb >= kv)
+        *(lds_v4u*)uintptr_t(st + kFStageB + wo + 4096 * r + 16 * l) = v4u_make(0, 0, 0, 0);
+  }
+};
+
 // Tile index -> origin.  When the tile grid splits evenly over the 8 XCDs, tile t
 // (which the scheduler places on lane t, and the dispatcher on XCD t % 8) is
 // mapped so that each XCD owns a compact band of 4-row groups: its tiles share A
@@ -534,7 +593,7 @@ VM_DEV void fast_origin(const MmaDesc& D, uint32_t tile, uint32_t* g, uint32_t* 
 // tile, then the whole block writes full rows with 16-byte (f32) or 8-byte
 // (16-bit) stores, applying the epilogue on the way.  No call is made while the
 // accumulators are live.
-template <bool F32>
+template <bool F32, bool RAG>
 VM_DEV void store_fast(Args A, const MmaDesc& D, const f32x16 (&acc)[4][4], uint32_t g, uint32_t m0, uint32_t n0) {
   constexpr int LD = 256 + 4;
   float* st = lds_ptr<float>();
@@ -563,6 +622,9 @@ VM_DEV void store_fast(Args A, const MmaDesc& D, const f32x16 (&acc)[4][4], uint
       const uint32_t idx = it * kBlock + threadIdx.x;
       const uint32_t rs = idx >> 6, c = (idx & 63) * 4;
       const uint32_t row = (rs >> 6) * 128 + h * 64 + (rs & 63);
+      if constexpr (RAG) {
+        if (m0 + row >= D.M || n0 + c >= D.N) continue;   // N % 8 == 0: 4 columns all in or all out
+      }
       v4f x = *reinterpret_cast<const v4f*>(st + rs * LD + c);
       const uint32_t off = row * D.N + c;
       for (int k = 0; k < nm; ++k) {
@@ -588,7 +650,7 @@ VM_DEV void store_fast(Args A, const MmaDesc& D, const f32x16 (&acc)[4][4], uint
   }
 }
 
-template <bool BF16>
+template <bool BF16, bool RAG>
 VM_LEAF void mma_tile16_fast(Args A, const MmaDesc* Dp, uint32_t tile) {
   A = uargs(A);
   const MmaDesc D = load_desc(Dp);
@@ -606,9 +668,11 @@ VM_LEAF void mma_tile16_fast(Args A, const MmaDesc* Dp, uint32_t tile) {
   for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
-  const uint32_t nk = K / kFBK;
+  const uint32_t nk = RAG ? (K + kFBK - 1) / kFBK : K / kFBK;
   FastDma dm;
-  dm.init(K, N);
+  RaggedDma rd;
+  if constexpr (RAG) rd.init(a, b, D.M, N, K, m0, n0);
+  else dm.init(K, N);
   auto slab_a = [&](uint32_t s) { return a + uint64_t(s) * kFBK * 2; };
   auto slab_b = [&](uint32_t s) { return b + uint64_t(s) * kFBK * N * 2; };
   // Fragment addresses within a stage.  A, block i, k step kk: row wm 128 + 32 i +
@@ -647,13 +711,22 @@ VM_LEAF void mma_tile16_fast(Args A, const MmaDesc* Dp, uint32_t tile) {
   const uint32_t st0 = lds0, st1 = lds0 + kFStage;
   __syncthreads();                      // the previous user of the LDS is done
 #pragma unroll
-  for (int r = 0; r < 16; ++r) dm.round(slab_a(0), slab_b(0), K, N, st0, r);
+  for (int r = 0; r < 16; ++r) {
+    if constexpr (RAG) rd.round(0, st0, r);
+    else dm.round(slab_a(0), slab_b(0), K, N, st0, r);
+  }
   if (nk > 1) {
 #pragma unroll
-    for (int r = 0; r < 8; ++r) dm.round(slab_a(1), slab_b(1), K, N, st1, r);
+    for (int r = 0; r < 8; ++r) {
+      if constexpr (RAG) rd.round(1, st1, r);
+      else dm.round(slab_a(1), slab_b(1), K, N, st1, r);
+    }
     wait_vm8();                         // slab 0 landed; slab 1's A rounds may be in flight
   } else {
     wait_vm0();
+    if constexpr (RAG) {
+      if (K % kFBK) rd.zero(0, st0);
+    }
   }
   __syncthreads();
   frags(0, st0, 0);
@@ -680,7 +753,10 @@ VM_LEAF void mma_tile16_fast(Args A, const MmaDesc* Dp, uint32_t tile) {
       for (int r = 0; r < 16; ++r) {
         mfma_r(0, r);
         __builtin_amdgcn_sched_barrier(0);
-        if (r & 1) dm.round(a, bn, K, N, nxt, 8 + (r >> 1));
+        if (r & 1) {
+          if constexpr (RAG) rd.round(ks + 1, nxt, 8 + (r >> 1));
+          else dm.round(a, bn, K, N, nxt, 8 + (r >> 1));
+        }
         __builtin_amdgcn_sched_barrier(0);
       }
     } else {
@@ -696,6 +772,9 @@ VM_LEAF void mma_tile16_fast(Args A, const MmaDesc* Dp, uint32_t tile) {
     mfmas(0);
     __builtin_amdgcn_sched_barrier(0);
     wait_vm0();
+    if constexpr (RAG) {
+      if (ks + 2 == nk && (K % kFBK)) rd.zero(ks + 1, nxt);     // the last slab's k past K
+    }
     __syncthreads();
     frags(0, nxt, 0);
     __builtin_amdgcn_sched_barrier(0);
@@ -705,7 +784,10 @@ VM_LEAF void mma_tile16_fast(Args A, const MmaDesc* Dp, uint32_t tile) {
       for (int r = 0; r < 16; ++r) {
         mfma_r(1, r);
         __builtin_amdgcn_sched_barrier(0);
-        if (r & 1) dm.round(an, b, K, N, cur, r >> 1);
+        if (r & 1) {
+          if constexpr (RAG) rd.round(ks + 2, cur, r >> 1);
+          else dm.round(an, b, K, N, cur, r >> 1);
+        }
         __builtin_amdgcn_sched_barrier(0);
       }
     } else {
@@ -717,8 +799,8 @@ VM_LEAF void mma_tile16_fast(Args A, const MmaDesc* Dp, uint32_t tile) {
   for (; ks + 2 < nk; ++ks) slab(ks, std::true_type(), std::true_type());
   if (ks + 1 < nk) slab(ks++, std::false_type(), std::true_type());
   if (ks < nk) slab(ks, std::false_type(), std::false_type());
-  if (D.dt == DT_F32) store_fast<true>(A, D, acc, g, m0, n0);
-  else store_fast<false>(A, D, acc, g, m0, n0);
+  if (D.dt == DT_F32) store_fast<true, RAG>(A, D, acc, g, m0, n0);
+  else store_fast<false, RAG>(A, D, acc, g, m0, n0);
 }
 
 // ---------------------------------------------------------------------------------
@@ -923,8 +1005,8 @@ VM_LEAF void mma_tile32_fast(Args A, const MmaDesc* Dp, uint32_t tile) {
     if (ks + 1 < nk) st.store(lds + ((ks + 1) & 1) * kF32Buf);
     __syncthreads();
   }
-  if (D.dt == DT_F32) store_fast<true>(A, D, acc, g, m0, n0);
-  else store_fast<false>(A, D, acc, g, m0, n0);
+  if (D.dt == DT_F32) store_fast<true, false>(A, D, acc, g, m0, n0);
+  else store_fast<false, false>(A, D, acc, g, m0, n0);
 }
 
 // LDS bytes the matmul tile op needs at its largest tile.
@@ -966,6 +1048,11 @@ VM_DEV void mma_tiles(Args A, uint32_t ti, uint32_t lo, uint32_t hi) {
   const bool fast = D.S == 1 && h16 && T == 256 && !D.av && !D.bv && D.M % 256 == 0 && D.N % 256 == 0 && D.K % kFBK == 0 &&
                     D.N < (1u << 22) && ((uintptr_t(D.a) | uintptr_t(D.b)) & 15) == 0 &&
                     (D.dt == DT_F32 || D.dt == DT_BF16 || D.dt == DT_F16) && epi_inline_ok(A, D.epi);
+  // the same tile for ragged shapes: 16-byte rows (K, N multiples of 8), offsets
+  // within 32 bits (RaggedDma)
+  const bool fastr = !fast && D.S == 1 && h16 && T == 256 && !D.av && !D.bv && D.K >= 8 && D.K % 8 == 0 && D.N % 8 == 0 &&
+                     D.K < (1u << 22) && D.N < (1u << 22) && ((uintptr_t(D.a) | uintptr_t(D.b)) & 15) == 0 &&
+                     (D.dt == DT_F32 || D.dt == DT_BF16 || D.dt == DT_F16) && epi_inline_ok(A, D.epi);
   const bool fast32 = D.S == 1 && D.adt == DT_F32 && T == 256 && !D.av && !D.bv && D.M % 256 == 0 && D.N % 256 == 0 &&
                       D.K % kF32BK == 0 && D.N < (1u << 22) && ((uintptr_t(D.a) | uintptr_t(D.b)) & 15) == 0 &&
                       (D.dt == DT_F32 || D.dt == DT_BF16 || D.dt == DT_F16) && epi_inline_ok(A, D.epi);
@@ -980,8 +1067,11 @@ VM_DEV void mma_tiles(Args A, uint32_t ti, uint32_t lo, uint32_t hi) {
     if (fast32) {
       mma_tile32_fast(A, &D, tile);
     } else if (fast) {
-      if (bf) mma_tile16_fast<true>(A, &D, tile);
-      else mma_tile16_fast<false>(A, &D, tile);
+      if (bf) mma_tile16_fast<true, false>(A, &D, tile);
+      else mma_tile16_fast<false, false>(A, &D, tile);
+    } else if (fastr) {
+      if (bf) mma_tile16_fast<true, true>(A, &D, tile);
+      else mma_tile16_fast<false, true>(A, &D, tile);
     } else if (h16) {
       if (T == 256) { if (bf) mma_tile16<256, true>(A, &D, tile); else mma_tile16<256, false>(A, &D, tile); }
       else if (T == 128) { if (bf) mma_tile16<128, true>(A, &D, tile); else mma_tile16<128, false>(A, &D, tile); }

@@ -14,7 +14,7 @@ import numpy as np
 import pytest
 
 import vmprogs as P
-from gpu_util import as_f32, assert_product_elementwise, assert_rel, attention_abs_scale, blob_for, run_both, runtime
+from gpu_util import as_f32, assert_product_elementwise, assert_rel, attention_abs_scale, blob_for, run_both, run_gpu, runtime
 from oracle import vmref
 from pjrt_amd import graph as G
 from pjrt_amd import vmprogram as V
@@ -431,6 +431,47 @@ def test_dot_fast_path_exact(dt, Gb, M, K, N):
     g.output(g.dot(x, y, tile=256))
     got, _ = run_both(g.build(), [a, b], oracle=None)
     np.testing.assert_array_equal(got[0], np.matmul(a.astype(np.float64), b.astype(np.float64)))
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+@pytest.mark.parametrize("Gb,M,K,N", [(1, 300, 200, 264), (1, 256, 72, 512), (1, 512, 40, 256), (2, 130, 136, 520),
+                                      (1, 9, 8, 8), (1, 777, 1000, 1032)])
+def test_dot_fast_path_ragged_exact(dt, Gb, M, K, N):
+    """The 16-bit fast path on ragged shapes (256 x 256 tiles with M or N not a
+    multiple of 256, or K not a multiple of 64; K and N multiples of 8): edge rows
+    and columns read clamped addresses and are not stored, the last slab's k past
+    K are zeroed in LDS.  K = 40 and 8 are one short slab, 72 two slabs, 200 and
+    136 several with a tail, 1000 sixteen.  Integer-valued operands give the
+    exact product, twice in a row."""
+    rng = np.random.default_rng(77)
+    a = rng.integers(-3, 4, (Gb, M, K)).astype(np.float32)
+    b = rng.integers(-3, 4, (Gb, K, N)).astype(np.float32)
+    g = G.Graph()
+    x, y = g.input(a.shape, dt), g.input(b.shape, dt)
+    g.output(g.dot(x, y, tile=256))
+    blob, _ = blob_for(g.build())
+    print(f"[gpu] case: ragged fast path {dt} G={Gb} M={M} K={K} N={N}", file=sys.stderr, flush=True)
+    want = np.matmul(a.astype(np.float64), b.astype(np.float64))
+    for _ in range(2):
+        got = run_gpu(blob, [a, b])
+        np.testing.assert_array_equal(got[0], want)
+
+
+def test_dot_fast_path_ragged_epilogue():
+    """A ragged fast-path tile with a fused epilogue (affine, + residual, GELU) and
+    a bf16 output, against the oracle: the residual is read only inside the
+    output."""
+    rng = np.random.default_rng(78)
+    M, K, N = 300, 200, 264
+    a = rng.integers(-2, 3, (M, K)).astype(np.float32)
+    b = rng.integers(-2, 3, (K, N)).astype(np.float32)
+    res = (rng.standard_normal((M, N)) * 2).astype(np.float32)
+    g = G.Graph()
+    x, y, r = g.input(a.shape, "bf16"), g.input(b.shape, "bf16"), g.input(res.shape)
+    g.output(g.dot(x, y, out_dtype="bf16", tile=256, residual=r,
+                   epilogue=[(V.SUB_AFFINE, 0, 0.125, -0.5), (V.SUB_ADD, 1, 0.0, 0.0), (V.SUB_GELU, 0, 0.0, 0.0)]))
+    got, want = run_both(g.build(), [a, b, res], oracle="tensor")
+    assert_rel(as_f32(got[0], V.DT_BF16), as_f32(want[0], V.DT_BF16), BF16_ULP, 1e-6, "ragged fast epilogue")
 
 
 @pytest.mark.parametrize("in_dt,out_dt", [("bf16", "bf16"), ("f32", "f32"), ("f32", "bf16")])

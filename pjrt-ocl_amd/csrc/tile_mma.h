@@ -623,7 +623,7 @@ VM_DEV void store_fast(Args A, const MmaDesc& D, const f32x16 (&acc)[4][4], uint
       const uint32_t rs = idx >> 6, c = (idx & 63) * 4;
       const uint32_t row = (rs >> 6) * 128 + h * 64 + (rs & 63);
       if constexpr (RAG) {
-        if (m0 + row >= D.M || n0 + c >= D.N) continue;   // N % 8 == 0: 4 columns all in or all out
+        if (m0 + row >= D.M || n0 + c >= D.N) continue;   // N % 4 == 0: 4 columns all in or all out
       }
       v4f x = *reinterpret_cast<const v4f*>(st + rs * LD + c);
       const uint32_t off = row * D.N + c;
@@ -945,6 +945,27 @@ struct F32Stage {
 #pragma unroll
     for (int j = 0; j < 4; ++j) rb[j] = *(const VM_G v4f*)(b + (uint64_t(t / 64 + 4 * j) * N + (t % 64) * 4) * 4);
   }
+  // The same chunks of slab s for a ragged tile (K, N multiples of 4): rows past
+  // M re-read row M - 1 and columns past N the last 4 (computed, not stored); k
+  // past K re-read the last k and are zeroed in registers, in both operands.
+  // a = A[g, m0, 0], b = B[g, 0, n0].  The loads are not predicated, so none of
+  // them waits behind a branch.
+  VM_DEV void load_ragged(const gbyte* a, const gbyte* b, uint32_t s, uint32_t M, uint32_t K, uint32_t N, uint32_t m0,
+                          uint32_t n0) {
+    const uint32_t t = threadIdx.x, k0 = s * kF32BK;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t row = min(m0 + t / 4 + 64 * j, M - 1) - m0, k = k0 + (t % 4) * 4;
+      const v4f v = *(const VM_G v4f*)(a + (uint64_t(row) * K + min(k, K - 4)) * 4);
+      ra[j] = k < K ? v : v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t k = k0 + t / 64 + 4 * j, n = min(n0 + (t % 64) * 4, N - 4) - n0;
+      const v4f v = *(const VM_G v4f*)(b + (uint64_t(min(k, K - 1)) * N + n) * 4);
+      rb[j] = k < K ? v : v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+  }
   VM_DEV void store(float* s) const {
     const uint32_t t = threadIdx.x;
 #pragma unroll
@@ -954,6 +975,7 @@ struct F32Stage {
   }
 };
 
+template <bool RAG>
 VM_LEAF void mma_tile32_fast(Args A, const MmaDesc* Dp, uint32_t tile) {
   A = uargs(A);
   const MmaDesc D = load_desc(Dp);
@@ -970,9 +992,10 @@ VM_LEAF void mma_tile32_fast(Args A, const MmaDesc* Dp, uint32_t tile) {
   for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
-  const uint32_t nk = K / kF32BK;
+  const uint32_t nk = RAG ? (K + kF32BK - 1) / kF32BK : K / kF32BK;
   F32Stage st;
-  st.load(a, b, K, N);
+  if constexpr (RAG) st.load_ragged(a, b, 0, D.M, K, N, m0, n0);
+  else st.load(a, b, K, N);
   __syncthreads();                      // the previous user of the LDS is done
   st.store(lds);
   __syncthreads();
@@ -980,7 +1003,10 @@ VM_LEAF void mma_tile32_fast(Args A, const MmaDesc* Dp, uint32_t tile) {
   const uint32_t fb = kF32A + (lane >> 5) * 8 * kF32LdB + wn * 128 + (lane & 31);
   for (uint32_t ks = 0; ks < nk; ++ks) {
     const float* cur = lds + (ks & 1) * kF32Buf;
-    if (ks + 1 < nk) st.load(a + uint64_t(ks + 1) * kF32BK * 4, b + uint64_t(ks + 1) * kF32BK * N * 4, K, N);
+    if (ks + 1 < nk) {
+      if constexpr (RAG) st.load_ragged(a, b, ks + 1, D.M, K, N, m0, n0);
+      else st.load(a + uint64_t(ks + 1) * kF32BK * 4, b + uint64_t(ks + 1) * kF32BK * N * 4, K, N);
+    }
     float bfr[2][4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) bfr[0][j] = cur[fb + j * 32];
@@ -1005,8 +1031,8 @@ VM_LEAF void mma_tile32_fast(Args A, const MmaDesc* Dp, uint32_t tile) {
     if (ks + 1 < nk) st.store(lds + ((ks + 1) & 1) * kF32Buf);
     __syncthreads();
   }
-  if (D.dt == DT_F32) store_fast<true, false>(A, D, acc, g, m0, n0);
-  else store_fast<false, false>(A, D, acc, g, m0, n0);
+  if (D.dt == DT_F32) store_fast<true, RAG>(A, D, acc, g, m0, n0);
+  else store_fast<false, RAG>(A, D, acc, g, m0, n0);
 }
 
 // LDS bytes the matmul tile op needs at its largest tile.
@@ -1056,6 +1082,9 @@ VM_DEV void mma_tiles(Args A, uint32_t ti, uint32_t lo, uint32_t hi) {
   const bool fast32 = D.S == 1 && D.adt == DT_F32 && T == 256 && !D.av && !D.bv && D.M % 256 == 0 && D.N % 256 == 0 &&
                       D.K % kF32BK == 0 && D.N < (1u << 22) && ((uintptr_t(D.a) | uintptr_t(D.b)) & 15) == 0 &&
                       (D.dt == DT_F32 || D.dt == DT_BF16 || D.dt == DT_F16) && epi_inline_ok(A, D.epi);
+  const bool fast32r = !fast32 && D.S == 1 && D.adt == DT_F32 && T == 256 && !D.av && !D.bv && D.K >= 4 &&
+                       D.K % 4 == 0 && D.N % 4 == 0 && D.N < (1u << 22) && ((uintptr_t(D.a) | uintptr_t(D.b)) & 15) == 0 &&
+                       (D.dt == DT_F32 || D.dt == DT_BF16 || D.dt == DT_F16) && epi_inline_ok(A, D.epi);
   for (uint32_t ts = lo; ts < hi; ++ts) {
     uint32_t tile = ts;
     if (D.S > 1) {                      // split ts % S of output tile ts / S
@@ -1065,7 +1094,9 @@ VM_DEV void mma_tiles(Args A, uint32_t ti, uint32_t lo, uint32_t hi) {
       D.k1 = min(D.k0 + ksh, D.K);
     }
     if (fast32) {
-      mma_tile32_fast(A, &D, tile);
+      mma_tile32_fast<false>(A, &D, tile);
+    } else if (fast32r) {
+      mma_tile32_fast<true>(A, &D, tile);
     } else if (fast) {
       if (bf) mma_tile16_fast<true, false>(A, &D, tile);
       else mma_tile16_fast<false, false>(A, &D, tile);

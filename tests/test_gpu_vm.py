@@ -433,16 +433,17 @@ def test_dot_fast_path_exact(dt, Gb, M, K, N):
     np.testing.assert_array_equal(got[0], np.matmul(a.astype(np.float64), b.astype(np.float64)))
 
 
-@pytest.mark.parametrize("dt", ["bf16", "f16"])
+@pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
 @pytest.mark.parametrize("Gb,M,K,N", [(1, 300, 200, 264), (1, 256, 72, 512), (1, 512, 40, 256), (2, 130, 136, 520),
-                                      (1, 9, 8, 8), (1, 777, 1000, 1032)])
+                                      (1, 9, 8, 8), (1, 777, 1000, 1032), (1, 100, 36, 132)])
 def test_dot_fast_path_ragged_exact(dt, Gb, M, K, N):
-    """The 16-bit fast path on ragged shapes (256 x 256 tiles with M or N not a
-    multiple of 256, or K not a multiple of 64; K and N multiples of 8): edge rows
-    and columns read clamped addresses and are not stored, the last slab's k past
-    K are zeroed in LDS.  K = 40 and 8 are one short slab, 72 two slabs, 200 and
-    136 several with a tail, 1000 sixteen.  Integer-valued operands give the
-    exact product, twice in a row."""
+    """The fast paths on ragged shapes (256 x 256 tiles with M or N not a multiple
+    of 256, or K not a multiple of the slab; 16-bit with K and N multiples of 8,
+    f32 with multiples of 4): edge rows and columns read clamped addresses and are
+    not stored, the k past K are zeroed (in LDS for 16-bit, in registers for f32).
+    K = 40 and 8 are one short 16-bit slab, 72 two slabs, 200 and 136 several with
+    a tail, 1000 sixteen; 100 x 36 x 132 takes the f32 ragged tile and the 16-bit
+    general one.  Integer-valued operands give the exact product, twice in a row."""
     rng = np.random.default_rng(77)
     a = rng.integers(-3, 4, (Gb, M, K)).astype(np.float32)
     b = rng.integers(-3, 4, (Gb, K, N)).astype(np.float32)

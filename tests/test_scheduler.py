@@ -161,6 +161,28 @@ def test_mma_autotile_picks_parallel_tile():
     assert (sched.tasks[0].p3 >> 24) & 0xF == V.MMA_TILE_CODES[64]
 
 
+def test_mma_autotile_prefers_fast_16bit_tile():
+    """16-bit matmuls the 256-wide fast tile takes keep 256 down to an eighth of
+    the lanes (36 tiles of 256 for 1536^3 on 256 lanes); f32, views, K or N not a
+    multiple of 8, and too few tiles fall back to the count rule."""
+    def tile(M, K, N, dt, view=False):
+        g = G.Graph()
+        a = g.input((M, K), dt)
+        if view:
+            b = g.transpose_view(g.input((N, K), dt), (1, 0))
+        else:
+            b = g.input((K, N), dt)
+        g.output(g.dot(a, b))
+        t = S.schedule_program(g.build(), S.DeviceConfig(nlanes=256, mma_t=128)).tasks[0]
+        return V.MMA_CODE_TILE[(t.p3 >> 24) & 0xF]
+    assert tile(1536, 1536, 1536, "bf16") == 256
+    assert tile(3000, 3000, 3000, "f16") == 256
+    assert tile(1536, 1536, 1536, "f32") == 64          # 6 x 6 tiles of 256, 144 of 128: the count rule
+    assert tile(1024, 1024, 1024, "bf16") == 64         # 16 tiles of 256: too few
+    assert tile(1536, 1536, 1532, "bf16") != 256        # N not a multiple of 8
+    assert tile(1536, 1536, 1536, "bf16", view=True) != 256
+
+
 # --- K-split matmuls (extension) -----------------------------------------------------
 
 def test_mma_split_k_choice():

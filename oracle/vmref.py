@@ -984,13 +984,16 @@ class TaskRunner:
         K = (K[_view_index(aux, kv, H * hd * C)] if kv else K[:H * hd * C]).reshape(H, hd, C)
         Vv = (Vv[_view_index(aux, vv, H * C * hd)] if vv else Vv[:H * C * hd]).reshape(H, C, hd)
         out = self.m.load_f(t.dst, t.dt)[:H * T * hd].reshape(H, T, hd).copy()
-        tiles = range(lo, min(hi, H * T))
-        heads = sorted({tile // T for tile in tiles})
+        # tile = head * Tp + row, each head's rows padded to Tp = whole 256-row
+        # blocks (tiles past T are empty)
+        Tp = -(-T // 256) * 256
+        tiles = [tile for tile in range(lo, min(hi, H * Tp)) if tile % Tp < T]
+        heads = sorted({tile // Tp for tile in tiles})
         for g in heads:
             O = attention(Q[g:g + 1], K[g:g + 1], Vv[g:g + 1], scale, causal)[0]
             for tile in tiles:
-                if tile // T == g:
-                    out[g, tile % T] = O[tile % T]
+                if tile // Tp == g:
+                    out[g, tile % Tp] = O[tile % Tp]
         self.m.store_f(t.dst, slice(0, H * T * hd), out.reshape(-1), t.dt)
 
     # 21: decode-step attention (extension): tile = head * S + split, p4 = H | S << 16;
@@ -1188,7 +1191,7 @@ def _whole_tiles(t: Task, ew_ts: int, mma_t: int) -> int:
     if t.top == 19:
         return max(1, p[0]) * max(1, p[3])
     if t.top == 14:
-        return max(1, p[1] * p[2])
+        return max(1, p[1] * (-(-p[2] // 256) * 256))        # each head's rows padded to 256-row blocks
     if t.top == 20:
         return max(1, p[3]) * -(-p[1] // p[4])
     if t.top == 21:

@@ -2,7 +2,8 @@
 // with f32 statistics (reference semantics: ops/attention.cl:49-159,
 // python/pjrt_ocl/ops/attention.py:53-64).  Task: a = Q, b = K, p0 = V,
 // p1 = H, p2 = T, p3 = aux descriptor {H, T, C, hd, scale bits, causal, qv, kv, vv}.
-// Tiles are query rows (H*T of them); causal masks key c > m + (C - T).
+// Tiles are query rows, each head's padded to whole 256-row blocks (H * Tp tiles,
+// Tp = T rounded up to 256; tiles past T are empty); causal masks key c > m + (C - T).
 //
 // Matrix-core path (bf16/f16, hd = 64 or 128, scale > 0, K read through the usual
 // [H,hd,C] transpose view of a [H,C,hd] buffer): a lane takes 256 query rows, 64
@@ -424,10 +425,13 @@ VM_TILE void attn_rows_generic(Args A, uint32_t ti, uint32_t lo, uint32_t hi) {
   const gbyte* Vb = resolve(A, t.p[0]);
   gbyte* Ob = resolve(A, t.dst);
   const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  hi = min(hi, H * T);
+  // tile = head * Tp + row, each head's rows padded to whole 256-row blocks
+  const uint32_t Tp = (T + kAttnRows - 1) / kAttnRows * kAttnRows;
+  hi = min(hi, H * Tp);
   constexpr int kMaxD = 4;               // hd <= 256
   for (uint32_t tile = lo + wave; tile < hi; tile += kWaves) {
-    const uint32_t h = tile / T, m = tile % T;
+    const uint32_t h = tile / Tp, m = tile % Tp;
+    if (m >= T) continue;                // padding past the head's rows
     const int32_t qlim = int32_t(m) + int32_t(C) - int32_t(T);
     float mrun = -INFINITY, lrun = 0.0f;
     float o[kMaxD] = {0.f, 0.f, 0.f, 0.f};
@@ -485,20 +489,23 @@ VM_DEV bool is_kt_view(const VM_K int32_t* aux, uint32_t kv, uint32_t H, uint32_
 }
 
 // The lane's query blocks: per head, the virtual 256-row blocks intersecting
-// [lo, hi), each mapped to its real block (zig-zag when causal and every block is
-// whole, since it maps virtual onto real blocks).  One call per lane, so the
-// register save / restore of the call is paid once.
+// [lo, hi), each mapped to its real block (zig-zag when causal, so that chunks of
+// equally many blocks cost about the same).  A head's tiles are its rows padded
+// to whole blocks (Tp rows): the scheduler cuts chunks on block boundaries, so no
+// block is split between lanes, and the rows of the last real block past T are
+// computed and not stored.  One call per lane, so the register save / restore of
+// the call is paid once.
 template <int HD, bool BF16>
 VM_LEAF void attn_fast(Args A, uint32_t ti, uint32_t lo, uint32_t hi) {
   A = uargs(A);
   const VM_K Task& t = task_of(A, ti);
   const AttnDesc P = attn_desc(A, t);
   const uint32_t T = P.T;
-  hi = min(hi, P.H * T);
-  const uint32_t nb = (T + kAttnRows - 1) / kAttnRows;
-  const bool zig = P.causal && T % kAttnRows == 0;
-  for (uint32_t h = lo / T; h * T < hi; ++h) {
-    const uint32_t a = max(lo, h * T) - h * T, b = min(hi - h * T, T);     // virtual rows [a, b)
+  const uint32_t nb = (T + kAttnRows - 1) / kAttnRows, Tp = nb * kAttnRows;
+  hi = min(hi, P.H * Tp);
+  const bool zig = P.causal;
+  for (uint32_t h = lo / Tp; h * Tp < hi; ++h) {
+    const uint32_t a = max(lo, h * Tp) - h * Tp, b = min(hi - h * Tp, Tp);     // virtual rows [a, b)
     for (uint32_t vb = a / kAttnRows; vb * kAttnRows < b; ++vb) {
       const uint32_t rb = zig ? ((vb & 1) ? nb - 1 - (vb >> 1) : (vb >> 1)) : vb;
       const uint32_t vrow0 = vb * kAttnRows;

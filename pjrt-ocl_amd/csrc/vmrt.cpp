@@ -393,7 +393,7 @@ struct Checker {
       case TOP_RED_SEG: case TOP_SOFTMAX_SEG: case TOP_LAYERNORM_SEG:
         return std::max<uint64_t>(1, t.p[0]);
       case TOP_ARGMAX_SEG: return std::max<uint64_t>(1, uint64_t(t.p[0]) * std::max<uint32_t>(1, t.p[3]));
-      case TOP_FLASH_ATTN: return std::max<uint64_t>(1, uint64_t(t.p[1]) * t.p[2]);
+      case TOP_FLASH_ATTN: return std::max<uint64_t>(1, uint64_t(t.p[1]) * (cdiv(t.p[2], 256) * 256));   // rows padded to 256-row blocks
       case TOP_GEMV: return t.p[4] ? std::max<uint64_t>(1, t.p[3]) * cdiv(t.p[1], t.p[4]) : 0;
       case TOP_DECODE_ATTN: return std::max<uint64_t>(1, uint64_t(t.p[4] & 0xFFFF) * std::max<uint32_t>(1, t.p[4] >> 16));
       default: return 0;

@@ -189,12 +189,22 @@ def n_tiles(task: V.Task, cfg: DeviceConfig) -> int:
     if top == V.TOP_ARGMAX_SEG:
         return max(1, task.p0) * max(1, task.p3)
     if top == V.TOP_FLASH_ATTN:
-        return max(1, task.p1 * task.p2)
+        return max(1, task.p1 * attn_rows_padded(task.p2))
     if top == V.TOP_GEMV:
         return max(1, task.p3) * -(-task.p1 // task.p4)
     if top == V.TOP_DECODE_ATTN:
         return max(1, (task.p4 & 0xFFFF) * max(1, task.p4 >> 16))
     raise ScheduleError(f"n_tiles: unknown tile_op {top}")
+
+
+# Flash attention tiles: one per query row, each head's rows padded to whole
+# 256-row blocks (the matrix-core kernel's block), so that chunks of whole blocks
+# never split one between lanes; tiles past a head's T are empty.
+ATTN_BLOCK_ROWS = 256
+
+
+def attn_rows_padded(T: int) -> int:
+    return -(-T // ATTN_BLOCK_ROWS) * ATTN_BLOCK_ROWS
 
 
 # --- skinny matmuls (TOP_GEMV) ------------------------------------------------------
@@ -823,11 +833,9 @@ def _tile_quantum(task: V.Task, cfg: DeviceConfig, prog: V.VMProgram) -> int:
     """Preferred chunk granularity in tiles (chunk boundaries on multiples of
     it keep the kernel's multi-row blocks whole)."""
     if task.tile_op == V.TOP_FLASH_ATTN:
-        # the matrix-core kernel works on 256-row blocks of one head
-        T = task.p2
-        if T % 256 == 0:
-            return 256
-        return T if T < 256 else 64
+        # the matrix-core kernel works on 256-row blocks of one head, and each
+        # head's tiles are padded to whole blocks (attn_rows_padded)
+        return ATTN_BLOCK_ROWS
     return 1
 
 

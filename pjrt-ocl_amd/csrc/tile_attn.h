@@ -5,8 +5,9 @@
 // Tiles are query rows, each head's padded to whole 256-row blocks (H * Tp tiles,
 // Tp = T rounded up to 256; tiles past T are empty); causal masks key c > m + (C - T).
 //
-// Matrix-core path (bf16/f16, hd = 64 or 128, scale > 0, K read through the usual
-// [H,hd,C] transpose view of a [H,C,hd] buffer): a lane takes 256 query rows, 64
+// Matrix-core path (bf16/f16, hd = 64 or 128, or any other multiple of 8 up to
+// 128 run as the next of the two on zero-padded rows, scale > 0, K read through
+// the usual [H,hd,C] transpose view of a [H,C,hd] buffer): a lane takes 256 query rows, 64
 // per wave as two 32-row sub-tiles, and streams K/V in 64-key blocks that go
 // from global memory straight into LDS (global_load_lds_dwordx4; double-buffered,
 // one barrier per block).  Per sub-tile each wave computes
@@ -119,8 +120,13 @@ VM_DEV uint32_t pack_h2(float a, float b) {
 
 // One 256-row query block of head h against keys [0, kend).  Real rows row0 + i;
 // the caller's span owns virtual rows [vlo, vhi) of the virtual block starting at
-// vrow0 (the zig-zag order maps virtual block -> real block).
-template <int HD, bool BF16>
+// vrow0 (the zig-zag order maps virtual block -> real block).  With PAD the
+// operands' rows hold P.hd < HD elements (a multiple of 8) and the block computes
+// as if each row were zero-padded to HD: Q's missing chunks are zeros in
+// registers, the LDS slots of K and V chunks past P.hd are zeroed once per sweep
+// by the lanes that own them (which skip those transfers), and O's columns past
+// P.hd are not stored.
+template <int HD, bool BF16, bool PAD>
 VM_DEV void attn_block_mfma(Args A, uint32_t ti, uint32_t h, uint32_t row0, uint32_t vrow0, uint32_t vlo,
                             uint32_t vhi) {
   const VM_K Task& t = task_of(A, ti);
@@ -132,13 +138,14 @@ VM_DEV void attn_block_mfma(Args A, uint32_t ti, uint32_t h, uint32_t row0, uint
   vhi = uni(vhi);
   typedef AttnLds<HD> L;
   const uint32_t T = P.T, C = P.C, dt = (t.tile_op >> 8) & 0xFF;
+  const uint32_t hd = PAD ? uni(P.hd) : uint32_t(HD);     // elements per stored row
   constexpr int KS = HD / 16;            // MFMA steps over hd for S
   constexpr int DB = HD / 32;            // 32-row d blocks of O^T
   const uint32_t lane = threadIdx.x & 63, wave = uni(threadIdx.x >> 6), g = lane >> 5;
   const uint32_t qw0 = row0 + 64 * wave;                    // this wave's first row
-  const VM_G uint16_t* Q = gcast<uint16_t>(resolve(A, t.a)) + uint64_t(h) * T * HD;
-  const VM_G uint16_t* K = gcast<uint16_t>(resolve(A, t.b)) + uint64_t(h) * C * HD;
-  const VM_G uint16_t* V = gcast<uint16_t>(resolve(A, t.p[0])) + uint64_t(h) * C * HD;
+  const VM_G uint16_t* Q = gcast<uint16_t>(resolve(A, t.a)) + uint64_t(h) * T * hd;
+  const VM_G uint16_t* K = gcast<uint16_t>(resolve(A, t.b)) + uint64_t(h) * C * hd;
+  const VM_G uint16_t* V = gcast<uint16_t>(resolve(A, t.p[0])) + uint64_t(h) * C * hd;
   gbyte* Ob = resolve(A, t.dst);
 
   // Q^T fragments (B operand) of both sub-tiles: column = query, 8 consecutive hd
@@ -148,7 +155,9 @@ VM_DEV void attn_block_mfma(Args A, uint32_t ti, uint32_t h, uint32_t row0, uint
   for (int u = 0; u < 2; ++u) {
     const uint32_t qr = min(qw0 + 32 * u + (lane & 31), T - 1);
 #pragma unroll
-    for (int s = 0; s < KS; ++s) qf[u][s] = *(const VM_G u16x8*)(Q + uint64_t(qr) * HD + s * 16 + 8 * g);
+    for (int s = 0; s < KS; ++s)
+      qf[u][s] = (!PAD || 16 * s + 8 * g < hd) ? *(const VM_G u16x8*)(Q + uint64_t(qr) * hd + s * 16 + 8 * g)
+                                                : u16x8{};
   }
   f32x16 o[2][DB];
 #pragma unroll
@@ -184,18 +193,35 @@ VM_DEV void attn_block_mfma(Args A, uint32_t ti, uint32_t h, uint32_t row0, uint
   const uint32_t dslot = (16 * lane) % L::kRow / 16;
   const uint32_t dk = (dslot ^ kswz<HD>(dr)) * 16, dv = (dslot ^ vswz<HD>(dr)) * 16;
   constexpr uint32_t kRowsPerRound = 4096 / L::kRow;
+  const uint32_t grow = 2 * hd;                                      // global bytes per key row
+  // the swizzles repeat every kRowsPerRound rows, so a lane fetches the same
+  // chunk in every round: with PAD it lies inside the row always or never
+  const bool kon = !PAD || dk < grow, von = !PAD || dv < grow;
   const gbyte* Kg = (const gbyte*)K;
   const gbyte* Vg = (const gbyte*)V;
   auto dma_block = [&](uint32_t st, uint32_t kb) {
 #pragma unroll
     for (uint32_t j = 0; j < L::kRounds; ++j) {
       const uint32_t key = min(kb * kAttnKeys + j * kRowsPerRound + dr, C - 1);
-      dma16(Kg, key * L::kRow + dk, st + 4096 * j + wo);
+      if (kon) dma16(Kg, key * grow + dk, st + 4096 * j + wo);
     }
 #pragma unroll
     for (uint32_t j = 0; j < L::kRounds; ++j) {
       const uint32_t key = min(kb * kAttnKeys + j * kRowsPerRound + dr, C - 1);
-      dma16(Vg, key * L::kRow + dv, st + L::kKBytes + 4096 * j + wo);
+      if (von) dma16(Vg, key * grow + dv, st + L::kKBytes + 4096 * j + wo);
+    }
+  };
+  // PAD: zeros in the K and V slots of both stages that no transfer fills
+  auto zero_pad = [&]() {
+    if constexpr (PAD) {
+#pragma unroll
+      for (uint32_t j = 0; j < L::kRounds; ++j)
+#pragma unroll
+        for (uint32_t sg = 0; sg < 2; ++sg) {
+          const uint32_t off = sg * L::kStage + 4096 * j + wo + 16 * lane;
+          if (!kon) *(__attribute__((address_space(3))) v4u*)(LB + off) = v4u_make(0, 0, 0, 0);
+          if (!von) *(__attribute__((address_space(3))) v4u*)(LB + off + L::kKBytes) = v4u_make(0, 0, 0, 0);
+        }
     }
   };
   auto zero_tail = [&](uint32_t st, uint32_t kb) {
@@ -350,6 +376,7 @@ VM_DEV void attn_block_mfma(Args A, uint32_t ti, uint32_t h, uint32_t row0, uint
   if (P.causal) nfull = min(nfull, wq_lo >= kAttnKeys - 1 ? uint32_t(wq_lo - (kAttnKeys - 1)) / kAttnKeys + 1 : 0u);
   auto sweep = [&](auto fn) {
     __syncthreads();                    // LDS free from the previous user
+    zero_pad();
     if (nblk) dma_block(st0, 0);
     // every global load so far (the Q fragments too) has landed: said explicitly
     // so the compiler's wait counting does not carry the Q loads into the loop
@@ -396,13 +423,14 @@ VM_DEV void attn_block_mfma(Args A, uint32_t ti, uint32_t h, uint32_t row0, uint
     const float l = l_part[u] + xor32(l_part[u]);
     if (q < T && vrow0 + ql >= vlo && vrow0 + ql < vhi) {
       const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-      const uint64_t obase = (uint64_t(h) * T + q) * HD;
+      const uint64_t obase = (uint64_t(h) * T + q) * hd;
 #pragma unroll
       for (int db = 0; db < DB; ++db) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const uint32_t d = db * 32 + 8 * j + 4 * g;
-          st4(Ob, dt, obase + d,
+          if (!PAD || d < hd)
+            st4(Ob, dt, obase + d,
               v4f_make(o[u][db][4 * j] * inv, o[u][db][4 * j + 1] * inv, o[u][db][4 * j + 2] * inv,
                        o[u][db][4 * j + 3] * inv));
         }
@@ -495,7 +523,7 @@ VM_DEV bool is_kt_view(const VM_K int32_t* aux, uint32_t kv, uint32_t H, uint32_
 // block is split between lanes, and the rows of the last real block past T are
 // computed and not stored.  One call per lane, so the register save / restore of
 // the call is paid once.
-template <int HD, bool BF16>
+template <int HD, bool BF16, bool PAD>
 VM_LEAF void attn_fast(Args A, uint32_t ti, uint32_t lo, uint32_t hi) {
   A = uargs(A);
   const VM_K Task& t = task_of(A, ti);
@@ -509,7 +537,7 @@ VM_LEAF void attn_fast(Args A, uint32_t ti, uint32_t lo, uint32_t hi) {
     for (uint32_t vb = a / kAttnRows; vb * kAttnRows < b; ++vb) {
       const uint32_t rb = zig ? ((vb & 1) ? nb - 1 - (vb >> 1) : (vb >> 1)) : vb;
       const uint32_t vrow0 = vb * kAttnRows;
-      attn_block_mfma<HD, BF16>(A, ti, h, rb * kAttnRows, vrow0, max(a, vrow0), min(b, vrow0 + kAttnRows));
+      attn_block_mfma<HD, BF16, PAD>(A, ti, h, rb * kAttnRows, vrow0, max(a, vrow0), min(b, vrow0 + kAttnRows));
     }
   }
 }
@@ -519,16 +547,22 @@ VM_DEV void flash_attn_tiles(Args A, uint32_t ti, uint32_t lo, uint32_t hi) {
   const VM_K Task& t = task_of(A, ti);
   const AttnDesc P = attn_desc(A, t);
   const uint32_t adt = (t.tile_op >> 16) & 0xFF, dt = (t.tile_op >> 8) & 0xFF;
-  const bool fast = (adt == DT_BF16 || adt == DT_F16) && (P.hd == 64 || P.hd == 128) && !P.qv && !P.vv &&
-                    is_kt_view(aux_of(A), P.kv, P.H, P.C, P.hd) && P.scale > 0.0f &&
+  // head sizes other than 64 and 128 (multiples of 8 up to 128) run the next
+  // larger kernel on zero-padded rows
+  const bool fast = (adt == DT_BF16 || adt == DT_F16) && P.hd % 8 == 0 && P.hd >= 8 && P.hd <= 128 && !P.qv &&
+                    !P.vv && is_kt_view(aux_of(A), P.kv, P.H, P.C, P.hd) && P.scale > 0.0f &&
                     (dt == DT_F32 || dt == DT_BF16 || dt == DT_F16);
   if (!fast) return attn_rows_generic(A, ti, lo, hi);
   if (adt == DT_BF16) {
-    if (P.hd == 128) attn_fast<128, true>(A, ti, lo, hi);
-    else attn_fast<64, true>(A, ti, lo, hi);
+    if (P.hd == 128) attn_fast<128, true, false>(A, ti, lo, hi);
+    else if (P.hd == 64) attn_fast<64, true, false>(A, ti, lo, hi);
+    else if (P.hd > 64) attn_fast<128, true, true>(A, ti, lo, hi);
+    else attn_fast<64, true, true>(A, ti, lo, hi);
   } else {
-    if (P.hd == 128) attn_fast<128, false>(A, ti, lo, hi);
-    else attn_fast<64, false>(A, ti, lo, hi);
+    if (P.hd == 128) attn_fast<128, false, false>(A, ti, lo, hi);
+    else if (P.hd == 64) attn_fast<64, false, false>(A, ti, lo, hi);
+    else if (P.hd > 64) attn_fast<128, false, true>(A, ti, lo, hi);
+    else attn_fast<64, false, true>(A, ti, lo, hi);
   }
 }
 

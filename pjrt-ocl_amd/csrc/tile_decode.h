@@ -30,9 +30,10 @@
 // output; f32 arithmetic.
 //
 // krow: the key cache holds rows [H, C, hd] (the layout a JAX decoder keeps,
-// tools/bench_decode.py:44-52) instead of K^T; hd is a power of two.  The score
-// pass then reads keys the way the P.V pass reads values: hd / 8 threads per
-// key, each a 16-byte run of channels, summed by lane shuffles.
+// tools/bench_decode.py:44-52) instead of K^T.  The score pass then reads keys
+// the way the P.V pass reads values: hd / 8 threads per key, each a 16-byte run
+// of channels, summed by lane shuffles over the key's group of threads, which is
+// rounded up to a power of two (the group's extra threads add 0).
 // masked: the decoder stored k and v at column pos before attending over the
 // keys up to pos (dynamic_update_slice, then a key <= pos mask): pos is clamped
 // to [0, C - 1] as the store's start is, and a negative pos leaves every key
@@ -97,22 +98,28 @@ VM_DEV void decode_attn_split(Args A, uint32_t ti, uint32_t tile) {
   const uint32_t oc = nk ? min(o, nk / 8 - 1) : 0;
   const uint32_t kcol = min(k0 + 8 * oc, C - 8);
   const uint32_t dpt = (hd + 31) / 32;                        // <= kDecKU
-  // P.V (and the key rows of krow): thread (cg = tid % cgs, rg = tid / cgs)
+  // P.V (and the key rows of krow): thread (cg = tid % cgp, rg = tid / cgp)
   // holds channels [8 cg, +8) of rows rg, rg + rpp, ...; rows past nk re-read
-  // the last row (not accumulated)
-  const uint32_t cgs = hd / 8, rpp = kBlock / cgs;
-  const uint32_t cg = tid % cgs, rg = min(tid / cgs, rpp - 1);
+  // the last row (not accumulated).  cgs = hd / 8 threads cover a row; krow
+  // rounds the group up to cgp, a power of two (dividing 64: hd <= 256), whose
+  // threads past cgs re-read the row's last channels and add nothing.
+  const uint32_t cgs = hd / 8;
+  const uint32_t cgp = krow && cgs > 1 ? 1u << (32 - __builtin_clz(cgs - 1)) : cgs;
+  const uint32_t rpp = kBlock / cgp;
+  const uint32_t cg = tid % cgp, rg = min(tid / cgp, rpp - 1);
+  const bool cg_on = cg < cgs;
+  const uint32_t cg8 = min(cg, cgs - 1) * 8;               // channel offset read
   const uint32_t vpt = (per + rpp - 1) / rpp;                 // <= kDecKU
   Raw kr[kDecKU];
   float qd[kDecKU];
   Raw qrow;
   if (krow) {
-    qrow = gemv_ld<DT>(q, cg * 8);
+    qrow = gemv_ld<DT>(q, cg8);
 #pragma unroll
     for (uint32_t u = 0; u < kDecKU; ++u)
       if (u < vpt) {
         const uint32_t r = nk ? min(rg + rpp * u, nk - 1) : 0;
-        kr[u] = gemv_ld<DT>(kt, uint64_t(min(k0 + r, C - 1)) * hd + cg * 8);
+        kr[u] = gemv_ld<DT>(kt, uint64_t(min(k0 + r, C - 1)) * hd + cg8);
       }
   } else {
 #pragma unroll
@@ -128,9 +135,9 @@ VM_DEV void decode_attn_split(Args A, uint32_t ti, uint32_t tile) {
   for (uint32_t u = 0; u < kDecKU; ++u)
     if (u < vpt) {
       const uint32_t r = nk ? min(rg + rpp * u, nk - 1) : 0;
-      vr[u] = gemv_ld<DT>(vc, (uint64_t(min(k0 + r, C - 1)) * hd + cg * 8));
+      vr[u] = gemv_ld<DT>(vc, (uint64_t(min(k0 + r, C - 1)) * hd + cg8));
     }
-  const Raw vnew = gemv_ld<DT>(vn, cg * 8);
+  const Raw vnew = gemv_ld<DT>(vn, cg8);
   float qn = 0.0f;
   if (tid < hd) qn = load_f(q, DT, tid) * load_f(kn, DT, tid);
 
@@ -157,9 +164,9 @@ VM_DEV void decode_attn_split(Args A, uint32_t ti, uint32_t tile) {
         float sdot = 0.0f;
 #pragma unroll
         for (int j = 0; j < 8; ++j) sdot = fmaf(qv[j], w[j], sdot);
-        // the cgs threads of a key are adjacent lanes of one wave (cgs is a
-        // power of two dividing 64)
-        for (uint32_t msk = cgs >> 1; msk >= 1; msk >>= 1) sdot += __shfl_xor(sdot, msk, 64);
+        if (!cg_on) sdot = 0.0f;
+        // the cgp threads of a key are adjacent lanes of one wave
+        for (uint32_t msk = cgp >> 1; msk >= 1; msk >>= 1) sdot += __shfl_xor(sdot, msk, 64);
         const uint32_t r = rg + rpp * u;
         if (cg == 0 && r < nk) sc[r] = sdot * scale;
       }
@@ -222,7 +229,7 @@ VM_DEV void decode_attn_split(Args A, uint32_t ti, uint32_t tile) {
   float ov[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) ov[j] = 0.0f;
-  if (tid / cgs < rpp) {
+  if (tid / cgp < rpp && cg_on) {
 #pragma unroll
     for (uint32_t u = 0; u < kDecKU; ++u) {
       const uint32_t r = rg + rpp * u;

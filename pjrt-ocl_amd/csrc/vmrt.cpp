@@ -626,12 +626,10 @@ struct Checker {
       }
       case TOP_DECODE_ATTN: {
         const uint64_t H = t.p[4] & 0xFFFF, S = t.p[4] >> 16, hd = t.p[5] & 0xFFFF, C = t.p[6];
-        const bool krow = (t.p[5] >> 16) & 1;
         if (dt != adt || (adt != DT_F32 && adt != DT_BF16 && adt != DT_F16)) return fail(ti, "decode attention dtype");
         if (H < 1 || hd < 8 || hd > 256 || hd % 8 || C < 8 || C % 8 || S > kDecMaxSplits)
           return fail(ti, "decode attention shape");
-        if ((t.p[5] >> 18) != 0 || (krow && (hd & (hd - 1))))
-          return fail(ti, "decode attention flags (key rows need a power-of-two hd)");
+        if ((t.p[5] >> 18) != 0) return fail(ti, "decode attention flags");
         if (((C + std::max<uint64_t>(S, 1) - 1) / std::max<uint64_t>(S, 1) + 7) / 8 * 8 > kDecSplitKeys)
           return fail(ti, "decode attention: more than 64 cache keys per split");
         if (!has(t.a, H * hd, adt) || !has(t.p[1], H * hd, adt) || !has(t.p[2], H * hd, adt))

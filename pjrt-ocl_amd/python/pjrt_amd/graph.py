@@ -482,7 +482,7 @@ class Graph:
         its new key/value straight from where they were computed and the cache
         update can run beside the next matmul.  q, k, v: [H, hd] (any shape of
         H * hd elements); cache_kt: [H, hd, C], or the key rows [H, C, hd] with
-        ``krow`` (hd a power of two); cache_v: [H, C, hd]; pos: i32 scalar,
+        ``krow``; cache_v: [H, C, hd]; pos: i32 scalar,
         clamped to [0, C].  All float operands share one dtype; the output
         [H, hd] has it too.  Equals the decomposed dot -> (mask beyond pos) ->
         softmax -> dot chain with pos's column of the cache holding k and v.
@@ -510,8 +510,6 @@ class Graph:
             raise GraphError("decode_attention: pos is an i32 scalar")
         if hd % 8 or hd > 256 or C % 8 or C > 0xFFFF:
             raise GraphError("decode_attention: hd and C must be multiples of 8 (hd <= 256)")
-        if krow and hd & (hd - 1):
-            raise GraphError("decode_attention: key rows need a power-of-two hd")
         dst = self._new((H, hd), q.dtype)
         desc = self.add_aux([hd | int(krow) << 16 | int(masked) << 17, k.buf, v.buf, pos.buf,
                              V.f32_bits(scale)])

@@ -1014,7 +1014,7 @@ def fuse_attention(prog: V.VMProgram) -> None:
             free = sorted(consumed + [dot1, si] + mid + ([d2i] if tail else []))
             qa, kb, vb = D1.a, D1.b, D2.b
             placed = []
-            if adt in (V.DT_BF16, V.DT_F16) and hd in (64, 128) and scale > 0 and \
+            if adt in (V.DT_BF16, V.DT_F16) and hd % 8 == 0 and 8 <= hd <= 128 and scale > 0 and \
                     (qv or vv or not (kv and prog.aux[kv - 1:kv + 7] == kt)):
                 # the matrix-core kernel reads Q and V as plain [G, rows, hd]
                 # and K as the transpose of a plain [G, C, hd]: strided operands
@@ -1250,7 +1250,7 @@ def _match_decode(prog, ix, sc, consts, outs, si):
     if m is None:
         return None
     kc, vc, kbuf, vbuf, posb, C, masked, dk, dv = m
-    if hd % 8 or hd > 256 or C % 8 or C < 8 or C > 0xFFFF or (krow and hd & (hd - 1)):
+    if hd % 8 or hd > 256 or C % 8 or C < 8 or C > 0xFFFF:
         return None
     # nothing rewrites what the fused op reads between its sources and ``last``
     # (no region op in between either: its sub-list could)

@@ -53,7 +53,7 @@ which does not use them is byte-for-byte a reference program):
   | masked << 17, p6 C, p7 scale bits; tile = head * S + split, each split at
   most 64 cache keys, combined by the last split through the task's scratch.
   ``pos`` (i32 scalar) is clamped to [0, C].  ``krow``: the key cache holds
-  rows [H, C, hd] instead of K^T (hd a power of two).  ``masked``: the
+  rows [H, C, hd] instead of K^T.  ``masked``: the
   decoder's form that stores k, v at pos before attending over keys <= pos:
   pos is clamped to [0, C - 1] and a negative pos gives a NaN output.
 

@@ -652,7 +652,11 @@ def test_dot_views_batch_epilogue():
 @pytest.mark.parametrize("dt,hd,causal,T,C", [("bf16", 128, True, 256, 256), ("bf16", 128, False, 128, 384),
                                               ("bf16", 64, True, 384, 512), ("f16", 128, True, 128, 128),
                                               ("bf16", 128, True, 96, 200), ("f16", 64, False, 64, 130),
-                                              ("f32", 32, True, 40, 56), ("bf16", 80, False, 64, 100)])
+                                              ("f32", 32, True, 40, 56), ("bf16", 80, False, 64, 100),
+                                              # head sizes run on the zero-padded 128 / 64 kernels
+                                              ("f16", 96, True, 300, 300), ("bf16", 120, True, 257, 320),
+                                              ("bf16", 40, False, 200, 264), ("f16", 8, True, 64, 70),
+                                              ("bf16", 72, False, 513, 130)])
 def test_flash_attention(dt, hd, causal, T, C):
     rng = np.random.default_rng(1004)
     H = 3
@@ -676,7 +680,7 @@ def test_flash_attention(dt, hd, causal, T, C):
                                f"flash {dt} hd {hd}")
 
 
-@pytest.mark.parametrize("hd", [64, 128])
+@pytest.mark.parametrize("hd", [64, 128, 96, 24])
 def test_flash_attention_partial_block_inf_value(hd):
     """Matrix-core path with a partial last key block (C = 200): every query sees
     key C - 1, whose value row is +inf, so every output is +inf.  The block's
@@ -696,14 +700,17 @@ def test_flash_attention_partial_block_inf_value(hd):
     assert np.isposinf(got[0]).all(), int(np.isnan(got[0]).sum())
 
 
-@pytest.mark.parametrize("dt,causal,T,C,target", [("bf16", True, 512, 512, 150.0), ("f16", False, 256, 384, 22.0)])
-def test_flash_attention_score_jump(dt, causal, T, C, target):
+@pytest.mark.parametrize("dt,causal,T,C,target,hd", [("bf16", True, 512, 512, 150.0, 128),
+                                                     ("f16", False, 256, 384, 22.0, 128),
+                                                     ("bf16", True, 300, 320, 150.0, 96)])
+def test_flash_attention_score_jump(dt, causal, T, C, target, hd):
     """A key late in the sequence whose scaled score with one query is `target`
     above the rest: probabilities against the first block's maximum would
     overflow (f32 for bf16 at 150, f16 at 22), so the kernel must take its exact
-    two-pass route for that block; the result still matches float64 math."""
+    two-pass route for that block; the result still matches float64 math (also
+    with a padded head size, whose zeroed slots every sweep sets again)."""
     rng = np.random.default_rng(1006)
-    H, hd = 2, 128
+    H = 2
     q = rng.standard_normal((H, T, hd)).astype(np.float32)
     k = rng.standard_normal((H, C, hd)).astype(np.float32)
     v = rng.standard_normal((H, C, hd)).astype(np.float32)
@@ -740,6 +747,9 @@ def test_flash_attention_score_jump(dt, causal, T, C, target):
     ("f16", 3, 256, 1032, 1030, None, "krow"),         # 32 threads per key row
     ("bf16", 2, 128, 2056, 2050, 1500, "krow"),        # 33 splits, a dominant early key
     ("f32", 1, 8, 64, 33, "new", "krow masked"),       # one thread per key row
+    ("bf16", 4, 96, 640, 600, None, "krow masked"),    # 12 threads per key row, in groups of 16
+    ("f16", 3, 24, 136, 100, "new", "krow"),           # 3 threads per key row, in groups of 4
+    ("f32", 2, 80, 1032, 1031, 700, "krow"),           # 10 of 16, 17 splits, a dominant early key
     ("f32", 2, 16, 32, -1, None, "masked"),            # no key left: NaN, as the softmax makes it
 ])
 def test_decode_attention(dt, H, hd, C, pos, jump, mode):

@@ -365,18 +365,20 @@ def test_gpt_decode_program_lowers_to_the_decoder(mode, monkeypatch):
         assert not [i for i in body if i.op in (V.OP_GATHER_STRIDED, V.OP_CONVERT, V.OP_COPY_F32) and i.n == cache]
 
 
-def test_gpt_prefill_attention_gets_the_matrix_core_layout():
+@pytest.mark.parametrize("d", [128, 192])
+def test_gpt_prefill_attention_gets_the_matrix_core_layout(d):
     """The prefill's attention reads q, k, v as head views of the fused QKV
     projection; the flash fusion gathers them into the matrix-core kernel's
-    layout (Q, V plain [H, T, hd], K the transpose of a plain [H, T, hd]), and
-    the decoder's tokens and logits are unchanged."""
+    layout (Q, V plain [H, T, hd], K the transpose of a plain [H, T, hd]), also
+    for a head size (96) that kernel runs zero-padded, and the decoder's tokens
+    and logits are unchanged."""
     from pjrt_amd import configs as CF
     from pjrt_amd import stablehlo_configs as SC
-    c = CF.GptConfig(layers=1, d=128, heads=2, mlp=128, vocab=97, prompt=64, steps=4)
+    c = CF.GptConfig(layers=1, d=d, heads=2, mlp=128, vocab=97, prompt=64, steps=4)
     prog = L.lower_text(SC.gpt_decode(c, emit_logits=True))
     (fa,) = [i for i in prog.instrs if i.op == V.OP_FLASH_ATTN]
     G, M, C, hd, _, causal, qv, kv, vv = prog.aux[fa.aux:fa.aux + 9]
-    assert (G, M, C, hd, causal, qv, vv) == (2, 64, 64, 64, 1, 0, 0)
+    assert (G, M, C, hd, causal, qv, vv) == (2, 64, 64, d // 2, 1, 0, 0)
     assert prog.aux[kv - 1:kv + 7] == [3, G, hd, C, C * hd, 1, hd, 0]
     args = CF.gpt_inputs(c, seed=3)
     first, toks, logits = run(prog, args)

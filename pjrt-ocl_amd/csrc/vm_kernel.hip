@@ -218,9 +218,12 @@ __global__ __launch_bounds__(kBlock, 1) void vm_main(VmArgs args) {
           __hip_atomic_fetch_add(A->stats + 3, __builtin_amdgcn_s_memrealtime() - tw, __ATOMIC_RELAXED,
                                  __HIP_MEMORY_SCOPE_AGENT);
       }
+      // One call site: the dispatch switch is inlined once, with the register
+      // saving around each of its calls (two copies, one per stats mode, made
+      // the kernel 79 KB instead of 46 KB and cost C5 7 %).
+      const uint64_t t0 = A->stats ? __builtin_amdgcn_s_memrealtime() : 0;
+      exec_tiles(A, en.task, en.tile_lo, en.tile_hi);
       if (A->stats) {
-        const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
-        exec_tiles(A, en.task, en.tile_lo, en.tile_hi);
         __syncthreads();
         if (threadIdx.x == 0) {
           const uint64_t dt = __builtin_amdgcn_s_memrealtime() - t0;
@@ -229,8 +232,6 @@ __global__ __launch_bounds__(kBlock, 1) void vm_main(VmArgs args) {
           __hip_atomic_fetch_max(st + 1, dt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
           __hip_atomic_fetch_add(st + 2, uint64_t(1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
-      } else {
-        exec_tiles(A, en.task, en.tile_lo, en.tile_hi);
       }
       if (en.signal_flag != FLAG_NONE) flag_signal(A, en.signal_flag, phase_tag(A, nbar));
     }

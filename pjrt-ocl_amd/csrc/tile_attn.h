@@ -51,7 +51,19 @@ struct AttnLds {
   static constexpr uint32_t kRounds = kKBytes / 4096;         // block-wide 16-byte transfers per operand
   static constexpr int kBytes = 2 * int(kStage);
 };
-constexpr int kAttnLdsBytes = AttnLds<128>::kBytes;
+// f32 path (attn_block_f32): keys per streamed block, query rows per block, and
+// its two LDS buffers of K and V rows padded to HD + 2 floats
+constexpr int kAttnF32Keys = 32;
+constexpr int kAttnF32Rows = 128;
+template <int HD>
+struct AttnF32Lds {
+  static constexpr uint32_t kRS = HD + 2;                       // floats per LDS row
+  static constexpr uint32_t kOp = kAttnF32Keys * kRS;           // floats per operand block
+  static constexpr uint32_t kBuf = 2 * kOp;                     // K block, then V block
+  static constexpr int kBytes = int(2 * kBuf * 4);              // two buffers
+};
+constexpr int kAttnF32LdsBytes = AttnF32Lds<128>::kBytes;
+constexpr int kAttnLdsBytes = AttnLds<128>::kBytes > kAttnF32LdsBytes ? AttnLds<128>::kBytes : kAttnF32LdsBytes;
 
 // Slot swizzles of the 16-byte hd chunks of key row r (chunk c at slot c ^ swz).
 // K (ds_read_b128 fragments, rows kperm-ordered): distinct bank groups for any 16
@@ -542,6 +554,222 @@ VM_LEAF void attn_fast(Args A, uint32_t ti, uint32_t lo, uint32_t hi) {
   }
 }
 
+// ---- f32 operands -------------------------------------------------------------------
+// Matrix-core path for f32 Q/K/V (hd a multiple of 4 up to 128, run as 64 or 128 on
+// zero-padded rows; scale > 0; K read through the usual [H,hd,C] transpose view of
+// a [H,C,hd] buffer): v_mfma_f32_32x32x2f32, so products and sums stay f32.  A lane
+// takes 128 query rows at a time, 32 per wave (one 32x32 S^T tile per 32-key block),
+// and streams K and V in 32-key blocks through registers into two LDS buffers whose
+// rows are padded to HD + 2 floats: the 32 keys a half wave reads for S^T, and the
+// 32 channels it reads for V^T, then lie in distinct banks.
+//   S^T (32 keys x 32 queries) = sum over hd of K Q^T.  MFMA step 2c + e takes hd
+//   4c + 2g + e in lane group g = lane / 32, so a lane reads one 8-byte pair of its
+//   key row per two steps (two accumulation chains, c even / odd, added at the end).
+//   O^T (HD x 32 queries) += V^T P^T.  Step s takes key 8 (s / 4) + 4 g + s % 4 in
+//   lane group g, the key that register s of the S^T accumulator holds, so P^T is
+//   the S^T registers themselves.
+// Online softmax in base 2 with the usual per-block rescale of O and l.  Keys past C
+// are masked; their V rows are staged as zeros, so 0-weight keys add 0.
+
+// One 128-row query block of head h (real rows row0 .., virtual rows vrow0 .., the
+// caller's span owns virtual rows [vlo, vhi)) against keys [0, kend).
+template <int HD>
+VM_DEV void attn_block_f32(Args A, uint32_t ti, uint32_t h, uint32_t row0, uint32_t vrow0, uint32_t vlo,
+                           uint32_t vhi) {
+  const VM_K Task& t = task_of(A, ti);
+  const AttnDesc P = attn_desc(A, t);
+  h = uni(h);
+  row0 = uni(row0);
+  vrow0 = uni(vrow0);
+  vlo = uni(vlo);
+  vhi = uni(vhi);
+  typedef AttnF32Lds<HD> L;
+  typedef __attribute__((address_space(3))) float lds_f;
+  typedef __attribute__((address_space(3))) f32x2_t lds_f2;
+  constexpr uint32_t NC = HD / 4;                              // 4-float chunks per row
+  constexpr int DB = HD / 32;                                  // 32-channel blocks of O^T
+  constexpr uint32_t NR = kAttnF32Keys * NC / kBlock;         // staged chunks per thread and operand
+  static_assert(NR * kBlock == kAttnF32Keys * NC, "whole staging rounds");
+  const uint32_t T = P.T, C = P.C, hd = uni(P.hd), dt = (t.tile_op >> 8) & 0xFF;
+  const uint32_t hc = hd / 4;                                  // chunks inside the row
+  const uint32_t lane = threadIdx.x & 63, wave = uni(threadIdx.x >> 6), g = lane >> 5, j = lane & 31;
+  const uint32_t qw0 = row0 + 32 * wave;                       // this wave's first row
+  const VM_G float* Q = gcast<float>(resolve(A, t.a)) + uint64_t(h) * T * hd;
+  const VM_G float* K = gcast<float>(resolve(A, t.b)) + uint64_t(h) * C * hd;
+  const VM_G float* V = gcast<float>(resolve(A, t.p[0])) + uint64_t(h) * C * hd;
+  gbyte* Ob = resolve(A, t.dst);
+
+  // Q^T fragments: step 2c + e <- Q[q][4c + 2g + e]; rows past T re-read row T - 1
+  // (not stored); chunks past hd are zero (4c < hd is uniform: hd % 4 == 0)
+  float qf[2 * NC];
+  {
+    const uint32_t qr = min(qw0 + j, T - 1);
+#pragma unroll
+    for (uint32_t c = 0; c < NC; ++c) {
+      f32x2_t x = {0.0f, 0.0f};
+      if (4 * c < hd) x = *(const VM_G f32x2_t*)(Q + uint64_t(qr) * hd + 4 * c + 2 * g);
+      qf[2 * c] = x.x;
+      qf[2 * c + 1] = x.y;
+    }
+  }
+  f32x16 o[DB];
+#pragma unroll
+  for (int i = 0; i < DB; ++i) o[i] = f32x16{};
+  float m_run = -INFINITY, l_part = 0.0f;
+  const float sl2 = P.scale * 1.4426950408889634f;
+
+  // keys this block needs: up to its last row's causal limit
+  const int32_t shift = int32_t(C) - int32_t(T);
+  const uint32_t qmax = min(row0 + kAttnF32Rows, T) - 1;
+  uint32_t kend = C;
+  if (P.causal) kend = min(C, uint32_t(max(0, int32_t(qmax) + shift + 1)));
+  const uint32_t nblk = (kend + kAttnF32Keys - 1) / kAttnF32Keys;
+  const bool wave_rows = qw0 < T;
+  const int32_t wq_hi = int32_t(min(qw0 + 31, T - 1)) + shift;   // last visible key of the wave's last row
+  const int32_t qlim = int32_t(qw0 + j) + shift;                  // this lane's row's last visible key
+
+  // Staging: chunk f = r kBlock + threadIdx.x of a block is key f / NC, chunk f % NC.
+  // Keys past C re-read key C - 1 and chunks past hd re-read the row's last chunk
+  // (no load behind a lane-dependent branch); both are replaced by zeros in the
+  // LDS copy where they would matter (V rows past C, chunks past hd).
+  const uint32_t lds0 = uni(uint32_t(reinterpret_cast<uintptr_t>(lds_ptr<lds_u8>())));
+  v4f ks[NR], vs[NR];
+  auto load = [&](uint32_t kb) {
+#pragma unroll
+    for (uint32_t r = 0; r < NR; ++r) {
+      const uint32_t f = r * kBlock + threadIdx.x, key = f / NC, c = min(f % NC, hc - 1);
+      const uint64_t e = uint64_t(min(kb * kAttnF32Keys + key, C - 1)) * hd + 4 * c;
+      ks[r] = *(const VM_G v4f*)(K + e);
+      vs[r] = *(const VM_G v4f*)(V + e);
+    }
+  };
+  auto store = [&](uint32_t buf, uint32_t kb) {
+#pragma unroll
+    for (uint32_t r = 0; r < NR; ++r) {
+      const uint32_t f = r * kBlock + threadIdx.x, key = f / NC, c = f % NC;
+      const bool in = c < hc;
+      const v4f z = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+      const v4f kx = in ? ks[r] : z;
+      const v4f vx = in && kb * kAttnF32Keys + key < C ? vs[r] : z;
+      lds_f* kd = (lds_f*)uintptr_t(lds0 + 4 * (buf * L::kBuf + key * L::kRS + 4 * c));
+      *(lds_f2*)kd = f32x2_t{kx.x, kx.y};
+      *(lds_f2*)(kd + 2) = f32x2_t{kx.z, kx.w};
+      *(lds_f2*)(kd + L::kOp) = f32x2_t{vx.x, vx.y};
+      *(lds_f2*)(kd + L::kOp + 2) = f32x2_t{vx.z, vx.w};
+    }
+  };
+
+  auto body = [&](uint32_t buf, uint32_t key0) {
+    const lds_f* Kr = (const lds_f*)uintptr_t(lds0 + 4 * (buf * L::kBuf + j * L::kRS + 2 * g));
+    const lds_f* Vb = (const lds_f*)uintptr_t(lds0 + 4 * (buf * L::kBuf + L::kOp + j));
+    f32x16 s0 = f32x16{}, s1 = f32x16{};
+#pragma unroll
+    for (uint32_t c = 0; c < NC; c += 2) {
+      const f32x2_t k0 = *(const lds_f2*)(Kr + 4 * c);
+      const f32x2_t k1 = *(const lds_f2*)(Kr + 4 * c + 4);
+      s0 = __builtin_amdgcn_mfma_f32_32x32x2f32(k0.x, qf[2 * c], s0, 0, 0, 0);
+      s1 = __builtin_amdgcn_mfma_f32_32x32x2f32(k1.x, qf[2 * c + 2], s1, 0, 0, 0);
+      s0 = __builtin_amdgcn_mfma_f32_32x32x2f32(k0.y, qf[2 * c + 1], s0, 0, 0, 0);
+      s1 = __builtin_amdgcn_mfma_f32_32x32x2f32(k1.y, qf[2 * c + 3], s1, 0, 0, 0);
+    }
+    f32x16 s = s0 + s1;
+    // masked entries (keys past the row's causal limit or past C) -> -inf
+    const int32_t lim = (P.causal ? min(qlim, int32_t(C) - 1) : int32_t(C) - 1) - int32_t(key0);
+#pragma unroll
+    for (int v = 0; v < 16; ++v)
+      if (int32_t(8 * (v >> 2) + 4 * g + (v & 3)) > lim) s[v] = -INFINITY;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s[v]);
+    mx = fmaxf(mx, xor32(mx));
+    const float m_new = fmaxf(m_run, mx * sl2);
+    const float mu = m_new == -INFINITY ? 0.0f : m_new;
+    const float alpha = __builtin_amdgcn_exp2f(m_run - mu);     // 0 while nothing is accumulated
+    m_run = m_new;
+    float rs = 0.0f;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      s[v] = __builtin_amdgcn_exp2f(fmaf(s[v], sl2, -mu));
+      rs += s[v];
+    }
+    l_part = fmaf(l_part, alpha, rs);
+#pragma unroll
+    for (int i = 0; i < DB; ++i) o[i] *= alpha;
+#pragma unroll
+    for (int st = 0; st < 16; ++st) {
+      const uint32_t key = 8 * (st >> 2) + 4 * g + (st & 3);
+#pragma unroll
+      for (int i = 0; i < DB; ++i)
+        o[i] = __builtin_amdgcn_mfma_f32_32x32x2f32(Vb[key * L::kRS + 32 * i], s[st], o[i], 0, 0, 0);
+    }
+  };
+
+  // Per block: the next block's loads go out, this block is computed, then the
+  // next block is written to the other buffer (its last reader passed the
+  // previous barrier) and a barrier publishes it.  Blocks past the wave's last
+  // row's causal limit are skipped (the wave still stages and syncs).
+  __syncthreads();                      // LDS free from the previous user
+  if (nblk) {
+    load(0);
+    store(0, 0);
+  }
+  __syncthreads();
+  for (uint32_t kb = 0; kb < nblk; ++kb) {
+    if (kb + 1 < nblk) load(kb + 1);
+    if (wave_rows && (!P.causal || int32_t(kb * kAttnF32Keys) <= wq_hi)) body(kb & 1, kb * kAttnF32Keys);
+    if (kb + 1 < nblk) store((kb + 1) & 1, kb + 1);
+    __syncthreads();
+  }
+
+  const float l = l_part + xor32(l_part);
+  const uint32_t q = qw0 + j, vq = vrow0 + 32 * wave + j;
+  if (q < T && vq >= vlo && vq < vhi) {
+    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+    const uint64_t obase = (uint64_t(h) * T + q) * hd;
+#pragma unroll
+    for (int i = 0; i < DB; ++i)
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        const uint32_t d = 32 * i + 8 * jj + 4 * g;
+        if (d < hd)
+          st4(Ob, dt, obase + d,
+              v4f_make(o[i][4 * jj] * inv, o[i][4 * jj + 1] * inv, o[i][4 * jj + 2] * inv, o[i][4 * jj + 3] * inv));
+      }
+  }
+}
+
+// The lane's query blocks in the order attn_fast takes them (virtual 256-row
+// blocks, zig-zag when causal), each as two 128-row halves.
+template <int HD>
+VM_DEV void attn_f32_lane(Args A, uint32_t ti, uint32_t lo, uint32_t hi) {
+  const VM_K Task& t = task_of(A, ti);
+  const AttnDesc P = attn_desc(A, t);
+  const uint32_t T = P.T;
+  const uint32_t nb = (T + kAttnRows - 1) / kAttnRows, Tp = nb * kAttnRows;
+  hi = min(hi, P.H * Tp);
+  const bool zig = P.causal;
+  for (uint32_t h = lo / Tp; h * Tp < hi; ++h) {
+    const uint32_t a = max(lo, h * Tp) - h * Tp, b = min(hi - h * Tp, Tp);     // virtual rows [a, b)
+    for (uint32_t vb = a / kAttnRows; vb * kAttnRows < b; ++vb) {
+      const uint32_t rb = zig ? ((vb & 1) ? nb - 1 - (vb >> 1) : (vb >> 1)) : vb;
+      const uint32_t vrow0 = vb * kAttnRows;
+      for (uint32_t hf = 0; hf < 2; ++hf) {
+        const uint32_t r0 = rb * kAttnRows + hf * kAttnF32Rows;
+        if (r0 < T)
+          attn_block_f32<HD>(A, ti, h, r0, vrow0 + hf * kAttnF32Rows, max(a, vrow0), min(b, vrow0 + kAttnRows));
+      }
+    }
+  }
+}
+
+// One leaf for both head classes, so the kernel has one call site for it.
+VM_LEAF void attn_f32_run(Args A, uint32_t ti, uint32_t lo, uint32_t hi) {
+  A = uargs(A);
+  const AttnDesc P = attn_desc(A, task_of(A, ti));
+  if (P.hd > 64) attn_f32_lane<128>(A, ti, lo, hi);
+  else attn_f32_lane<64>(A, ti, lo, hi);
+}
+
 VM_DEV void flash_attn_tiles(Args A, uint32_t ti, uint32_t lo, uint32_t hi) {
   A = uargs(A);
   const VM_K Task& t = task_of(A, ti);
@@ -552,6 +780,10 @@ VM_DEV void flash_attn_tiles(Args A, uint32_t ti, uint32_t lo, uint32_t hi) {
   const bool fast = (adt == DT_BF16 || adt == DT_F16) && P.hd % 8 == 0 && P.hd >= 8 && P.hd <= 128 && !P.qv &&
                     !P.vv && is_kt_view(aux_of(A), P.kv, P.H, P.C, P.hd) && P.scale > 0.0f &&
                     (dt == DT_F32 || dt == DT_BF16 || dt == DT_F16);
+  const bool fast32 = adt == DT_F32 && P.hd % 4 == 0 && P.hd >= 4 && P.hd <= 128 && !P.qv && !P.vv &&
+                      is_kt_view(aux_of(A), P.kv, P.H, P.C, P.hd) && P.scale > 0.0f &&
+                      (dt == DT_F32 || dt == DT_BF16 || dt == DT_F16);
+  if (fast32) return attn_f32_run(A, ti, lo, hi);
   if (!fast) return attn_rows_generic(A, ti, lo, hi);
   if (adt == DT_BF16) {
     if (P.hd == 128) attn_fast<128, true, false>(A, ti, lo, hi);

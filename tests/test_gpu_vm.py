@@ -656,7 +656,11 @@ def test_dot_views_batch_epilogue():
                                               # head sizes run on the zero-padded 128 / 64 kernels
                                               ("f16", 96, True, 300, 300), ("bf16", 120, True, 257, 320),
                                               ("bf16", 40, False, 200, 264), ("f16", 8, True, 64, 70),
-                                              ("bf16", 72, False, 513, 130)])
+                                              ("bf16", 72, False, 513, 130),
+                                              # f32 matrix-core kernel (128-row blocks, 32-key blocks)
+                                              ("f32", 64, True, 300, 300), ("f32", 128, False, 200, 264),
+                                              ("f32", 100, True, 129, 200), ("f32", 128, True, 640, 700),
+                                              ("f32", 4, False, 33, 40)])
 def test_flash_attention(dt, hd, causal, T, C):
     rng = np.random.default_rng(1004)
     H = 3
@@ -672,7 +676,8 @@ def test_flash_attention(dt, hd, causal, T, C):
     g.output(g.flash_attention(Q, K, Vv, 1.0 / np.sqrt(hd), causal, out_dtype="f32"))
     got, _ = run_both(g.build(), [q, k, v], oracle=None)
     want = vmref.attention(q, np.transpose(k, (0, 2, 1)), v, 1.0 / np.sqrt(hd), causal)
-    tol = 1e-3 if dt == "f32" else 1e-2
+    # f32: f32 products and sums (matrix cores or the row kernel); 16-bit: P in bf16 / f16
+    tol = 2e-5 if dt == "f32" else 1e-2
     err = np.abs(got[0] - want).max() / max(1e-6, np.abs(want).max())
     assert err <= tol, err
     assert_product_elementwise(got[0], want.astype(np.float64),
@@ -680,20 +685,21 @@ def test_flash_attention(dt, hd, causal, T, C):
                                f"flash {dt} hd {hd}")
 
 
-@pytest.mark.parametrize("hd", [64, 128, 96, 24])
-def test_flash_attention_partial_block_inf_value(hd):
+@pytest.mark.parametrize("hd,dt", [(64, "bf16"), (128, "bf16"), (96, "bf16"), (24, "bf16"), (128, "f32"), (36, "f32")])
+def test_flash_attention_partial_block_inf_value(hd, dt):
     """Matrix-core path with a partial last key block (C = 200): every query sees
     key C - 1, whose value row is +inf, so every output is +inf.  The block's
     slots past C hold copies of key C - 1 and get probability 0; they must add 0
-    (zeroed), not 0 * inf = NaN."""
+    (zeroed), not 0 * inf = NaN.  f32: the staged V rows past C are zeros."""
     rng = np.random.default_rng(1005)
     H, T, C = 2, 64, 200
-    q = vmref.bf16_to_f32(vmref.f32_to_bf16(rng.standard_normal((H, T, hd)).astype(np.float32)))
-    k = vmref.bf16_to_f32(vmref.f32_to_bf16(rng.standard_normal((H, C, hd)).astype(np.float32)))
-    v = vmref.bf16_to_f32(vmref.f32_to_bf16(rng.standard_normal((H, C, hd)).astype(np.float32)))
+    cast = (lambda x: vmref.bf16_to_f32(vmref.f32_to_bf16(x))) if dt == "bf16" else (lambda x: x)
+    q = cast(rng.standard_normal((H, T, hd)).astype(np.float32))
+    k = cast(rng.standard_normal((H, C, hd)).astype(np.float32))
+    v = cast(rng.standard_normal((H, C, hd)).astype(np.float32))
     v[:, C - 1, :] = np.inf
     g = G.Graph()
-    Q, K, Vv = g.input(q.shape, "bf16"), g.input(k.shape, "bf16"), g.input(v.shape, "bf16")
+    Q, K, Vv = g.input(q.shape, dt), g.input(k.shape, dt), g.input(v.shape, dt)
     g.output(g.flash_attention(Q, K, Vv, 1.0 / np.sqrt(hd), False, out_dtype="f32"))
     got, _ = run_both(g.build(), [q, k, v], oracle=None)
     assert np.isposinf(vmref.attention(q, np.transpose(k, (0, 2, 1)), v, 1.0 / np.sqrt(hd), False)).all()

@@ -140,16 +140,19 @@ def test_dot_general_dtypes(dt, out):
         np.testing.assert_array_equal(got, want)
 
 
+@pytest.mark.parametrize("dt", ["bf16", "f32"])
 @pytest.mark.parametrize("causal", [True, False])
-def test_attention_config4_becomes_flash_attention(causal):
+def test_attention_config4_becomes_flash_attention(causal, dt):
     """Config 4's shape of program (bf16 Q/K/V, f32 scores, optional causal mask
-    by iota compare, softmax, bf16 P): one OP_FLASH_ATTN with the causal flag,
-    K read through the plain transpose view the MFMA kernel takes, within the
-    bf16 attention tolerance of float64 math and of the unfused program."""
+    by iota compare, softmax, bf16 P; or the same program in f32): one
+    OP_FLASH_ATTN with the causal flag, K read through the plain transpose view
+    the matrix-core kernels take, within the attention tolerance of float64
+    math and of the unfused program."""
     B, Hh, T, D = 1, 2, 32, 16
     rng = np.random.default_rng(1004)
-    q, k, v = (bf16(rng.standard_normal((B, Hh, T, D))) for _ in range(3))
-    prog, (got,), (plain,) = both(H.attention(B, Hh, T, D, causal=causal), [q, k, v])
+    cast = bf16 if dt == "bf16" else (lambda x: np.asarray(x, np.float32))
+    q, k, v = (cast(rng.standard_normal((B, Hh, T, D))) for _ in range(3))
+    prog, (got,), (plain,) = both(H.attention(B, Hh, T, D, dt=dt, causal=causal), [q, k, v])
     assert live_ops(prog) == [V.OP_FLASH_ATTN]
     fa = next(i for i in prog.instrs if i.op == V.OP_FLASH_ATTN)
     G, Mq, C, hd, sbits, cflag, qv, kv, vv = prog.aux[fa.aux:fa.aux + 9]
@@ -162,9 +165,12 @@ def test_attention_config4_becomes_flash_attention(causal):
     p = np.exp(s - s.max(-1, keepdims=True))
     p /= p.sum(-1, keepdims=True)
     want = p @ v
-    gf, pf = vmref.bf16_to_f32(got), vmref.bf16_to_f32(plain)
-    assert np.abs(gf - want).max() <= 1e-2 * np.abs(want).max()
-    assert np.abs(gf - pf).max() <= 1e-2 * np.abs(pf).max()
+    if dt == "bf16":
+        gf, pf, tol = vmref.bf16_to_f32(got), vmref.bf16_to_f32(plain), 1e-2
+    else:
+        gf, pf, tol = np.asarray(got, np.float32), np.asarray(plain, np.float32), 1e-5
+    assert np.abs(gf - want).max() <= tol * np.abs(want).max()
+    assert np.abs(gf - pf).max() <= tol * np.abs(pf).max()
 
 
 def test_argmax_variadic_reduce():

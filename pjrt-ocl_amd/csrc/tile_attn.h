@@ -453,7 +453,7 @@ VM_DEV void attn_block_mfma(Args A, uint32_t ti, uint32_t h, uint32_t row0, uint
 
 // Generic path: any head size, dtype or view.  One wave per query row; lanes split
 // the keys of a 64-key chunk, then the hd outputs.
-VM_TILE void attn_rows_generic(Args A, uint32_t ti, uint32_t lo, uint32_t hi) {
+VM_DEV void attn_rows_generic(Args A, uint32_t ti, uint32_t lo, uint32_t hi) {
   A = uargs(A);
   const VM_K Task& t = task_of(A, ti);
   const AttnDesc P = attn_desc(A, t);
@@ -533,10 +533,9 @@ VM_DEV bool is_kt_view(const VM_K int32_t* aux, uint32_t kv, uint32_t H, uint32_
 // equally many blocks cost about the same).  A head's tiles are its rows padded
 // to whole blocks (Tp rows): the scheduler cuts chunks on block boundaries, so no
 // block is split between lanes, and the rows of the last real block past T are
-// computed and not stored.  One call per lane, so the register save / restore of
-// the call is paid once.
+// computed and not stored.
 template <int HD, bool BF16, bool PAD>
-VM_LEAF void attn_fast(Args A, uint32_t ti, uint32_t lo, uint32_t hi) {
+VM_DEV void attn_fast(Args A, uint32_t ti, uint32_t lo, uint32_t hi) {
   A = uargs(A);
   const VM_K Task& t = task_of(A, ti);
   const AttnDesc P = attn_desc(A, t);
@@ -762,15 +761,18 @@ VM_DEV void attn_f32_lane(Args A, uint32_t ti, uint32_t lo, uint32_t hi) {
   }
 }
 
-// One leaf for both head classes, so the kernel has one call site for it.
-VM_LEAF void attn_f32_run(Args A, uint32_t ti, uint32_t lo, uint32_t hi) {
+VM_DEV void attn_f32_run(Args A, uint32_t ti, uint32_t lo, uint32_t hi) {
   A = uargs(A);
   const AttnDesc P = attn_desc(A, task_of(A, ti));
   if (P.hd > 64) attn_f32_lane<128>(A, ti, lo, hi);
   else attn_f32_lane<64>(A, ti, lo, hi);
 }
 
-VM_DEV void flash_attn_tiles(Args A, uint32_t ti, uint32_t lo, uint32_t hi) {
+// One leaf holds every attention variant inlined, so the kernel's dispatch switch
+// has a single call site for the op.  Each call site costs the kernel code and
+// register moves around it: with the ten variants as leaves of their own, the
+// kernel's decode loop (C5) ran 3 % slower.
+VM_LEAF void flash_attn_tiles(Args A, uint32_t ti, uint32_t lo, uint32_t hi) {
   A = uargs(A);
   const VM_K Task& t = task_of(A, ti);
   const AttnDesc P = attn_desc(A, t);

@@ -63,7 +63,13 @@ struct AttnF32Lds {
   static constexpr int kBytes = int(2 * kBuf * 4);              // two buffers
 };
 constexpr int kAttnF32LdsBytes = AttnF32Lds<128>::kBytes;
-constexpr int kAttnLdsBytes = AttnLds<128>::kBytes > kAttnF32LdsBytes ? AttnLds<128>::kBytes : kAttnF32LdsBytes;
+// wide 16-bit path (attn_block_h16w, hd up to 256): 32-key blocks of K rows padded
+// to 528 bytes and V rows padded to 576 bytes, two buffers
+constexpr uint32_t kAttnWKRow = 528, kAttnWVRow = 576;
+constexpr uint32_t kAttnWBuf = kAttnF32Keys * (kAttnWKRow + kAttnWVRow);
+constexpr int kAttnWLdsBytes = int(2 * kAttnWBuf);
+constexpr int kAttnLdsBytes0 = AttnLds<128>::kBytes > kAttnF32LdsBytes ? AttnLds<128>::kBytes : kAttnF32LdsBytes;
+constexpr int kAttnLdsBytes = kAttnLdsBytes0 > kAttnWLdsBytes ? kAttnLdsBytes0 : kAttnWLdsBytes;
 
 // Slot swizzles of the 16-byte hd chunks of key row r (chunk c at slot c ^ swz).
 // K (ds_read_b128 fragments, rows kperm-ordered): distinct bank groups for any 16
@@ -738,9 +744,10 @@ VM_DEV void attn_block_f32(Args A, uint32_t ti, uint32_t h, uint32_t row0, uint3
 }
 
 // The lane's query blocks in the order attn_fast takes them (virtual 256-row
-// blocks, zig-zag when causal), each as two 128-row halves.
-template <int HD>
-VM_DEV void attn_f32_lane(Args A, uint32_t ti, uint32_t lo, uint32_t hi) {
+// blocks, zig-zag when causal), each as two 128-row halves: blk(h, real first
+// row, virtual first row, virtual rows [vlo, vhi) the span owns).
+template <class Blk>
+VM_DEV void attn_lane128(Args A, uint32_t ti, uint32_t lo, uint32_t hi, Blk blk) {
   const VM_K Task& t = task_of(A, ti);
   const AttnDesc P = attn_desc(A, t);
   const uint32_t T = P.T;
@@ -754,8 +761,7 @@ VM_DEV void attn_f32_lane(Args A, uint32_t ti, uint32_t lo, uint32_t hi) {
       const uint32_t vrow0 = vb * kAttnRows;
       for (uint32_t hf = 0; hf < 2; ++hf) {
         const uint32_t r0 = rb * kAttnRows + hf * kAttnF32Rows;
-        if (r0 < T)
-          attn_block_f32<HD>(A, ti, h, r0, vrow0 + hf * kAttnF32Rows, max(a, vrow0), min(b, vrow0 + kAttnRows));
+        if (r0 < T) blk(h, r0, vrow0 + hf * kAttnF32Rows, max(a, vrow0), min(b, vrow0 + kAttnRows));
       }
     }
   }
@@ -764,8 +770,206 @@ VM_DEV void attn_f32_lane(Args A, uint32_t ti, uint32_t lo, uint32_t hi) {
 VM_DEV void attn_f32_run(Args A, uint32_t ti, uint32_t lo, uint32_t hi) {
   A = uargs(A);
   const AttnDesc P = attn_desc(A, task_of(A, ti));
-  if (P.hd > 64) attn_f32_lane<128>(A, ti, lo, hi);
-  else attn_f32_lane<64>(A, ti, lo, hi);
+  if (P.hd > 64)
+    attn_lane128(A, ti, lo, hi, [&](uint32_t h, uint32_t r0, uint32_t v0, uint32_t vl, uint32_t vh) {
+      attn_block_f32<128>(A, ti, h, r0, v0, vl, vh);
+    });
+  else
+    attn_lane128(A, ti, lo, hi, [&](uint32_t h, uint32_t r0, uint32_t v0, uint32_t vl, uint32_t vh) {
+      attn_block_f32<64>(A, ti, h, r0, v0, vl, vh);
+    });
+}
+
+// ---- wide 16-bit rows (hd up to 256) ---------------------------------------------------
+// bf16 / f16 Q/K/V with hd a multiple of 8 in (128, 256], run as 256 on zero-padded
+// rows (scale > 0, K through the usual transpose view): the f32 path's structure
+// (128 query rows per lane, 32 per wave, 32-key blocks staged through registers
+// into two LDS buffers) with v_mfma_f32_32x32x16_{bf16,f16}.
+//   S^T (32 keys x 32 queries): MFMA step s takes hd [16 s + 8 g, +8) in lane
+//   group g, one 16-byte read of the lane's key row (rows padded to 528 bytes, so
+//   the 16 lanes of a read pass hit distinct banks).
+//   O^T (256 x 32 queries) += V^T P^T in two 16-key steps: element i of lane group
+//   g in step ps is S^T register 8 ps + i, key 16 ps + 8 (i / 4) + 4 g + i % 4, so
+//   P^T is the packed S^T registers.  The matching V^T operand is two
+//   ds_read_b64_tr_b16 (in each group of 16 lanes, lane 4e + q points at key row
+//   k0 + e, channels d0 + 4q .. +3, and receives channel d0 + lane % 16 at rows
+//   k0 .. k0 + 3), at rows 16 ps + 4 g and 16 ps + 8 + 4 g; V rows padded to 576
+//   bytes, so a 32-lane pass covers the 64 banks once.
+// Online softmax in base 2 with the per-block rescale of O and l; the row sum adds
+// the rounded probabilities (the ones the MFMA multiplies).
+template <bool BF16>
+VM_DEV void attn_block_h16w(Args A, uint32_t ti, uint32_t h, uint32_t row0, uint32_t vrow0, uint32_t vlo,
+                            uint32_t vhi) {
+  const VM_K Task& t = task_of(A, ti);
+  const AttnDesc P = attn_desc(A, t);
+  h = uni(h);
+  row0 = uni(row0);
+  vrow0 = uni(vrow0);
+  vlo = uni(vlo);
+  vhi = uni(vhi);
+  constexpr int HD = 256;
+  constexpr uint32_t NC = HD / 8;                              // 16-byte chunks per row
+  constexpr int KS = HD / 16;                                  // MFMA steps of S^T
+  constexpr int DB = HD / 32;                                  // 32-channel blocks of O^T
+  constexpr uint32_t NR = kAttnF32Keys * NC / kBlock;         // staged chunks per thread and operand
+  static_assert(NR * kBlock == kAttnF32Keys * NC, "whole staging rounds");
+  const uint32_t T = P.T, C = P.C, hd = uni(P.hd), dt = (t.tile_op >> 8) & 0xFF;
+  const uint32_t hc = hd / 8;                                  // chunks inside the row
+  const uint32_t lane = threadIdx.x & 63, wave = uni(threadIdx.x >> 6), g = lane >> 5, j = lane & 31;
+  const uint32_t qw0 = row0 + 32 * wave;
+  const VM_G uint16_t* Q = gcast<uint16_t>(resolve(A, t.a)) + uint64_t(h) * T * hd;
+  const VM_G uint16_t* K = gcast<uint16_t>(resolve(A, t.b)) + uint64_t(h) * C * hd;
+  const VM_G uint16_t* V = gcast<uint16_t>(resolve(A, t.p[0])) + uint64_t(h) * C * hd;
+  gbyte* Ob = resolve(A, t.dst);
+
+  // Q^T fragments: step s <- Q[q][16 s + 8 g, +8); rows past T re-read row T - 1
+  // (not stored); chunks past hd re-read the row's last chunk and are zeroed
+  u16x8 qf[KS];
+  {
+    const uint32_t qr = min(qw0 + j, T - 1);
+#pragma unroll
+    for (int st = 0; st < KS; ++st) {
+      const uint32_t c = 2 * st + g;
+      const u16x8 x = *(const VM_G u16x8*)(Q + uint64_t(qr) * hd + 8 * min(c, hc - 1));
+      qf[st] = c < hc ? x : u16x8{};
+    }
+  }
+  f32x16 o[DB];
+#pragma unroll
+  for (int i = 0; i < DB; ++i) o[i] = f32x16{};
+  float m_run = -INFINITY, l_part = 0.0f;
+  const float sl2 = P.scale * 1.4426950408889634f;
+
+  const int32_t shift = int32_t(C) - int32_t(T);
+  const uint32_t qmax = min(row0 + kAttnF32Rows, T) - 1;
+  uint32_t kend = C;
+  if (P.causal) kend = min(C, uint32_t(max(0, int32_t(qmax) + shift + 1)));
+  const uint32_t nblk = (kend + kAttnF32Keys - 1) / kAttnF32Keys;
+  const bool wave_rows = qw0 < T;
+  const int32_t wq_hi = int32_t(min(qw0 + 31, T - 1)) + shift;
+  const int32_t qlim = int32_t(qw0 + j) + shift;
+
+  // Staging as in the f32 path: chunk f = r kBlock + threadIdx.x of a block is key
+  // f / NC, chunk f % NC; keys past C re-read key C - 1 (their V rows are staged as
+  // zeros), chunks past hd re-read the last chunk (staged as zeros).
+  const uint32_t lds0 = uni(uint32_t(reinterpret_cast<uintptr_t>(lds_ptr<lds_u8>())));
+  typedef __attribute__((address_space(3))) v4u lds_v4u;
+  v4u ks[NR], vs[NR];
+  auto load = [&](uint32_t kb) {
+#pragma unroll
+    for (uint32_t r = 0; r < NR; ++r) {
+      const uint32_t f = r * kBlock + threadIdx.x, key = f / NC, c = min(f % NC, hc - 1);
+      const uint64_t e = uint64_t(min(kb * kAttnF32Keys + key, C - 1)) * hd + 8 * c;
+      ks[r] = *(const VM_G v4u*)(K + e);
+      vs[r] = *(const VM_G v4u*)(V + e);
+    }
+  };
+  auto store = [&](uint32_t buf, uint32_t kb) {
+    const uint32_t kbase = lds0 + buf * kAttnWBuf, vbase = kbase + kAttnF32Keys * kAttnWKRow;
+#pragma unroll
+    for (uint32_t r = 0; r < NR; ++r) {
+      const uint32_t f = r * kBlock + threadIdx.x, key = f / NC, c = f % NC;
+      const bool in = c < hc;
+      const v4u z = v4u_make(0, 0, 0, 0);
+      *(lds_v4u*)uintptr_t(kbase + key * kAttnWKRow + 16 * c) = in ? ks[r] : z;
+      *(lds_v4u*)uintptr_t(vbase + key * kAttnWVRow + 16 * c) = in && kb * kAttnF32Keys + key < C ? vs[r] : z;
+    }
+  };
+  // V^T read addresses (block db, step ps, first read; the second is 8 rows on)
+  const uint32_t e4 = (lane >> 2) & 3, q4 = lane & 3, hcol = (lane >> 4) & 1;
+  const uint32_t vcol = 2 * (16 * hcol + 4 * q4);             // bytes within a 32-channel block
+
+  auto body = [&](uint32_t buf, uint32_t key0) {
+    const uint32_t kbase = lds0 + buf * kAttnWBuf, vbase = kbase + kAttnF32Keys * kAttnWKRow;
+    const uint32_t kr = kbase + j * kAttnWKRow + 16 * g;
+    f32x16 s0 = f32x16{}, s1 = f32x16{};
+#pragma unroll
+    for (int st = 0; st < KS; st += 2) {
+      const u16x8 k0 = *(const lds_u16x8*)uintptr_t(kr + 32 * st);
+      const u16x8 k1 = *(const lds_u16x8*)uintptr_t(kr + 32 * st + 32);
+      s0 = mfma16<BF16>(k0, qf[st], s0);
+      s1 = mfma16<BF16>(k1, qf[st + 1], s1);
+    }
+    f32x16 s = s0 + s1;
+    const int32_t lim = (P.causal ? min(qlim, int32_t(C) - 1) : int32_t(C) - 1) - int32_t(key0);
+#pragma unroll
+    for (int v = 0; v < 16; ++v)
+      if (int32_t(8 * (v >> 2) + 4 * g + (v & 3)) > lim) s[v] = -INFINITY;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s[v]);
+    mx = fmaxf(mx, xor32(mx));
+    const float m_new = fmaxf(m_run, mx * sl2);
+    const float mu = m_new == -INFINITY ? 0.0f : m_new;
+    const float alpha = __builtin_amdgcn_exp2f(m_run - mu);
+    m_run = m_new;
+    u16x8 pf[2];
+    float rs = 0.0f;
+#pragma unroll
+    for (int ps = 0; ps < 2; ++ps) {
+      float e[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) e[i] = __builtin_amdgcn_exp2f(fmaf(s[8 * ps + i], sl2, -mu));
+      const v4u w = v4u_make(pack_h2<BF16>(e[0], e[1]), pack_h2<BF16>(e[2], e[3]), pack_h2<BF16>(e[4], e[5]),
+                             pack_h2<BF16>(e[6], e[7]));
+      pf[ps] = __builtin_bit_cast(u16x8, w);
+      rs = dot2_ones<BF16>(w.x, rs);
+      rs = dot2_ones<BF16>(w.y, rs);
+      rs = dot2_ones<BF16>(w.z, rs);
+      rs = dot2_ones<BF16>(w.w, rs);
+    }
+    l_part = fmaf(l_part, alpha, rs);
+#pragma unroll
+    for (int i = 0; i < DB; ++i) o[i] *= alpha;
+#pragma unroll
+    for (int ps = 0; ps < 2; ++ps) {
+      const uint32_t r0 = vbase + (16 * ps + 4 * g + e4) * kAttnWVRow + vcol;
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)uintptr_t(r0 + 64 * db));
+        const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)uintptr_t(r0 + 8 * kAttnWVRow + 64 * db));
+        const u16x8 vf = __builtin_bit_cast(u16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+        o[db] = mfma16<BF16>(vf, pf[ps], o[db]);
+      }
+    }
+  };
+
+  __syncthreads();                      // LDS free from the previous user
+  if (nblk) {
+    load(0);
+    store(0, 0);
+  }
+  __syncthreads();
+  for (uint32_t kb = 0; kb < nblk; ++kb) {
+    if (kb + 1 < nblk) load(kb + 1);
+    if (wave_rows && (!P.causal || int32_t(kb * kAttnF32Keys) <= wq_hi)) body(kb & 1, kb * kAttnF32Keys);
+    if (kb + 1 < nblk) store((kb + 1) & 1, kb + 1);
+    __syncthreads();
+  }
+
+  const float l = l_part + xor32(l_part);
+  const uint32_t q = qw0 + j, vq = vrow0 + 32 * wave + j;
+  if (q < T && vq >= vlo && vq < vhi) {
+    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+    const uint64_t obase = (uint64_t(h) * T + q) * hd;
+#pragma unroll
+    for (int i = 0; i < DB; ++i)
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        const uint32_t d = 32 * i + 8 * jj + 4 * g;
+        if (d < hd)
+          st4(Ob, dt, obase + d,
+              v4f_make(o[i][4 * jj] * inv, o[i][4 * jj + 1] * inv, o[i][4 * jj + 2] * inv, o[i][4 * jj + 3] * inv));
+      }
+  }
+}
+
+template <bool BF16>
+VM_DEV void attn_h16w_run(Args A, uint32_t ti, uint32_t lo, uint32_t hi) {
+  A = uargs(A);
+  attn_lane128(A, ti, lo, hi, [&](uint32_t h, uint32_t r0, uint32_t v0, uint32_t vl, uint32_t vh) {
+    attn_block_h16w<BF16>(A, ti, h, r0, v0, vl, vh);
+  });
 }
 
 // One leaf holds every attention variant inlined, so the kernel's dispatch switch
@@ -786,6 +990,10 @@ VM_LEAF void flash_attn_tiles(Args A, uint32_t ti, uint32_t lo, uint32_t hi) {
                       is_kt_view(aux_of(A), P.kv, P.H, P.C, P.hd) && P.scale > 0.0f &&
                       (dt == DT_F32 || dt == DT_BF16 || dt == DT_F16);
   if (fast32) return attn_f32_run(A, ti, lo, hi);
+  const bool wide = (adt == DT_BF16 || adt == DT_F16) && P.hd % 8 == 0 && P.hd > 128 && P.hd <= 256 && !P.qv &&
+                    !P.vv && is_kt_view(aux_of(A), P.kv, P.H, P.C, P.hd) && P.scale > 0.0f &&
+                    (dt == DT_F32 || dt == DT_BF16 || dt == DT_F16);
+  if (wide) return adt == DT_BF16 ? attn_h16w_run<true>(A, ti, lo, hi) : attn_h16w_run<false>(A, ti, lo, hi);
   if (!fast) return attn_rows_generic(A, ti, lo, hi);
   if (adt == DT_BF16) {
     if (P.hd == 128) attn_fast<128, true, false>(A, ti, lo, hi);

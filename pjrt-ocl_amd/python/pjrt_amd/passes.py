@@ -1014,7 +1014,7 @@ def fuse_attention(prog: V.VMProgram) -> None:
             free = sorted(consumed + [dot1, si] + mid + ([d2i] if tail else []))
             qa, kb, vb = D1.a, D1.b, D2.b
             placed = []
-            if (adt in (V.DT_BF16, V.DT_F16) and hd % 8 == 0 and 8 <= hd <= 128 or
+            if (adt in (V.DT_BF16, V.DT_F16) and hd % 8 == 0 and 8 <= hd <= 256 or
                     adt == V.DT_F32 and hd % 4 == 0 and 4 <= hd <= 128) and scale > 0 and \
                     (qv or vv or not (kv and prog.aux[kv - 1:kv + 7] == kt)):
                 # the matrix-core kernel reads Q and V as plain [G, rows, hd]

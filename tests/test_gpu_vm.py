@@ -660,7 +660,10 @@ def test_dot_views_batch_epilogue():
                                               # f32 matrix-core kernel (128-row blocks, 32-key blocks)
                                               ("f32", 64, True, 300, 300), ("f32", 128, False, 200, 264),
                                               ("f32", 100, True, 129, 200), ("f32", 128, True, 640, 700),
-                                              ("f32", 4, False, 33, 40)])
+                                              ("f32", 4, False, 33, 40),
+                                              # wide 16-bit kernel (hd in (128, 256])
+                                              ("bf16", 256, True, 300, 300), ("f16", 256, False, 129, 200),
+                                              ("bf16", 192, True, 640, 700), ("f16", 136, True, 64, 90)])
 def test_flash_attention(dt, hd, causal, T, C):
     rng = np.random.default_rng(1004)
     H = 3
@@ -685,7 +688,8 @@ def test_flash_attention(dt, hd, causal, T, C):
                                f"flash {dt} hd {hd}")
 
 
-@pytest.mark.parametrize("hd,dt", [(64, "bf16"), (128, "bf16"), (96, "bf16"), (24, "bf16"), (128, "f32"), (36, "f32")])
+@pytest.mark.parametrize("hd,dt", [(64, "bf16"), (128, "bf16"), (96, "bf16"), (24, "bf16"), (128, "f32"), (36, "f32"),
+                                   (256, "bf16"), (200, "f16")])
 def test_flash_attention_partial_block_inf_value(hd, dt):
     """Matrix-core path with a partial last key block (C = 200): every query sees
     key C - 1, whose value row is +inf, so every output is +inf.  The block's
@@ -708,7 +712,8 @@ def test_flash_attention_partial_block_inf_value(hd, dt):
 
 @pytest.mark.parametrize("dt,causal,T,C,target,hd", [("bf16", True, 512, 512, 150.0, 128),
                                                      ("f16", False, 256, 384, 22.0, 128),
-                                                     ("bf16", True, 300, 320, 150.0, 96)])
+                                                     ("bf16", True, 300, 320, 150.0, 96),
+                                                     ("bf16", True, 300, 320, 150.0, 256)])
 def test_flash_attention_score_jump(dt, causal, T, C, target, hd):
     """A key late in the sequence whose scaled score with one query is `target`
     above the rest: probabilities against the first block's maximum would

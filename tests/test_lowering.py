@@ -371,13 +371,13 @@ def test_gpt_decode_program_lowers_to_the_decoder(mode, monkeypatch):
         assert not [i for i in body if i.op in (V.OP_GATHER_STRIDED, V.OP_CONVERT, V.OP_COPY_F32) and i.n == cache]
 
 
-@pytest.mark.parametrize("d", [128, 192])
+@pytest.mark.parametrize("d", [128, 192, 512])
 def test_gpt_prefill_attention_gets_the_matrix_core_layout(d):
     """The prefill's attention reads q, k, v as head views of the fused QKV
     projection; the flash fusion gathers them into the matrix-core kernel's
     layout (Q, V plain [H, T, hd], K the transpose of a plain [H, T, hd]), also
-    for a head size (96) that kernel runs zero-padded, and the decoder's tokens
-    and logits are unchanged."""
+    for a head size (96) that kernel runs zero-padded and for the wide kernel's
+    256, and the decoder's tokens and logits are unchanged."""
     from pjrt_amd import configs as CF
     from pjrt_amd import stablehlo_configs as SC
     c = CF.GptConfig(layers=1, d=d, heads=2, mlp=128, vocab=97, prompt=64, steps=4)

@@ -4,6 +4,9 @@
 // p1 = H, p2 = T, p3 = aux descriptor {H, T, C, hd, scale bits, causal, qv, kv, vv}.
 // Tiles are query rows, each head's padded to whole 256-row blocks (H * Tp tiles,
 // Tp = T rounded up to 256; tiles past T are empty); causal masks key c > m + (C - T).
+// Four paths, all in one leaf (flash_attn_tiles): the 16-bit matrix-core path
+// below (attn_block_mfma), f32 operands (attn_block_f32), 16-bit rows wider than
+// 128 (attn_block_h16w), and the general row kernel (attn_rows_generic).
 //
 // Matrix-core path (bf16/f16, hd = 64 or 128, or any other multiple of 8 up to
 // 128 run as the next of the two on zero-padded rows, scale > 0, K read through

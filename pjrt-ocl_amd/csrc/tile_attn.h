@@ -443,7 +443,9 @@ VM_DEV void attn_block_mfma(Args A, uint32_t ti, uint32_t h, uint32_t row0, uint
     const uint32_t q = row0 + ql;
     const float l = l_part[u] + xor32(l_part[u]);
     if (q < T && vrow0 + ql >= vlo && vrow0 + ql < vhi) {
-      const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+      // a row with no visible key (causal, T > C) has l = 0 and O = 0 and stores NaN,
+      // as the reference's kernel does (attention.cl:155) and softmax of a -inf row
+      const float inv = 1.0f / l;
       const uint64_t obase = (uint64_t(h) * T + q) * hd;
 #pragma unroll
       for (int db = 0; db < DB; ++db) {
@@ -520,7 +522,9 @@ VM_DEV void attn_rows_generic(Args A, uint32_t ti, uint32_t lo, uint32_t hi) {
         }
       }
     }
-    const float inv = lrun > 0.0f ? 1.0f / lrun : 0.0f;
+    // a row with no visible key (causal, T > C) has l = 0 and O = 0 and stores NaN,
+    // as the reference's kernel does (attention.cl:155) and softmax of a -inf row
+    const float inv = 1.0f / lrun;
 #pragma unroll
     for (int j = 0; j < kMaxD; ++j) {
       const uint32_t d = lane + 64 * j;
@@ -732,7 +736,9 @@ VM_DEV void attn_block_f32(Args A, uint32_t ti, uint32_t h, uint32_t row0, uint3
   const float l = l_part + xor32(l_part);
   const uint32_t q = qw0 + j, vq = vrow0 + 32 * wave + j;
   if (q < T && vq >= vlo && vq < vhi) {
-    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+    // a row with no visible key (causal, T > C) has l = 0 and O = 0 and stores NaN,
+    // as the reference's kernel does (attention.cl:155) and softmax of a -inf row
+    const float inv = 1.0f / l;
     const uint64_t obase = (uint64_t(h) * T + q) * hd;
 #pragma unroll
     for (int i = 0; i < DB; ++i)
@@ -953,7 +959,9 @@ VM_DEV void attn_block_h16w(Args A, uint32_t ti, uint32_t h, uint32_t row0, uint
   const float l = l_part + xor32(l_part);
   const uint32_t q = qw0 + j, vq = vrow0 + 32 * wave + j;
   if (q < T && vq >= vlo && vq < vhi) {
-    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+    // a row with no visible key (causal, T > C) has l = 0 and O = 0 and stores NaN,
+    // as the reference's kernel does (attention.cl:155) and softmax of a -inf row
+    const float inv = 1.0f / l;
     const uint64_t obase = (uint64_t(h) * T + q) * hd;
 #pragma unroll
     for (int i = 0; i < DB; ++i)

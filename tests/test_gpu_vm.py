@@ -710,6 +710,34 @@ def test_flash_attention_partial_block_inf_value(hd, dt):
     assert np.isposinf(got[0]).all(), int(np.isnan(got[0]).sum())
 
 
+@pytest.mark.parametrize("dt,hd", [("bf16", 128), ("f16", 64), ("bf16", 96), ("f32", 64), ("bf16", 256),
+                                   ("f32", 200)])
+def test_flash_attention_rows_without_keys(dt, hd):
+    """Causal with more queries than keys (T > C): query m sees keys up to
+    m + C - T, so the first T - C rows see none.  The reference's kernel divides
+    by the running sum (0) and the softmax of an all -inf row is NaN, so those
+    rows are NaN; the rest match float64 math.  Each matrix-core path (16-bit,
+    padded head, f32, wide 16-bit) and the row kernel (f32, hd 200)."""
+    rng = np.random.default_rng(1007)
+    H, T, C = 2, 300, 100
+    q, k, v = (rng.standard_normal((H, n, hd)).astype(np.float32) for n in (T, C, C))
+    if dt == "bf16":
+        q, k, v = (vmref.bf16_to_f32(vmref.f32_to_bf16(t)) for t in (q, k, v))
+    elif dt == "f16":
+        q, k, v = (t.astype(np.float16).astype(np.float32) for t in (q, k, v))
+    g = G.Graph()
+    Q, K, Vv = g.input(q.shape, dt), g.input(k.shape, dt), g.input(v.shape, dt)
+    g.output(g.flash_attention(Q, K, Vv, 1.0 / np.sqrt(hd), True, out_dtype="f32"))
+    got, _ = run_both(g.build(), [q, k, v], oracle=None)
+    with np.errstate(invalid="ignore"):
+        want = vmref.attention(q, np.transpose(k, (0, 2, 1)), v, 1.0 / np.sqrt(hd), True)
+    assert np.isnan(want[:, :T - C]).all() and np.isfinite(want[:, T - C:]).all()
+    np.testing.assert_array_equal(np.isnan(got[0]), np.isnan(want))
+    tol = 2e-5 if dt == "f32" else 1e-2
+    err = np.abs(got[0][:, T - C:] - want[:, T - C:]).max() / np.abs(want[:, T - C:]).max()
+    assert err <= tol, err
+
+
 @pytest.mark.parametrize("dt,causal,T,C,target,hd", [("bf16", True, 512, 512, 150.0, 128),
                                                      ("f16", False, 256, 384, 22.0, 128),
                                                      ("bf16", True, 300, 320, 150.0, 96),

@@ -505,6 +505,28 @@ def test_flash_attention_brute_force(causal):
     np.testing.assert_allclose(got, attention_loops(q, k, v, 0.5, causal), rtol=1e-5, atol=1e-6)
 
 
+def test_flash_attention_rows_without_keys_are_nan():
+    """Causal with T > C: query m sees keys j <= m + C - T, so rows m < T - C see
+    none.  The reference's kernel normalises by its running sum, 0 for such a
+    row (pjrt_plugin/kernels/ops/attention.cl:153-157, run_l starts at 0 and
+    only masked keys add 0), so the row is 0 * inf = NaN, as the softmax of an
+    all -inf row is.  The oracle stores NaN there and matches the brute force on
+    the other rows."""
+    rng = np.random.default_rng(16)
+    H, T, C, hd = 2, 7, 3, 4
+    q = rng.standard_normal((H, T, hd)).astype(np.float32)
+    k = rng.standard_normal((H, C, hd)).astype(np.float32)
+    v = rng.standard_normal((H, C, hd)).astype(np.float32)
+    g = G.Graph()
+    Q, K, Vv = g.input(q.shape), g.input(k.shape), g.input(v.shape)
+    g.output(g.flash_attention(Q, K, Vv, 0.5, True))
+    with np.errstate(invalid="ignore", divide="ignore"):
+        (got,) = both(g.build(), [q, k, v])
+    assert np.isnan(got[:, :T - C]).all()
+    want = attention_loops(q[:, T - C:], k, v, 0.5, True)    # the last C rows: query m - (T - C) of a T = C problem
+    np.testing.assert_allclose(got[:, T - C:], want, rtol=1e-5, atol=1e-6)
+
+
 def decode_attention_loops(q, Kt, Vc, k, v, pos, scale):
     """Brute-force decode step with Python loops: keys are the cache columns
     [0, p) then the step's own key, p = pos clamped to [0, C]."""

@@ -501,9 +501,19 @@ def _auto_mma_tile(M: int, N: int, G: int, cfg: DeviceConfig, adt: int = V.DT_F3
     multiples of 8) keeps 256 down to an eighth of the lanes: measured on MI355X,
     bf16 1536^3 0.045 ms against 0.113 with the general tile the count rule picks,
     3072^3 0.073 against 0.248, 2048^3 0.054 against 0.068; at 1024^3 (16 tiles)
-    the general tiles win, 0.030 against 0.034."""
-    if (adt in (V.DT_BF16, V.DT_F16) and not views and K >= 8 and K % 8 == 0 and N % 8 == 0
-            and math.ceil(M / 256) * math.ceil(N / 256) * G * 8 >= cfg.nlanes):
+    the general tiles win, 0.030 against 0.034.  A long K (>= 4096) with at most
+    a sixth of the lanes' worth of 256-wide tiles takes 128-wide tiles instead,
+    which the K split then spreads over the lanes (one 256 x 256 x 4096 tile is
+    ~90 us of one CU's matrix cores): bf16 256x4096x4096 0.058 ms against 0.095,
+    512x2048x4096 0.058 against 0.095, 128x4096x4096 0.051 against 0.059,
+    512x4096x4096 0.079 against 0.088, 512x4096x11008 0.154 against 0.207; with
+    48 or more 256-wide tiles (768x4096x4096, 384x8192x4096) or K <= 3072 the
+    rules above win."""
+    t256 = math.ceil(M / 256) * math.ceil(N / 256) * G
+    fast16 = adt in (V.DT_BF16, V.DT_F16) and not views and K >= 8 and K % 8 == 0 and N % 8 == 0
+    if fast16 and K >= 4096 and t256 * 6 < cfg.nlanes:
+        return 128
+    if fast16 and t256 * 8 >= cfg.nlanes:
         return 256
     for t in (256, 128, 64):
         if math.ceil(M / t) * math.ceil(N / t) * G >= cfg.nlanes:

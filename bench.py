@@ -14,7 +14,7 @@ flash attention (B4 H16 S2048 d128, bf16) as TFLOP/s against their MFMA roofline
 and config 5 (GPT decoder, greedy decode) as tokens/s against the per-token HBM
 bytes.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workloads c1,c2,c3,c3_bf16,c3_f32,c4,c5,copy]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workloads c1,c2,c3,c3_bf16,c3_f32,c4,attn_variants,c5,copy]
                     [--no-cpu] [--skip-c2] [--c2-cache both|cold|warm] [--no-vendor]
 
 "copy" adds a plain device-to-device copy of 128 MiB, the calibration kernel for
@@ -425,24 +425,32 @@ print(2.0 * {M} * {N} * {K} / (e0.elapsed_time(e1) / {steps} * 1e-3) / 1e12)
         return None
 
 
-def bench_attention(rt, steps, warmup, B=4, H=16, S=2048, D=128, with_cpu=False):
+def bench_attention(rt, steps, warmup, B=4, H=16, S=2048, D=128, with_cpu=False, dt="bf16"):
+    """Causal flash attention [B*H, S, D] in `dt` (config 4: bf16, d 128; the
+    f32 and d-256 entries are the same shape on the f32 and wide-head kernels,
+    informational, not BASELINE configs)."""
     from pjrt_amd import graph as G
     from pjrt_amd import vmprogram as V
     rng = np.random.default_rng(1004)
     shape = (B * H, S, D)
-    q, k, v = (V.f32_to_bf16(rng.standard_normal(shape, dtype=np.float32)) for _ in range(3))
+    if dt == "f32":
+        q, k, v = (rng.standard_normal(shape, dtype=np.float32) for _ in range(3))
+        as_f32 = lambda t: t
+    else:
+        q, k, v = (V.f32_to_bf16(rng.standard_normal(shape, dtype=np.float32)) for _ in range(3))
+        as_f32 = V.bf16_to_f32
     g = G.Graph()
-    Q, K, Vv = g.input(shape, "bf16"), g.input(shape, "bf16"), g.input(shape, "bf16")
-    g.output(g.flash_attention(Q, K, Vv, 1.0 / math.sqrt(D), True, out_dtype="bf16"))
+    Q, K, Vv = g.input(shape, dt), g.input(shape, dt), g.input(shape, dt)
+    g.output(g.flash_attention(Q, K, Vv, 1.0 / math.sqrt(D), True, out_dtype=dt))
     lp = rt.compile(g.build())
     dev_in = [rt.to_device(q), rt.to_device(k), rt.to_device(v)]
     dev_out = lp.alloc_outputs()
     ms_step, ms_kernel = time_program(rt, lp, dev_in, dev_out, steps, warmup)
-    o = V.bf16_to_f32(dev_out[0].to_host(np.uint16, shape))
+    o = dev_out[0].to_host(np.float32, shape) if dt == "f32" else V.bf16_to_f32(dev_out[0].to_host(np.uint16, shape))
     # check two heads against float64 math: softmax(scale * q k^T, causal) v
     errs = []
     for h in (0, B * H - 1):
-        qh, kh, vh = (V.bf16_to_f32(t[h]).astype(np.float64) for t in (q, k, v))
+        qh, kh, vh = (as_f32(t[h]).astype(np.float64) for t in (q, k, v))
         s = (qh @ kh.T) / math.sqrt(D)
         s[np.triu_indices(S, 1)] = -np.inf
         p = np.exp(s - s.max(1, keepdims=True))
@@ -453,10 +461,10 @@ def bench_attention(rt, steps, warmup, B=4, H=16, S=2048, D=128, with_cpu=False)
     for buf in dev_in + dev_out:
         buf.free()
     lp.close()
-    res = {"workload": f"C4 causal flash attention B{B} H{H} S{S} d{D} bf16",
+    res = {"workload": f"{'C4 ' if dt == 'bf16' and D == 128 else ''}causal flash attention B{B} H{H} S{S} d{D} {dt}",
            "tflops": round(flops / (ms_step * 1e-3) / 1e12, 2), "ms_per_step": ms_step, "kernel_ms": ms_kernel,
-           "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": MFMA_PEAK_TFLOPS["bf16"],
-                        "unit": "TFLOP/s", "frac": round(tf / MFMA_PEAK_TFLOPS["bf16"], 4)},
+           "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": MFMA_PEAK_TFLOPS[dt],
+                        "unit": "TFLOP/s", "frac": round(tf / MFMA_PEAK_TFLOPS[dt], 4)},
            "max_rel_err_2_heads": max(errs)}
     if with_cpu:
         log("C4 CPU baseline")
@@ -853,6 +861,12 @@ def run(args, rt):
     if "c4" in wl:
         log("C4")
         extra["c4"] = bench_attention(rt, max(5, args.steps // 5), 2, with_cpu=not args.no_cpu)
+    if "c4" in wl or "attn_variants" in wl:
+        # the same causal shape on the f32 kernel and with 256-wide bf16 heads
+        # (informational: not BASELINE configs)
+        log("attention variants")
+        extra["c4_f32"] = bench_attention(rt, max(3, args.steps // 10), 1, dt="f32")
+        extra["c4_d256"] = bench_attention(rt, max(3, args.steps // 10), 1, D=256)
     if "c1" in wl:
         log("C1")
         extra["c1"] = bench_c1(rt, max(5, args.steps), not args.no_cpu)

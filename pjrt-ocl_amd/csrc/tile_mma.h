@@ -74,10 +74,14 @@ struct MmaCfg {
 // Epilogue kinds the lowering fuses into a matmul store (affine, GELU, a binary op
 // with the residual or a per-column operand), evaluated inline by the fast path:
 // a call would force the 256 live accumulator AGPRs through scratch.
+// micro-ops a fast tile's store applies from registers (decoded once per tile)
+constexpr int kFastEpi = 4;
+
 VM_DEV bool epi_inline_ok(Args A, uint32_t epi) {
   if (!epi) return true;
   const VM_K int32_t* e = aux_of(A) + (epi - 1);
   const int nm = e[0];
+  if (nm > kFastEpi) return false;
   for (int k = 0; k < nm; ++k) {
     const uint32_t kind = uint32_t(e[1 + 4 * k]);
     if (!(kind == SUB_AFFINE || kind == SUB_GELU || kind == SUB_COPY || kind <= SUB_DIV || kind == SUB_MAX ||
@@ -85,6 +89,21 @@ VM_DEV bool epi_inline_ok(Args A, uint32_t epi) {
       return false;
   }
   return true;
+}
+
+// epi_inline on four values with one dispatch on the (uniform) kind
+VM_DEV v4f epi_inline4(uint32_t kind, v4f x, v4f y, float s, float t) {
+  switch (kind) {
+    case SUB_AFFINE: return v4f_make(fmaf(x.x, s, t), fmaf(x.y, s, t), fmaf(x.z, s, t), fmaf(x.w, s, t));
+    case SUB_GELU: return v4f_make(gelu(x.x), gelu(x.y), gelu(x.z), gelu(x.w));
+    case SUB_ADD: return v4f_make(x.x + y.x, x.y + y.y, x.z + y.z, x.w + y.w);
+    case SUB_MUL: return v4f_make(x.x * y.x, x.y * y.y, x.z * y.z, x.w * y.w);
+    case SUB_SUB: return v4f_make(x.x - y.x, x.y - y.y, x.z - y.z, x.w - y.w);
+    case SUB_DIV: return v4f_make(x.x / y.x, x.y / y.y, x.z / y.z, x.w / y.w);
+    case SUB_MAX: return v4f_make(fmaxf(x.x, y.x), fmaxf(x.y, y.y), fmaxf(x.z, y.z), fmaxf(x.w, y.w));
+    case SUB_MIN: return v4f_make(fminf(x.x, y.x), fminf(x.y, y.y), fminf(x.z, y.z), fminf(x.w, y.w));
+    default: return x;
+  }
 }
 
 VM_DEV float epi_inline(uint32_t kind, float x, float y, float s, float t) {
@@ -603,7 +622,39 @@ VM_DEV void store_fast(Args A, const MmaDesc& D, const f32x16 (&acc)[4][4], uint
   gbyte* d = D.d + tile0 * (F32 ? 4 : 2);
   const bool bf = D.dt == DT_BF16;
   const VM_K int32_t* e = aux_of(A) + (D.epi ? D.epi - 1 : 0);
-  const int nm = D.epi ? e[0] : 0;
+  const int nm = D.epi ? uni(e[0]) : 0;                   // <= kFastEpi (epi_inline_ok)
+  // the micro-ops, decoded once: scalar registers, not a descriptor read and a
+  // branch per component in every step (bias + GELU on 512x2304x768 bf16: the
+  // store loop held 2561 branches)
+  uint32_t ek[kFastEpi], esrc[kFastEpi];
+  float es4[kFastEpi], et4[kFastEpi];
+  bool src1 = false, src2 = false;
+#pragma unroll
+  for (int k = 0; k < kFastEpi; ++k) {
+    ek[k] = esrc[k] = 0;
+    es4[k] = et4[k] = 0.0f;
+    if (k < nm) {                                         // uniform: never reads past the descriptor
+      ek[k] = uni(e[1 + 4 * k]);
+      esrc[k] = uni(e[2 + 4 * k]);
+      es4[k] = __int_as_float(uni(e[3 + 4 * k]));
+      et4[k] = __int_as_float(uni(e[4 + 4 * k]));
+      src1 |= esrc[k] == 1;
+      src2 |= esrc[k] == 2;
+    }
+  }
+  // Epilogue operands are read ahead of the stores: loads and stores share one
+  // in-order counter, so a load issued after a store makes its wait drain the
+  // store too (read inside the store loop, a bias took 512x2304x768 bf16 from
+  // 31.5 to 57.4 us).  The per-column operand (src 2) covers the same 4 columns
+  // of a thread in every step, so it is read once; the per-element one (src 1)
+  // is read one step ahead.  Ragged edges read clamped (valid) addresses; their
+  // results are not stored.  The step loop stays rolled, one copy per half:
+  // unrolled with the micro-op dispatch in every copy, the tile grew past the
+  // 128 KiB reach of a short branch, and the compiler's long branches reused the
+  // return address registers (s[30:31]) of this leaf without saving them.
+  const uint32_t cth = (threadIdx.x & 63) * 4;                       // the thread's columns in every step
+  v4f ycol = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+  if (src2) ycol = *(const VM_G v4f*)(D.res + uint64_t(RAG ? min(n0 + cth, D.N - 4) : n0 + cth) * 4);
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     __syncthreads();
@@ -617,8 +668,45 @@ VM_DEV void store_fast(Args A, const MmaDesc& D, const f32x16 (&acc)[4][4], uint
         for (int v = 0; v < 16; ++v) st[(r0 + 8 * (v >> 2) + (v & 3)) * LD + c] = acc[2 * h + ii][j][v];
       }
     __syncthreads();
+    // step it: idx = it kBlock + threadIdx.x -> row (rs >> 6) 128 + h 64 + rs % 64, columns c .. c + 3;
+    // the residual (src 1) of step it + 1 is read before step it's store
+    auto res_at = [&](uint32_t it) -> v4f {
+      const uint32_t rs = (it * kBlock + threadIdx.x) >> 6;
+      uint32_t row = (rs >> 6) * 128 + h * 64 + (rs & 63), col = cth;
+      if constexpr (RAG) {
+        row = min(row, D.M - 1 - m0);
+        col = min(col, D.N - 4 - n0);
+      }
+      return *(const VM_G v4f*)(D.res + (tile0 + uint64_t(row) * D.N + col) * 4);
+    };
+    if (nm == 0) {
+      // no epilogue: the plain store (C3)
+#pragma unroll 4
+      for (uint32_t it = 0; it < 32; ++it) {
+        const uint32_t idx = it * kBlock + threadIdx.x;
+        const uint32_t rs = idx >> 6, c = (idx & 63) * 4;
+        const uint32_t row = (rs >> 6) * 128 + h * 64 + (rs & 63);
+        if constexpr (RAG) {
+          if (m0 + row >= D.M || n0 + c >= D.N) continue;
+        }
+        const v4f x = *reinterpret_cast<const v4f*>(st + rs * LD + c);
+        const uint32_t off = row * D.N + c;
+        if constexpr (F32) {
+          *(VM_G v4f*)(d + off * 4u) = x;
+        } else {
+          const uint32_t lo = bf ? pack_bf16x2(x.x, x.y) : (uint32_t(f32_to_f16(x.x)) | uint32_t(f32_to_f16(x.y)) << 16);
+          const uint32_t hi = bf ? pack_bf16x2(x.z, x.w) : (uint32_t(f32_to_f16(x.z)) | uint32_t(f32_to_f16(x.w)) << 16);
+          *(VM_G v2u*)(d + off * 2u) = v2u_make(lo, hi);
+        }
+      }
+      continue;
+    }
+    v4f ynext = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    if (src1) ynext = res_at(0);
 #pragma unroll 2
     for (uint32_t it = 0; it < 32; ++it) {
+      const v4f ycur = ynext;
+      if (src1 && it + 1 < 32) ynext = res_at(it + 1);
       const uint32_t idx = it * kBlock + threadIdx.x;
       const uint32_t rs = idx >> 6, c = (idx & 63) * 4;
       const uint32_t row = (rs >> 6) * 128 + h * 64 + (rs & 63);
@@ -627,17 +715,13 @@ VM_DEV void store_fast(Args A, const MmaDesc& D, const f32x16 (&acc)[4][4], uint
       }
       v4f x = *reinterpret_cast<const v4f*>(st + rs * LD + c);
       const uint32_t off = row * D.N + c;
-      for (int k = 0; k < nm; ++k) {
-        const uint32_t kind = uint32_t(e[1 + 4 * k]), src = uint32_t(e[2 + 4 * k]);
-        const float s = __int_as_float(e[3 + 4 * k]), t = __int_as_float(e[4 + 4 * k]);
-        v4f y = x;
-        if (src == 1) y = *(const VM_G v4f*)(D.res + (tile0 + off) * 4);
-        else if (src == 2) y = *(const VM_G v4f*)(D.res + (uint64_t(n0) + c) * 4);
-        else if (src == 3) y = v4f{s, s, s, s};
-        x.x = epi_inline(kind, x.x, y.x, s, t);
-        x.y = epi_inline(kind, x.y, y.y, s, t);
-        x.z = epi_inline(kind, x.z, y.z, s, t);
-        x.w = epi_inline(kind, x.w, y.w, s, t);
+#pragma unroll
+      for (int k = 0; k < kFastEpi; ++k) {
+        if (k < nm) {
+          const v4f y = esrc[k] == 1 ? ycur : esrc[k] == 2 ? ycol
+                      : esrc[k] == 3 ? v4f_make(es4[k], es4[k], es4[k], es4[k]) : x;
+          x = epi_inline4(ek[k], x, y, es4[k], et4[k]);
+        }
       }
       if constexpr (F32) {
         *(VM_G v4f*)(d + off * 4u) = x;

@@ -377,6 +377,49 @@ def test_gather_scatter_16_byte_runs(ew_ts):
     np.testing.assert_array_equal(got[10], e.transpose(1, 0, 2))
 
 
+@pytest.mark.parametrize("ew_ts", [64, 4096])
+def test_gather_and_dynamic_slice_row_runs(ew_ts):
+    """The 16-byte row-run paths of take_rows (OP_GATHER_INDEX) and dynamic
+    slice / update slice: bf16 rows of 768 and f32 rows of 16 with ids past both
+    ends (clamped), a dynamic slice and update at a row start (aligned runs),
+    and at a column offset of 3 (not 16-byte aligned: the element path).
+    Bit-exact against the oracle, tiles cut inside rows at ew_ts 64."""
+    rng = np.random.default_rng(62)
+    tb16 = V.f32_to_bf16(rng.standard_normal((40, 768)).astype(np.float32))
+    tb32 = rng.standard_normal((30, 16)).astype(np.float32)
+    ids = np.array([5, 0, 39, 77, -3, 12, 30, 1], np.int32)
+    cache = V.f32_to_bf16(rng.standard_normal((4, 48, 64)).astype(np.float32))
+    upd = V.f32_to_bf16(rng.standard_normal((4, 8, 64)).astype(np.float32))
+    small = rng.standard_normal((3, 5, 8)).astype(np.float32)
+    pos = np.array([17], np.int32)
+    g = G.Graph()
+    t16, t32 = g.input(tb16.shape, "bf16"), g.input(tb32.shape)
+    ix = g.input(ids.shape, "i32")
+    cv, uv = g.input(cache.shape, "bf16"), g.input(upd.shape, "bf16")
+    sm = g.input(small.shape)
+    ps = g.reshape(g.input((1,), "i32"), ())
+    zero = g.const(np.array(0, np.int32))
+    three = g.const(np.array(3, np.int32))
+    outs = [g.take_rows(t16, ix), g.take_rows(t32, ix),
+            g.dynamic_slice(cv, [zero, ps, zero], (4, 8, 64)),          # row runs
+            g.dynamic_slice(sm, [zero, zero, three], (3, 5, 4))]        # column offset 3: element path
+    c1 = g.unary("copy", cv)
+    g.dynamic_update_slice(c1, uv, [zero, ps, zero])                    # row runs (scatter)
+    c2 = g.unary("copy", sm)
+    g.dynamic_update_slice(c2, g.slice(sm, (0, 0, 0), (3, 5, 4)), [zero, zero, three])
+    outs += [c1, c2]
+    g.output(*outs)
+    got, want = run_both(g.build(), [tb16, tb32, ids, cache, upd, small, pos], ew_ts=ew_ts)
+    for k, (gv, wv) in enumerate(zip(got, want)):
+        np.testing.assert_array_equal(gv, wv, err_msg=f"output {k}")
+    clip = np.clip(ids, 0, None)
+    np.testing.assert_array_equal(got[0], tb16[np.minimum(clip, 39)])
+    np.testing.assert_array_equal(got[2], cache[:, 17:25])
+    want_c1 = cache.copy()
+    want_c1[:, 17:25] = upd
+    np.testing.assert_array_equal(got[4], want_c1)
+
+
 # --- matmul --------------------------------------------------------------------------------------
 
 @pytest.mark.parametrize("dt", ["f32", "bf16"])

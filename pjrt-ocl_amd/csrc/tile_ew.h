@@ -133,10 +133,25 @@ VM_DEV void ew_h16_range(gbyte* dp, const gbyte* ap, const gbyte* bp, uint64_t e
 
 // Strided view index (the reference's vmo_view_idx, ew.cl:174-185): element i of
 // a view {rank, dims[rank], strides[rank], src_off} -> flat source index.
+// Below 2^32 (every element index a tensor of this runtime holds) the
+// quotients and remainders are taken in 32 bits: a 64-bit division is a long
+// software sequence, and with two viewed operands of rank 3 it made an
+// elementwise tile of 4096 elements cost 20-45 us (C5 prefill's broadcast bias
+// adds and the attention output's transposed read).
 VM_DEV int64_t view_index(const VM_K int32_t* aux, uint32_t off, uint64_t i) {
   const VM_K int32_t* x = aux + off;
   const int rank = x[0];
-  int64_t rem = int64_t(i), o = x[1 + 2 * rank];
+  int64_t o = x[1 + 2 * rank];
+  if (i <= 0xFFFFFFFFull) {
+    uint32_t rem = uint32_t(i);
+    for (int e = rank - 1; e >= 0; --e) {
+      const uint32_t dim = uint32_t(x[1 + e]);              // dims are positive
+      o += int64_t(rem % dim) * int64_t(x[1 + rank + e]);
+      rem /= dim;
+    }
+    return o;
+  }
+  int64_t rem = int64_t(i);
   for (int e = rank - 1; e >= 0; --e) {
     const int64_t dim = x[1 + e];
     o += (rem % dim) * int64_t(x[1 + rank + e]);
@@ -225,6 +240,8 @@ VM_DEV bool cmp_pred(uint32_t p, T x, T y) {
 // Numeric conversion (ew.cl:532-588): integer <-> integer through 64 bits keeping
 // the low bits; otherwise through double, with float -> int saturating and NaN -> 0
 // (XLA's convert semantics), bool = (v != 0).
+VM_DEV float quiet_nan(float v) { return v != v ? __uint_as_float(__float_as_uint(v) | 0x400000u) : v; }
+
 VM_DEV void convert_elem(const gbyte* a, uint32_t adt, gbyte* d, uint32_t dt, uint64_t i) {
   const bool a_int = adt == DT_I32 || adt == DT_U32 || adt == DT_I64 || adt == DT_BOOL;
   const bool d_int = dt == DT_I32 || dt == DT_U32 || dt == DT_I64;
@@ -312,16 +329,28 @@ VM_DEV void ew_special(Args A, uint32_t ti, uint64_t e0, uint64_t e1) {
       return;
     }
     case SUB_CONVERT:
-      if (adt == DT_F32 && dt == DT_BF16 && ((uintptr_t(a) | uintptr_t(d)) & 15) == 0) {
-        const uint64_t nv = (e1 - e0) >> 2;
-        const VM_G v4f* a4 = (const VM_G v4f*)(gcast<float>(a) + e0);
-        VM_G v2u* d4 = (VM_G v2u*)(gcast<uint16_t>(d) + e0);
-        for (uint64_t j = tid; j < nv; j += kBlock) {
-          const v4f x = a4[j];
-          d4[j] = v2u_make(pack_bf16x2(x.x, x.y), pack_bf16x2(x.z, x.w));
+      // f32 / bf16 / f16 to one another: four elements a step through ld4 / st4,
+      // four steps' loads issued before the first store (one element a step, each
+      // waiting on its own load, a tile of 4096 cost 9-10 us).  The reference
+      // converts through a double (ew.cl:556-576), which sets a signalling NaN's
+      // quiet bit and keeps its payload; the widening here is exact, so the quiet
+      // bit is set explicitly.
+      if ((adt == DT_F32 || adt == DT_BF16 || adt == DT_F16) && (dt == DT_F32 || dt == DT_BF16 || dt == DT_F16) &&
+          (e0 & 3) == 0 && ((uintptr_t(a) | uintptr_t(d)) & 15) == 0) {
+        constexpr uint32_t U = 4;
+        const uint64_t q1 = e1 >> 2;
+        for (uint64_t q = (e0 >> 2) + tid; q < q1; q += U * kBlock) {
+          v4f x[U];
+#pragma unroll
+          for (uint32_t k = 0; k < U; ++k)
+            if (q + k * kBlock < q1) x[k] = ld4(a, adt, 4 * (q + k * kBlock));
+#pragma unroll
+          for (uint32_t k = 0; k < U; ++k)
+            if (q + k * kBlock < q1)
+              st4(d, dt, 4 * (q + k * kBlock), v4f_make(quiet_nan(x[k].x), quiet_nan(x[k].y),
+                                                        quiet_nan(x[k].z), quiet_nan(x[k].w)));
         }
-        for (uint64_t i = e0 + (nv << 2) + tid; i < e1; i += kBlock)
-          gcast<uint16_t>(d)[i] = f32_to_bf16(gcast<float>(a)[i]);
+        for (uint64_t i = (q1 << 2) + tid; i < e1; i += kBlock) convert_elem(a, adt, d, dt, i);
         return;
       }
       for (uint64_t i = e0 + tid; i < e1; i += kBlock) convert_elem(a, adt, d, dt, i);
@@ -405,19 +434,40 @@ VM_DEV void ew_float_scalar(Args A, uint32_t ti, uint64_t e0, uint64_t e1) {
   const bool viewable = is_bin(sub) || is_un(sub);
   const uint32_t av = viewable ? t.p[2] : 0u, bv = viewable ? t.p[3] : 0u;
   const VM_K int32_t* aux = aux_of(A);
-  for (uint64_t i = e0 + threadIdx.x; i < e1; i += kBlock) {
-    float r;
-    if (sub == SUB_IOTA_FLAT) {
-      r = float(i);
-    } else if (sub == SUB_FILL) {
-      r = s;
-    } else {
-      const float x = load_f(a, dt, av ? uint64_t(view_index(aux, av - 1, i)) : i);
-      if (sub == SUB_AFFINE) r = fmaf(x, s, tt);
-      else if (is_bin(sub)) r = ew_bin(sub, x, load_f(b, dt, bv ? uint64_t(view_index(aux, bv - 1, i)) : i));
-      else r = ew_un(sub, x);
+  const bool ld_a = sub != SUB_IOTA_FLAT && sub != SUB_FILL, ld_b = is_bin(sub);
+  // four elements a step: their (viewed) loads are issued before the first result
+  // is computed, the result code itself stays rolled (libm-heavy subops)
+  constexpr uint32_t U = 4;
+  for (uint64_t i0 = e0 + threadIdx.x; i0 < e1; i0 += U * kBlock) {
+    float xa[U], xb[U];
+#pragma unroll
+    for (uint32_t k = 0; k < U; ++k) {
+      const uint64_t i = i0 + k * kBlock;
+      xa[k] = xb[k] = 0.0f;
+      if (i < e1 && ld_a) {
+        xa[k] = load_f(a, dt, av ? uint64_t(view_index(aux, av - 1, i)) : i);
+        if (ld_b) xb[k] = load_f(b, dt, bv ? uint64_t(view_index(aux, bv - 1, i)) : i);
+      }
     }
-    store_f(d, dt, i, r);
+#pragma unroll 1
+    for (uint32_t k = 0; k < U; ++k) {
+      const uint64_t i = i0 + k * kBlock;
+      if (i >= e1) break;
+      const float x = k == 0 ? xa[0] : k == 1 ? xa[1] : k == 2 ? xa[2] : xa[3];
+      float r;
+      if (sub == SUB_IOTA_FLAT) {
+        r = float(i);
+      } else if (sub == SUB_FILL) {
+        r = s;
+      } else if (sub == SUB_AFFINE) {
+        r = fmaf(x, s, tt);
+      } else if (ld_b) {
+        r = ew_bin(sub, x, k == 0 ? xb[0] : k == 1 ? xb[1] : k == 2 ? xb[2] : xb[3]);
+      } else {
+        r = ew_un(sub, x);
+      }
+      store_f(d, dt, i, r);
+    }
   }
 }
 

@@ -248,26 +248,6 @@ VM_TILE void red_strided_tiles(Args A, uint32_t ti, uint32_t lo, uint32_t hi) {
 template <int NV>
 struct Row { v4f v[NV]; };
 
-VM_DEV v4f ld4(const gbyte* p, uint32_t dt, uint64_t e) {   // e: element index (multiple of 4)
-  if (dt == DT_F32) return *(const VM_G v4f*)(gcast<float>(p) + e);
-  const v2u w = *(const VM_G v2u*)(gcast<uint16_t>(p) + e);
-  if (dt == DT_BF16)
-    return v4f_make(__uint_as_float(w.x << 16), __uint_as_float(w.x & 0xFFFF0000u),
-                       __uint_as_float(w.y << 16), __uint_as_float(w.y & 0xFFFF0000u));
-  return v4f_make(f16_to_f32(w.x & 0xFFFF), f16_to_f32(w.x >> 16), f16_to_f32(w.y & 0xFFFF),
-                     f16_to_f32(w.y >> 16));
-}
-VM_DEV void st4(gbyte* p, uint32_t dt, uint64_t e, v4f v) {
-  if (dt == DT_F32) {
-    *(VM_G v4f*)(gcast<float>(p) + e) = v;
-  } else if (dt == DT_BF16) {
-    *(VM_G v2u*)(gcast<uint16_t>(p) + e) = v2u_make(pack_bf16x2(v.x, v.y), pack_bf16x2(v.z, v.w));
-  } else {
-    *(VM_G v2u*)(gcast<uint16_t>(p) + e) = v2u_make(f32_to_f16(v.x) | (uint32_t(f32_to_f16(v.y)) << 16),
-                                                         f32_to_f16(v.z) | (uint32_t(f32_to_f16(v.w)) << 16));
-  }
-}
-
 template <int NV>
 VM_DEV void row_load(Row<NV>& r, const gbyte* p, uint32_t dt, uint64_t base, uint32_t nv4) {
 #pragma unroll

@@ -168,6 +168,28 @@ VM_DEV void store_f(gbyte* base, uint32_t dt, uint64_t i, float v) {
   }
 }
 
+// Four f32 / bf16 / f16 elements e..e+3 as f32 (e a multiple of 4, base 16-byte
+// aligned) and back.
+VM_DEV v4f ld4(const gbyte* p, uint32_t dt, uint64_t e) {   // e: element index (multiple of 4)
+  if (dt == DT_F32) return *(const VM_G v4f*)(gcast<float>(p) + e);
+  const v2u w = *(const VM_G v2u*)(gcast<uint16_t>(p) + e);
+  if (dt == DT_BF16)
+    return v4f_make(__uint_as_float(w.x << 16), __uint_as_float(w.x & 0xFFFF0000u),
+                       __uint_as_float(w.y << 16), __uint_as_float(w.y & 0xFFFF0000u));
+  return v4f_make(f16_to_f32(w.x & 0xFFFF), f16_to_f32(w.x >> 16), f16_to_f32(w.y & 0xFFFF),
+                     f16_to_f32(w.y >> 16));
+}
+VM_DEV void st4(gbyte* p, uint32_t dt, uint64_t e, v4f v) {
+  if (dt == DT_F32) {
+    *(VM_G v4f*)(gcast<float>(p) + e) = v;
+  } else if (dt == DT_BF16) {
+    *(VM_G v2u*)(gcast<uint16_t>(p) + e) = v2u_make(pack_bf16x2(v.x, v.y), pack_bf16x2(v.z, v.w));
+  } else {
+    *(VM_G v2u*)(gcast<uint16_t>(p) + e) = v2u_make(f32_to_f16(v.x) | (uint32_t(f32_to_f16(v.y)) << 16),
+                                                         f32_to_f16(v.z) | (uint32_t(f32_to_f16(v.w)) << 16));
+  }
+}
+
 // ---- wave64 reductions through DPP ----------------------------------------------
 // quad_perm [1,0,3,2] and [2,3,0,1], then row_ror 4 and 8: every lane of a
 // 16-lane row holds the row total; four v_readlane_b32 combine the rows.

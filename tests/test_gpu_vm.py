@@ -144,6 +144,57 @@ def test_compare_select_convert_bitcast_isfinite():
         np.testing.assert_array_equal(gv.view(np.uint8), wv.view(np.uint8), err_msg=f"output {k}")
 
 
+@pytest.mark.parametrize("ew_ts", [256, 64])
+def test_convert_between_float_types(ew_ts):
+    """f32 / bf16 / f16 to one another (four elements a step, ragged tail one at a
+    time), bit-exact with the oracle: NaN, Inf, -0, f16 overflow and f16 denormals
+    in the f32 input, every bit pattern class (signalling NaNs too) in the 16-bit
+    inputs."""
+    rng = np.random.default_rng(14)
+    n = 4099
+    a = (rng.standard_normal(n) * 100).astype(np.float32)
+    a[::11] = np.nan
+    a[::13] = -np.inf
+    a[::17] = 7.0e4
+    a[::19] = 3.0e-6
+    a[::23] = -0.0
+    hb = rng.integers(0, 2 ** 16, n, dtype=np.uint64).astype(np.uint16)
+    hf = rng.integers(0, 2 ** 16, n, dtype=np.uint64).astype(np.uint16).view(np.float16)
+    g = G.Graph()
+    x, xb, xf = g.input((n,)), g.input((n,), "bf16"), g.input((n,), "f16")
+    g.output(g.convert(x, "bf16"), g.convert(x, "f16"), g.convert(xb, "f32"), g.convert(xb, "f16"),
+             g.convert(xf, "f32"), g.convert(xf, "bf16"))
+    ins = [a.view(np.uint32)] * 2 + [hb] * 2 + [hf.view(np.uint16)] * 2
+    got, want = run_both(g.build(), [a, hb, hf], ew_ts=ew_ts)
+    bad = {}
+    for k, (gv, wv) in enumerate(zip(got, want)):
+        u = np.uint16 if gv.itemsize == 2 else np.uint32
+        gb, wb = gv.view(u), wv.view(u)
+        idx = np.nonzero(gb != wb)[0]
+        if idx.size:
+            bad[k] = (idx.size, [(hex(int(ins[k][i])), hex(int(gb[i])), hex(int(wb[i]))) for i in idx[:4]])
+    assert not bad, bad
+
+
+@pytest.mark.parametrize("ew_ts", [256, 64])
+def test_ew_viewed_operands(ew_ts):
+    """f32 elementwise ops reading a transposed view and a broadcast view in place
+    (the per-element path, four elements' loads a step) over a ragged size,
+    against the oracle."""
+    rng = np.random.default_rng(15)
+    A, B, C = 7, 33, 19
+    at = rng.standard_normal((C, B, A)).astype(np.float32)
+    bias = rng.standard_normal(B).astype(np.float32)
+    g = G.Graph()
+    xt, bb = g.input((C, B, A)), g.input((B,))
+    x = g.transpose_view(xt, (2, 1, 0))                        # [A,B,C] view of [C,B,A]
+    y = g.broadcast_view(bb, (A, B, C), (1,))
+    g.output(g.add(x, y), g.mul(y, x), g.sub(x, y), g.unary("exp", x), g.unary("tanh", y))
+    got, want = run_both(g.build(), [at, bias], ew_ts=ew_ts)
+    for k, (gv, wv) in enumerate(zip(got, want)):
+        assert_rel(gv, wv, 4e-6, 1e-6, f"op {k}")
+
+
 def test_convert_f32_to_bf16_bit_patterns():
     """f32 -> bf16 rounds to nearest even, bit-exact with the closed-form rule
     (u + 0x7fff + ((u >> 16) & 1)) >> 16 (vm_common.cl:66-70), NaN kept a quiet NaN,

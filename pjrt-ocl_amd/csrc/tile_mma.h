@@ -290,21 +290,28 @@ VM_TILE v4u gather_chunk(Args A, const gbyte* base, uint32_t view, uint64_t lin,
 // ---------------------------------------------------------------------------------
 // 16-bit operands (bf16 / f16)
 // ---------------------------------------------------------------------------------
-constexpr int kBK16 = 32;                 // K slab (elements)
-constexpr int kLdA16 = kBK16 + 8;         // A row stride in LDS (elements): 80 B
+constexpr int kBK16 = 32;                 // K-split granularity (elements)
+// K slab of a general tile: every tile edge stages T * kBK = 8192 elements per
+// operand and slab (four 16-byte loads per thread), so the small tiles of
+// skinny products (a few hundred rows, prefill-style) take one memory round
+// trip, LDS store and block barrier per 128 k rather than per 32.  With 32-deep
+// slabs a 64 x 64 tile of a 512 x 768 x 3072 bf16 product took 93 us.
 template <int T>
 struct Lds16 {
+  static constexpr int kBK = T == 64 ? 128 : T == 128 ? 64 : 32;
+  static constexpr int kLdA = kBK + 8;    // A row stride (elements): 16-byte aligned, padded against bank conflicts
   static constexpr int kLdB = T + 4;      // B row stride (elements): 8-byte aligned rows
-  static constexpr int kA = T * kLdA16;   // elements
-  static constexpr int kB = kBK16 * kLdB;
+  static constexpr int kA = T * kLdA;     // elements
+  static constexpr int kB = kBK * kLdB;
   static constexpr int kBuf = kA + kB;
   static constexpr int kBytes = 2 * kBuf * 2;   // double buffered, 2 bytes each
 };
 
 template <int T>
 struct Stage16 {
-  // A: T rows x 32 k = T*4 chunks of 8 elements; B: 32 rows x T cols = 4T chunks.
-  static constexpr int kChunks = T * 4 / kBlock;
+  // A: T rows x kBK k in chunks of 8 elements; B: kBK rows x T cols, the same count.
+  static constexpr int kBK = Lds16<T>::kBK, kRowChunks = kBK / 8;
+  static constexpr int kChunks = T * kRowChunks / kBlock;
   v4u ra[kChunks];
   v4u rb[kChunks];
 
@@ -312,7 +319,7 @@ struct Stage16 {
 #pragma unroll
     for (int j = 0; j < kChunks; ++j) {
       const uint32_t c = threadIdx.x + j * kBlock;
-      const uint32_t m = m0 + (c >> 2), k = k0 + (c & 3) * 8;
+      const uint32_t m = m0 + c / kRowChunks, k = k0 + (c % kRowChunks) * 8;
       const uint64_t lin = (uint64_t(g) * D.M + m) * D.K + k;
       const bool in = m < D.M && k < D.k1;
       if (vec) ra[j] = in ? gld((const VM_G v4u*)(gcast<uint16_t>(D.a) + lin)) : v4u_make(0, 0, 0, 0);
@@ -334,7 +341,7 @@ struct Stage16 {
 #pragma unroll
     for (int j = 0; j < kChunks; ++j) {
       const uint32_t c = threadIdx.x + j * kBlock;
-      *reinterpret_cast<v4u*>(la + (c >> 2) * kLdA16 + (c & 3) * 8) = ra[j];
+      *reinterpret_cast<v4u*>(la + (c / kRowChunks) * Lds16<T>::kLdA + (c % kRowChunks) * 8) = ra[j];
     }
 #pragma unroll
     for (int j = 0; j < kChunks; ++j) {
@@ -408,7 +415,8 @@ VM_TILE void mma_tile16(Args A, const MmaDesc* Dp, uint32_t tile) {
 #pragma unroll
     for (int j = 0; j < C::kBN; ++j) acc[i][j] = f32x16{};
 
-  const uint32_t nk = (D.k1 - D.k0 + kBK16 - 1) / kBK16;
+  constexpr int kBK = Lds16<T>::kBK;
+  const uint32_t nk = (D.k1 - D.k0 + kBK - 1) / kBK;
   Stage16<T> st;
   st.load(A, D, g, m0, n0, D.k0, vec);
   __syncthreads();                      // previous user of the LDS is done
@@ -416,16 +424,16 @@ VM_TILE void mma_tile16(Args A, const MmaDesc* Dp, uint32_t tile) {
   __syncthreads();
   for (uint32_t ks = 0; ks < nk; ++ks) {
     const uint16_t* cur = lds + (ks & 1) * Lds16<T>::kBuf;
-    if (ks + 1 < nk) st.load(A, D, g, m0, n0, D.k0 + (ks + 1) * kBK16, vec);
+    if (ks + 1 < nk) st.load(A, D, g, m0, n0, D.k0 + (ks + 1) * kBK, vec);
     const uint16_t* la = cur;
     const uint16_t* lb = cur + Lds16<T>::kA;
 #pragma unroll
-    for (int kk = 0; kk < kBK16; kk += 16) {
+    for (int kk = 0; kk < kBK; kk += 16) {
       const uint32_t kq = kk + (lane >> 5) * 8;
       u16x8 af[C::kBM], bf[C::kBN];
 #pragma unroll
       for (int bm = 0; bm < C::kBM; ++bm)
-        af[bm] = *reinterpret_cast<const u16x8*>(la + (wm * (T / 2) + bm * 32 + (lane & 31)) * kLdA16 + kq);
+        af[bm] = *reinterpret_cast<const u16x8*>(la + (wm * (T / 2) + bm * 32 + (lane & 31)) * Lds16<T>::kLdA + kq);
 #pragma unroll
       for (int bn = 0; bn < C::kBN; ++bn) {
         const uint32_t cidx = wn * (T / 2) + bn * 32 + (lane & 31);
@@ -1120,7 +1128,8 @@ VM_LEAF void mma_tile32_fast(Args A, const MmaDesc* Dp, uint32_t tile) {
 }
 
 // LDS bytes the matmul tile op needs at its largest tile.
-constexpr int kMmaLdsBytes0 = Lds16<256>::kBytes > Lds32<256>::kBytes ? Lds16<256>::kBytes : Lds32<256>::kBytes;
+constexpr int kMaxI(int a, int b) { return a > b ? a : b; }
+constexpr int kMmaLdsBytes0 = kMaxI(kMaxI(Lds16<256>::kBytes, Lds16<128>::kBytes), kMaxI(Lds16<64>::kBytes, Lds32<256>::kBytes));
 constexpr int kMmaLdsBytes1 = kFastLdsBytes > kMmaLdsBytes0 ? kFastLdsBytes : kMmaLdsBytes0;
 constexpr int kMmaLdsBytes = kF32FastLdsBytes > kMmaLdsBytes1 ? kF32FastLdsBytes : kMmaLdsBytes1;
 

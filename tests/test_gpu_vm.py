@@ -178,19 +178,28 @@ def test_convert_between_float_types(ew_ts):
 
 @pytest.mark.parametrize("ew_ts", [256, 64])
 def test_ew_viewed_operands(ew_ts):
-    """f32 elementwise ops reading a transposed view and a broadcast view in place
-    (the per-element path, four elements' loads a step) over a ragged size,
-    against the oracle."""
+    """f32 elementwise ops reading views in place, against the oracle: a
+    transposed view and a middle-axis broadcast (per-element path, decoded
+    index maps), row and matrix broadcasts with source offsets that are
+    multiples of four (16-byte periodic path) and one that is not (per-element
+    again)."""
     rng = np.random.default_rng(15)
-    A, B, C = 7, 33, 19
+    A, B, C = 7, 33, 20
     at = rng.standard_normal((C, B, A)).astype(np.float32)
+    xp = rng.standard_normal((A, B, C)).astype(np.float32)
     bias = rng.standard_normal(B).astype(np.float32)
+    row = rng.standard_normal(C + 2).astype(np.float32)
+    mat = rng.standard_normal(B * C + 4).astype(np.float32)
     g = G.Graph()
-    xt, bb = g.input((C, B, A)), g.input((B,))
+    xt, xc, bb, rr, mm = g.input((C, B, A)), g.input((A, B, C)), g.input((B,)), g.input((C + 2,)), g.input((B * C + 4,))
     x = g.transpose_view(xt, (2, 1, 0))                        # [A,B,C] view of [C,B,A]
     y = g.broadcast_view(bb, (A, B, C), (1,))
-    g.output(g.add(x, y), g.mul(y, x), g.sub(x, y), g.unary("exp", x), g.unary("tanh", y))
-    got, want = run_both(g.build(), [at, bias], ew_ts=ew_ts)
+    r0 = g.view(rr, (A, B, C), (0, 0, 1))                      # row broadcast, P = C
+    m4 = g.view(mm, (A, B, C), (0, C, 1), 4)                   # matrix broadcast, P = B*C, offset 4
+    r2 = g.view(rr, (A, B, C), (0, 0, 1), 2)                   # offset 2: not 16-byte aligned
+    g.output(g.add(x, y), g.mul(y, x), g.sub(x, y), g.unary("exp", x), g.unary("tanh", y),
+             g.add(xc, r0), g.mul(m4, xc), g.sub(r0, m4), g.maximum(xc, r2), g.div(r2, r0), g.minimum(m4, xc))
+    got, want = run_both(g.build(), [at, xp, bias, row, mat], ew_ts=ew_ts)
     for k, (gv, wv) in enumerate(zip(got, want)):
         assert_rel(gv, wv, 4e-6, 1e-6, f"op {k}")
 

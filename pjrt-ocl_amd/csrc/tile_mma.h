@@ -300,7 +300,10 @@ template <int T>
 struct Lds16 {
   static constexpr int kBK = T == 64 ? 128 : T == 128 ? 64 : 32;
   static constexpr int kLdA = kBK + 8;    // A row stride (elements): 16-byte aligned, padded against bank conflicts
-  static constexpr int kLdB = T + 4;      // B row stride (elements): 8-byte aligned rows
+  // B row stride (elements): 8-byte aligned rows, (T + 32) / 2 = 16 or 48 dwords
+  // mod 64, so the four rows x two 16-column halves a half wave's transposed
+  // read touches fall on eight distinct 8-bank groups
+  static constexpr int kLdB = T + 32;
   static constexpr int kA = T * kLdA;     // elements
   static constexpr int kB = kBK * kLdB;
   static constexpr int kBuf = kA + kB;
@@ -352,6 +355,11 @@ struct Stage16 {
     }
   }
 };
+
+typedef __attribute__((address_space(3))) uint8_t lds_u8;
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+typedef __attribute__((address_space(3))) u16x8 lds_u16x8;
 
 template <bool BF16>
 VM_DEV f32x16 mfma16(const u16x8& a, const u16x8& b, const f32x16& c) {
@@ -434,13 +442,19 @@ VM_TILE void mma_tile16(Args A, const MmaDesc* Dp, uint32_t tile) {
 #pragma unroll
       for (int bm = 0; bm < C::kBM; ++bm)
         af[bm] = *reinterpret_cast<const u16x8*>(la + (wm * (T / 2) + bm * 32 + (lane & 31)) * Lds16<T>::kLdA + kq);
+      // B fragment: column lane % 32, k = kq .. kq + 7, as two ds_read_b64_tr_b16.
+      // In each group of 16 lanes, lane 4e + q points at row kq + e (+ 4),
+      // columns c0 + 4q .. + 3 (c0: the group's 16 columns); the transposed read
+      // gives lane i column c0 + i at the four rows.  (Eight 16-bit LDS reads
+      // per fragment made the LDS the bound of the small tiles.)
 #pragma unroll
       for (int bn = 0; bn < C::kBN; ++bn) {
-        const uint32_t cidx = wn * (T / 2) + bn * 32 + (lane & 31);
-        u16x8 v;
-#pragma unroll
-        for (int q = 0; q < 8; ++q) v[q] = lb[(kq + q) * Lds16<T>::kLdB + cidx];
-        bf[bn] = v;
+        const uint32_t j = lane & 15;
+        const uint32_t col = wn * (T / 2) + bn * 32 + (lane & 16) + 4 * (j & 3);
+        const uint16_t* p = lb + (kq + (j >> 2)) * Lds16<T>::kLdB + col;
+        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)p);
+        const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p + 4 * Lds16<T>::kLdB));
+        bf[bn] = __builtin_bit_cast(u16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
       }
 #pragma unroll
       for (int bm = 0; bm < C::kBM; ++bm)
@@ -484,10 +498,6 @@ constexpr int kFastLdsBytes = 2 * int(kFStage) > kFStoreBytes ? 2 * int(kFStage)
 // so rows of opposite parity never meet.
 VM_DEV uint32_t aswz(uint32_t r) { return (((r >> 1) & 3) << 1) | ((r >> 3) & 1); }
 
-typedef __attribute__((address_space(3))) uint8_t lds_u8;
-typedef short s16x4 __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
-typedef __attribute__((address_space(3))) u16x8 lds_u16x8;
 
 // One 16-byte global -> LDS transfer per lane: lane l of the wave writes LDS bytes
 // [lds + 16 l, +16) with base[voff].  Issued from asm: the compiler, which cannot

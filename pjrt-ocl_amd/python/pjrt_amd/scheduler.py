@@ -508,11 +508,15 @@ def _auto_mma_tile(M: int, N: int, G: int, cfg: DeviceConfig, adt: int = V.DT_F3
     512x2048x4096 0.058 against 0.095, 128x4096x4096 0.051 against 0.059,
     512x4096x4096 0.079 against 0.088, 512x4096x11008 0.154 against 0.207; with
     48 or more 256-wide tiles (768x4096x4096, 384x8192x4096) or K <= 3072 the
-    rules above win."""
+    rules above win.  Where the 64-wide tiles fit the lanes in one round they
+    take it (their 128-deep K slabs and transposed B reads): 256x4096x4096
+    0.042 ms against 0.053 with 128, 128x4096x4096 0.036 against 0.049; with
+    more than a round of them (512x4096x11008) 128 stays ahead, 0.125 against
+    0.186."""
     t256 = math.ceil(M / 256) * math.ceil(N / 256) * G
     fast16 = adt in (V.DT_BF16, V.DT_F16) and not views and K >= 8 and K % 8 == 0 and N % 8 == 0
     if fast16 and K >= 4096 and t256 * 6 < cfg.nlanes:
-        return 128
+        return 64 if math.ceil(M / 64) * math.ceil(N / 64) * G <= cfg.nlanes else 128
     if fast16 and t256 * 8 >= cfg.nlanes:
         return 256
     for t in (256, 128, 64):

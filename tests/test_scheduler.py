@@ -185,19 +185,25 @@ def test_mma_autotile_prefers_fast_16bit_tile():
 
 def test_mma_autotile_long_k_skinny_takes_split_128():
     """A long K (>= 4096) with few 256-wide tiles (fewer than a sixth of the
-    lanes) takes 128-wide tiles, which the K split spreads over the lanes; 48 or
-    more 256-wide tiles, or a shorter K, keep the other rules."""
+    lanes) takes 128-wide tiles, which the K split spreads over the lanes, or
+    64-wide ones where those fit the lanes in one round; 48 or more 256-wide
+    tiles, or a shorter K, keep the other rules."""
     def task(M, K, N, dt="bf16"):
         g = G.Graph()
         g.output(g.dot(g.input((M, K), dt), g.input((K, N), dt)))
         return S.schedule_program(g.build(), S.DeviceConfig(nlanes=256, mma_t=128)).tasks[0]
     edge = lambda t: V.MMA_CODE_TILE[(t.p3 >> 24) & 0xF]
     split = lambda t: 1 << (t.p3 >> 28)
-    for M, K, N in ((256, 4096, 4096), (512, 4096, 2048), (128, 4096, 4096), (512, 4096, 4096), (512, 11008, 4096)):
+    for M, K, N in ((512, 4096, 4096), (512, 11008, 4096)):
         t = task(M, K, N)
         assert edge(t) == 128, (M, K, N)
         tiles = -(-M // 128) * -(-N // 128)
         assert split(t) > 1 and tiles * split(t) <= 256, (M, K, N, split(t))
+    for M, K, N in ((256, 4096, 4096), (512, 4096, 2048), (128, 4096, 4096)):   # 256, 256, 128 tiles of 64
+        t = task(M, K, N)
+        assert edge(t) == 64, (M, K, N)
+        tiles = -(-M // 64) * -(-N // 64)
+        assert tiles * split(t) <= 256 and (split(t) > 1) == (tiles * 2 <= 256), (M, K, N, split(t))
     assert edge(task(768, 4096, 4096)) == 256           # 48 tiles of 256
     assert edge(task(384, 4096, 8192)) == 256           # 64 tiles of 256
     assert edge(task(256, 3072, 768)) != 128            # K below 4096

@@ -124,6 +124,37 @@ VM_DEV bool gather_wide(const VM_K int32_t* aux, uint32_t x, gbyte* d, const gby
   return true;
 }
 
+// A view whose every stride is 0 (or whose dim is 1): one source element
+// broadcast, as the lowering emits for a constant broadcast into a buffer (the
+// decoder's zero-filled K/V caches).  One load, then 16-byte stores of the
+// replicated bits; the element path took 126 us for a 960 KB cache.  Returns
+// false when the view does not qualify.
+VM_DEV bool gather_splat(const VM_K int32_t* aux, uint32_t x, gbyte* d, const gbyte* a, uint64_t e0, uint64_t e1,
+                         uint32_t es) {
+  const int rank = aux[x];
+  if (rank < 0 || rank > 8 || 16 % es || (uintptr_t(d) & 15)) return false;
+  for (int e = 0; e < rank; ++e)
+    if (aux[x + 1 + rank + e] != 0 && aux[x + 1 + e] != 1) return false;
+  const uint64_t per = 16 / es;
+  if (e0 % per) return false;
+  const int64_t off = aux[x + 1 + 2 * rank];
+  uint32_t lo, hi;
+  if (es == 8) {
+    const uint64_t v = gcast<uint64_t>(a)[off];
+    lo = uint32_t(v);
+    hi = uint32_t(v >> 32);
+  } else {
+    lo = hi = es == 4 ? gcast<uint32_t>(a)[off] : es == 2 ? uint32_t(gcast<uint16_t>(a)[off]) * 0x00010001u
+                                                         : uint32_t(a[off]) * 0x01010101u;
+  }
+  const v4u pat = v4u_make(lo, hi, lo, hi);
+  const uint64_t c1 = e1 / per;
+  VM_G v4u* dv = (VM_G v4u*)d;
+  for (uint64_t c = e0 / per + threadIdx.x; c < c1; c += kBlock) dv[c] = pat;
+  for (uint64_t i = c1 * per + threadIdx.x; i < e1; i += kBlock) copy_elem(d, i, a, uint64_t(off), es);
+  return true;
+}
+
 VM_TILE void gather_tiles(Args A, uint32_t ti, uint32_t lo, uint32_t hi, bool scatter) {
   A = uargs(A);
   const VM_K Task& t = task_of(A, ti);
@@ -138,6 +169,7 @@ VM_TILE void gather_tiles(Args A, uint32_t ti, uint32_t lo, uint32_t hi, bool sc
   const int rank = aux[t.p[0]];
   // e0 is a multiple of ew_ts (a multiple of 16), e1 too or the element count,
   // which a qualifying view makes a multiple of the elements per 16 bytes
+  if (!scatter && gather_splat(aux, t.p[0], d, a, e0, e1, es)) return;
   if (gather_wide(aux, t.p[0], d, a, e0, e1, es, scatter)) return;
   if (rank > 8) {        // wide maps: direct evaluation per element
     for (uint64_t i = e0 + threadIdx.x; i < e1; i += kBlock) {

@@ -310,6 +310,38 @@ struct Lds16 {
   static constexpr int kBytes = 2 * kBuf * 2;   // double buffered, 2 bytes each
 };
 
+// How a general tile reads one operand's chunks of `per` consecutive logical
+// elements (8 16-bit or 4 f32, one 16-byte access): mode 0, straight from the
+// row-major operand (no view, rows a multiple of `per`, 16-byte aligned base);
+// mode 1, from the view's index of the chunk start (a view of rank <=
+// kViewRank whose innermost dim is contiguous, with that extent, the other
+// strides and the offset multiples of `per`, so each chunk is one aligned run:
+// the lowered decoder's attention output read as [tokens, heads * head_dim]);
+// mode 2, element by element (anything else).  Mode 1 (taken for A only) took
+// the lowered C5 prefill's output projection from 151 to 40 us per entry.
+struct OperandRead {
+  uint32_t mode;
+  ViewMap map;
+};
+VM_DEV OperandRead operand_read(const VM_K int32_t* aux, uint32_t view, const gbyte* base, uint32_t row_len,
+                                uint64_t n_elems, uint32_t per) {
+  OperandRead r;
+  r.map = view_map(aux, 0);
+  const bool aligned = (uintptr_t(base) & 15) == 0 && row_len % per == 0;
+  if (!view) {
+    r.mode = aligned ? 0u : 2u;
+    return r;
+  }
+  r.map = view_map(aux, view);
+  bool ok = aligned && n_elems <= 0xFFFFFFFFull && r.map.rank >= 1 && r.map.rank <= kViewRank &&
+            r.map.stride[0] == 1 && r.map.dim[0].d % per == 0 && r.map.off % per == 0;
+#pragma unroll
+  for (int k = 1; k < kViewRank; ++k)
+    if (k < r.map.rank && r.map.stride[k] % int32_t(per) != 0) ok = false;
+  r.mode = ok ? 1u : 2u;
+  return r;
+}
+
 template <int T>
 struct Stage16 {
   // A: T rows x kBK k in chunks of 8 elements; B: kBK rows x T cols, the same count.
@@ -318,15 +350,20 @@ struct Stage16 {
   v4u ra[kChunks];
   v4u rb[kChunks];
 
-  VM_DEV void load(Args A, const MmaDesc& D, uint32_t g, uint32_t m0, uint32_t n0, uint32_t k0, bool vec) {
+  VM_DEV void load(Args A, const MmaDesc& D, uint32_t g, uint32_t m0, uint32_t n0, uint32_t k0, const OperandRead& ar,
+                   const OperandRead& br) {
+    const VM_K int32_t* aux = aux_of(A);
 #pragma unroll
     for (int j = 0; j < kChunks; ++j) {
       const uint32_t c = threadIdx.x + j * kBlock;
       const uint32_t m = m0 + c / kRowChunks, k = k0 + (c % kRowChunks) * 8;
       const uint64_t lin = (uint64_t(g) * D.M + m) * D.K + k;
       const bool in = m < D.M && k < D.k1;
-      if (vec) ra[j] = in ? gld((const VM_G v4u*)(gcast<uint16_t>(D.a) + lin)) : v4u_make(0, 0, 0, 0);
-      else ra[j] = in ? gather_chunk(A, D.a, D.av, lin, D.k1 - k, 2) : v4u_make(0, 0, 0, 0);
+      if (ar.mode != 2)   // modes 0 and 1: view_at is the identity without a view
+        ra[j] = in ? gld((const VM_G v4u*)(gcast<uint16_t>(D.a) + (ar.mode ? view_at(ar.map, aux, D.av, uint32_t(lin)) : lin)))
+                   : v4u_make(0, 0, 0, 0);
+      else
+        ra[j] = in ? gather_chunk(A, D.a, D.av, lin, D.k1 - k, 2) : v4u_make(0, 0, 0, 0);
     }
 #pragma unroll
     for (int j = 0; j < kChunks; ++j) {
@@ -334,8 +371,10 @@ struct Stage16 {
       const uint32_t k = k0 + c / (T / 8), n = n0 + (c % (T / 8)) * 8;
       const uint64_t lin = (uint64_t(g) * D.K + k) * D.N + n;
       const bool in = k < D.k1 && n < D.N;
-      if (vec) rb[j] = in ? gld((const VM_G v4u*)(gcast<uint16_t>(D.b) + lin)) : v4u_make(0, 0, 0, 0);
-      else rb[j] = in ? gather_chunk(A, D.b, D.bv, lin, D.N - n, 2) : v4u_make(0, 0, 0, 0);
+      if (br.mode == 0)
+        rb[j] = in ? gld((const VM_G v4u*)(gcast<uint16_t>(D.b) + lin)) : v4u_make(0, 0, 0, 0);
+      else
+        rb[j] = in ? gather_chunk(A, D.b, D.bv, lin, D.N - n, 2) : v4u_make(0, 0, 0, 0);
     }
   }
   VM_DEV void store(uint16_t* lds) const {
@@ -415,7 +454,11 @@ VM_TILE void mma_tile16(Args A, const MmaDesc* Dp, uint32_t tile) {
   tile_origin(D, uni(tile), T, &g, &m0, &n0);
   const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const uint32_t wm = wave >> 1, wn = wave & 1;
-  const bool vec = !D.av && !D.bv && (D.K % 8) == 0 && (D.N % 8) == 0 && ((uintptr_t(D.a) | uintptr_t(D.b)) & 15) == 0;
+  const OperandRead ar = operand_read(aux_of(A), D.av, D.a, D.K, uint64_t(D.G) * D.M * D.K, 8);
+  // B (the weight, in every program seen) has no mode 1: viewed weights are
+  // transposes, whose innermost dim is not contiguous
+  OperandRead br = operand_read(aux_of(A), D.bv, D.b, D.N, uint64_t(D.G) * D.K * D.N, 8);
+  if (br.mode == 1) br.mode = 2;
 
   f32x16 acc[C::kBM][C::kBN];
 #pragma unroll
@@ -426,13 +469,13 @@ VM_TILE void mma_tile16(Args A, const MmaDesc* Dp, uint32_t tile) {
   constexpr int kBK = Lds16<T>::kBK;
   const uint32_t nk = (D.k1 - D.k0 + kBK - 1) / kBK;
   Stage16<T> st;
-  st.load(A, D, g, m0, n0, D.k0, vec);
+  st.load(A, D, g, m0, n0, D.k0, ar, br);
   __syncthreads();                      // previous user of the LDS is done
   st.store(lds);
   __syncthreads();
   for (uint32_t ks = 0; ks < nk; ++ks) {
     const uint16_t* cur = lds + (ks & 1) * Lds16<T>::kBuf;
-    if (ks + 1 < nk) st.load(A, D, g, m0, n0, D.k0 + (ks + 1) * kBK, vec);
+    if (ks + 1 < nk) st.load(A, D, g, m0, n0, D.k0 + (ks + 1) * kBK, ar, br);
     const uint16_t* la = cur;
     const uint16_t* lb = cur + Lds16<T>::kA;
 #pragma unroll

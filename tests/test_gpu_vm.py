@@ -677,6 +677,52 @@ def test_gemv_epilogue_bf16_out():
     assert_rel(got[1], want[1], 1e-5, 1e-5, "gemv affine + residual")
 
 
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+def test_dot_operand_views_with_contiguous_runs(dt):
+    """General matmul tiles reading operand views: A as the [tokens, heads *
+    head_dim] view of a [heads, tokens, head_dim] tensor (the lowered decoder's
+    attention output), read through 16-byte runs; B as the [K, N] view of
+    column blocks [N / 32, K, 32] (element path); then a head size of 12, whose
+    runs are not whole 16-byte chunks (element path for A too).  Integer
+    operands keep every product exact, so the results equal the oracle's bit
+    for bit."""
+    rng = np.random.default_rng(31)
+    for H, S, hd, N, tile in ((4, 96, 64, 96, 64), (4, 96, 64, 96, 128), (3, 70, 12, 64, 64)):
+        K = H * hd
+        att = rng.integers(-2, 3, (H, S, hd)).astype(np.float32)
+        wb = rng.integers(-2, 3, (N // 32, K, 32)).astype(np.float32)
+        cvt = (lambda x: vmref.f32_to_bf16(x)) if dt == "bf16" else (lambda x: x.astype(np.float16))
+        g = G.Graph()
+        ai, bi = g.input(att.shape, dt), g.input(wb.shape, dt)
+        a3 = g.view(ai, (S, H, hd), (hd, S * hd, 1))
+        b3 = g.view(bi, (K, N // 32, 32), (32, K * 32, 1))
+        a2 = G.Tensor(a3.buf, (S, K), a3.dtype, view=a3.view)
+        b2 = G.Tensor(b3.buf, (K, N), b3.dtype, view=b3.view)
+        g.output(g.dot(a2, b2, tile=tile))
+        got, want = run_both(g.build(), [cvt(att), cvt(wb)], oracle="tensor")
+        ref = att.transpose(1, 0, 2).reshape(S, K) @ wb.transpose(1, 0, 2).reshape(K, N)
+        np.testing.assert_array_equal(got[0], want[0], err_msg=f"{(H, S, hd, N, tile)}")
+        np.testing.assert_array_equal(got[0], ref.astype(np.float32), err_msg=f"{(H, S, hd, N, tile)}")
+
+
+@pytest.mark.parametrize("ew_ts", [256, 64])
+def test_broadcast_of_one_element(ew_ts):
+    """A view with every stride 0 (a constant broadcast into a buffer, as the
+    lowering emits for zero-filled caches): one load and 16-byte stores, the
+    ragged end element by element, for 1-, 2-, 4- and 8-byte elements."""
+    shape = (7, 9, 13)
+    g = G.Graph()
+    srcs = [np.array([3.25], np.float32), vmref.f32_to_bf16(np.array([-1.5], np.float32)),
+            np.array([-123456789012], np.int64), np.array([True])]
+    dts = ["f32", "bf16", "i64", "bool"]
+    ins = [g.input((1,), d) for d in dts]
+    g.output(*[g.materialize(g.view(t, shape, (0, 0, 0))) for t in ins])
+    got, want = run_both(g.build(), srcs, ew_ts=ew_ts)
+    for k, (gv, wv) in enumerate(zip(got, want)):
+        np.testing.assert_array_equal(gv, wv, err_msg=dts[k])
+        assert (np.asarray(gv).reshape(-1) == np.asarray(srcs[k]).reshape(-1)[0]).all(), dts[k]
+
+
 def _gemv_chain(dt, M, seed):
     """x -> three skinny matmuls in a row (each a phase after a grid barrier) ->
     a fourth against weights the program rewrites first.  Integer operands in
